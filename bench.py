@@ -1,0 +1,179 @@
+"""Benchmark: rows/s and achieved HBM GB/s of the full sampling chain.
+
+One step is one rl_sampler_sample_rows call over the whole batch of logit rows
+already resident in HBM: repetition penalty over each row's 64-id window,
+temperature, top-k, top-p, min-p and the draw against a host-drawn uniform,
+writing token, kept count, used flag and the kept (id, prob) candidates.
+
+Default workload: 1024 rows x 248320 f32 logits, N(0, 2^2) plus 16 spikes per
+row in [8, 14); T 0.6, top-k 20, top-p 0.95, min-p 0, repeat penalty 1.2 over
+64-id windows. Other workload shapes are parity cases (tests/) and can be timed
+with --workload.
+
+Prints one JSON line. `roofline.achieved` is the workload's algorithmic bytes
+per call divided by the average duration of a call, timed with HIP events on
+the stream the kernels run on. `cpu_baseline` times the oracle (the C
+restatement of the reference sampler) on one host core over a bounded sample
+of the same rows.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "rust-llm_amd"))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default=None)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="budget for the CPU-baseline sample (0 skips it)")
+    ap.add_argument("--no-candidates", action="store_true",
+                    help="skip the candidate outputs (tokens only)")
+    return ap.parse_args()
+
+
+def cpu_baseline(wl, logits, windows, wlen, uniforms, settings, budget_s):
+    """The oracle on one host core over rows of the same workload, cycling
+    until the time budget is spent. Returns rows/s and the sample size."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+
+    import oracle
+    osets = [oracle.Sampling(s.temperature, s.top_p, s.min_p, s.repeat_penalty, s.top_k, s.repeat_last_n, s.seed)
+             for s in settings]
+    rows = logits.shape[0]
+    batch = min(rows, 16)
+    done = 0
+    t0 = time.perf_counter()
+    r0 = 0
+    while True:
+        sl = slice(r0, r0 + batch)
+        oracle.pick_rows(logits[sl], osets[sl], windows[sl], wlen[sl], uniforms[sl], cand_cap=1)
+        done += batch
+        r0 = (r0 + batch) % (rows - batch + 1)
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return done / el, done, el
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: every box here has one GPU and the sampler's rows are "
+              "independent, so a multi-GPU run is not part of this build (asked for --gpus %d)" % args.gpus,
+              file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import rl_sampler as R
+    import workloads as W
+
+    name = args.workload or W.BENCH_WORKLOAD
+    wl = W.WORKLOADS[name]
+    dev = torch.device("cuda:0")
+    t0 = time.time()
+    logits, windows, wlen = wl.generate()
+    settings = wl.settings_list()
+    uniforms = wl.uniforms()
+    print("[bench] generated %s (%d x %d) in %.1fs" % (name, wl.rows, wl.vocab, time.time() - t0),
+          file=sys.stderr, flush=True)
+    d_logits = torch.from_numpy(logits).to(dev)
+    d_win = torch.from_numpy(windows.view(np.int32)).to(dev)
+    d_wlen = torch.from_numpy(wlen.view(np.int32)).to(dev)
+    d_uni = torch.from_numpy(uniforms).to(dev)
+    ctx = R.DeviceSampler(wl.rows, wl.vocab, max_window=W.WINDOW)
+    ctx.configure(settings)
+    cs = 0 if args.no_candidates else ctx.required_cand_stride()
+    out_tok = torch.empty(wl.rows, dtype=torch.int32, device=dev)
+    out_kept = torch.empty(wl.rows, dtype=torch.int32, device=dev)
+    out_used = torch.empty(wl.rows, dtype=torch.uint8, device=dev)
+    out_ids = torch.empty((wl.rows, cs), dtype=torch.int32, device=dev) if cs else None
+    out_probs = torch.empty((wl.rows, cs), dtype=torch.float32, device=dev) if cs else None
+    stream = torch.cuda.current_stream()
+
+    def step():
+        ctx.sample_rows(d_logits, wl.rows, d_logits.stride(0), out_tok, out_kept, out_used, windows=d_win,
+                        window_stride=W.WINDOW, window_len=d_wlen, uniforms=d_uni, out_ids=out_ids,
+                        out_probs=out_probs, cand_stride=cs, stream=stream.cuda_stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    t_wall = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    per_call_ms = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    mean_ms = sum(per_call_ms) / len(per_call_ms)
+    median_ms = per_call_ms[len(per_call_ms) // 2]
+    ms_per_step = wall * 1e3 / args.steps
+    rows_per_s = wl.rows / (ms_per_step / 1e3)
+    alg_bytes = wl.algorithmic_bytes() if cs else wl.algorithmic_bytes(kept_out=0)
+    achieved = alg_bytes / (mean_ms / 1e3) / 1e9
+    print("[bench] %s: wall %.3f ms/step, events mean %.3f median %.3f min %.3f max %.3f ms" % (
+        name, ms_per_step, mean_ms, median_ms, per_call_ms[0], per_call_ms[-1]), file=sys.stderr, flush=True)
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        rate, n, el = cpu_baseline(wl, logits, windows, wlen, uniforms, settings, args.cpu_seconds)
+        cpu = {"value": round(rate, 2), "unit": "rows/s", "cores": 1, "kind": "port",
+               "sample": "%d rows of the same workload (%s) through the oracle on one host core in %.1f s"
+                         % (n, name, el)}
+        print("[bench] cpu baseline %.1f rows/s over %d rows" % (rate, n), file=sys.stderr, flush=True)
+
+    s0 = settings[0]
+    line = {
+        "metric": "rows/s + achieved HBM GB/s, %dx%d fp32 logits, full sampling chain" % (wl.rows, wl.vocab),
+        "value": round(rows_per_s, 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded generator, rust-llm_amd/csrc/workloads.c)",
+        "config": {
+            "workload": "%s: %s" % (name, wl.description),
+            "rows": wl.rows,
+            "vocab": wl.vocab,
+            "temperature": s0.temperature, "top_k": s0.top_k, "top_p": s0.top_p, "min_p": s0.min_p,
+            "repeat_penalty": s0.repeat_penalty, "repeat_last_n": s0.repeat_last_n,
+            "candidates_out": bool(cs),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_call": alg_bytes,
+            "call_ms_mean": round(mean_ms, 5),
+            "call_ms_median": round(median_ms, 5),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

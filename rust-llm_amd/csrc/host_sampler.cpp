@@ -1,0 +1,482 @@
+// Host side of the drop-in: the reference's Sampler API over the device ABI.
+//
+// crates/rust-llm/src/sample.rs keeps, per Sampler, the settings, a ring of
+// recent tokens and an Rng (:132-151), and runs the whole pick on the CPU. Here
+// the same state stays on the host and the pick runs on the GPU: the window is
+// uploaded as recent[..filled], the uniform is pre-drawn from a clone of the
+// Rng, and the clone is committed only when the device reports that the row
+// drew (sample.rs:349), so the stream advances exactly as the reference's does.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <new>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "rl_error.h"
+#include "rl_sampler.h"
+#include "rl_sampler_host.h"
+
+namespace {
+
+int herr(int code, const std::string &m) {
+    rl::set_last_error(m);
+    return code;
+}
+
+uint64_t rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+
+bool penalises(const rl_sampling &s) { return s.repeat_penalty != 1.0f && s.repeat_last_n > 0; }
+
+bool same(const rl_sampling &a, const rl_sampling &b) { return std::memcmp(&a, &b, sizeof a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+void rl_rng_seeded(rl_rng *r, uint64_t seed) {
+    uint64_t z = seed;
+    for (int i = 0; i < 4; ++i) {  // splitmix64, sample.rs:375-381
+        z += 0x9E3779B97F4A7C15ull;
+        uint64_t v = z;
+        v = (v ^ (v >> 30)) * 0xBF58476D1CE4E5B9ull;
+        v = (v ^ (v >> 27)) * 0x94D049BB133111EBull;
+        r->s[i] = v ^ (v >> 31);
+    }
+}
+
+uint64_t rl_rng_next_u64(rl_rng *r) {  // xoshiro256++, sample.rs:387-398
+    uint64_t *s = r->s;
+    const uint64_t out = rotl(s[0] + s[3], 23) + s[0];
+    const uint64_t t = s[1] << 17;
+    s[2] ^= s[0];
+    s[3] ^= s[1];
+    s[1] ^= s[2];
+    s[0] ^= s[3];
+    s[2] ^= t;
+    s[3] = rotl(s[3], 45);
+    return out;
+}
+
+float rl_rng_next_f32(rl_rng *r) {  // sample.rs:401-403
+    return (float)(rl_rng_next_u64(r) >> 40) / (float)(1u << 24);
+}
+
+rl_sampling rl_sampling_default(void) {  // sample.rs:88-100
+    rl_sampling s{};
+    s.temperature = 0.6f;
+    s.top_k = 20;
+    s.top_p = 0.95f;
+    s.min_p = 0.0f;
+    s.repeat_penalty = 1.0f;
+    s.repeat_last_n = 64;
+    s.seed = 0;
+    return s;
+}
+
+rl_sampling rl_sampling_greedy(void) {  // sample.rs:71-79
+    rl_sampling s{};
+    s.temperature = 0.0f;
+    s.top_k = 0;
+    s.top_p = 1.0f;
+    s.min_p = 0.0f;
+    s.repeat_penalty = 1.0f;
+    s.repeat_last_n = 0;
+    s.seed = 0;
+    return s;
+}
+
+uint64_t rl_entropy_seed(void) {
+    std::random_device rd;
+    return ((uint64_t)rd() << 32) ^ rd();
+}
+
+}  // extern "C"
+
+struct rl_host_sampler {
+    int device = 0;
+    size_t vocab = 0;
+    rl_sampling set{};
+    uint32_t max_rows = 1;
+    uint32_t wcap = 0;  // window capacity per row on the device
+    std::vector<uint32_t> recent;
+    size_t at = 0, filled = 0;
+    rl_rng rng{};
+    rl_sampler_ctx *ctx = nullptr;
+    std::vector<rl_sampling> configured;  // what ctx was last configured with
+    uint64_t cand_cap = 1;
+    // device buffers
+    float *d_row = nullptr;
+    uint32_t *d_windows = nullptr, *d_wlen = nullptr, *d_token = nullptr, *d_kept = nullptr;
+    float *d_uniforms = nullptr;
+    uint8_t *d_used = nullptr;
+    uint32_t *d_ids = nullptr;
+    float *d_probs = nullptr;
+    // pinned host staging
+    uint32_t *h_windows = nullptr, *h_wlen = nullptr, *h_token = nullptr, *h_kept = nullptr;
+    float *h_uniforms = nullptr;
+    uint8_t *h_used = nullptr;
+    // the last call's survivors (Sampler::candidates)
+    std::vector<uint32_t> cand_ids;
+    std::vector<float> cand_probs;
+    size_t kept = 0;
+    // the last verify, uncommitted
+    struct Verified {
+        uint32_t token, kept;
+        uint8_t used;
+        float uniform;
+        std::vector<uint32_t> ids;
+        std::vector<float> probs;
+    };
+    std::vector<Verified> verified;
+    uint32_t next_commit = 0;
+    const float *v_rows = nullptr;
+    uint64_t v_stride = 0;
+    void *v_stream = nullptr;
+    std::vector<uint32_t> v_drafts;
+
+    ~rl_host_sampler() {
+        for (void *p : {(void *)d_row, (void *)d_windows, (void *)d_wlen, (void *)d_token, (void *)d_kept,
+                        (void *)d_uniforms, (void *)d_used, (void *)d_ids, (void *)d_probs})
+            if (p) (void)hipFree(p);
+        for (void *p : {(void *)h_windows, (void *)h_wlen, (void *)h_token, (void *)h_kept, (void *)h_uniforms,
+                        (void *)h_used})
+            if (p) (void)hipHostFree(p);
+        rl_sampler_destroy(ctx);
+    }
+
+    void remember(uint32_t t) {  // sample.rs:205-212
+        if (recent.empty()) return;
+        recent[at] = t;
+        at = (at + 1) % recent.size();
+        filled = std::min(filled + 1, recent.size());
+    }
+
+    // Configures the device context for `rows` rows of these settings.
+    int ensure_configured(const std::vector<rl_sampling> &want) {
+        if (configured.size() == want.size() &&
+            std::equal(want.begin(), want.end(), configured.begin(), same))
+            return RL_OK;
+        const int rc = rl_sampler_configure(ctx, want.data(), (uint32_t)want.size());
+        if (rc != RL_OK) return rc;
+        configured = want;
+        return RL_OK;
+    }
+
+    // The window row `i` of a verify sees: the ring after remembering
+    // drafts[0..i), as recent[..filled].
+    size_t window_after(const uint32_t *drafts, uint32_t i, uint32_t *out) const {
+        if (recent.empty()) return 0;
+        std::vector<uint32_t> r = recent;
+        size_t a = at, f = filled;
+        for (uint32_t d = 0; d < i; ++d) {
+            r[a] = drafts[d];
+            a = (a + 1) % r.size();
+            f = std::min(f + 1, r.size());
+        }
+        std::copy(r.begin(), r.begin() + f, out);
+        return f;
+    }
+
+    // Uploads windows/uniforms for `rows` rows, runs the device, and brings
+    // back tokens, kept counts and the used flags. Candidates stay on device.
+    int run(const float *d_logits, uint64_t stride, uint32_t rows, void *stream) {
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        hipError_t e = hipMemcpyAsync(d_windows, h_windows, (size_t)rows * wcap * 4, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(d_wlen, h_wlen, rows * 4, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(d_uniforms, h_uniforms, rows * 4, hipMemcpyHostToDevice, st);
+        if (e != hipSuccess) return herr(RL_ERR_DEVICE, hipGetErrorString(e));
+        const int rc = rl_sampler_sample_rows(ctx, d_logits, stride, rows, (uint32_t)vocab, d_windows, wcap, d_wlen,
+                                              d_uniforms, d_token, d_kept, d_used, d_ids, d_probs, cand_cap, stream);
+        if (rc != RL_OK) return rc;
+        e = hipMemcpyAsync(h_token, d_token, rows * 4, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(h_kept, d_kept, rows * 4, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(h_used, d_used, rows, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return herr(RL_ERR_DEVICE, hipGetErrorString(e));
+        return RL_OK;
+    }
+
+    int fetch_candidates(uint32_t row, uint32_t n, std::vector<uint32_t> &ids, std::vector<float> &probs,
+                         void *stream) {
+        ids.resize(n);
+        probs.resize(n);
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        hipError_t e = hipMemcpyAsync(ids.data(), d_ids + (uint64_t)row * cand_cap, n * 4, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(probs.data(), d_probs + (uint64_t)row * cand_cap, n * 4, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return herr(RL_ERR_DEVICE, hipGetErrorString(e));
+        return RL_OK;
+    }
+
+    int sample_device(const float *d_logits, size_t n, uint32_t *token, void *stream) {
+        if (n != vocab) return herr(RL_ERR_VOCAB, "this sampler was built for a different vocabulary");
+        int rc = ensure_configured(std::vector<rl_sampling>(1, set));
+        if (rc != RL_OK) return rc;
+        const bool pen = penalises(set) && filled > 0;
+        h_wlen[0] = pen ? (uint32_t)filled : 0u;
+        if (pen) std::copy(recent.begin(), recent.begin() + filled, h_windows);
+        rl_rng probe = rng;
+        h_uniforms[0] = rl_rng_next_f32(&probe);
+        rc = run(d_logits, vocab, 1, stream);
+        if (rc != RL_OK) return rc;
+        rc = fetch_candidates(0, h_kept[0], cand_ids, cand_probs, stream);
+        if (rc != RL_OK) return rc;
+        kept = h_kept[0];
+        if (h_used[0]) rng = probe;
+        *token = h_token[0];
+        remember(*token);  // sample.rs:217
+        verified.clear();
+        return RL_OK;
+    }
+};
+
+extern "C" {
+
+int rl_host_sampler_new(int device, size_t vocab, const rl_sampling *set, uint32_t max_rows,
+                        rl_host_sampler **out) {
+    if (!out || !set || vocab == 0 || vocab > 0xFFFFFFF0u || max_rows == 0)
+        return herr(RL_ERR_ARGUMENT, "bad argument");
+    *out = nullptr;
+    if (set->repeat_last_n > 2048) return herr(RL_ERR_CAPACITY, "repeat_last_n above 2048");
+    auto *s = new (std::nothrow) rl_host_sampler();
+    if (!s) return herr(RL_ERR_CAPACITY, "out of host memory");
+    s->device = device;
+    s->vocab = vocab;
+    s->set = *set;
+    s->max_rows = max_rows;
+    s->recent.assign((size_t)set->repeat_last_n, 0u);
+    s->wcap = std::max<uint32_t>(1u, (uint32_t)set->repeat_last_n);
+    rl_rng_seeded(&s->rng, set->seed);
+    // Candidate slots the settings can keep (sample.rs:159: the whole
+    // vocabulary unless greedy).
+    s->cand_cap = !(set->temperature <= 0.0f)
+                      ? ((set->top_k == 0 || set->top_k >= vocab) ? vocab : set->top_k)
+                      : 1;
+    int rc = rl_sampler_create(device, max_rows, (uint32_t)vocab, s->wcap, &s->ctx);
+    if (rc != RL_OK) {
+        delete s;
+        return rc;
+    }
+    int prev = 0;
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(device);
+    hipError_t e = hipMalloc(&s->d_row, vocab * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->d_windows, (size_t)max_rows * s->wcap * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->d_wlen, max_rows * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->d_token, max_rows * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->d_kept, max_rows * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->d_uniforms, max_rows * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->d_used, max_rows);
+    if (e == hipSuccess) e = hipMalloc(&s->d_ids, (size_t)max_rows * s->cand_cap * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->d_probs, (size_t)max_rows * s->cand_cap * 4);
+    if (e == hipSuccess) e = hipHostMalloc(&s->h_windows, (size_t)max_rows * s->wcap * 4);
+    if (e == hipSuccess) e = hipHostMalloc(&s->h_wlen, max_rows * 4);
+    if (e == hipSuccess) e = hipHostMalloc(&s->h_token, max_rows * 4);
+    if (e == hipSuccess) e = hipHostMalloc(&s->h_kept, max_rows * 4);
+    if (e == hipSuccess) e = hipHostMalloc(&s->h_uniforms, max_rows * 4);
+    if (e == hipSuccess) e = hipHostMalloc(&s->h_used, max_rows);
+    (void)hipSetDevice(prev);
+    if (e != hipSuccess) {
+        delete s;
+        return herr(RL_ERR_DEVICE, hipGetErrorString(e));
+    }
+    s->cand_ids.reserve(s->cand_cap);
+    s->cand_probs.reserve(s->cand_cap);
+    *out = s;
+    return RL_OK;
+}
+
+void rl_host_sampler_free(rl_host_sampler *s) { delete s; }
+
+rl_sampling rl_host_sampler_settings(const rl_host_sampler *s) { return s->set; }
+
+void rl_host_sampler_reset(rl_host_sampler *s) {  // sample.rs:194-198
+    s->at = 0;
+    s->filled = 0;
+    s->kept = 0;
+    s->verified.clear();
+}
+
+void rl_host_sampler_remember(rl_host_sampler *s, uint32_t token) { s->remember(token); }
+
+int rl_host_sampler_sample_device(rl_host_sampler *s, const float *device_row, size_t n, uint32_t *token,
+                                  void *stream) {
+    if (!s || !device_row || !token) return herr(RL_ERR_ARGUMENT, "null argument");
+    return s->sample_device(device_row, n, token, stream);
+}
+
+int rl_host_sampler_sample(rl_host_sampler *s, const float *host_logits, size_t n, uint32_t *token) {
+    if (!s || !host_logits || !token) return herr(RL_ERR_ARGUMENT, "null argument");
+    if (n != s->vocab) return herr(RL_ERR_VOCAB, "this sampler was built for a different vocabulary");
+    const hipError_t e = hipMemcpy(s->d_row, host_logits, n * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return herr(RL_ERR_DEVICE, hipGetErrorString(e));
+    return s->sample_device(s->d_row, n, token, nullptr);
+}
+
+size_t rl_host_sampler_candidates(const rl_host_sampler *s, const uint32_t **ids, const float **probs) {
+    *ids = s->cand_ids.data();
+    *probs = s->cand_probs.data();
+    return s->kept;
+}
+
+void rl_host_sampler_rng(const rl_host_sampler *s, rl_rng *out) { *out = s->rng; }
+
+int rl_host_sampler_verify(rl_host_sampler *s, const float *device_rows, uint64_t row_stride, size_t n,
+                           const uint32_t *drafts, uint32_t n_drafts, uint32_t *picks, void *stream) {
+    if (!s || !device_rows || !picks || (n_drafts && !drafts)) return herr(RL_ERR_ARGUMENT, "null argument");
+    if (n != s->vocab) return herr(RL_ERR_VOCAB, "this sampler was built for a different vocabulary");
+    const uint32_t rows = n_drafts + 1;
+    if (rows > s->max_rows) return herr(RL_ERR_CAPACITY, "more verify rows than max_rows");
+    int rc = s->ensure_configured(std::vector<rl_sampling>(rows, s->set));
+    if (rc != RL_OK) return rc;
+    const bool pen = penalises(s->set);
+    rl_rng probe = s->rng;
+    const bool greedy = s->set.temperature <= 0.0f;
+    for (uint32_t i = 0; i < rows; ++i) {
+        const size_t f = pen ? s->window_after(drafts, i, s->h_windows + (size_t)i * s->wcap) : 0;
+        s->h_wlen[i] = (uint32_t)f;
+        s->h_uniforms[i] = greedy ? 0.0f : rl_rng_next_f32(&probe);  // one draw per drawing row
+    }
+    rc = s->run(device_rows, row_stride, rows, stream);
+    if (rc != RL_OK) return rc;
+    s->verified.assign(rows, {});
+    for (uint32_t i = 0; i < rows; ++i) {
+        auto &v = s->verified[i];
+        v.token = s->h_token[i];
+        v.kept = s->h_kept[i];
+        v.used = s->h_used[i];
+        v.uniform = s->h_uniforms[i];
+        rc = s->fetch_candidates(i, v.kept, v.ids, v.probs, stream);
+        if (rc != RL_OK) return rc;
+        picks[i] = v.token;
+    }
+    s->next_commit = 0;
+    s->v_rows = device_rows;
+    s->v_stride = row_stride;
+    s->v_stream = stream;
+    s->v_drafts.assign(drafts, drafts + n_drafts);
+    return RL_OK;
+}
+
+int rl_host_sampler_commit_verified(rl_host_sampler *s, uint32_t row) {
+    if (!s) return herr(RL_ERR_ARGUMENT, "null sampler");
+    if (row != s->next_commit || row >= s->verified.size())
+        return herr(RL_ERR_ARGUMENT, "verify rows are committed in order, once");
+    auto &v = s->verified[row];
+    // The row was sampled with the uniform the stream would give if every
+    // earlier row drew; an earlier row with no finite maximum drew nothing, so
+    // recompute this one with the uniform the stream really gives now.
+    rl_rng probe = s->rng;
+    const float u = rl_rng_next_f32(&probe);
+    if (!(s->set.temperature <= 0.0f) && u != v.uniform) {
+        const bool pen = penalises(s->set) && s->filled > 0;
+        s->h_wlen[0] = pen ? (uint32_t)s->filled : 0u;
+        if (pen) std::copy(s->recent.begin(), s->recent.begin() + s->filled, s->h_windows);
+        s->h_uniforms[0] = u;
+        int rc = s->ensure_configured(std::vector<rl_sampling>(1, s->set));
+        if (rc == RL_OK) rc = s->run(s->v_rows + (uint64_t)row * s->v_stride, s->vocab, 1, s->v_stream);
+        if (rc == RL_OK) rc = s->fetch_candidates(0, s->h_kept[0], v.ids, v.probs, s->v_stream);
+        if (rc != RL_OK) return rc;
+        v.token = s->h_token[0];
+        v.kept = s->h_kept[0];
+        v.used = s->h_used[0];
+    }
+    if (v.used) s->rng = probe;
+    s->cand_ids = v.ids;
+    s->cand_probs = v.probs;
+    s->kept = v.kept;
+    s->remember(v.token);
+    s->next_commit = row + 1;
+    return RL_OK;
+}
+
+int rl_host_sample_batch(rl_host_sampler *const *samplers, uint32_t n, const float *device_logits,
+                         uint64_t row_stride, size_t vocab, uint32_t *tokens, void *stream) {
+    if (!samplers || n == 0 || !device_logits || !tokens) return herr(RL_ERR_ARGUMENT, "bad argument");
+    rl_host_sampler *h = samplers[0];
+    if (n > h->max_rows) return herr(RL_ERR_CAPACITY, "more samplers than the first one's max_rows");
+    std::vector<rl_sampling> want(n);
+    std::vector<rl_rng> probes(n);
+    for (uint32_t i = 0; i < n; ++i) {
+        rl_host_sampler *s = samplers[i];
+        if (s->vocab != vocab || vocab != h->vocab)
+            return herr(RL_ERR_VOCAB, "this sampler was built for a different vocabulary");
+        if (s->filled > h->wcap) return herr(RL_ERR_CAPACITY, "a window longer than the first sampler's");
+        if (s->cand_cap > h->cand_cap) return herr(RL_ERR_CAPACITY, "a sampler keeps more candidates than the first");
+        want[i] = s->set;
+        const bool pen = penalises(s->set) && s->filled > 0;
+        h->h_wlen[i] = pen ? (uint32_t)s->filled : 0u;
+        if (pen) std::copy(s->recent.begin(), s->recent.begin() + s->filled, h->h_windows + (size_t)i * h->wcap);
+        probes[i] = s->rng;
+        h->h_uniforms[i] = rl_rng_next_f32(&probes[i]);
+    }
+    int rc = h->ensure_configured(want);
+    if (rc != RL_OK) return rc;
+    rc = h->run(device_logits, row_stride, n, stream);
+    if (rc != RL_OK) return rc;
+    std::vector<uint32_t> ids;
+    std::vector<float> probs;
+    std::vector<uint32_t> tok(h->h_token, h->h_token + n), kept(h->h_kept, h->h_kept + n);
+    std::vector<uint8_t> used(h->h_used, h->h_used + n);
+    for (uint32_t i = 0; i < n; ++i) {
+        rl_host_sampler *s = samplers[i];
+        rc = h->fetch_candidates(i, kept[i], s->cand_ids, s->cand_probs, stream);
+        if (rc != RL_OK) return rc;
+        s->kept = kept[i];
+        if (used[i]) s->rng = probes[i];
+        tokens[i] = tok[i];
+        s->remember(tok[i]);
+        s->verified.clear();
+    }
+    return RL_OK;
+}
+
+int rl_host_argmax(int device, const float *logits, size_t n, uint32_t *out) {
+    if (!logits || !out || n == 0 || n > 0xFFFFFFF0u) return herr(RL_ERR_ARGUMENT, "bad argument");
+    struct Cache {
+        rl_sampler_ctx *ctx = nullptr;
+        float *d = nullptr;
+        uint32_t *tok = nullptr;
+        size_t cap = 0;
+        int device = -1;
+        ~Cache() {
+            if (d) (void)hipFree(d);
+            if (tok) (void)hipFree(tok);
+            rl_sampler_destroy(ctx);
+        }
+    };
+    thread_local Cache c;
+    int prev = 0;
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(device);
+    if (c.cap != n || c.device != device) {
+        if (c.d) (void)hipFree(c.d);
+        if (c.tok) (void)hipFree(c.tok);
+        rl_sampler_destroy(c.ctx);
+        c = Cache();
+        int rc = rl_sampler_create(device, 1, (uint32_t)n, 0, &c.ctx);
+        if (rc != RL_OK) {
+            (void)hipSetDevice(prev);
+            return rc;
+        }
+        if (hipMalloc(&c.d, n * 4) != hipSuccess || hipMalloc(&c.tok, 4) != hipSuccess) {
+            (void)hipSetDevice(prev);
+            return herr(RL_ERR_DEVICE, "hipMalloc");
+        }
+        c.cap = n;
+        c.device = device;
+    }
+    hipError_t e = hipMemcpy(c.d, logits, n * 4, hipMemcpyHostToDevice);
+    int rc = RL_OK;
+    if (e == hipSuccess) rc = rl_argmax_rows(c.ctx, c.d, n, 1, (uint32_t)n, c.tok, nullptr);
+    if (e == hipSuccess && rc == RL_OK) e = hipMemcpy(out, c.tok, 4, hipMemcpyDeviceToHost);
+    (void)hipSetDevice(prev);
+    if (e != hipSuccess) return herr(RL_ERR_DEVICE, hipGetErrorString(e));
+    return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,180 @@
+// Device-side helpers shared by the sampler kernels: the reference's orders as
+// integer keys, wave primitives for wave64, and the recent-token window set.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rl_sampler.h"
+
+namespace rl {
+
+constexpr uint32_t WAVE = 64;
+constexpr uint32_t EMPTY_ID = 0xFFFFFFFFu;
+
+// ---------------------------------------------------------------- orders --
+// f32::total_cmp (used by the selection and sort, sample.rs:282-286) as an
+// unsigned key: a larger key is later in the total order. -NaN < -inf < ... <
+// -0 < +0 < ... < +inf < +NaN.
+__device__ __forceinline__ uint32_t total_key(float v) {
+    const uint32_t b = __float_as_uint(v);
+    return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_value(uint32_t k) {
+    const uint32_t b = (k & 0x80000000u) ? (k ^ 0x80000000u) : ~k;
+    return __uint_as_float(b);
+}
+
+// Descending logit then ascending id, as one u64 that is larger for the
+// candidate that comes first. Composite 0 is never a real candidate (it would
+// need id 0xFFFFFFFF), so it pads buffers.
+__device__ __forceinline__ uint64_t composite(uint32_t key, uint32_t id) {
+    return ((uint64_t)key << 32) | (uint32_t)~id;
+}
+__device__ __forceinline__ uint32_t comp_key(uint64_t c) { return (uint32_t)(c >> 32); }
+__device__ __forceinline__ uint32_t comp_id(uint64_t c) { return ~(uint32_t)c; }
+
+// argmax's order (sample.rs:118-128): IEEE '>' from a start of -inf, so NaN
+// and -inf never win and -0 ties +0. As a key: 0 for NaN and -inf (they lose
+// to everything, and a row of only those returns id 0), else the total-order
+// key of v + 0.0 (which maps -0 to +0).
+__device__ __forceinline__ uint32_t argmax_key(float v) {
+    return (v > -__builtin_inff()) ? total_key(v + 0.0f) : 0u;
+}
+
+// sample.rs:249-253: a positive logit is divided by the penalty, anything
+// else (including -0 and NaN) multiplied.
+__device__ __forceinline__ float penalize(float v, float p) { return v > 0.0f ? v / p : v * p; }
+
+__device__ __forceinline__ bool penalises(const rl_sampling &s) {
+    return s.repeat_penalty != 1.0f && s.repeat_last_n > 0;  // sample.rs:82-84
+}
+
+// ---------------------------------------------------------- wave helpers --
+__device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+__device__ __forceinline__ uint32_t uniform_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
+    const uint32_t lo = uniform_u32((uint32_t)v);
+    const uint32_t hi = uniform_u32((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ float uniform_f32(float v) { return __uint_as_float(uniform_u32(__float_as_uint(v))); }
+
+__device__ __forceinline__ uint32_t read_lane_u32(uint32_t v, uint32_t lane) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)lane);
+}
+__device__ __forceinline__ float read_lane_f32(float v, uint32_t lane) {
+    return __uint_as_float(read_lane_u32(__float_as_uint(v), lane));
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    for (int m = 32; m >= 1; m >>= 1) {
+        const uint64_t o = shfl_xor_u64(v, m);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+__device__ __forceinline__ float wave_maxnum_f32(float v) {
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+
+// Orders this wave's LDS accesses: everything written before is visible to
+// every lane of the wave after.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Bitonic sort, descending, of n (a power of two, >= 2) u64 entries in LDS by
+// one wave.
+__device__ __forceinline__ void wave_sort_desc(uint64_t *buf, uint32_t n) {
+    const uint32_t lane = lane_id();
+    for (uint32_t size = 2; size <= n; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t t = lane; t < n / 2; t += WAVE) {
+                const uint32_t i = 2 * t - (t & (stride - 1));
+                const uint32_t j = i + stride;
+                const uint64_t x = buf[i], y = buf[j];
+                const bool desc = (i & size) == 0;
+                if (desc ? (x < y) : (x > y)) {
+                    buf[i] = y;
+                    buf[j] = x;
+                }
+            }
+            wave_lds_sync();
+        }
+    }
+}
+
+// ------------------------------------------------------ the window set ---
+// The recent-token window as an open-addressed set in LDS, built once per
+// workgroup: slot ids (EMPTY_ID when free) and the raw logit of each id, so the
+// penalised value can be formed without writing the logits. Inserting an id
+// twice keeps one slot, which is the reference's once-per-distinct-id rule
+// (sample.rs:242-247); ids >= vocab are skipped (sample.rs:248).
+struct WindowSet {
+    uint32_t *ids;
+    float *vals;
+    uint32_t bits;  // log2(slots)
+    uint32_t slots;
+};
+
+__device__ __forceinline__ uint32_t window_hash(uint32_t id, uint32_t bits) {
+    return (id * 0x9E3779B1u) >> (32u - bits);
+}
+
+__device__ __forceinline__ bool window_contains(const WindowSet &w, uint32_t id) {
+    uint32_t s = window_hash(id, w.bits);
+    for (;;) {
+        const uint32_t v = w.ids[s];
+        if (v == id) return true;
+        if (v == EMPTY_ID) return false;
+        s = (s + 1) & (w.slots - 1);
+    }
+}
+
+// Whole-workgroup: clears the set, inserts window[0..len), and gathers each
+// distinct id's raw logit from `row`. Ends with a barrier.
+__device__ __forceinline__ void window_build(WindowSet &w, const uint32_t *window, uint32_t len,
+                                             uint32_t vocab, const float *row, bool active) {
+    for (uint32_t i = threadIdx.x; i < w.slots; i += blockDim.x) w.ids[i] = EMPTY_ID;
+    __syncthreads();
+    if (active) {
+        for (uint32_t i = threadIdx.x; i < len; i += blockDim.x) {
+            const uint32_t id = window[i];
+            if (id >= vocab) continue;
+            uint32_t s = window_hash(id, w.bits);
+            for (;;) {
+                const uint32_t old = atomicCAS(&w.ids[s], EMPTY_ID, id);
+                if (old == EMPTY_ID) {
+                    w.vals[s] = row[id];
+                    break;
+                }
+                if (old == id) break;
+                s = (s + 1) & (w.slots - 1);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+}  // namespace rl

@@ -1,0 +1,321 @@
+// C ABI of the gfx950 token sampler (include/rl_sampler.h): context lifetime,
+// per-row path planning, and the launches. Kernels are in sampler_kernels.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "rl_error.h"
+#include "rl_sampler.h"
+#include "sampler_kernels.h"
+
+using namespace rl;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string &msg) {
+    rl::set_last_error(msg);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(RL_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+constexpr uint32_t MAX_WINDOW = 2048;
+constexpr uint32_t TARGET_WGS = 1024;  // enough workgroups to cover 256 CUs four deep
+constexpr uint32_t FULL_GROUP_MAX = 256;
+constexpr uint32_t CHUNK_SLOTS = 2 * TARGET_WGS;
+
+enum class Path : uint8_t { Stream, Full };
+
+// Which device path a row's settings take (see sampler_kernels.h).
+Path plan_row(const rl_sampling &s, uint32_t vocab) {
+    if (s.temperature <= 0.0f) return Path::Stream;
+    if (s.top_k >= 1 && s.top_k <= KMAX && s.top_k < vocab) return Path::Stream;
+    return Path::Full;
+}
+
+uint64_t row_cand_need(const rl_sampling &s, uint32_t vocab) {
+    if (s.temperature <= 0.0f) return 1;
+    if (s.top_k == 0 || s.top_k >= vocab) return vocab;
+    return s.top_k;
+}
+
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = true;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+}  // namespace
+
+void rl::set_last_error(const std::string &msg) { g_last_error = msg; }
+
+struct rl_sampler_ctx {
+    int device = 0;
+    uint32_t max_rows = 0, vocab = 0, max_window = 0, hash_bits = 0, full_group = 0;
+    rl_sampling *d_settings = nullptr;
+    uint32_t *d_stream_rows = nullptr, *d_full_rows = nullptr;
+    uint64_t *d_chunk_cands = nullptr;
+    uint32_t *d_chunk_counts = nullptr;
+    uint32_t *d_keyA = nullptr, *d_idA = nullptr, *d_keyB = nullptr, *d_idB = nullptr;
+    float *d_probs = nullptr;
+    float *d_part_max = nullptr;
+    uint64_t *d_part_am = nullptr;
+    uint64_t *d_argmax_part = nullptr;
+    std::vector<void *> owned;
+    // Host copy of the plan made by configure.
+    uint32_t configured = 0;
+    std::vector<uint32_t> stream_rows, full_rows;  // ascending
+    uint64_t cand_need = 0;
+    bool any_drawing = false;
+
+    template <class T>
+    hipError_t alloc(T **p, size_t count) {
+        void *v = nullptr;
+        const hipError_t e = hipMalloc(&v, std::max<size_t>(count, 1) * sizeof(T));
+        if (e == hipSuccess) {
+            owned.push_back(v);
+            *p = static_cast<T *>(v);
+        }
+        return e;
+    }
+    ~rl_sampler_ctx() {
+        for (void *p : owned) (void)hipFree(p);
+    }
+};
+
+extern "C" {
+
+const char *rl_sampler_last_error(void) { return g_last_error.c_str(); }
+
+int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t max_window,
+                      rl_sampler_ctx **out) {
+    if (!out) return fail(RL_ERR_ARGUMENT, "out is null");
+    *out = nullptr;
+    if (max_rows == 0 || vocab == 0) return fail(RL_ERR_ARGUMENT, "max_rows and vocab must be positive");
+    if (max_window > MAX_WINDOW)
+        return fail(RL_ERR_CAPACITY, "max_window above " + std::to_string(MAX_WINDOW));
+    DeviceGuard g(device);
+    if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select device " + std::to_string(device));
+    auto *c = new (std::nothrow) rl_sampler_ctx();
+    if (!c) return fail(RL_ERR_CAPACITY, "out of host memory");
+    c->device = device;
+    c->max_rows = max_rows;
+    c->vocab = vocab;
+    c->max_window = max_window;
+    uint32_t bits = 6;
+    while ((1u << bits) < 2 * max_window) ++bits;
+    c->hash_bits = bits;
+    c->full_group = std::min(max_rows, FULL_GROUP_MAX);
+    const size_t fg = c->full_group, V = vocab;
+    hipError_t e = hipSuccess;
+    if (e == hipSuccess) e = c->alloc(&c->d_settings, max_rows);
+    if (e == hipSuccess) e = c->alloc(&c->d_stream_rows, max_rows);
+    if (e == hipSuccess) e = c->alloc(&c->d_full_rows, max_rows);
+    // Rows are split into chunks only while rows < TARGET_WGS, with
+    // chunks <= ceil(TARGET_WGS / rows), so rows * chunks < 2 * TARGET_WGS.
+    if (e == hipSuccess) e = c->alloc(&c->d_chunk_cands, (size_t)CHUNK_SLOTS * KMAX);
+    if (e == hipSuccess) e = c->alloc(&c->d_chunk_counts, (size_t)CHUNK_SLOTS);
+    if (e == hipSuccess) e = c->alloc(&c->d_keyA, fg * V);
+    if (e == hipSuccess) e = c->alloc(&c->d_idA, fg * V);
+    if (e == hipSuccess) e = c->alloc(&c->d_keyB, fg * V);
+    if (e == hipSuccess) e = c->alloc(&c->d_idB, fg * V);
+    if (e == hipSuccess) e = c->alloc(&c->d_probs, fg * V);
+    if (e == hipSuccess) e = c->alloc(&c->d_part_max, fg * MAX_CHUNKS);
+    if (e == hipSuccess) e = c->alloc(&c->d_part_am, fg * MAX_CHUNKS);
+    if (e == hipSuccess) e = c->alloc(&c->d_argmax_part, std::max<size_t>(CHUNK_SLOTS, max_rows));
+    if (e != hipSuccess) {
+        delete c;
+        return hip_fail(e, "hipMalloc");
+    }
+    *out = c;
+    return RL_OK;
+}
+
+void rl_sampler_destroy(rl_sampler_ctx *ctx) {
+    if (!ctx) return;
+    DeviceGuard g(ctx->device);
+    (void)hipDeviceSynchronize();
+    delete ctx;
+}
+
+int rl_sampler_configure(rl_sampler_ctx *ctx, const rl_sampling *settings, uint32_t rows) {
+    if (!ctx || !settings) return fail(RL_ERR_ARGUMENT, "null argument");
+    if (rows == 0 || rows > ctx->max_rows)
+        return fail(RL_ERR_CAPACITY, "rows must be in 1..max_rows");
+    DeviceGuard g(ctx->device);
+    if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select device");
+    std::vector<uint32_t> sr, fr;
+    uint64_t need = 0;
+    bool drawing = false;
+    for (uint32_t r = 0; r < rows; ++r) {
+        (plan_row(settings[r], ctx->vocab) == Path::Stream ? sr : fr).push_back(r);
+        need = std::max(need, row_cand_need(settings[r], ctx->vocab));
+        drawing = drawing || !(settings[r].temperature <= 0.0f);
+    }
+    hipError_t e = hipMemcpy(ctx->d_settings, settings, rows * sizeof(rl_sampling), hipMemcpyHostToDevice);
+    if (e == hipSuccess && !sr.empty())
+        e = hipMemcpy(ctx->d_stream_rows, sr.data(), sr.size() * sizeof(uint32_t), hipMemcpyHostToDevice);
+    if (e == hipSuccess && !fr.empty())
+        e = hipMemcpy(ctx->d_full_rows, fr.data(), fr.size() * sizeof(uint32_t), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy (configure)");
+    ctx->configured = rows;
+    ctx->stream_rows = std::move(sr);
+    ctx->full_rows = std::move(fr);
+    ctx->cand_need = need;
+    ctx->any_drawing = drawing;
+    return RL_OK;
+}
+
+int rl_sampler_required_cand_stride(const rl_sampler_ctx *ctx, uint64_t *out) {
+    if (!ctx || !out) return fail(RL_ERR_ARGUMENT, "null argument");
+    if (!ctx->configured) return fail(RL_ERR_NOT_CONFIGURED, "configure first");
+    *out = ctx->cand_need;
+    return RL_OK;
+}
+
+int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t row_stride,
+                           uint32_t rows, uint32_t vocab, const uint32_t *windows,
+                           uint32_t window_stride, const uint32_t *window_len,
+                           const float *uniforms, uint32_t *out_token, uint32_t *out_kept,
+                           uint8_t *out_used_uniform, uint32_t *out_cand_ids,
+                           float *out_cand_probs, uint64_t cand_stride, void *stream) {
+    if (!ctx) return fail(RL_ERR_ARGUMENT, "ctx is null");
+    if (!ctx->configured) return fail(RL_ERR_NOT_CONFIGURED, "configure first");
+    if (vocab != ctx->vocab)
+        return fail(RL_ERR_VOCAB, "this sampler was built for a different vocabulary");
+    if (rows == 0) return RL_OK;
+    if (rows > ctx->configured) return fail(RL_ERR_CAPACITY, "more rows than configured");
+    if (!logits || !out_token || !out_kept || !out_used_uniform)
+        return fail(RL_ERR_ARGUMENT, "null logits or outputs");
+    if (rows > 1 && row_stride < vocab) return fail(RL_ERR_ARGUMENT, "row_stride below vocab");
+    if ((out_cand_ids == nullptr) != (out_cand_probs == nullptr))
+        return fail(RL_ERR_ARGUMENT, "candidate ids and probs must both be given or both be null");
+    if (out_cand_ids && cand_stride < ctx->cand_need)
+        return fail(RL_ERR_CAPACITY, "cand_stride below rl_sampler_required_cand_stride");
+    if (window_len && windows && window_stride > ctx->max_window)
+        return fail(RL_ERR_CAPACITY, "window_stride above max_window");
+    if (ctx->any_drawing && !uniforms) return fail(RL_ERR_ARGUMENT, "uniforms are null");
+    DeviceGuard g(ctx->device);
+    if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select device");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+
+    RowIO io{};
+    io.logits = logits;
+    io.stride = rows > 1 ? row_stride : vocab;
+    io.vocab = vocab;
+    io.settings = ctx->d_settings;
+    io.windows = (windows && window_len) ? windows : nullptr;
+    io.wstride = (windows && window_len) ? window_stride : 0;
+    io.wlen = (windows && window_len) ? window_len : nullptr;
+    io.uniforms = uniforms;
+    io.out_token = out_token;
+    io.out_kept = out_kept;
+    io.out_used = out_used_uniform;
+    io.out_ids = out_cand_ids;
+    io.out_probs = out_cand_probs;
+    io.cand_stride = cand_stride;
+    io.hash_bits = ctx->hash_bits;
+    const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (io.stride % 4 == 0);
+
+    // Rows below `rows` on each path (the lists are ascending).
+    const uint32_t ns = (uint32_t)(std::lower_bound(ctx->stream_rows.begin(), ctx->stream_rows.end(), rows) -
+                                   ctx->stream_rows.begin());
+    const uint32_t nf = (uint32_t)(std::lower_bound(ctx->full_rows.begin(), ctx->full_rows.end(), rows) -
+                                   ctx->full_rows.begin());
+    if (ns > 0) {
+        RowIO s = io;
+        s.rows = ctx->d_stream_rows;
+        const uint32_t n4 = vocab / 4;
+        uint32_t chunks = (TARGET_WGS + ns - 1) / ns;
+        chunks = std::min(chunks, MAX_CHUNKS);
+        chunks = std::min(chunks, std::max(1u, n4 / (FAST_THREADS * UNROLL)));
+        s.chunks = std::max(chunks, 1u);
+        FastScratch sc{ctx->d_chunk_cands, ctx->d_chunk_counts};
+        const size_t lds = fast_lds_bytes(ctx->hash_bits);
+        dim3 grid(s.chunks, ns);
+        if (vec)
+            hipLaunchKernelGGL(k_stream<true>, grid, dim3(FAST_THREADS), lds, st, s, sc);
+        else
+            hipLaunchKernelGGL(k_stream<false>, grid, dim3(FAST_THREADS), lds, st, s, sc);
+        if (s.chunks > 1)
+            hipLaunchKernelGGL(k_stream_finalize, dim3(ns), dim3(WAVE),
+                               KMAX * sizeof(uint64_t) + window_lds_bytes(ctx->hash_bits), st, s, sc);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return hip_fail(e, "stream kernels");
+    }
+    for (uint32_t g0 = 0; g0 < nf; g0 += ctx->full_group) {
+        const uint32_t ng = std::min(ctx->full_group, nf - g0);
+        RowIO f = io;
+        f.rows = ctx->d_full_rows + g0;
+        f.chunks = std::max(1u, std::min(MAX_CHUNKS, (TARGET_WGS + ng - 1) / ng));
+        f.chunks = std::min(f.chunks, std::max(1u, vocab / 4096));
+        FullScratch fs{ctx->d_keyA, ctx->d_idA, ctx->d_keyB, ctx->d_idB, ctx->d_probs, ctx->d_part_max,
+                       ctx->d_part_am};
+        hipLaunchKernelGGL(k_full_keys, dim3(f.chunks, ng), dim3(FULL_THREADS),
+                           window_lds_bytes(ctx->hash_bits), st, f, fs);
+        hipLaunchKernelGGL(k_full_sort, dim3(ng), dim3(SORT_THREADS), 0, st, f, fs);
+        hipLaunchKernelGGL(k_full_replay, dim3(ng), dim3(FULL_THREADS), 0, st, f, fs);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return hip_fail(e, "full-path kernels");
+    }
+    return RL_OK;
+}
+
+int rl_argmax_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t row_stride, uint32_t rows,
+                   uint32_t vocab, uint32_t *out_token, void *stream) {
+    if (!ctx) return fail(RL_ERR_ARGUMENT, "ctx is null");
+    if (vocab != ctx->vocab)
+        return fail(RL_ERR_VOCAB, "this sampler was built for a different vocabulary");
+    if (rows == 0) return RL_OK;
+    if (rows > ctx->max_rows) return fail(RL_ERR_CAPACITY, "more rows than max_rows");
+    if (!logits || !out_token) return fail(RL_ERR_ARGUMENT, "null logits or output");
+    if (rows > 1 && row_stride < vocab) return fail(RL_ERR_ARGUMENT, "row_stride below vocab");
+    DeviceGuard g(ctx->device);
+    if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select device");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const uint64_t stride = rows > 1 ? row_stride : vocab;
+    const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (stride % 4 == 0);
+    uint32_t chunks = std::min(MAX_CHUNKS, (TARGET_WGS + rows - 1) / rows);
+    chunks = std::max(1u, std::min(chunks, vocab / 4096));
+    dim3 grid(chunks, rows);
+    if (vec)
+        hipLaunchKernelGGL(k_argmax_part<true>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
+                           ctx->d_argmax_part);
+    else
+        hipLaunchKernelGGL(k_argmax_part<false>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
+                           ctx->d_argmax_part);
+    hipLaunchKernelGGL(k_argmax_final, dim3((rows + 255) / 256), dim3(256), 0, st, ctx->d_argmax_part, rows,
+                       chunks, out_token);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "argmax kernels");
+    return RL_OK;
+}
+
+int rl_sampler_expf_range(uint32_t lo_bits, uint64_t count, float *out, void *stream) {
+    if (!out) return fail(RL_ERR_ARGUMENT, "out is null");
+    if (count == 0) return RL_OK;
+    if (count > (1ull << 32) - lo_bits) return fail(RL_ERR_ARGUMENT, "range past 0xFFFFFFFF");
+    const uint64_t blocks = (count + 255) / 256;
+    hipLaunchKernelGGL(k_expf_range, dim3((uint32_t)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), lo_bits,
+                       count, out);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "expf kernel");
+    return RL_OK;
+}
+
+}  // extern "C"
