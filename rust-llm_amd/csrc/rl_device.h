@@ -11,6 +11,13 @@ namespace rl {
 constexpr uint32_t WAVE = 64;
 constexpr uint32_t EMPTY_ID = 0xFFFFFFFFu;
 
+// Address-space-qualified pointers: LDS accesses compile to ds_* and HBM
+// accesses to global_* instructions. Generic (flat) accesses would be counted
+// against both the LDS and the memory wait counters, so an LDS access in the
+// streaming loop would wait for every load in flight.
+#define RL_LDS __attribute__((address_space(3)))
+#define RL_GLB __attribute__((address_space(1)))
+
 // ---------------------------------------------------------------- orders --
 // f32::total_cmp (used by the selection and sort, sample.rs:282-286) as an
 // unsigned key: a larger key is later in the total order. -NaN < -inf < ... <
@@ -96,33 +103,49 @@ __device__ __forceinline__ float wave_maxnum_f32(float v) {
     return v;
 }
 
+// Bitonic sort of one u64 per lane across the wave, descending: lane i ends
+// with the i-th largest of the 64 values.
+__device__ __forceinline__ uint64_t wave_sort64_desc(uint64_t v) {
+    const uint32_t lane = lane_id();
+#pragma unroll
+    for (uint32_t size = 2; size <= WAVE; size <<= 1) {
+#pragma unroll
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            const uint64_t o = shfl_xor_u64(v, (int)stride);
+            const bool lower = (lane & stride) == 0;
+            const bool desc = (lane & size) == 0;
+            const bool keep_max = lower == desc;
+            v = keep_max ? (o > v ? o : v) : (o < v ? o : v);
+        }
+    }
+    return v;
+}
+
+// The 64 largest of two descending lane-vectors (lane i holds the i-th of
+// each), descending: the elementwise max of a and reversed b is a bitonic
+// sequence holding the top 64, which a half-cleaner cascade sorts.
+__device__ __forceinline__ uint64_t wave_merge64_desc(uint64_t a, uint64_t b) {
+    const uint32_t lane = lane_id();
+    const uint32_t src = (WAVE - 1 - lane) * 4;
+    const uint32_t blo = (uint32_t)__builtin_amdgcn_ds_bpermute((int)src, (int)(uint32_t)b);
+    const uint32_t bhi = (uint32_t)__builtin_amdgcn_ds_bpermute((int)src, (int)(uint32_t)(b >> 32));
+    const uint64_t br = ((uint64_t)bhi << 32) | blo;
+    uint64_t v = a > br ? a : br;
+#pragma unroll
+    for (uint32_t stride = WAVE / 2; stride > 0; stride >>= 1) {
+        const uint64_t o = shfl_xor_u64(v, (int)stride);
+        const bool lower = (lane & stride) == 0;
+        v = lower ? (o > v ? o : v) : (o < v ? o : v);
+    }
+    return v;
+}
+
 // Orders this wave's LDS accesses: everything written before is visible to
 // every lane of the wave after.
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Bitonic sort, descending, of n (a power of two, >= 2) u64 entries in LDS by
-// one wave.
-__device__ __forceinline__ void wave_sort_desc(uint64_t *buf, uint32_t n) {
-    const uint32_t lane = lane_id();
-    for (uint32_t size = 2; size <= n; size <<= 1) {
-        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            for (uint32_t t = lane; t < n / 2; t += WAVE) {
-                const uint32_t i = 2 * t - (t & (stride - 1));
-                const uint32_t j = i + stride;
-                const uint64_t x = buf[i], y = buf[j];
-                const bool desc = (i & size) == 0;
-                if (desc ? (x < y) : (x > y)) {
-                    buf[i] = y;
-                    buf[j] = x;
-                }
-            }
-            wave_lds_sync();
-        }
-    }
 }
 
 // ------------------------------------------------------ the window set ---
@@ -132,11 +155,20 @@ __device__ __forceinline__ void wave_sort_desc(uint64_t *buf, uint32_t n) {
 // twice keeps one slot, which is the reference's once-per-distinct-id rule
 // (sample.rs:242-247); ids >= vocab are skipped (sample.rs:248).
 struct WindowSet {
-    uint32_t *ids;
-    float *vals;
+    RL_LDS uint32_t *ids;
+    RL_LDS float *vals;
     uint32_t bits;  // log2(slots)
     uint32_t slots;
 };
+
+__device__ __forceinline__ WindowSet window_set(void *lds_base, uint32_t bits) {
+    WindowSet w;
+    w.bits = bits;
+    w.slots = 1u << bits;
+    w.ids = (RL_LDS uint32_t *)lds_base;
+    w.vals = (RL_LDS float *)(w.ids + w.slots);
+    return w;
+}
 
 __device__ __forceinline__ uint32_t window_hash(uint32_t id, uint32_t bits) {
     return (id * 0x9E3779B1u) >> (32u - bits);
@@ -154,7 +186,7 @@ __device__ __forceinline__ bool window_contains(const WindowSet &w, uint32_t id)
 
 // Whole-workgroup: clears the set, inserts window[0..len), and gathers each
 // distinct id's raw logit from `row`. Ends with a barrier.
-__device__ __forceinline__ void window_build(WindowSet &w, const uint32_t *window, uint32_t len,
+__device__ __forceinline__ void window_build(const WindowSet &w, const uint32_t *window, uint32_t len,
                                              uint32_t vocab, const float *row, bool active) {
     for (uint32_t i = threadIdx.x; i < w.slots; i += blockDim.x) w.ids[i] = EMPTY_ID;
     __syncthreads();
@@ -164,9 +196,9 @@ __device__ __forceinline__ void window_build(WindowSet &w, const uint32_t *windo
             if (id >= vocab) continue;
             uint32_t s = window_hash(id, w.bits);
             for (;;) {
-                const uint32_t old = atomicCAS(&w.ids[s], EMPTY_ID, id);
+                const uint32_t old = atomicCAS((uint32_t *)&w.ids[s], EMPTY_ID, id);
                 if (old == EMPTY_ID) {
-                    w.vals[s] = row[id];
+                    w.vals[s] = ((const RL_GLB float *)row)[id];
                     break;
                 }
                 if (old == id) break;

@@ -246,15 +246,14 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
         chunks = std::min(chunks, std::max(1u, n4 / (FAST_THREADS * UNROLL)));
         s.chunks = std::max(chunks, 1u);
         FastScratch sc{ctx->d_chunk_cands, ctx->d_chunk_counts};
-        const size_t lds = fast_lds_bytes(ctx->hash_bits);
+        const size_t lds = window_lds_bytes(ctx->hash_bits);
         dim3 grid(s.chunks, ns);
         if (vec)
             hipLaunchKernelGGL(k_stream<true>, grid, dim3(FAST_THREADS), lds, st, s, sc);
         else
             hipLaunchKernelGGL(k_stream<false>, grid, dim3(FAST_THREADS), lds, st, s, sc);
         if (s.chunks > 1)
-            hipLaunchKernelGGL(k_stream_finalize, dim3(ns), dim3(WAVE),
-                               KMAX * sizeof(uint64_t) + window_lds_bytes(ctx->hash_bits), st, s, sc);
+            hipLaunchKernelGGL(k_stream_finalize, dim3(ns), dim3(WAVE), window_lds_bytes(ctx->hash_bits), st, s, sc);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return hip_fail(e, "stream kernels");
     }

@@ -77,72 +77,105 @@ __device__ __forceinline__ void write_single(const RowIO &a, uint32_t row, uint3
     }
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 template <bool VEC>
-__device__ __forceinline__ float4 load4(const float *row, uint32_t f) {
+__device__ __forceinline__ f32x4 load4(const float *row, uint32_t f) {
+    const RL_GLB float *g = (const RL_GLB float *)row;
     if constexpr (VEC) {
-        return reinterpret_cast<const float4 *>(row)[f];
+        return ((const RL_GLB f32x4 *)g)[f];
     } else {
-        const float *p = row + 4ull * f;
-        return make_float4(p[0], p[1], p[2], p[3]);
+        const RL_GLB float *p = g + 4ull * f;
+        return f32x4{p[0], p[1], p[2], p[3]};
     }
 }
 
+__device__ __forceinline__ uint64_t read_lane_u64(uint64_t v, uint32_t lane) {
+    return ((uint64_t)read_lane_u32((uint32_t)(v >> 32), lane) << 32) | read_lane_u32((uint32_t)v, lane);
+}
+
 // ------------------------------------------------- per-wave candidates ---
-struct WaveCands {
-    uint64_t *buf;       // LDS, WBUF entries
-    uint64_t *shared_T;  // LDS, the workgroup's threshold
-    uint64_t T;          // everything kept is > T (a k-th best seen somewhere)
-    float thr;           // value of T's key: a cheap necessary test
+// A wave of the stream kernel keeps candidates in an LDS buffer of WBUF
+// composites. T is a lower bound on the row's k-th best composite (this wave's
+// k-th best so far, or another wave's, shared through an LDS atomic max):
+// nothing <= T can be among the row's k best. `thr` is the value of T's key,
+// a one-compare necessary test for composite > T.
+struct Stream {
+    RL_LDS uint64_t *buf;
+    RL_LDS uint64_t *shared_T;
+    uint64_t T;
+    float thr;
     uint32_t cnt;
     uint32_t k;
     bool greedy;
 };
 
-// Necessary condition for composite(x) > T, one compare: in greedy mode the
-// starting -FLT_MAX also drops NaN and -inf, which argmax never picks; in
-// sampled mode !(x < thr) lets NaN through to the exact test.
-__device__ __forceinline__ bool prefilter(const WaveCands &w, float x) {
-    return w.greedy ? (x >= w.thr) : !(x < w.thr);
-}
+struct Compacted {
+    uint64_t T;
+    uint32_t cnt;
+};
 
-__device__ __forceinline__ void take_threshold(WaveCands &w, uint64_t t) {
+// Necessary condition for composite(x) > T, one compare. !(x < thr) lets NaN
+// through to the exact test (a NaN sorts first in the total order); in greedy
+// mode the starting -FLT_MAX drops -inf, and the exact test drops NaN, which
+// argmax never picks.
+__device__ __forceinline__ bool prefilter(const Stream &w, float x) { return !(x < w.thr); }
+
+__device__ __forceinline__ void raise_threshold(Stream &w, uint64_t t) {
     if (t > w.T) {
         w.T = t;
         w.thr = key_value(comp_key(t));
     }
 }
 
-__device__ __forceinline__ void refresh(WaveCands &w) {
-    const uint64_t s = uniform_u64(__hip_atomic_load((unsigned long long *)w.shared_T, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_WORKGROUP));
-    take_threshold(w, s);
+__device__ __forceinline__ uint64_t load_shared_T(RL_LDS uint64_t *p) {
+    return uniform_u64(__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
 }
 
-// Keeps the wave's k best, sorted, and raises the threshold to the k-th.
-__device__ __noinline__ void compact(WaveCands &w) {
+__device__ __forceinline__ void publish_threshold(RL_LDS uint64_t *p, uint64_t t) {
+    if (lane_id() == 0) __hip_atomic_fetch_max(p, t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Keeps the k best of buf[0..cnt) (cnt <= WBUF), sorted, at buf[0..min(cnt, k))
+// and returns the raised threshold. Register-resident: lane i holds buf[i],
+// buf[i+64], ...; each column is sorted across the wave and the columns are
+// merged pairwise.
+__device__ __noinline__ Compacted compact(RL_LDS uint64_t *buf, uint32_t cnt, uint32_t k, uint64_t T,
+                                          RL_LDS uint64_t *shared_T) {
     const uint32_t lane = lane_id();
     wave_lds_sync();
-    for (uint32_t i = lane; i < WBUF; i += WAVE)
-        if (i >= w.cnt) w.buf[i] = 0;
-    wave_lds_sync();
-    wave_sort_desc(w.buf, WBUF);
-    if (w.cnt >= w.k) {
-        const uint64_t t = uniform_u64(w.buf[w.k - 1]);
-        w.cnt = w.k;
-        take_threshold(w, t);
-        if (lane == 0) atomicMax((unsigned long long *)w.shared_T, (unsigned long long)w.T);
+    uint64_t v[WBUF / WAVE];
+#pragma unroll
+    for (uint32_t i = 0; i < WBUF / WAVE; ++i) {
+        const uint32_t j = lane + i * WAVE;
+        v[i] = j < cnt ? buf[j] : 0ull;
     }
-    refresh(w);
+#pragma unroll
+    for (uint32_t i = 0; i < WBUF / WAVE; ++i) v[i] = wave_sort64_desc(v[i]);
+    const uint64_t top = wave_merge64_desc(wave_merge64_desc(v[0], v[1]), wave_merge64_desc(v[2], v[3]));
+    const uint32_t n = cnt < k ? cnt : k;
+    if (lane < n) buf[lane] = top;
+    if (cnt >= k) {
+        const uint64_t t = read_lane_u64(top, k - 1);
+        if (t > T) T = t;
+        publish_threshold(shared_T, T);
+    }
+    const uint64_t s = load_shared_T(shared_T);
+    if (s > T) T = s;
+    wave_lds_sync();
+    return {T, n};
 }
 
 // Appends this wave's passing lanes (ballot compaction), compacting first when
 // the buffer would overflow.
-__device__ __forceinline__ void offer(WaveCands &w, bool pass, uint64_t c) {
+__device__ __forceinline__ void offer(Stream &w, bool pass, uint64_t c) {
     uint64_t m = ballot(pass);
     if (m == 0) return;
     uint32_t n = __popcll(m);
     if (w.cnt + n > WBUF) {
-        compact(w);
+        const Compacted r = compact(w.buf, w.cnt, w.k, w.T, w.shared_T);
+        w.cnt = r.cnt;
+        raise_threshold(w, r.T);
         pass = pass && (c > w.T);
         m = ballot(pass);
         if (m == 0) return;
@@ -152,9 +185,13 @@ __device__ __forceinline__ void offer(WaveCands &w, bool pass, uint64_t c) {
     w.cnt += n;
 }
 
+__device__ __forceinline__ uint32_t stream_key(const Stream &w, float x) {
+    return w.greedy ? total_key(x + 0.0f) : total_key(x);
+}
+
 template <bool CHECK>
-__device__ __forceinline__ void offer_group(WaveCands &w, const WindowSet &ws, bool pen, float4 v,
-                                            uint32_t id0, uint32_t nvalid) {
+__device__ __forceinline__ void offer_group(Stream &w, const WindowSet &ws, bool pen, f32x4 v, uint32_t id0,
+                                            uint32_t nvalid) {
     const float x[4] = {v.x, v.y, v.z, v.w};
     bool any = false;
 #pragma unroll
@@ -165,45 +202,54 @@ __device__ __forceinline__ void offer_group(WaveCands &w, const WindowSet &ws, b
         bool p = (!CHECK || c < nvalid) && prefilter(w, x[c]);
         uint64_t comp = 0;
         if (p) {
-            const uint32_t key = w.greedy ? total_key(x[c] + 0.0f) : total_key(x[c]);
-            comp = composite(key, id0 + c);
-            p = comp > w.T;
+            comp = composite(stream_key(w, x[c]), id0 + c);
+            p = comp > w.T && (!w.greedy || x[c] >= -3.40282347e38f);
             if (p && pen) p = !window_contains(ws, id0 + c);
         }
         offer(w, p, comp);
     }
 }
 
-// k-way merge of sorted lists (one list per lane) by repeated wave max; writes
-// the best k to out and returns how many there were.
-__device__ __forceinline__ uint32_t merge_heads(const uint64_t *lists, uint32_t list_stride,
-                                                const uint32_t *counts, uint32_t nlists, uint32_t k,
-                                                uint64_t *out) {
-    const uint32_t lane = lane_id();
-    const uint32_t cnt = lane < nlists ? counts[lane] : 0u;
-    uint32_t pos = 0;
-    uint32_t n = 0;
-    for (; n < k; ++n) {
-        const uint64_t h = pos < cnt ? lists[(uint64_t)lane * list_stride + pos] : 0ull;
-        const uint64_t mx = wave_max_u64(h);
-        if (mx == 0) break;
-        if (pos < cnt && h == mx) ++pos;
-        if (lane == 0) out[n] = mx;
+// A first threshold from the wave's first tile: each lane's best element
+// (window ids excluded), then the k-th best of those 64 lane maxima. At least
+// k distinct elements reach it, so it is a valid bound.
+__device__ __forceinline__ void bootstrap(Stream &w, const WindowSet &ws, bool pen, const f32x4 *A, uint32_t base) {
+    const uint32_t tid = threadIdx.x;
+    uint64_t bound = ~0ull, best = 0;
+    for (uint32_t attempt = 0; attempt < 4; ++attempt) {
+        best = 0;
+#pragma unroll
+        for (uint32_t u = 0; u < UNROLL; ++u) {
+            const float x[4] = {A[u].x, A[u].y, A[u].z, A[u].w};
+            const uint32_t id0 = 4 * (base + u * FAST_THREADS + tid);
+#pragma unroll
+            for (uint32_t c = 0; c < 4; ++c) {
+                const bool ok = !w.greedy || x[c] >= -3.40282347e38f;
+                const uint64_t comp = composite(stream_key(w, x[c]), id0 + c);
+                if (ok && comp < bound && comp > best) best = comp;
+            }
+        }
+        if (!pen || best == 0 || !window_contains(ws, comp_id(best))) break;
+        bound = best;
+        best = 0;
     }
-    wave_lds_sync();
-    return n;
+    const uint64_t sorted = wave_sort64_desc(best);
+    const uint64_t t = read_lane_u64(sorted, w.k - 1);
+    raise_threshold(w, t);
+    publish_threshold(w.shared_T, w.T);
 }
 
 // The row's f32::max fold over the penalised logits and its argmax, by one
 // wave re-reading the row. Only for a row whose k best are all +NaN, where the
 // candidates do not reveal the largest non-NaN value.
-__device__ __noinline__ void rescan_row(const float *rowp, uint32_t vocab, const WindowSet &ws,
-                                        bool pen, float penalty, float *out_max, uint32_t *out_tok) {
+__device__ __noinline__ void rescan_row(const float *rowp, uint32_t vocab, const WindowSet &ws, bool pen,
+                                        float penalty, float *out_max, uint32_t *out_tok) {
     const uint32_t lane = lane_id();
+    const RL_GLB float *g = (const RL_GLB float *)rowp;
     float mx = -__builtin_inff();
     uint64_t am = 0;
     for (uint32_t e = lane; e < vocab; e += WAVE) {
-        float x = rowp[e];
+        float x = g[e];
         if (pen && window_contains(ws, e)) x = penalize(x, penalty);
         mx = fmaxf(mx, x);
         const uint64_t c = composite(argmax_key(x), e);
@@ -214,22 +260,21 @@ __device__ __noinline__ void rescan_row(const float *rowp, uint32_t vocab, const
     *out_tok = comp_key(am) == 0 ? 0u : comp_id(am);
 }
 
-// The reference's tail (sample.rs:259-358) over the row's best nL candidates
-// L (sorted, descending), by one wave: candidate j sits in lane j. The
-// sequential f64 and f32 sums are replayed in candidate order with readlane,
-// so every lane computes the same bits the reference does.
-__device__ __noinline__ void finalize_row(const RowIO &a, uint32_t row, const rl_sampling &s,
-                                          uint32_t k, const uint64_t *L, uint32_t nL,
-                                          const WindowSet &ws, bool pen, const float *rowp) {
+// The reference's tail (sample.rs:259-358) over the row's best nL candidates,
+// by one wave: lane j holds candidate j (composite c, 0 past nL), in
+// descending order. The sequential f64 and f32 sums are replayed in candidate
+// order with readlane, so every lane computes the bits the reference does.
+__device__ __noinline__ void finalize_row(const RowIO &a, uint32_t row, const rl_sampling &s, uint32_t k,
+                                          uint64_t c, uint32_t nL, const WindowSet &ws, bool pen,
+                                          const float *rowp) {
     const uint32_t lane = lane_id();
     if (s.temperature <= 0.0f) {  // greedy: argmax (sample.rs:259-265)
-        const uint64_t c0 = nL ? uniform_u64(L[0]) : 0ull;
-        const uint32_t tok = (comp_key(c0) == 0) ? 0u : comp_id(c0);
+        const uint64_t c0 = read_lane_u64(c, 0);
+        const uint32_t tok = (nL == 0 || comp_key(c0) == 0) ? 0u : comp_id(c0);
         if (lane == 0) write_single(a, row, tok);
         return;
     }
     const bool in = lane < nL;
-    const uint64_t c = in ? L[lane] : 0ull;
     const float v = key_value(comp_key(c));
     const uint32_t id = comp_id(c);
     const bool isnan_v = v != v;
@@ -319,38 +364,19 @@ __device__ __noinline__ void finalize_row(const RowIO &a, uint32_t row, const rl
     }
 }
 
-// LDS layout of the stream kernel (dynamic shared memory).
-struct FastLds {
-    uint64_t *wbufs;     // FAST_WAVES * WBUF
-    uint64_t *mlist;     // KMAX
-    uint64_t *shared_T;  // 1
-    uint32_t *wcount;    // FAST_WAVES
-    WindowSet ws;
-};
-
-__host__ __device__ constexpr size_t fast_lds_bytes(uint32_t hash_bits) {
-    return (FAST_WAVES * WBUF + KMAX + 2) * sizeof(uint64_t) + FAST_WAVES * sizeof(uint32_t) +
-           ((size_t)1 << hash_bits) * (sizeof(uint32_t) + sizeof(float));
+__host__ __device__ constexpr size_t window_lds_bytes(uint32_t hash_bits) {
+    return ((size_t)1 << hash_bits) * (sizeof(uint32_t) + sizeof(float));
 }
 
-__device__ __forceinline__ FastLds fast_lds(uint8_t *smem, uint32_t hash_bits) {
-    FastLds l;
-    l.wbufs = reinterpret_cast<uint64_t *>(smem);
-    l.mlist = l.wbufs + FAST_WAVES * WBUF;
-    l.shared_T = l.mlist + KMAX;
-    l.wcount = reinterpret_cast<uint32_t *>(l.shared_T + 2);
-    l.ws.bits = hash_bits;
-    l.ws.slots = 1u << hash_bits;
-    l.ws.ids = l.wcount + FAST_WAVES;
-    l.ws.vals = reinterpret_cast<float *>(l.ws.ids + l.ws.slots);
-    return l;
-}
-
-// grid (chunks, rows on this path), FAST_THREADS threads.
+// grid (chunks, rows on this path), FAST_THREADS threads. Dynamic LDS: the
+// window set.
 template <bool VEC>
 __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc) {
+    __shared__ uint64_t s_buf[FAST_WAVES * WBUF];
+    __shared__ uint64_t s_T;
+    __shared__ uint32_t s_cnt[FAST_WAVES];
     extern __shared__ __align__(16) uint8_t smem[];
-    FastLds l = fast_lds(smem, a.hash_bits);
+    const WindowSet ws = window_set(smem, a.hash_bits);
     const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
     const uint32_t row = a.rows[slot];
     const rl_sampling s = a.settings[row];
@@ -360,20 +386,9 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
     const bool pen = penalises(s) && wl > 0;
     const float *rowp = a.logits + (uint64_t)row * a.stride;
     const uint32_t V = a.vocab;
-    const uint32_t wave = threadIdx.x / WAVE;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = tid / WAVE;
     const uint32_t lane = lane_id();
-
-    if (threadIdx.x == 0) *l.shared_T = 0;
-    window_build(l.ws, a.windows + (uint64_t)row * a.wstride, wl, V, rowp, pen);
-
-    WaveCands w;
-    w.buf = l.wbufs + wave * WBUF;
-    w.shared_T = l.shared_T;
-    w.T = 0;
-    w.thr = greedy ? -3.40282347e38f : -__builtin_inff();
-    w.cnt = 0;
-    w.k = k;
-    w.greedy = greedy;
 
     const uint32_t n4 = V / 4;
     const uint32_t q0 = (uint32_t)((uint64_t)chunk * n4 / a.chunks);
@@ -381,58 +396,68 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
     constexpr uint32_t STEP = FAST_THREADS * UNROLL;
     const uint32_t ntiles = (q1 - q0) / STEP;
 
-    float4 A[UNROLL], B[UNROLL];
+    // The first tile's loads go out before the window set is built.
+    f32x4 A[UNROLL], B[UNROLL];
     if (ntiles > 0) {
 #pragma unroll
-        for (uint32_t u = 0; u < UNROLL; ++u) A[u] = load4<VEC>(rowp, q0 + u * FAST_THREADS + threadIdx.x);
+        for (uint32_t u = 0; u < UNROLL; ++u) A[u] = load4<VEC>(rowp, q0 + u * FAST_THREADS + tid);
     }
+    RL_LDS uint64_t *lT = (RL_LDS uint64_t *)&s_T;
+    if (tid == 0) *lT = 0;
+    window_build(ws, a.windows + (uint64_t)row * a.wstride, wl, V, rowp, pen);
+
+    Stream w;
+    w.buf = (RL_LDS uint64_t *)s_buf + wave * WBUF;
+    w.shared_T = lT;
+    w.T = 0;
+    w.thr = greedy ? -3.40282347e38f : -__builtin_inff();
+    w.cnt = 0;
+    w.k = k;
+    w.greedy = greedy;
+
+    if (ntiles > 0) bootstrap(w, ws, pen, A, q0);
     for (uint32_t t = 0; t < ntiles; t += 2) {
         const uint32_t b0 = q0 + t * STEP, b1 = b0 + STEP, b2 = b1 + STEP;
         if (t + 1 < ntiles) {
 #pragma unroll
-            for (uint32_t u = 0; u < UNROLL; ++u) B[u] = load4<VEC>(rowp, b1 + u * FAST_THREADS + threadIdx.x);
+            for (uint32_t u = 0; u < UNROLL; ++u) B[u] = load4<VEC>(rowp, b1 + u * FAST_THREADS + tid);
         }
 #pragma unroll
-        for (uint32_t u = 0; u < UNROLL; ++u) {
-            const uint32_t f = b0 + u * FAST_THREADS + threadIdx.x;
-            offer_group<false>(w, l.ws, pen, A[u], 4 * f, 4);
-        }
+        for (uint32_t u = 0; u < UNROLL; ++u) offer_group<false>(w, ws, pen, A[u], 4 * (b0 + u * FAST_THREADS + tid), 4);
         if (t + 2 < ntiles) {
 #pragma unroll
-            for (uint32_t u = 0; u < UNROLL; ++u) A[u] = load4<VEC>(rowp, b2 + u * FAST_THREADS + threadIdx.x);
+            for (uint32_t u = 0; u < UNROLL; ++u) A[u] = load4<VEC>(rowp, b2 + u * FAST_THREADS + tid);
         }
         if (t + 1 < ntiles) {
 #pragma unroll
-            for (uint32_t u = 0; u < UNROLL; ++u) {
-                const uint32_t f = b1 + u * FAST_THREADS + threadIdx.x;
-                offer_group<false>(w, l.ws, pen, B[u], 4 * f, 4);
-            }
+            for (uint32_t u = 0; u < UNROLL; ++u)
+                offer_group<false>(w, ws, pen, B[u], 4 * (b1 + u * FAST_THREADS + tid), 4);
         }
-        refresh(w);
+        raise_threshold(w, load_shared_T(lT));
     }
     // The chunk's partial tile, then the row's last vocab % 4 elements.
     const uint32_t rb = q0 + ntiles * STEP;
     for (uint32_t u = 0; u < UNROLL; ++u) {
-        const uint32_t f = rb + u * FAST_THREADS + threadIdx.x;
+        const uint32_t f = rb + u * FAST_THREADS + tid;
         const bool ok = f < q1;
-        const float4 v = ok ? load4<VEC>(rowp, f) : make_float4(0.f, 0.f, 0.f, 0.f);
-        offer_group<true>(w, l.ws, pen, v, 4 * f, ok ? 4u : 0u);
+        const f32x4 v = ok ? load4<VEC>(rowp, f) : f32x4{0.f, 0.f, 0.f, 0.f};
+        offer_group<true>(w, ws, pen, v, 4 * f, ok ? 4u : 0u);
     }
     if (chunk == a.chunks - 1) {
-        const uint32_t e = 4 * n4 + threadIdx.x;
+        const uint32_t e = 4 * n4 + tid;
         const bool ok = e < V;
-        const float x = ok ? rowp[e] : 0.0f;
-        offer_group<true>(w, l.ws, pen, make_float4(x, 0.f, 0.f, 0.f), e, ok ? 1u : 0u);
+        const float x = ok ? ((const RL_GLB float *)rowp)[e] : 0.0f;
+        offer_group<true>(w, ws, pen, f32x4{x, 0.f, 0.f, 0.f}, e, ok ? 1u : 0u);
     }
     // The window's ids with their penalised values, once per row.
     if (pen && chunk == 0) {
-        for (uint32_t base = wave * WAVE; base < l.ws.slots; base += FAST_THREADS) {
+        for (uint32_t base = wave * WAVE; base < ws.slots; base += FAST_THREADS) {
             const uint32_t i = base + lane;
-            const uint32_t id = i < l.ws.slots ? l.ws.ids[i] : EMPTY_ID;
+            const uint32_t id = i < ws.slots ? ws.ids[i] : EMPTY_ID;
             bool p = false;
             uint64_t c = 0;
             if (id != EMPTY_ID) {
-                const float x = penalize(l.ws.vals[i], s.repeat_penalty);
+                const float x = penalize(ws.vals[i], s.repeat_penalty);
                 const uint32_t key = greedy ? argmax_key(x) : total_key(x);
                 c = composite(key, id);
                 p = (!greedy || key != 0) && c > w.T;
@@ -440,16 +465,27 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
             offer(w, p, c);
         }
     }
-    compact(w);
-    if (lane == 0) l.wcount[wave] = w.cnt;
+    const Compacted r = compact(w.buf, w.cnt, k, w.T, lT);
+    if (lane == 0) s_cnt[wave] = r.cnt;
     __syncthreads();
     if (wave != 0) return;
-    const uint32_t nL = merge_heads(l.wbufs, WBUF, l.wcount, FAST_WAVES, k, l.mlist);
+    // Merge the four sorted lists: lane i of list j is candidate i of wave j.
+    const RL_LDS uint64_t *lb = (const RL_LDS uint64_t *)s_buf;
+    uint64_t top = lane < s_cnt[0] ? lb[lane] : 0ull;
+    uint32_t total = s_cnt[0];
+#pragma unroll
+    for (uint32_t j = 1; j < FAST_WAVES; ++j) {
+        const uint64_t o = lane < s_cnt[j] ? lb[j * WBUF + lane] : 0ull;
+        top = wave_merge64_desc(top, o);
+        total += s_cnt[j];
+    }
+    const uint32_t nL = total < k ? total : k;
+    if (lane >= nL) top = 0;
     if (a.chunks == 1) {
-        finalize_row(a, row, s, k, l.mlist, nL, l.ws, pen, rowp);
+        finalize_row(a, row, s, k, top, nL, ws, pen, rowp);
     } else {
         uint64_t *dst = sc.chunk_cands + ((uint64_t)slot * a.chunks + chunk) * KMAX;
-        if (lane < nL) dst[lane] = l.mlist[lane];
+        if (lane < nL) dst[lane] = top;
         if (lane == 0) sc.chunk_counts[slot * a.chunks + chunk] = nL;
     }
 }
@@ -457,12 +493,7 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
 // grid (rows on this path), one wave: merges the chunks' lists and finishes.
 __global__ __launch_bounds__(WAVE) void k_stream_finalize(RowIO a, FastScratch sc) {
     extern __shared__ __align__(16) uint8_t smem[];
-    uint64_t *mlist = reinterpret_cast<uint64_t *>(smem);
-    WindowSet ws;
-    ws.bits = a.hash_bits;
-    ws.slots = 1u << a.hash_bits;
-    ws.ids = reinterpret_cast<uint32_t *>(mlist + KMAX);
-    ws.vals = reinterpret_cast<float *>(ws.ids + ws.slots);
+    const WindowSet ws = window_set(smem, a.hash_bits);
     const uint32_t slot = blockIdx.x;
     const uint32_t row = a.rows[slot];
     const rl_sampling s = a.settings[row];
@@ -471,16 +502,24 @@ __global__ __launch_bounds__(WAVE) void k_stream_finalize(RowIO a, FastScratch s
     const uint32_t wl = window_len(a, row);
     const bool pen = penalises(s) && wl > 0;
     const float *rowp = a.logits + (uint64_t)row * a.stride;
+    const uint32_t lane = lane_id();
     window_build(ws, a.windows + (uint64_t)row * a.wstride, wl, a.vocab, rowp, pen);
-    const uint32_t nL = merge_heads(sc.chunk_cands + (uint64_t)slot * a.chunks * KMAX, KMAX,
-                                    sc.chunk_counts + slot * a.chunks, a.chunks, k, mlist);
-    finalize_row(a, row, s, k, mlist, nL, ws, pen, rowp);
+    const uint64_t *lists = sc.chunk_cands + (uint64_t)slot * a.chunks * KMAX;
+    const uint32_t *counts = sc.chunk_counts + slot * a.chunks;
+    uint64_t top = 0;
+    uint32_t total = 0;
+    for (uint32_t j = 0; j < a.chunks; ++j) {
+        const uint32_t n = counts[j];
+        const uint64_t o = lane < n ? lists[(uint64_t)j * KMAX + lane] : 0ull;
+        top = wave_merge64_desc(top, o);
+        total += n;
+    }
+    const uint32_t nL = total < k ? total : k;
+    if (lane >= nL) top = 0;
+    finalize_row(a, row, s, k, top, nL, ws, pen, rowp);
 }
 
 // ---------------------------------------------------------- FULL path ---
-__host__ __device__ constexpr size_t window_lds_bytes(uint32_t hash_bits) {
-    return ((size_t)1 << hash_bits) * (sizeof(uint32_t) + sizeof(float));
-}
 
 __device__ __forceinline__ uint32_t full_k(const rl_sampling &s, uint32_t V) {
     return s.top_k == 0 ? V : (s.top_k < V ? (uint32_t)s.top_k : V);  // sample.rs:289
@@ -493,11 +532,7 @@ __device__ __forceinline__ bool identity_order(const rl_sampling &s, uint32_t V)
 // id order, plus per-chunk f32::max fold and argmax.
 __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch f) {
     extern __shared__ __align__(16) uint8_t smem[];
-    WindowSet ws;
-    ws.bits = a.hash_bits;
-    ws.slots = 1u << a.hash_bits;
-    ws.ids = reinterpret_cast<uint32_t *>(smem);
-    ws.vals = reinterpret_cast<float *>(ws.ids + ws.slots);
+    const WindowSet ws = window_set(smem, a.hash_bits);
     __shared__ float red_max[FULL_THREADS / WAVE];
     __shared__ uint64_t red_am[FULL_THREADS / WAVE];
     const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
@@ -812,7 +847,7 @@ __global__ __launch_bounds__(FAST_THREADS) void k_argmax_part(const float *logit
     const uint32_t q1 = (uint32_t)((uint64_t)(chunk + 1) * n4 / chunks);
     uint64_t best = 0;
     for (uint32_t f = q0 + threadIdx.x; f < q1; f += FAST_THREADS) {
-        const float4 v = load4<VEC>(rowp, f);
+        const f32x4 v = load4<VEC>(rowp, f);
         const float x[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (uint32_t c = 0; c < 4; ++c) {
