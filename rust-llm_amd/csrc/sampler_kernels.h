@@ -211,8 +211,10 @@ __device__ __forceinline__ void offer_group(Stream &w, const WindowSet &ws, bool
 }
 
 // A first threshold from the wave's first tile: each lane's best element
-// (window ids excluded), then the k-th best of those 64 lane maxima. At least
-// k distinct elements reach it, so it is a valid bound.
+// (window ids excluded), then the k-th best t of those 64 lane maxima. At
+// least k distinct elements are >= t, so nothing below t is among the row's k
+// best; the threshold is t - 1 because the k elements >= t are not in any
+// buffer yet and must still pass the strict test composite > T.
 __device__ __forceinline__ void bootstrap(Stream &w, const WindowSet &ws, bool pen, const f32x4 *A, uint32_t base) {
     const uint32_t tid = threadIdx.x;
     uint64_t bound = ~0ull, best = 0;
@@ -235,7 +237,7 @@ __device__ __forceinline__ void bootstrap(Stream &w, const WindowSet &ws, bool p
     }
     const uint64_t sorted = wave_sort64_desc(best);
     const uint64_t t = read_lane_u64(sorted, w.k - 1);
-    raise_threshold(w, t);
+    raise_threshold(w, t ? t - 1 : 0ull);
     publish_threshold(w.shared_T, w.T);
 }
 
