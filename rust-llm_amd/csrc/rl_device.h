@@ -103,41 +103,79 @@ __device__ __forceinline__ float wave_maxnum_f32(float v) {
     return v;
 }
 
-// Bitonic sort of one u64 per lane across the wave, descending: lane i ends
-// with the i-th largest of the 64 values.
-__device__ __forceinline__ uint64_t wave_sort64_desc(uint64_t v) {
-    const uint32_t lane = lane_id();
-#pragma unroll
-    for (uint32_t size = 2; size <= WAVE; size <<= 1) {
-#pragma unroll
-        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            const uint64_t o = shfl_xor_u64(v, (int)stride);
-            const bool lower = (lane & stride) == 0;
-            const bool desc = (lane & size) == 0;
-            const bool keep_max = lower == desc;
-            v = keep_max ? (o > v ? o : v) : (o < v ? o : v);
-        }
+// Lane exchange: lane i receives v from lane i ^ S, using DPP row operations
+// for S <= 8 and the gfx950 permlane swaps for 16 and 32 (VALU ops, no LDS
+// round trip). Lane layouts as measured on gfx950: quad_perm [1,0,3,2] and
+// [2,3,0,1] are xor 1 and xor 2; row_shl:4 / row_shr:4 read lane i+4 / i-4
+// within a row of 16; row_ror:8 reads lane i^8; permlane16_swap(v, v) returns
+// {rows 0,0,2,2; rows 1,1,3,3} and permlane32_swap(v, v) {low, low; high,
+// high} halves.
+template <uint32_t S>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+    if constexpr (S == 1) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+    } else if constexpr (S == 2) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+    } else if constexpr (S == 4) {
+        const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x104, 0xF, 0xF, false);
+        const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);
+        return (lane_id() & 4) ? dn : up;
+    } else if constexpr (S == 8) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
+    } else if constexpr (S == 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane_id() & 16) ? p[0] : p[1];
+    } else {
+        static_assert(S == 32, "lane_xor stride");
+        const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane_id() & 32) ? p[0] : p[1];
     }
+}
+
+template <uint32_t S>
+__device__ __forceinline__ uint64_t lane_xor64(uint64_t v) {
+    return ((uint64_t)lane_xor<S>((uint32_t)(v >> 32)) << 32) | lane_xor<S>((uint32_t)v);
+}
+
+// One compare-exchange stage of a bitonic network across the wave: lanes i
+// and i^STRIDE, blocks of SIZE lanes alternately descending and ascending
+// (the final SIZE = 64 block runs in the direction DESC).
+template <uint32_t SIZE, uint32_t STRIDE, bool DESC>
+__device__ __forceinline__ uint64_t bitonic_stage(uint64_t v) {
+    const uint32_t lane = lane_id();
+    const uint64_t o = lane_xor64<STRIDE>(v);
+    const bool lower = (lane & STRIDE) == 0;
+    const bool block_desc = ((lane & SIZE) == 0) == DESC;
+    const bool keep_max = lower == block_desc;
+    const bool o_big = o > v;
+    return (keep_max == o_big) ? o : v;
+}
+
+template <uint32_t SIZE, uint32_t STRIDE, bool DESC>
+__device__ __forceinline__ uint64_t bitonic_merge(uint64_t v) {
+    v = bitonic_stage<SIZE, STRIDE, DESC>(v);
+    if constexpr (STRIDE > 1) v = bitonic_merge<SIZE, STRIDE / 2, DESC>(v);
     return v;
 }
 
-// The 64 largest of two descending lane-vectors (lane i holds the i-th of
-// each), descending: the elementwise max of a and reversed b is a bitonic
-// sequence holding the top 64, which a half-cleaner cascade sorts.
-__device__ __forceinline__ uint64_t wave_merge64_desc(uint64_t a, uint64_t b) {
-    const uint32_t lane = lane_id();
-    const uint32_t src = (WAVE - 1 - lane) * 4;
-    const uint32_t blo = (uint32_t)__builtin_amdgcn_ds_bpermute((int)src, (int)(uint32_t)b);
-    const uint32_t bhi = (uint32_t)__builtin_amdgcn_ds_bpermute((int)src, (int)(uint32_t)(b >> 32));
-    const uint64_t br = ((uint64_t)bhi << 32) | blo;
-    uint64_t v = a > br ? a : br;
-#pragma unroll
-    for (uint32_t stride = WAVE / 2; stride > 0; stride >>= 1) {
-        const uint64_t o = shfl_xor_u64(v, (int)stride);
-        const bool lower = (lane & stride) == 0;
-        v = lower ? (o > v ? o : v) : (o < v ? o : v);
-    }
-    return v;
+template <uint32_t SIZE, bool DESC>
+__device__ __forceinline__ uint64_t bitonic_sort(uint64_t v) {
+    if constexpr (SIZE > 2) v = bitonic_sort<SIZE / 2, DESC>(v);
+    return bitonic_merge<SIZE, SIZE / 2, DESC>(v);
+}
+
+// Sorts one u64 per lane across the wave: lane i ends with the i-th largest
+// (DESC) or the i-th smallest.
+template <bool DESC>
+__device__ __forceinline__ uint64_t wave_sort64(uint64_t v) {
+    return bitonic_sort<WAVE, DESC>(v);
+}
+
+// The 64 largest of a (descending across lanes) and b (ascending),
+// descending: max(a_i, b_i) is a bitonic sequence holding the top 64, which a
+// half-cleaner cascade sorts.
+__device__ __forceinline__ uint64_t wave_merge64(uint64_t a_desc, uint64_t b_asc) {
+    return bitonic_merge<WAVE, WAVE / 2, true>(a_desc > b_asc ? a_desc : b_asc);
 }
 
 // Orders this wave's LDS accesses: everything written before is visible to

@@ -21,7 +21,6 @@ namespace rl {
 constexpr uint32_t FAST_THREADS = 256;
 constexpr uint32_t FAST_WAVES = FAST_THREADS / WAVE;
 constexpr uint32_t KMAX = 64;     // largest top_k the stream path takes (one per lane)
-constexpr uint32_t WBUF = 256;    // per-wave candidate buffer
 constexpr uint32_t UNROLL = 8;    // float4 loads per thread per tile
 constexpr uint32_t MAX_CHUNKS = 32;
 constexpr uint32_t FULL_THREADS = 256;
@@ -79,14 +78,28 @@ __device__ __forceinline__ void write_single(const RowIO &a, uint32_t row, uint3
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Row loads are nontemporal: each logit is read once, so they should not
+// displace anything from the caches.
 template <bool VEC>
 __device__ __forceinline__ f32x4 load4(const float *row, uint32_t f) {
     const RL_GLB float *g = (const RL_GLB float *)row;
     if constexpr (VEC) {
-        return ((const RL_GLB f32x4 *)g)[f];
+        return __builtin_nontemporal_load((const RL_GLB f32x4 *)g + f);
     } else {
         const RL_GLB float *p = g + 4ull * f;
-        return f32x4{p[0], p[1], p[2], p[3]};
+        return f32x4{__builtin_nontemporal_load(p), __builtin_nontemporal_load(p + 1),
+                     __builtin_nontemporal_load(p + 2), __builtin_nontemporal_load(p + 3)};
+    }
+}
+
+// One tile of UNROLL float4 per thread, starting at float4 index `base`;
+// with GUARD, indices at or past `end` read as nothing.
+template <bool VEC, bool GUARD>
+__device__ __forceinline__ void load_tile(f32x4 *dst, const float *row, uint32_t base, uint32_t end) {
+#pragma unroll
+    for (uint32_t u = 0; u < UNROLL; ++u) {
+        const uint32_t f = base + u * FAST_THREADS + threadIdx.x;
+        if (!GUARD || f < end) dst[u] = load4<VEC>(row, f);
     }
 }
 
@@ -95,24 +108,30 @@ __device__ __forceinline__ uint64_t read_lane_u64(uint64_t v, uint32_t lane) {
 }
 
 // ------------------------------------------------- per-wave candidates ---
-// A wave of the stream kernel keeps candidates in an LDS buffer of WBUF
-// composites. T is a lower bound on the row's k-th best composite (this wave's
-// k-th best so far, or another wave's, shared through an LDS atomic max):
-// nothing <= T can be among the row's k best. `thr` is the value of T's key,
-// a one-compare necessary test for composite > T.
+// A wave of the stream kernel keeps candidates in an LDS buffer. T is a lower
+// bound on the row's k-th best composite (this wave's k-th best so far, or
+// another wave's, shared through an LDS atomic max): nothing <= T can be among
+// the row's k best. `thr` is the value of T's key, a one-compare necessary
+// test for composite > T. Candidates are appended without a capacity check;
+// the buffer holds KMAX entries plus one half-tile's worth, and compaction
+// runs before every half-tile whose passers might not fit. The kernel makes
+// no function calls: a call would give every wave a scratch frame, and with
+// it a slower launch and spills around the call sites.
+constexpr uint32_t HALF = UNROLL / 2;                  // float4 per thread per half-tile
+constexpr uint32_t HALF_ELEMS = HALF * 4 * WAVE;        // elements a wave filters per half-tile
+constexpr uint32_t SLACK = 48;                          // new candidates between compactions
+constexpr uint32_t CBUF = KMAX + SLACK + HALF_ELEMS;    // per-wave candidate buffer
+
 struct Stream {
     RL_LDS uint64_t *buf;
     RL_LDS uint64_t *shared_T;
+    WindowSet ws;
     uint64_t T;
     float thr;
     uint32_t cnt;
     uint32_t k;
     bool greedy;
-};
-
-struct Compacted {
-    uint64_t T;
-    uint32_t cnt;
+    bool pen;
 };
 
 // Necessary condition for composite(x) > T, one compare. !(x < thr) lets NaN
@@ -122,6 +141,7 @@ struct Compacted {
 __device__ __forceinline__ bool prefilter(const Stream &w, float x) { return !(x < w.thr); }
 
 __device__ __forceinline__ void raise_threshold(Stream &w, uint64_t t) {
+    t = uniform_u64(t);
     if (t > w.T) {
         w.T = t;
         w.thr = key_value(comp_key(t));
@@ -136,53 +156,42 @@ __device__ __forceinline__ void publish_threshold(RL_LDS uint64_t *p, uint64_t t
     if (lane_id() == 0) __hip_atomic_fetch_max(p, t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Keeps the k best of buf[0..cnt) (cnt <= WBUF), sorted, at buf[0..min(cnt, k))
-// and returns the raised threshold. Register-resident: lane i holds buf[i],
-// buf[i+64], ...; each column is sorted across the wave and the columns are
-// merged pairwise.
-__device__ __noinline__ Compacted compact(RL_LDS uint64_t *buf, uint32_t cnt, uint32_t k, uint64_t T,
-                                          RL_LDS uint64_t *shared_T) {
+// Sorts this wave's candidates, 64 at a time across the wave, keeps the k best
+// at buf[0..cnt) and raises the threshold to the k-th. Penalised window ids
+// enter the buffer unchecked (a hash lookup per passing element would stall
+// the loop on LDS); they are dropped here, so the threshold is the k-th best of
+// non-window elements only. Returns the sorted best 64 (lane i holds the i-th).
+__device__ __forceinline__ uint64_t compact(Stream &w) {
     const uint32_t lane = lane_id();
     wave_lds_sync();
-    uint64_t v[WBUF / WAVE];
-#pragma unroll
-    for (uint32_t i = 0; i < WBUF / WAVE; ++i) {
-        const uint32_t j = lane + i * WAVE;
-        v[i] = j < cnt ? buf[j] : 0ull;
+    uint64_t top = 0;
+    uint32_t valid = 0;
+    for (uint32_t base = 0; base < w.cnt; base += WAVE) {
+        const uint32_t j = base + lane;
+        uint64_t v = j < w.cnt ? w.buf[j] : 0ull;
+        if (w.pen && v != 0 && window_contains(w.ws, comp_id(v))) v = 0;
+        valid += (uint32_t)__popcll(ballot(v != 0));
+        top = wave_merge64(top, wave_sort64<false>(v));
     }
-#pragma unroll
-    for (uint32_t i = 0; i < WBUF / WAVE; ++i) v[i] = wave_sort64_desc(v[i]);
-    const uint64_t top = wave_merge64_desc(wave_merge64_desc(v[0], v[1]), wave_merge64_desc(v[2], v[3]));
-    const uint32_t n = cnt < k ? cnt : k;
-    if (lane < n) buf[lane] = top;
-    if (cnt >= k) {
-        const uint64_t t = read_lane_u64(top, k - 1);
-        if (t > T) T = t;
-        publish_threshold(shared_T, T);
-    }
-    const uint64_t s = load_shared_T(shared_T);
-    if (s > T) T = s;
     wave_lds_sync();
-    return {T, n};
+    const uint32_t n = uniform_u32(valid < w.k ? valid : w.k);
+    if (lane < n) w.buf[lane] = top;
+    w.cnt = n;
+    if (valid >= w.k) {
+        raise_threshold(w, read_lane_u64(top, w.k - 1));
+        publish_threshold(w.shared_T, w.T);
+    }
+    raise_threshold(w, load_shared_T(w.shared_T));
+    wave_lds_sync();
+    return top;
 }
 
-// Appends this wave's passing lanes (ballot compaction), compacting first when
-// the buffer would overflow.
+// Appends this wave's passing lanes (ballot compaction).
 __device__ __forceinline__ void offer(Stream &w, bool pass, uint64_t c) {
-    uint64_t m = ballot(pass);
+    const uint64_t m = ballot(pass);
     if (m == 0) return;
-    uint32_t n = __popcll(m);
-    if (w.cnt + n > WBUF) {
-        const Compacted r = compact(w.buf, w.cnt, w.k, w.T, w.shared_T);
-        w.cnt = r.cnt;
-        raise_threshold(w, r.T);
-        pass = pass && (c > w.T);
-        m = ballot(pass);
-        if (m == 0) return;
-        n = __popcll(m);
-    }
     if (pass) w.buf[w.cnt + lanes_below(m)] = c;
-    w.cnt += n;
+    w.cnt += (uint32_t)__popcll(m);
 }
 
 __device__ __forceinline__ uint32_t stream_key(const Stream &w, float x) {
@@ -190,8 +199,7 @@ __device__ __forceinline__ uint32_t stream_key(const Stream &w, float x) {
 }
 
 template <bool CHECK>
-__device__ __forceinline__ void offer_group(Stream &w, const WindowSet &ws, bool pen, f32x4 v, uint32_t id0,
-                                            uint32_t nvalid) {
+__device__ __forceinline__ void offer_group(Stream &w, f32x4 v, uint32_t id0, uint32_t nvalid) {
     const float x[4] = {v.x, v.y, v.z, v.w};
     bool any = false;
 #pragma unroll
@@ -199,14 +207,25 @@ __device__ __forceinline__ void offer_group(Stream &w, const WindowSet &ws, bool
     if (ballot(any) == 0) return;
 #pragma unroll
     for (uint32_t c = 0; c < 4; ++c) {
-        bool p = (!CHECK || c < nvalid) && prefilter(w, x[c]);
-        uint64_t comp = 0;
-        if (p) {
-            comp = composite(stream_key(w, x[c]), id0 + c);
-            p = comp > w.T && (!w.greedy || x[c] >= -3.40282347e38f);
-            if (p && pen) p = !window_contains(ws, id0 + c);
-        }
+        const uint64_t comp = composite(stream_key(w, x[c]), id0 + c);
+        const bool p = (!CHECK || c < nvalid) && prefilter(w, x[c]) && comp > w.T &&
+                       (!w.greedy || x[c] >= -3.40282347e38f);
         offer(w, p, comp);
+    }
+}
+
+// Filters one tile (UNROLL float4 per thread) in two halves, compacting
+// before a half whose passers might not fit.
+template <bool GUARD>
+__device__ __forceinline__ void process_tile(Stream &w, const f32x4 *T, uint32_t base, uint32_t end) {
+#pragma unroll
+    for (uint32_t h = 0; h < 2; ++h) {
+        if (w.cnt >= w.k + SLACK) compact(w);  // then cnt <= k, and k + SLACK + HALF_ELEMS <= CBUF
+#pragma unroll
+        for (uint32_t u = h * HALF; u < (h + 1) * HALF; ++u) {
+            const uint32_t f = base + u * FAST_THREADS + threadIdx.x;
+            offer_group<GUARD>(w, T[u], 4 * f, (!GUARD || f < end) ? 4u : 0u);
+        }
     }
 }
 
@@ -215,7 +234,7 @@ __device__ __forceinline__ void offer_group(Stream &w, const WindowSet &ws, bool
 // least k distinct elements are >= t, so nothing below t is among the row's k
 // best; the threshold is t - 1 because the k elements >= t are not in any
 // buffer yet and must still pass the strict test composite > T.
-__device__ __forceinline__ void bootstrap(Stream &w, const WindowSet &ws, bool pen, const f32x4 *A, uint32_t base) {
+__device__ __forceinline__ void bootstrap(Stream &w, const f32x4 *A, uint32_t base) {
     const uint32_t tid = threadIdx.x;
     uint64_t bound = ~0ull, best = 0;
     for (uint32_t attempt = 0; attempt < 4; ++attempt) {
@@ -231,11 +250,11 @@ __device__ __forceinline__ void bootstrap(Stream &w, const WindowSet &ws, bool p
                 if (ok && comp < bound && comp > best) best = comp;
             }
         }
-        if (!pen || best == 0 || !window_contains(ws, comp_id(best))) break;
+        if (!w.pen || best == 0 || !window_contains(w.ws, comp_id(best))) break;
         bound = best;
         best = 0;
     }
-    const uint64_t sorted = wave_sort64_desc(best);
+    const uint64_t sorted = wave_sort64<true>(best);
     const uint64_t t = read_lane_u64(sorted, w.k - 1);
     raise_threshold(w, t ? t - 1 : 0ull);
     publish_threshold(w.shared_T, w.T);
@@ -244,8 +263,8 @@ __device__ __forceinline__ void bootstrap(Stream &w, const WindowSet &ws, bool p
 // The row's f32::max fold over the penalised logits and its argmax, by one
 // wave re-reading the row. Only for a row whose k best are all +NaN, where the
 // candidates do not reveal the largest non-NaN value.
-__device__ __noinline__ void rescan_row(const float *rowp, uint32_t vocab, const WindowSet &ws, bool pen,
-                                        float penalty, float *out_max, uint32_t *out_tok) {
+__device__ __forceinline__ void rescan_row(const float *rowp, uint32_t vocab, const WindowSet &ws, bool pen,
+                                           float penalty, float *out_max, uint32_t *out_tok) {
     const uint32_t lane = lane_id();
     const RL_GLB float *g = (const RL_GLB float *)rowp;
     float mx = -__builtin_inff();
@@ -266,9 +285,9 @@ __device__ __noinline__ void rescan_row(const float *rowp, uint32_t vocab, const
 // by one wave: lane j holds candidate j (composite c, 0 past nL), in
 // descending order. The sequential f64 and f32 sums are replayed in candidate
 // order with readlane, so every lane computes the bits the reference does.
-__device__ __noinline__ void finalize_row(const RowIO &a, uint32_t row, const rl_sampling &s, uint32_t k,
-                                          uint64_t c, uint32_t nL, const WindowSet &ws, bool pen,
-                                          const float *rowp) {
+__device__ __forceinline__ void finalize_row(const RowIO &a, uint32_t row, const rl_sampling &s, uint32_t k,
+                                             uint64_t c, uint32_t nL, const WindowSet &ws, bool pen,
+                                             const float *rowp) {
     const uint32_t lane = lane_id();
     if (s.temperature <= 0.0f) {  // greedy: argmax (sample.rs:259-265)
         const uint64_t c0 = read_lane_u64(c, 0);
@@ -366,6 +385,37 @@ __device__ __noinline__ void finalize_row(const RowIO &a, uint32_t row, const rl
     }
 }
 
+// Merges the window's distinct ids, with their penalised values
+// (sample.rs:242-255), into the wave's sorted candidates `top`; returns how
+// many were offered. In greedy mode ids whose penalised value argmax could
+// never pick (NaN, -inf) are left out.
+__device__ __forceinline__ uint32_t merge_window(uint64_t &top, const WindowSet &ws, float penalty, bool greedy) {
+    const uint32_t lane = lane_id();
+    uint32_t offered = 0;
+    for (uint32_t base = 0; base < ws.slots; base += WAVE) {
+        const uint32_t i = base + lane;
+        const uint32_t id = ws.ids[i];
+        uint64_t c = 0;
+        if (id != EMPTY_ID) {
+            const float x = penalize(ws.vals[i], penalty);
+            const uint32_t key = greedy ? argmax_key(x) : total_key(x);
+            if (!greedy || key != 0) c = composite(key, id);
+        }
+        const uint64_t present = ballot(c != 0);
+        if (present == 0) continue;
+        offered += (uint32_t)__popcll(present);
+        top = wave_merge64(top, wave_sort64<false>(c));
+    }
+    return offered;
+}
+
+// A sorted (descending) list of n <= 64 composites as an ascending lane
+// vector: lane i holds list[63 - i], zeros where the list is shorter.
+__device__ __forceinline__ uint64_t ascending_from(const uint64_t *list, uint32_t n) {
+    const uint32_t j = WAVE - 1 - lane_id();
+    return j < n ? list[j] : 0ull;
+}
+
 __host__ __device__ constexpr size_t window_lds_bytes(uint32_t hash_bits) {
     return ((size_t)1 << hash_bits) * (sizeof(uint32_t) + sizeof(float));
 }
@@ -374,7 +424,7 @@ __host__ __device__ constexpr size_t window_lds_bytes(uint32_t hash_bits) {
 // window set.
 template <bool VEC>
 __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc) {
-    __shared__ uint64_t s_buf[FAST_WAVES * WBUF];
+    __shared__ uint64_t s_buf[FAST_WAVES * CBUF];
     __shared__ uint64_t s_T;
     __shared__ uint32_t s_cnt[FAST_WAVES];
     extern __shared__ __align__(16) uint8_t smem[];
@@ -383,7 +433,7 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
     const uint32_t row = a.rows[slot];
     const rl_sampling s = a.settings[row];
     const bool greedy = s.temperature <= 0.0f;
-    const uint32_t k = greedy ? 1u : (uint32_t)s.top_k;
+    const uint32_t k = uniform_u32(greedy ? 1u : (uint32_t)s.top_k);
     const uint32_t wl = window_len(a, row);
     const bool pen = penalises(s) && wl > 0;
     const float *rowp = a.logits + (uint64_t)row * a.stride;
@@ -392,95 +442,82 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
     const uint32_t wave = tid / WAVE;
     const uint32_t lane = lane_id();
 
+    // Loop bounds are wave-uniform; readfirstlane keeps them in SGPRs so the
+    // loop control is scalar (the 64-bit division would leave them in VGPRs).
     const uint32_t n4 = V / 4;
-    const uint32_t q0 = (uint32_t)((uint64_t)chunk * n4 / a.chunks);
-    const uint32_t q1 = (uint32_t)((uint64_t)(chunk + 1) * n4 / a.chunks);
+    const uint32_t q0 = uniform_u32((uint32_t)((uint64_t)chunk * n4 / a.chunks));
+    const uint32_t q1 = uniform_u32((uint32_t)((uint64_t)(chunk + 1) * n4 / a.chunks));
     constexpr uint32_t STEP = FAST_THREADS * UNROLL;
-    const uint32_t ntiles = (q1 - q0) / STEP;
+    const uint32_t nfull = (q1 - q0) / STEP;                    // whole tiles
+    const uint32_t ntiles = nfull + ((q1 - q0) % STEP ? 1 : 0);  // plus a partial one
 
     // The first tile's loads go out before the window set is built.
     f32x4 A[UNROLL], B[UNROLL];
-    if (ntiles > 0) {
-#pragma unroll
-        for (uint32_t u = 0; u < UNROLL; ++u) A[u] = load4<VEC>(rowp, q0 + u * FAST_THREADS + tid);
-    }
+    if (nfull > 0)
+        load_tile<VEC, false>(A, rowp, q0, q1);
+    else if (ntiles > 0)
+        load_tile<VEC, true>(A, rowp, q0, q1);
     RL_LDS uint64_t *lT = (RL_LDS uint64_t *)&s_T;
     if (tid == 0) *lT = 0;
     window_build(ws, a.windows + (uint64_t)row * a.wstride, wl, V, rowp, pen);
 
     Stream w;
-    w.buf = (RL_LDS uint64_t *)s_buf + wave * WBUF;
+    w.buf = (RL_LDS uint64_t *)s_buf + wave * CBUF;
     w.shared_T = lT;
+    w.ws = ws;
     w.T = 0;
     w.thr = greedy ? -3.40282347e38f : -__builtin_inff();
     w.cnt = 0;
     w.k = k;
     w.greedy = greedy;
+    w.pen = pen;
 
-    if (ntiles > 0) bootstrap(w, ws, pen, A, q0);
+    if (nfull > 0) bootstrap(w, A, q0);
+    // Double-buffered: tile t+1 is in flight while tile t is filtered. The
+    // partial last tile goes through the same pipeline with guarded loads.
     for (uint32_t t = 0; t < ntiles; t += 2) {
         const uint32_t b0 = q0 + t * STEP, b1 = b0 + STEP, b2 = b1 + STEP;
-        if (t + 1 < ntiles) {
-#pragma unroll
-            for (uint32_t u = 0; u < UNROLL; ++u) B[u] = load4<VEC>(rowp, b1 + u * FAST_THREADS + tid);
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < UNROLL; ++u) offer_group<false>(w, ws, pen, A[u], 4 * (b0 + u * FAST_THREADS + tid), 4);
-        if (t + 2 < ntiles) {
-#pragma unroll
-            for (uint32_t u = 0; u < UNROLL; ++u) A[u] = load4<VEC>(rowp, b2 + u * FAST_THREADS + tid);
-        }
-        if (t + 1 < ntiles) {
-#pragma unroll
-            for (uint32_t u = 0; u < UNROLL; ++u)
-                offer_group<false>(w, ws, pen, B[u], 4 * (b1 + u * FAST_THREADS + tid), 4);
-        }
+        if (t + 1 < nfull)
+            load_tile<VEC, false>(B, rowp, b1, q1);
+        else if (t + 1 < ntiles)
+            load_tile<VEC, true>(B, rowp, b1, q1);
+        if (t < nfull)
+            process_tile<false>(w, A, b0, q1);
+        else
+            process_tile<true>(w, A, b0, q1);
+        if (t + 2 < nfull)
+            load_tile<VEC, false>(A, rowp, b2, q1);
+        else if (t + 2 < ntiles)
+            load_tile<VEC, true>(A, rowp, b2, q1);
+        if (t + 1 < nfull)
+            process_tile<false>(w, B, b1, q1);
+        else if (t + 1 < ntiles)
+            process_tile<true>(w, B, b1, q1);
         raise_threshold(w, load_shared_T(lT));
     }
-    // The chunk's partial tile, then the row's last vocab % 4 elements.
-    const uint32_t rb = q0 + ntiles * STEP;
-    for (uint32_t u = 0; u < UNROLL; ++u) {
-        const uint32_t f = rb + u * FAST_THREADS + tid;
-        const bool ok = f < q1;
-        const f32x4 v = ok ? load4<VEC>(rowp, f) : f32x4{0.f, 0.f, 0.f, 0.f};
-        offer_group<true>(w, ws, pen, v, 4 * f, ok ? 4u : 0u);
-    }
+    // The row's last vocab % 4 elements.
     if (chunk == a.chunks - 1) {
+        if (w.cnt >= w.k + SLACK) compact(w);
         const uint32_t e = 4 * n4 + tid;
         const bool ok = e < V;
         const float x = ok ? ((const RL_GLB float *)rowp)[e] : 0.0f;
-        offer_group<true>(w, ws, pen, f32x4{x, 0.f, 0.f, 0.f}, e, ok ? 1u : 0u);
+        offer_group<true>(w, f32x4{x, 0.f, 0.f, 0.f}, e, ok ? 1u : 0u);
     }
-    // The window's ids with their penalised values, once per row.
-    if (pen && chunk == 0) {
-        for (uint32_t base = wave * WAVE; base < ws.slots; base += FAST_THREADS) {
-            const uint32_t i = base + lane;
-            const uint32_t id = i < ws.slots ? ws.ids[i] : EMPTY_ID;
-            bool p = false;
-            uint64_t c = 0;
-            if (id != EMPTY_ID) {
-                const float x = penalize(ws.vals[i], s.repeat_penalty);
-                const uint32_t key = greedy ? argmax_key(x) : total_key(x);
-                c = composite(key, id);
-                p = (!greedy || key != 0) && c > w.T;
-            }
-            offer(w, p, c);
-        }
-    }
-    const Compacted r = compact(w.buf, w.cnt, k, w.T, lT);
-    if (lane == 0) s_cnt[wave] = r.cnt;
+    compact(w);
+    if (lane == 0) s_cnt[wave] = w.cnt;
     __syncthreads();
     if (wave != 0) return;
     // Merge the four sorted lists: lane i of list j is candidate i of wave j.
-    const RL_LDS uint64_t *lb = (const RL_LDS uint64_t *)s_buf;
+    const uint64_t *lb = (const uint64_t *)s_buf;
     uint64_t top = lane < s_cnt[0] ? lb[lane] : 0ull;
     uint32_t total = s_cnt[0];
 #pragma unroll
     for (uint32_t j = 1; j < FAST_WAVES; ++j) {
-        const uint64_t o = lane < s_cnt[j] ? lb[j * WBUF + lane] : 0ull;
-        top = wave_merge64_desc(top, o);
+        top = wave_merge64(top, ascending_from(lb + j * CBUF, s_cnt[j]));
         total += s_cnt[j];
     }
+    // The window's ids with their penalised values, once per row.
+    if (pen && chunk == 0) total += merge_window(top, ws, s.repeat_penalty, greedy);
     const uint32_t nL = total < k ? total : k;
     if (lane >= nL) top = 0;
     if (a.chunks == 1) {
@@ -512,8 +549,7 @@ __global__ __launch_bounds__(WAVE) void k_stream_finalize(RowIO a, FastScratch s
     uint32_t total = 0;
     for (uint32_t j = 0; j < a.chunks; ++j) {
         const uint32_t n = counts[j];
-        const uint64_t o = lane < n ? lists[(uint64_t)j * KMAX + lane] : 0ull;
-        top = wave_merge64_desc(top, o);
+        top = wave_merge64(top, ascending_from(lists + (uint64_t)j * KMAX, n));
         total += n;
     }
     const uint32_t nL = total < k ? total : k;
