@@ -38,7 +38,21 @@ def parse():
                     help="budget for the CPU-baseline sample (0 skips it)")
     ap.add_argument("--no-candidates", action="store_true",
                     help="skip the candidate outputs (tokens only)")
+    ap.add_argument("--calibration-copy", type=int, default=0,
+                    help="after the timed steps, run this many plain device copies of the logits "
+                         "(known bytes) so profiler byte counters can be scaled")
     return ap.parse_args()
+
+
+def traffic_bytes(workload):
+    """HBM bytes per launch of the dominant kernel, from the PMC runs recorded
+    in profiles/traffic.json (FETCH_SIZE + WRITE_SIZE scaled by a copy of known
+    size); None where no such run has been recorded for the workload."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            return json.load(f)[workload]["traffic_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def cpu_baseline(wl, logits, windows, wlen, uniforms, settings, budget_s):
@@ -129,6 +143,15 @@ def main():
     print("[bench] %s: wall %.3f ms/step, events mean %.3f median %.3f min %.3f max %.3f ms" % (
         name, ms_per_step, mean_ms, median_ms, per_call_ms[0], per_call_ms[-1]), file=sys.stderr, flush=True)
 
+    if args.calibration_copy > 0:
+        dst = torch.empty_like(d_logits)
+        for _ in range(args.calibration_copy):
+            dst.copy_(d_logits)
+        torch.cuda.synchronize()
+        print("[bench] calibration: %d copies of %d bytes" % (args.calibration_copy, d_logits.numel() * 4),
+              file=sys.stderr, flush=True)
+        del dst
+
     cpu = None
     if args.cpu_seconds > 0:
         rate, n, el = cpu_baseline(wl, logits, windows, wlen, uniforms, settings, args.cpu_seconds)
@@ -165,7 +188,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic_bytes(name),
             "algorithmic_bytes_per_call": alg_bytes,
             "call_ms_mean": round(mean_ms, 5),
             "call_ms_median": round(median_ms, 5),
