@@ -1,0 +1,199 @@
+"""Randomized differential tests of the GPU sampler against the oracle.
+
+Every row gets its own random settings (both device paths in one call), its
+own window (with repeats and ids past the vocabulary) and uniform; rows carry
+ties, signed zeros and special values. Results must match bit for bit (a NaN
+probability matches a NaN)."""
+import numpy as np
+import pytest
+
+import oracle as O
+import rl_sampler as R
+from conftest import as_oracle_settings
+
+pytestmark = pytest.mark.gpu
+
+TEMPS = [0.0, 0.05, 0.6, 1.0, 4.0]
+TOPP = [0.0, 0.5, 0.9, 0.999, 1.0]
+MINP = [0.0, 0.02, 0.3, 1.0]
+PEN = [1.0, 0.5, 1.3, 2.0]
+LASTN = [0, 4, 64]
+
+
+def random_settings(rng, V):
+    topk = [0, 1, 2, 5, 20, 63, 64, 65, max(V - 1, 1), V, 3 * V]
+    return R.sampling(float(rng.choice(TEMPS)), int(rng.choice(topk)), float(rng.choice(TOPP)),
+                      float(rng.choice(MINP)), float(rng.choice(PEN)), int(rng.choice(LASTN)),
+                      int(rng.integers(0, 1 << 30)))
+
+
+def random_rows(rng, rows, V, kind):
+    if kind == "normal":
+        x = rng.normal(0.0, 3.0, (rows, V)).astype(np.float32)
+    elif kind == "ties":
+        x = rng.choice(np.array([-1.5, -0.0, 0.0, 0.25, 2.0, 2.0], np.float32), (rows, V))
+    elif kind == "spikes":
+        x = rng.normal(0.0, 2.0, (rows, V)).astype(np.float32)
+        for r in range(rows):
+            x[r, rng.choice(V, min(V, 16), replace=False)] = rng.uniform(8, 14, min(V, 16))
+    else:
+        raise ValueError(kind)
+    return x
+
+
+def inject_specials(rng, x, frac):
+    specials = np.array([np.nan, -np.nan, np.inf, -np.inf, 0.0, -0.0, 3.4e38, -3.4e38], np.float32)
+    m = rng.random(x.shape) < frac
+    x[m] = rng.choice(specials, int(m.sum()))
+    return x
+
+
+def run_both(device, logits, settings, windows, wlen, uniforms, stride=None):
+    import torch
+    rows, V = logits.shape
+    stride = stride or V
+    buf = np.zeros((rows, stride), np.float32)
+    buf[:, :V] = logits
+    # a row stride that is not a multiple of 4 floats exercises the unaligned loads
+    flat = torch.from_numpy(buf.reshape(-1)).to(device)
+    ctx = R.DeviceSampler(rows, V, max_window=windows.shape[1])
+    ctx.configure(settings)
+    cs = ctx.required_cand_stride()
+    tok = torch.empty(rows, dtype=torch.int32, device=device)
+    kept = torch.empty_like(tok)
+    used = torch.empty(rows, dtype=torch.uint8, device=device)
+    ids = torch.empty((rows, cs), dtype=torch.int32, device=device)
+    probs = torch.empty((rows, cs), dtype=torch.float32, device=device)
+    ctx.sample_rows(flat, rows, stride, tok, kept, used,
+                    windows=torch.from_numpy(windows.view(np.int32)).to(device), window_stride=windows.shape[1],
+                    window_len=torch.from_numpy(wlen.view(np.int32)).to(device),
+                    uniforms=torch.from_numpy(uniforms).to(device), out_ids=ids, out_probs=probs,
+                    cand_stride=cs)
+    torch.cuda.synchronize()
+    got = dict(token=tok.cpu().numpy().view(np.uint32), kept=kept.cpu().numpy().view(np.uint32),
+               used=used.cpu().numpy(), ids=ids.cpu().numpy().view(np.uint32), probs=probs.cpu().numpy())
+    want = O.pick_rows(logits, [as_oracle_settings(s) for s in settings], windows, wlen, uniforms, cand_cap=cs)
+    return got, want
+
+
+def assert_match(label, got, want, settings):
+    for r in range(got["token"].size):
+        where = "%s row %d (%r)" % (label, r, settings[r])
+        assert got["token"][r] == want["token"][r], where
+        assert got["kept"][r] == want["kept"][r], where
+        assert got["used"][r] == want["used"][r], where
+        k = int(want["kept"][r])
+        assert np.array_equal(got["ids"][r, :k], want["ids"][r, :k]), where
+        gp, wp = got["probs"][r, :k], want["probs"][r, :k]
+        both_nan = np.isnan(gp) & np.isnan(wp)
+        assert np.array_equal(gp.view(np.uint32)[~both_nan], wp.view(np.uint32)[~both_nan]), where
+
+
+def make_case(rng, rows, V, kind, special=0.0, wl=16):
+    logits = random_rows(rng, rows, V, kind)
+    if special:
+        logits = inject_specials(rng, logits, special)
+    settings = [random_settings(rng, V) for _ in range(rows)]
+    windows = rng.integers(0, V + 8, (rows, wl)).astype(np.uint32)  # some ids past the vocabulary
+    windows[:, 1::3] = windows[:, 0:1]  # repeats
+    wlen = np.array([min(int(s.repeat_last_n), wl) if s.repeat_last_n else 0 for s in settings], np.uint32)
+    uniforms = rng.random(rows).astype(np.float32)
+    return logits, settings, windows, wlen, uniforms
+
+
+@pytest.mark.parametrize("V,rows,kind,special", [
+    (1003, 64, "normal", 0.0),
+    (2048, 64, "ties", 0.0),
+    (2048, 48, "ties", 0.05),
+    (4099, 32, "spikes", 0.002),
+    (5, 40, "normal", 0.1),
+    (151936, 3, "spikes", 0.0),
+    (151936, 2, "normal", 0.0005),
+])
+def test_random_rows_match_the_oracle(device, V, rows, kind, special):
+    rng = np.random.default_rng(V * 1000 + rows)
+    logits, settings, windows, wlen, uniforms = make_case(rng, rows, V, kind, special)
+    print("case V=%d rows=%d kind=%s special=%g" % (V, rows, kind, special), flush=True)
+    got, want = run_both(device, logits, settings, windows, wlen, uniforms)
+    assert_match("V=%d %s" % (V, kind), got, want, settings)
+
+
+def test_unaligned_row_stride(device):
+    rng = np.random.default_rng(7)
+    logits, settings, windows, wlen, uniforms = make_case(rng, 16, 4099, "spikes", 0.001)
+    got, want = run_both(device, logits, settings, windows, wlen, uniforms, stride=4099 + 3)
+    assert_match("stride 4102", got, want, settings)
+
+
+def test_rows_with_many_nans_and_infinities(device):
+    rng = np.random.default_rng(3)
+    V = 3000
+    logits = rng.normal(0, 1, (12, V)).astype(np.float32)
+    logits[0, :40] = np.nan                      # >= k positive NaNs: the rescan path
+    logits[1, :] = -np.inf                        # nothing finite
+    logits[2, :] = np.nan                         # nothing but NaN
+    logits[3, 100] = np.inf                       # +inf wins everything
+    logits[3, 200] = np.inf
+    logits[4, :] = -np.nan
+    logits[5, ::2] = -np.inf
+    logits[6, :25] = np.nan
+    logits[6, 30] = np.inf
+    logits[7, 5] = np.nan
+    logits[8, :] = 0.0
+    logits[8, 17] = -0.0
+    logits[9, :] = -0.0
+    logits[9, 11] = 0.0
+    logits[10, :64] = np.nan
+    logits[11, :] = 1.0
+    settings = []
+    for r in range(12):
+        for s in (R.sampling(0.7, 20, 0.9, 0.0, 1.3, 8, r), R.greedy_sampling(repeat_penalty=1.3, repeat_last_n=8)):
+            settings.append(s)
+    logits = np.repeat(logits, 2, axis=0)
+    rows = logits.shape[0]
+    windows = rng.integers(0, V, (rows, 8)).astype(np.uint32)
+    wlen = np.full(rows, 8, np.uint32)
+    uniforms = rng.random(rows).astype(np.float32)
+    got, want = run_both(device, logits, settings, windows, wlen, uniforms)
+    assert_match("special rows", got, want, settings)
+
+
+def test_argmax_rows_match_the_oracle(device):
+    import torch
+    rng = np.random.default_rng(9)
+    V = 70001
+    x = inject_specials(rng, random_rows(rng, 33, V, "ties"), 0.001)
+    x[0, :] = -np.inf
+    x[1, :] = np.nan
+    ctx = R.DeviceSampler(33, V, max_window=0)
+    out = torch.empty(33, dtype=torch.int32, device=device)
+    ctx.argmax_rows(torch.from_numpy(x).to(device), 33, V, out)
+    torch.cuda.synchronize()
+    assert out.cpu().numpy().tolist() == [O.argmax(x[r]) for r in range(33)]
+
+
+def test_errors_are_status_codes(device):
+    import torch
+    ctx = R.DeviceSampler(4, 100, max_window=8)
+    l = torch.zeros((4, 100), device=device)
+    o = torch.empty(4, dtype=torch.int32, device=device)
+    u8 = torch.empty(4, dtype=torch.uint8, device=device)
+    with pytest.raises(R.SamplerError) as e:
+        ctx.sample_rows(l, 4, 100, o, o, u8)
+    assert e.value.code == R.RL_ERR_NOT_CONFIGURED
+    ctx.configure([R.greedy_sampling()] * 4)
+    with pytest.raises(R.SamplerError) as e:
+        ctx.sample_rows(l, 4, 100, o, o, u8, vocab=99)
+    assert e.value.code == R.RL_ERR_VOCAB  # where the reference panics (sample.rs:222-226)
+    with pytest.raises(R.SamplerError) as e:
+        ctx.sample_rows(l, 5, 100, o, o, u8)
+    assert e.value.code == R.RL_ERR_CAPACITY
+    with pytest.raises(R.SamplerError) as e:
+        ctx.sample_rows(l, 4, 100, o, o, u8, windows=o, window_stride=9, window_len=o)
+    assert e.value.code == R.RL_ERR_CAPACITY
+    kept = torch.empty(4, dtype=torch.int32, device=device)
+    l[:, 37] = 1.0
+    ctx.sample_rows(l, 4, 100, o, kept, u8)  # and a good call still works
+    torch.cuda.synchronize()
+    assert o.cpu().tolist() == [37, 37, 37, 37]
+    assert kept.cpu().tolist() == [1, 1, 1, 1]
