@@ -723,16 +723,97 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
     }
 }
 
-// grid (slots), FULL_THREADS: the reference's tail over the whole (sorted or
-// identity-ordered) candidate list. The sequential sums run on thread 0 over
-// blocks staged in LDS; the min-p compaction and the normalisation are
-// parallel (both are elementwise and stable).
+// ------------------------------------------------------ FULL-path tail ---
+constexpr uint32_t FULL_WAVES = FULL_THREADS / WAVE;
+constexpr uint32_t SCAN_ITEMS = 16;  // elements per thread per scan tile
+
+__device__ __forceinline__ double block_sum_f64(double v, RL_LDS double *red) {
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    __syncthreads();
+    if (lane_id() == 0) red[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (uint32_t w = 0; w < FULL_WAVES; ++w) t += red[w];
+    return t;
+}
+
+__device__ __forceinline__ int block_min_i32(int v, RL_LDS int *red) {
+    for (int m = 32; m >= 1; m >>= 1) v = min(v, __shfl_xor(v, m));
+    __syncthreads();
+    if (lane_id() == 0) red[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    int t = red[0];
+    for (uint32_t w = 1; w < FULL_WAVES; ++w) t = min(t, red[w]);
+    return t;
+}
+
+// Exclusive prefix of v over the block's threads in thread order; *total gets
+// the block's sum. Only used where every partial sum is exact, so the order of
+// the additions does not matter.
+__device__ __forceinline__ double block_exclusive_f64(double v, RL_LDS double *red, double *total) {
+    const uint32_t lane = lane_id(), wave = threadIdx.x / WAVE;
+    double incl = v;
+    for (uint32_t d = 1; d < WAVE; d <<= 1) {
+        const double o = __shfl_up(incl, d);
+        if (lane >= d) incl += o;
+    }
+    __syncthreads();
+    if (lane == WAVE - 1) red[wave] = incl;
+    __syncthreads();
+    double before = 0.0, all = 0.0;
+    for (uint32_t w = 0; w < FULL_WAVES; ++w) {
+        if (w < wave) before += red[w];
+        all += red[w];
+    }
+    *total = all;
+    return before + incl - v;
+}
+
+// Binary exponent of a finite nonzero f32 (subnormals count as -126): every
+// such value is a multiple of 2^(exponent - 23).
+__device__ __forceinline__ int f32_exponent(float p) {
+    const int e = (int)((__float_as_uint(p) >> 23) & 0xFFu);
+    return e == 0 ? -126 : e - 127;
+}
+
+// Walks src[0..n) in order on thread 0, one LDS-staged block at a time; the
+// whole workgroup stages. body(stage, base, count) returns true to stop.
+template <class Body>
+__device__ __forceinline__ void staged_walk(const float *src, uint32_t n, RL_LDS float *stage,
+                                            RL_LDS uint32_t *stop, Body body) {
+    for (uint32_t b = 0; b < n; b += STAGE) {
+        const uint32_t cnt = min(STAGE, n - b);
+        for (uint32_t i = threadIdx.x; i < cnt; i += FULL_THREADS) stage[i] = ((const RL_GLB float *)src)[b + i];
+        __syncthreads();
+        if (threadIdx.x == 0) *stop = body(stage, b, cnt) ? 1u : 0u;
+        __syncthreads();
+        if (*stop) break;
+    }
+}
+
+// grid (slots), FULL_THREADS: the reference's tail over the whole candidate
+// list (sorted, or in id order when neither top-k nor top-p needs an order).
+//
+// The reference sums in candidate order in f64 (sample.rs:307-324, :342).
+// When every probability is a multiple of 2^(e_min - 23) and the total is below
+// 2^(29 + e_min), every partial sum is exactly representable in f64, so the
+// sequential sums equal sums in any order: the mass, the top-p cut and the
+// normalising total are then block reductions and scans. Otherwise they are
+// replayed in order on one thread. The draw (f32, sample.rs:349-356) is always
+// replayed in order.
 __global__ __launch_bounds__(FULL_THREADS) void k_full_replay(RowIO a, FullScratch f) {
-    __shared__ float stage[STAGE];
-    __shared__ uint32_t wave_cnt[FULL_THREADS / WAVE];
-    __shared__ uint32_t sh_m, sh_done, sh_total;
-    __shared__ float sh_inv;
-    __shared__ double sh_target;
+    __shared__ float stage_[STAGE];
+    __shared__ double red_d_[FULL_WAVES];
+    __shared__ int red_i_[FULL_WAVES];
+    __shared__ uint32_t wave_cnt_[FULL_WAVES];
+    __shared__ uint32_t sh_m_, sh_stop_, sh_total_, sh_tok_;
+    __shared__ float sh_inv_;
+    __shared__ double sh_target_;
+    RL_LDS float *stage = (RL_LDS float *)stage_;
+    RL_LDS double *red_d = (RL_LDS double *)red_d_;
+    RL_LDS int *red_i = (RL_LDS int *)red_i_;
+    RL_LDS uint32_t *stop = (RL_LDS uint32_t *)&sh_stop_;
+
     const uint32_t slot = blockIdx.x;
     const uint32_t row = a.rows[slot];
     const rl_sampling s = a.settings[row];
@@ -746,52 +827,84 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_replay(RowIO a, FullScrat
         return;
     }
     const uint32_t k = full_k(s, V);
-    uint32_t *keys = f.keyA + (uint64_t)slot * V;
+    const uint32_t *keys = f.keyA + (uint64_t)slot * V;
     uint32_t *ids = f.idA + (uint64_t)slot * V;
     float *probs = f.probs + (uint64_t)slot * V;
-    for (uint32_t j = tid; j < k; j += FULL_THREADS)
-        probs[j] = expf_libm((key_value(keys[j]) - M) / s.temperature);  // sample.rs:309
-    if (tid == 0) {
-        sh_m = k;
-        sh_done = 0;
-    }
-    __syncthreads();
 
-    if (s.top_p < 1.0f) {  // sample.rs:307-324
-        double sum = 0.0;
-        for (uint32_t b = 0; b < k; b += STAGE) {
-            const uint32_t n = min(STAGE, k - b);
-            for (uint32_t i = tid; i < n; i += FULL_THREADS) stage[i] = probs[b + i];
-            __syncthreads();
-            if (tid == 0)
-                for (uint32_t i = 0; i < n; ++i) sum += (double)stage[i];
-            __syncthreads();
+    // exp (sample.rs:309), and what decides whether the f64 sums are exact.
+    int emin = 1 << 20;
+    uint32_t bad = 0;
+    double part = 0.0;
+    for (uint32_t j = tid; j < k; j += FULL_THREADS) {
+        const float p = expf_libm((key_value(keys[j]) - M) / s.temperature);
+        probs[j] = p;
+        if (!(p <= 3.40282347e38f)) {
+            bad = 1;  // NaN or +inf
+        } else if (p > 0.0f) {
+            emin = min(emin, f32_exponent(p));
         }
-        if (tid == 0) sh_target = (double)s.top_p * sum;
-        __syncthreads();
-        const double target = sh_target;
-        double cum = 0.0;
-        for (uint32_t b = 0; b < k; b += STAGE) {
-            const uint32_t n = min(STAGE, k - b);
-            for (uint32_t i = tid; i < n; i += FULL_THREADS) stage[i] = probs[b + i];
-            __syncthreads();
-            if (tid == 0) {
-                for (uint32_t i = 0; i < n; ++i) {
-                    cum += (double)stage[i];
-                    if (cum >= target) {
-                        sh_m = b + i + 1;
-                        sh_done = 1;
+        part += (double)p;
+    }
+    const double mass = block_sum_f64(part, red_d);
+    emin = block_min_i32(emin, red_i);
+    bad = (uint32_t)block_min_i32(bad ? 0 : 1, red_i) == 0 ? 1u : 0u;
+    const bool exact = !bad && (emin > 1000 || mass < ldexp(1.0, 29 + emin));
+
+    uint32_t m = k;
+    if (s.top_p < 1.0f) {  // sample.rs:313-324
+        if (exact) {
+            const double target = (double)s.top_p * mass;
+            double base = 0.0;
+            for (uint32_t t0 = 0; t0 < k; t0 += FULL_THREADS * SCAN_ITEMS) {
+                const uint32_t j0 = t0 + tid * SCAN_ITEMS;
+                double mine = 0.0;
+                for (uint32_t i = 0; i < SCAN_ITEMS && j0 + i < k; ++i) mine += (double)probs[j0 + i];
+                double tile_total;
+                double c = base + block_exclusive_f64(mine, red_d, &tile_total);
+                int first = 0x7FFFFFFF;
+                for (uint32_t i = 0; i < SCAN_ITEMS && j0 + i < k; ++i) {
+                    c += (double)probs[j0 + i];
+                    if (c >= target) {
+                        first = (int)(j0 + i);
                         break;
                     }
                 }
+                first = block_min_i32(first, red_i);
+                if (first != 0x7FFFFFFF) {
+                    m = (uint32_t)first + 1;
+                    break;
+                }
+                base += tile_total;
+            }
+        } else {
+            double sum = 0.0;
+            staged_walk(probs, k, stage, stop, [&](RL_LDS float *st, uint32_t, uint32_t cnt) {
+                for (uint32_t i = 0; i < cnt; ++i) sum += (double)st[i];
+                return false;
+            });
+            if (tid == 0) {
+                sh_target_ = (double)s.top_p * sum;
+                sh_m_ = k;
             }
             __syncthreads();
-            if (sh_done) break;
+            const double target = sh_target_;
+            double cum = 0.0;
+            staged_walk(probs, k, stage, stop, [&](RL_LDS float *st, uint32_t b, uint32_t cnt) {
+                for (uint32_t i = 0; i < cnt; ++i) {
+                    cum += (double)st[i];
+                    if (cum >= target) {
+                        sh_m_ = b + i + 1;
+                        return true;
+                    }
+                }
+                return false;
+            });
+            __syncthreads();
+            m = sh_m_;
         }
     }
-    uint32_t m = sh_m;
     if (s.min_p > 0.0f) {  // sample.rs:326-340, a stable in-place compaction
-        if (tid == 0) sh_total = 0;
+        if (tid == 0) sh_total_ = 0;
         __syncthreads();
         for (uint32_t b = 0; b < m; b += FULL_THREADS) {
             const uint32_t j = b + tid;
@@ -800,12 +913,12 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_replay(RowIO a, FullScrat
             const uint32_t id = ok ? ids[j] : 0u;
             const bool surv = ok && p >= s.min_p;
             const uint64_t bm = ballot(surv);
-            if (lane == 0) wave_cnt[wave] = (uint32_t)__popcll(bm);
+            if (lane == 0) wave_cnt_[wave] = (uint32_t)__popcll(bm);
             __syncthreads();
-            uint32_t before = sh_total, all = 0;
-            for (uint32_t w = 0; w < FULL_THREADS / WAVE; ++w) {
-                if (w < wave) before += wave_cnt[w];
-                all += wave_cnt[w];
+            uint32_t before = sh_total_, all = 0;
+            for (uint32_t w = 0; w < FULL_WAVES; ++w) {
+                if (w < wave) before += wave_cnt_[w];
+                all += wave_cnt_[w];
             }
             __syncthreads();
             if (surv) {
@@ -813,24 +926,28 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_replay(RowIO a, FullScrat
                 ids[dst] = id;
                 probs[dst] = p;
             }
-            if (tid == 0) sh_total += all;
+            if (tid == 0) sh_total_ += all;
             __syncthreads();
         }
-        m = sh_total > 1 ? sh_total : 1u;
+        m = sh_total_ > 1 ? sh_total_ : 1u;
     }
     // Normalise: f64 total in order, then f32 multiply (sample.rs:342-347).
-    double total = 0.0;
-    for (uint32_t b = 0; b < m; b += STAGE) {
-        const uint32_t n = min(STAGE, m - b);
-        for (uint32_t i = tid; i < n; i += FULL_THREADS) stage[i] = probs[b + i];
+    double total;
+    if (exact) {
+        double t = 0.0;
+        for (uint32_t j = tid; j < m; j += FULL_THREADS) t += (double)probs[j];
+        total = block_sum_f64(t, red_d);
+    } else {
+        double t = 0.0;
+        staged_walk(probs, m, stage, stop, [&](RL_LDS float *st, uint32_t, uint32_t cnt) {
+            for (uint32_t i = 0; i < cnt; ++i) t += (double)st[i];
+            return false;
+        });
+        if (tid == 0) sh_target_ = t;
         __syncthreads();
-        if (tid == 0)
-            for (uint32_t i = 0; i < n; ++i) total += (double)stage[i];
-        __syncthreads();
+        total = sh_target_;
     }
-    if (tid == 0) sh_inv = (float)(1.0 / total);
-    __syncthreads();
-    const float inv = sh_inv;
+    const float inv = (float)(1.0 / total);
     for (uint32_t j = tid; j < m; j += FULL_THREADS) {
         const float q = probs[j] * inv;
         probs[j] = q;
@@ -839,33 +956,47 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_replay(RowIO a, FullScrat
             a.out_probs[(uint64_t)row * a.cand_stride + j] = q;
         }
     }
-    if (tid == 0) {
-        sh_done = 0;
-        sh_m = ids[m - 1];  // f32 shortfall: the last candidate (sample.rs:357-358)
-    }
+    if (tid == 0) sh_tok_ = m - 1;  // f32 shortfall: the last candidate (sample.rs:357-358)
     __syncthreads();
     // The draw: f32 running sum against the host's uniform (sample.rs:349-356).
+    // q >= 0 (or NaN), so the running sum never decreases and a group of 16
+    // whose last sum is <= u holds no crossing; any other group (including one
+    // where a NaN entered) is scanned element by element.
     const float u = a.uniforms[row];
     float cum = 0.0f;
-    for (uint32_t b = 0; b < m; b += STAGE) {
-        const uint32_t n = min(STAGE, m - b);
-        for (uint32_t i = tid; i < n; i += FULL_THREADS) stage[i] = probs[b + i];
-        __syncthreads();
-        if (tid == 0) {
-            for (uint32_t i = 0; i < n; ++i) {
-                cum += stage[i];
-                if (cum > u) {
-                    sh_m = ids[b + i];
-                    sh_done = 1;
-                    break;
+    staged_walk(probs, m, stage, stop, [&](RL_LDS float *st, uint32_t b, uint32_t cnt) {
+        uint32_t i = 0;
+        for (; i + 16 <= cnt; i += 16) {
+            float c[16];
+            float x = cum;
+#pragma unroll
+            for (uint32_t t = 0; t < 16; ++t) {
+                x += st[i + t];
+                c[t] = x;
+            }
+            if (!(c[15] <= u)) {
+#pragma unroll
+                for (uint32_t t = 0; t < 16; ++t) {
+                    if (c[t] > u) {
+                        sh_tok_ = b + i + t;
+                        return true;
+                    }
                 }
             }
+            cum = x;
         }
-        __syncthreads();
-        if (sh_done) break;
-    }
+        for (; i < cnt; ++i) {
+            cum += st[i];
+            if (cum > u) {
+                sh_tok_ = b + i;
+                return true;
+            }
+        }
+        return false;
+    });
+    __syncthreads();
     if (tid == 0) {
-        a.out_token[row] = sh_m;
+        a.out_token[row] = ids[sh_tok_];
         a.out_kept[row] = m;
         a.out_used[row] = 1;
     }
