@@ -47,7 +47,9 @@ typedef struct rl_host_sampler rl_host_sampler;
 
 /* Sampler::new(vocab, set) (sample.rs:156-172): allocates everything,
  * including device buffers for up to `max_rows` rows per call (1 for plain
- * sampling; draft+1 for verify). */
+ * sampling; draft+1 for verify; the batch size for rl_host_sample_batch, where
+ * the first sampler's buffers serve the whole batch, so a sampler made with
+ * max_rows > 1 sizes its candidate buffers for the whole vocabulary). */
 int rl_host_sampler_new(int device, size_t vocab, const rl_sampling *set, uint32_t max_rows,
                         rl_host_sampler **out);
 void rl_host_sampler_free(rl_host_sampler *s);
@@ -71,17 +73,21 @@ void rl_host_sampler_rng(const rl_host_sampler *s, rl_rng *out);
 /* Speculative verify (generate.rs:412-450) in one device call: rows
  * 0..n_drafts of device logits, where row i follows drafts 0..i-1. Row i is
  * sampled with the window the sampler would hold after accepting drafts
- * 0..i-1 and with the uniform it would draw next. Nothing is committed: picks
- * lands in `picks` (n_drafts+1 entries) and the caller commits rows in order
- * with rl_host_sampler_commit_verified, stopping after the first row whose pick
- * differs from its draft, exactly as the generation loop consumes them. */
+ * 0..i-1 and with the uniform it would draw next if every earlier row drew.
+ * Nothing is committed: the picks land in `picks` (n_drafts+1 entries) and the
+ * caller commits rows in order with rl_host_sampler_commit_verified, stopping
+ * after the first row whose committed token differs from its draft, exactly
+ * as the generation loop consumes them. */
 int rl_host_sampler_verify(rl_host_sampler *s, const float *device_rows, uint64_t row_stride,
                            size_t n, const uint32_t *drafts, uint32_t n_drafts, uint32_t *picks,
                            void *stream);
 /* Commits row `row` of the last verify (rows must be committed 0, 1, 2, ...):
- * remembers its pick, advances the Rng if it drew, and makes its survivors the
- * sampler's candidates. */
-int rl_host_sampler_commit_verified(rl_host_sampler *s, uint32_t row);
+ * remembers its token, advances the Rng if it drew, and makes its survivors
+ * the sampler's candidates. The committed token is written to *token: it is
+ * the verify pick unless an earlier committed row drew nothing (no finite
+ * maximum, sample.rs:270-277), in which case the stream gives this row another
+ * uniform and the row is sampled again with it. */
+int rl_host_sampler_commit_verified(rl_host_sampler *s, uint32_t row, uint32_t *token);
 
 /* ---- Batched serving: one device call over many samplers ---- */
 /* Samples samplers[i] on device row i (logits + i*row_stride), as n separate

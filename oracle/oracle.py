@@ -185,8 +185,8 @@ class OracleSampler:
             raise MemoryError
 
     def __del__(self):
-        if getattr(self, "h", None):
-            lib().orc_sampler_free(self.h)
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.orc_sampler_free(self.h)
             self.h = None
 
     def remember(self, t):

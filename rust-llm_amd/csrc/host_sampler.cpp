@@ -253,9 +253,9 @@ int rl_host_sampler_new(int device, size_t vocab, const rl_sampling *set, uint32
     rl_rng_seeded(&s->rng, set->seed);
     // Candidate slots the settings can keep (sample.rs:159: the whole
     // vocabulary unless greedy).
-    s->cand_cap = !(set->temperature <= 0.0f)
-                      ? ((set->top_k == 0 || set->top_k >= vocab) ? vocab : set->top_k)
-                      : 1;
+    s->cand_cap = max_rows > 1 ? vocab
+                  : !(set->temperature <= 0.0f) ? ((set->top_k == 0 || set->top_k >= vocab) ? vocab : set->top_k)
+                                                : 1;
     int rc = rl_sampler_create(device, max_rows, (uint32_t)vocab, s->wcap, &s->ctx);
     if (rc != RL_OK) {
         delete s;
@@ -362,8 +362,8 @@ int rl_host_sampler_verify(rl_host_sampler *s, const float *device_rows, uint64_
     return RL_OK;
 }
 
-int rl_host_sampler_commit_verified(rl_host_sampler *s, uint32_t row) {
-    if (!s) return herr(RL_ERR_ARGUMENT, "null sampler");
+int rl_host_sampler_commit_verified(rl_host_sampler *s, uint32_t row, uint32_t *token) {
+    if (!s || !token) return herr(RL_ERR_ARGUMENT, "null argument");
     if (row != s->next_commit || row >= s->verified.size())
         return herr(RL_ERR_ARGUMENT, "verify rows are committed in order, once");
     auto &v = s->verified[row];
@@ -391,6 +391,7 @@ int rl_host_sampler_commit_verified(rl_host_sampler *s, uint32_t row) {
     s->kept = v.kept;
     s->remember(v.token);
     s->next_commit = row + 1;
+    *token = v.token;
     return RL_OK;
 }
 

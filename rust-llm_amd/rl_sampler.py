@@ -115,7 +115,7 @@ def lib():
         L.rl_host_sampler_rng.argtypes = [_vp, ctypes.POINTER(Rng)]
         L.rl_host_sampler_rng.restype = None
         L.rl_host_sampler_verify.argtypes = [_vp, _vp, _u64, ctypes.c_size_t, _vp, _u32, _vp, _vp]
-        L.rl_host_sampler_commit_verified.argtypes = [_vp, _u32]
+        L.rl_host_sampler_commit_verified.argtypes = [_vp, _u32, ctypes.POINTER(_u32)]
         L.rl_host_sample_batch.argtypes = [ctypes.POINTER(_vp), _u32, _vp, _u64, ctypes.c_size_t, _vp, _vp]
         _lib = L
     return _lib
@@ -311,7 +311,10 @@ class HostSampler:
         return picks
 
     def commit_verified(self, row):
-        _check(lib().rl_host_sampler_commit_verified(self.h, row))
+        """Commits verify row `row`; returns the committed token."""
+        out = _u32()
+        _check(lib().rl_host_sampler_commit_verified(self.h, row, ctypes.byref(out)))
+        return out.value
 
 
 def host_sample_batch(samplers, logits):
