@@ -192,12 +192,23 @@ __device__ __forceinline__ void wave_lds_sync() {
 // penalised value can be formed without writing the logits. Inserting an id
 // twice keeps one slot, which is the reference's once-per-distinct-id rule
 // (sample.rs:242-247); ids >= vocab are skipped (sample.rs:248).
+//
+// `top` holds the largest raw composite of any id in the set, under both the
+// total-order key and argmax's key: a candidate whose composite is above it
+// cannot be a window id, so the lookup is skipped for it. Once a stream's
+// threshold has passed the window's raw values, no lookup happens at all.
 struct WindowSet {
     RL_LDS uint32_t *ids;
     RL_LDS float *vals;
+    RL_LDS uint64_t *top;
     uint32_t bits;  // log2(slots)
     uint32_t slots;
 };
+
+// LDS bytes of a set with 2^bits slots: ids, raw values, then `top`.
+__host__ __device__ constexpr size_t window_lds_bytes(uint32_t hash_bits) {
+    return ((size_t)1 << hash_bits) * (sizeof(uint32_t) + sizeof(float)) + sizeof(uint64_t);
+}
 
 __device__ __forceinline__ WindowSet window_set(void *lds_base, uint32_t bits) {
     WindowSet w;
@@ -205,8 +216,13 @@ __device__ __forceinline__ WindowSet window_set(void *lds_base, uint32_t bits) {
     w.slots = 1u << bits;
     w.ids = (RL_LDS uint32_t *)lds_base;
     w.vals = (RL_LDS float *)(w.ids + w.slots);
+    w.top = (RL_LDS uint64_t *)(w.vals + w.slots);  // slots >= 64, so 8-byte aligned
     return w;
 }
+
+// The largest raw composite of the set's ids (0 for an empty set); valid after
+// window_build.
+__device__ __forceinline__ uint64_t window_top(const WindowSet &w) { return uniform_u64(*w.top); }
 
 __device__ __forceinline__ uint32_t window_hash(uint32_t id, uint32_t bits) {
     return (id * 0x9E3779B1u) >> (32u - bits);
@@ -222,26 +238,43 @@ __device__ __forceinline__ bool window_contains(const WindowSet &w, uint32_t id)
     }
 }
 
+// Empties the set (no barrier).
+__device__ __forceinline__ void window_clear(const WindowSet &w) {
+    for (uint32_t i = threadIdx.x; i < w.slots; i += blockDim.x) w.ids[i] = EMPTY_ID;
+    if (threadIdx.x == 0) *w.top = 0;
+}
+
+// Inserts id (< vocab); returns the slot when this call inserted it, EMPTY_ID
+// when the id was already there.
+__device__ __forceinline__ uint32_t window_insert(const WindowSet &w, uint32_t id) {
+    uint32_t s = window_hash(id, w.bits);
+    for (;;) {
+        const uint32_t old = atomicCAS((uint32_t *)&w.ids[s], EMPTY_ID, id);
+        if (old == EMPTY_ID) return s;
+        if (old == id) return EMPTY_ID;
+        s = (s + 1) & (w.slots - 1);
+    }
+}
+
+// Records the raw logit x of the id inserted at `slot`.
+__device__ __forceinline__ void window_store(const WindowSet &w, uint32_t slot, uint32_t id, float x) {
+    w.vals[slot] = x;
+    const uint32_t k0 = total_key(x), k1 = total_key(x + 0.0f);
+    __hip_atomic_fetch_max(w.top, composite(k0 > k1 ? k0 : k1, id), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 // Whole-workgroup: clears the set, inserts window[0..len), and gathers each
 // distinct id's raw logit from `row`. Ends with a barrier.
 __device__ __forceinline__ void window_build(const WindowSet &w, const uint32_t *window, uint32_t len,
                                              uint32_t vocab, const float *row, bool active) {
-    for (uint32_t i = threadIdx.x; i < w.slots; i += blockDim.x) w.ids[i] = EMPTY_ID;
+    window_clear(w);
     __syncthreads();
     if (active) {
         for (uint32_t i = threadIdx.x; i < len; i += blockDim.x) {
             const uint32_t id = window[i];
             if (id >= vocab) continue;
-            uint32_t s = window_hash(id, w.bits);
-            for (;;) {
-                const uint32_t old = atomicCAS((uint32_t *)&w.ids[s], EMPTY_ID, id);
-                if (old == EMPTY_ID) {
-                    w.vals[s] = ((const RL_GLB float *)row)[id];
-                    break;
-                }
-                if (old == id) break;
-                s = (s + 1) & (w.slots - 1);
-            }
+            const uint32_t slot = window_insert(w, id);
+            if (slot != EMPTY_ID) window_store(w, slot, id, ((const RL_GLB float *)row)[id]);
         }
     }
     __syncthreads();

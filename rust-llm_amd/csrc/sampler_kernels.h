@@ -92,14 +92,17 @@ __device__ __forceinline__ f32x4 load4(const float *row, uint32_t f) {
     }
 }
 
-// One tile of UNROLL float4 per thread, starting at float4 index `base`;
-// with GUARD, indices at or past `end` read as nothing.
-template <bool VEC, bool GUARD>
-__device__ __forceinline__ void load_tile(f32x4 *dst, const float *row, uint32_t base, uint32_t end) {
+// One tile is UNROLL float4 per thread, starting at float4 index `base`.
+// The same tile with indices at or past `end` clamped to end - 1 (end >= 1):
+// every lane loads, so no branch surrounds the loads. A branch around a load
+// keeps the compiler from counting the loads in flight, and it then waits for
+// all of them, the next tile's included, before the current tile is filtered.
+template <bool VEC>
+__device__ __forceinline__ void load_tile_clamped(f32x4 *dst, const float *row, uint32_t base, uint32_t end) {
 #pragma unroll
     for (uint32_t u = 0; u < UNROLL; ++u) {
         const uint32_t f = base + u * FAST_THREADS + threadIdx.x;
-        if (!GUARD || f < end) dst[u] = load4<VEC>(row, f);
+        dst[u] = load4<VEC>(row, f < end ? f : end - 1);
     }
 }
 
@@ -126,6 +129,7 @@ struct Stream {
     RL_LDS uint64_t *buf;
     RL_LDS uint64_t *shared_T;
     WindowSet ws;
+    uint64_t wtop;  // window_top(ws): candidates above it are not window ids
     uint64_t T;
     float thr;
     uint32_t cnt;
@@ -169,7 +173,7 @@ __device__ __forceinline__ uint64_t compact(Stream &w) {
     for (uint32_t base = 0; base < w.cnt; base += WAVE) {
         const uint32_t j = base + lane;
         uint64_t v = j < w.cnt ? w.buf[j] : 0ull;
-        if (w.pen && v != 0 && window_contains(w.ws, comp_id(v))) v = 0;
+        if (w.pen && v != 0 && v <= w.wtop && window_contains(w.ws, comp_id(v))) v = 0;
         valid += (uint32_t)__popcll(ballot(v != 0));
         top = wave_merge64(top, wave_sort64<false>(v));
     }
@@ -250,7 +254,7 @@ __device__ __forceinline__ void bootstrap(Stream &w, const f32x4 *A, uint32_t ba
                 if (ok && comp < bound && comp > best) best = comp;
             }
         }
-        if (!w.pen || best == 0 || !window_contains(w.ws, comp_id(best))) break;
+        if (!w.pen || best == 0 || best > w.wtop || !window_contains(w.ws, comp_id(best))) break;
         bound = best;
         best = 0;
     }
@@ -416,10 +420,6 @@ __device__ __forceinline__ uint64_t ascending_from(const uint64_t *list, uint32_
     return j < n ? list[j] : 0ull;
 }
 
-__host__ __device__ constexpr size_t window_lds_bytes(uint32_t hash_bits) {
-    return ((size_t)1 << hash_bits) * (sizeof(uint32_t) + sizeof(float));
-}
-
 // grid (chunks, rows on this path), FAST_THREADS threads. Dynamic LDS: the
 // window set.
 template <bool VEC>
@@ -451,20 +451,38 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
     const uint32_t nfull = (q1 - q0) / STEP;                    // whole tiles
     const uint32_t ntiles = nfull + ((q1 - q0) % STEP ? 1 : 0);  // plus a partial one
 
-    // The first tile's loads go out before the window set is built.
+    // Set-up, ordered so that no wait for one load also waits for a tile:
+    // the window ids are loaded first, then the first tile; the ids go into
+    // the set, and each id's raw logit is loaded and stored only after the
+    // bootstrap has consumed the tile. A window longer than the workgroup
+    // (rare) is built in full before any tile load.
+    const uint32_t *wrow = a.windows + (uint64_t)row * a.wstride;
+    const bool small_win = pen && wl <= FAST_THREADS;
+    if (pen && !small_win) window_build(ws, wrow, wl, V, rowp, true);
+    const uint32_t *idp = small_win ? wrow + (tid < wl ? tid : wl - 1) : a.rows + slot;
+    const uint32_t id_loaded = *(const RL_GLB uint32_t *)idp;  // unconditional, see load_tile_clamped
+    // The first tile. A row of fewer than 4 logits has no tile; it loads 16
+    // bytes of its own settings instead, so that this load needs no branch
+    // either.
     f32x4 A[UNROLL], B[UNROLL];
-    if (nfull > 0)
-        load_tile<VEC, false>(A, rowp, q0, q1);
-    else if (ntiles > 0)
-        load_tile<VEC, true>(A, rowp, q0, q1);
+    {
+        const bool any = ntiles > 0;
+        load_tile_clamped<VEC>(A, any ? rowp : (const float *)(a.settings + row), any ? q0 : 0u, any ? q1 : 1u);
+    }
     RL_LDS uint64_t *lT = (RL_LDS uint64_t *)&s_T;
     if (tid == 0) *lT = 0;
-    window_build(ws, a.windows + (uint64_t)row * a.wstride, wl, V, rowp, pen);
+    if (!pen || small_win) window_clear(ws);
+    __syncthreads();
+    const uint32_t my_id = (small_win && tid < wl) ? id_loaded : EMPTY_ID;
+    const uint32_t my_slot = my_id < V ? window_insert(ws, my_id) : EMPTY_ID;
+    const float my_raw = ((const RL_GLB float *)rowp)[my_slot != EMPTY_ID ? my_id : 0u];
+    __syncthreads();
 
     Stream w;
     w.buf = (RL_LDS uint64_t *)s_buf + wave * CBUF;
     w.shared_T = lT;
     w.ws = ws;
+    w.wtop = ~0ull;  // the raw logits are not in yet: check every candidate
     w.T = 0;
     w.thr = greedy ? -3.40282347e38f : -__builtin_inff();
     w.cnt = 0;
@@ -473,22 +491,20 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
     w.pen = pen;
 
     if (nfull > 0) bootstrap(w, A, q0);
-    // Double-buffered: tile t+1 is in flight while tile t is filtered. The
-    // partial last tile goes through the same pipeline with guarded loads.
+    if (my_slot != EMPTY_ID) window_store(ws, my_slot, my_id, my_raw);
+    __syncthreads();
+    w.wtop = window_top(ws);
+    // Double-buffered: tile t+1 is in flight while tile t is filtered. Loads
+    // past the chunk are clamped (they cost one cache line per wave), so the
+    // last, partial tile runs through the same loop.
     for (uint32_t t = 0; t < ntiles; t += 2) {
-        const uint32_t b0 = q0 + t * STEP, b1 = b0 + STEP, b2 = b1 + STEP;
-        if (t + 1 < nfull)
-            load_tile<VEC, false>(B, rowp, b1, q1);
-        else if (t + 1 < ntiles)
-            load_tile<VEC, true>(B, rowp, b1, q1);
+        const uint32_t b0 = q0 + t * STEP, b1 = b0 + STEP;
+        load_tile_clamped<VEC>(B, rowp, b1, q1);
         if (t < nfull)
             process_tile<false>(w, A, b0, q1);
         else
             process_tile<true>(w, A, b0, q1);
-        if (t + 2 < nfull)
-            load_tile<VEC, false>(A, rowp, b2, q1);
-        else if (t + 2 < ntiles)
-            load_tile<VEC, true>(A, rowp, b2, q1);
+        load_tile_clamped<VEC>(A, rowp, b1 + STEP, q1);
         if (t + 1 < nfull)
             process_tile<false>(w, B, b1, q1);
         else if (t + 1 < ntiles)
