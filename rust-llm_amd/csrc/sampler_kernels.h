@@ -392,8 +392,11 @@ __device__ __forceinline__ void finalize_row(const RowIO &a, uint32_t row, const
 // Merges the window's distinct ids, with their penalised values
 // (sample.rs:242-255), into the wave's sorted candidates `top`; returns how
 // many were offered. In greedy mode ids whose penalised value argmax could
-// never pick (NaN, -inf) are left out.
-__device__ __forceinline__ uint32_t merge_window(uint64_t &top, const WindowSet &ws, float penalty, bool greedy) {
+// never pick (NaN, -inf) are left out. When `top` already holds k candidates,
+// `floor` is the k-th of them and ids at or below it are left out too (they
+// cannot be among the k best), which usually leaves nothing to sort.
+__device__ __forceinline__ uint32_t merge_window(uint64_t &top, const WindowSet &ws, float penalty, bool greedy,
+                                                 uint64_t floor) {
     const uint32_t lane = lane_id();
     uint32_t offered = 0;
     for (uint32_t base = 0; base < ws.slots; base += WAVE) {
@@ -404,6 +407,7 @@ __device__ __forceinline__ uint32_t merge_window(uint64_t &top, const WindowSet 
             const float x = penalize(ws.vals[i], penalty);
             const uint32_t key = greedy ? argmax_key(x) : total_key(x);
             if (!greedy || key != 0) c = composite(key, id);
+            if (c <= floor) c = 0;
         }
         const uint64_t present = ballot(c != 0);
         if (present == 0) continue;
@@ -533,7 +537,8 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
         total += s_cnt[j];
     }
     // The window's ids with their penalised values, once per row.
-    if (pen && chunk == 0) total += merge_window(top, ws, s.repeat_penalty, greedy);
+    if (pen && chunk == 0)
+        total += merge_window(top, ws, s.repeat_penalty, greedy, total >= k ? read_lane_u64(top, k - 1) : 0ull);
     const uint32_t nL = total < k ? total : k;
     if (lane >= nL) top = 0;
     if (a.chunks == 1) {
