@@ -264,6 +264,21 @@ __device__ __forceinline__ void bootstrap(Stream &w, const f32x4 *A, uint32_t ba
     publish_threshold(w.shared_T, w.T);
 }
 
+// The workgroups sharing a CU are otherwise served oldest first: the first
+// one dispatched finishes its row long before the last, and the CU then
+// streams with fewer and fewer waves. Lowering a wave's priority as its row
+// progresses (3 up to half the tiles, 2 up to 80 %, 1 up to 95 %, then 0)
+// lets the waves that are behind issue first, so the rows on a CU finish
+// together. Priority only orders instruction issue; it changes no result.
+__device__ __forceinline__ void set_progress_priority(uint32_t done, uint32_t total) {
+    if (done * 20 >= total * 19)
+        __builtin_amdgcn_s_setprio(0);
+    else if (done * 5 >= total * 4)
+        __builtin_amdgcn_s_setprio(1);
+    else if (done * 2 >= total)
+        __builtin_amdgcn_s_setprio(2);
+}
+
 // The row's f32::max fold over the penalised logits and its argmax, by one
 // wave re-reading the row. Only for a row whose k best are all +NaN, where the
 // candidates do not reveal the largest non-NaN value.
@@ -494,6 +509,8 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
     w.greedy = greedy;
     w.pen = pen;
 
+    // Wave priority falls as the row progresses (see set_progress_priority).
+    __builtin_amdgcn_s_setprio(3);
     if (nfull > 0) bootstrap(w, A, q0);
     if (my_slot != EMPTY_ID) window_store(ws, my_slot, my_id, my_raw);
     __syncthreads();
@@ -514,7 +531,9 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
         else if (t + 1 < ntiles)
             process_tile<true>(w, B, b1, q1);
         raise_threshold(w, load_shared_T(lT));
+        set_progress_priority(t + 2, ntiles);
     }
+    __builtin_amdgcn_s_setprio(0);
     // The row's last vocab % 4 elements.
     if (chunk == a.chunks - 1) {
         if (w.cnt >= w.k + SLACK) compact(w);
