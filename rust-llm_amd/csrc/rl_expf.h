@@ -36,7 +36,11 @@ __device__ __constant__ uint64_t EXP2_32_TAB[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-__device__ __forceinline__ float expf_libm(float x) {
+// tab(i) returns EXP2_32_TAB[i]; kernels that evaluate many exps pass a copy
+// of the table in LDS (copy_exp_table), since a per-lane index into constant
+// memory is a dependent global load on every call.
+template <class Tab>
+__device__ __forceinline__ float expf_libm_t(float x, Tab tab) {
     // Polynomial for 2^(r/32), coefficients pre-divided by 32^3, 32^2, 32.
     const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
     const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
@@ -57,7 +61,7 @@ __device__ __forceinline__ float expf_libm(float x) {
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd -= SHIFT;
     const double r = __builtin_fma(INV_LN2_32, xd, -kd);
-    const uint64_t t = EXP2_32_TAB[ki & 31u] + (ki << 47);
+    const uint64_t t = tab((uint32_t)(ki & 31u)) + (ki << 47);
     const double s = __longlong_as_double((long long)t);
     const double z = __builtin_fma(C0, r, C1);
     const double r2 = r * r;
@@ -66,5 +70,21 @@ __device__ __forceinline__ float expf_libm(float x) {
     y = y * s;
     return (float)y;
 }
+
+__device__ __forceinline__ float expf_libm(float x) {
+    return expf_libm_t(x, [](uint32_t i) { return EXP2_32_TAB[i]; });
+}
+
+// Whole-workgroup: copies the table into `lds` (32 entries). Ends with a
+// barrier.
+__device__ __forceinline__ void copy_exp_table(__attribute__((address_space(3))) uint64_t *lds) {
+    if (threadIdx.x < 32) lds[threadIdx.x] = EXP2_32_TAB[threadIdx.x];
+    __syncthreads();
+}
+
+struct LdsExpTable {
+    const __attribute__((address_space(3))) uint64_t *t;
+    __device__ uint64_t operator()(uint32_t i) const { return t[i]; }
+};
 
 }  // namespace rl

@@ -268,7 +268,7 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
         hipLaunchKernelGGL(k_full_keys, dim3(f.chunks, ng), dim3(FULL_THREADS),
                            window_lds_bytes(ctx->hash_bits), st, f, fs);
         hipLaunchKernelGGL(k_full_sort, dim3(ng), dim3(SORT_THREADS), 0, st, f, fs);
-        hipLaunchKernelGGL(k_full_replay, dim3(ng), dim3(FULL_THREADS), 0, st, f, fs);
+        hipLaunchKernelGGL(k_full_replay, dim3(ng), dim3(REPLAY_THREADS), 0, st, f, fs);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return hip_fail(e, "full-path kernels");
     }

@@ -15,6 +15,7 @@
 #pragma once
 #include "rl_device.h"
 #include "rl_expf.h"
+#include "rl_seqsum.h"
 
 namespace rl {
 
@@ -764,17 +765,55 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
 }
 
 // ------------------------------------------------------ FULL-path tail ---
-constexpr uint32_t FULL_WAVES = FULL_THREADS / WAVE;
-constexpr uint32_t SCAN_ITEMS = 16;  // elements per thread per scan tile
+constexpr uint32_t REPLAY_THREADS = 512;  // 8 waves: up to 256 VGPRs each, no spills
+constexpr uint32_t REPLAY_WAVES = REPLAY_THREADS / WAVE;
+constexpr uint32_t SEQ_ITEMS = 8;  // terms per thread per tile of the sum replay
 
-__device__ __forceinline__ double block_sum_f64(double v, RL_LDS double *red) {
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+constexpr uint32_t UN = 4;  // elements per thread per step of the replay kernel's loops
+constexpr uint32_t CI = 8;  // contiguous elements per thread per step of the compaction
+
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, RL_LDS uint32_t *red) {
+    for (int m = 32; m >= 1; m >>= 1) v += (uint32_t)__shfl_xor((int)v, m);
     __syncthreads();
     if (lane_id() == 0) red[threadIdx.x / WAVE] = v;
     __syncthreads();
-    double t = 0.0;
-    for (uint32_t w = 0; w < FULL_WAVES; ++w) t += red[w];
+    uint32_t t = 0;
+    for (uint32_t w = 0; w < REPLAY_WAVES; ++w) t += red[w];
     return t;
+}
+
+__device__ __forceinline__ int64_t block_max_i64(int64_t v, RL_LDS int64_t *red) {
+    for (int m = 32; m >= 1; m >>= 1) {
+        const int64_t o = (int64_t)shfl_xor_u64((uint64_t)v, m);
+        v = o > v ? o : v;
+    }
+    __syncthreads();
+    if (lane_id() == 0) red[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    int64_t t = red[0];
+    for (uint32_t w = 1; w < REPLAY_WAVES; ++w) t = red[w] > t ? red[w] : t;
+    return t;
+}
+
+// Exclusive prefix of v over the workgroup's threads in thread order; *total
+// gets the sum.
+__device__ __forceinline__ uint32_t block_exclusive_u32(uint32_t v, RL_LDS uint32_t *red, uint32_t *total) {
+    const uint32_t lane = lane_id(), wave = threadIdx.x / WAVE;
+    uint32_t incl = v;
+    for (uint32_t d = 1; d < WAVE; d <<= 1) {
+        const uint32_t o = (uint32_t)__shfl_up((int)incl, d);
+        if (lane >= d) incl += o;
+    }
+    __syncthreads();
+    if (lane == WAVE - 1) red[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+    for (uint32_t w = 0; w < REPLAY_WAVES; ++w) {
+        if (w < wave) before += red[w];
+        all += red[w];
+    }
+    *total = all;
+    return before + incl - v;
 }
 
 __device__ __forceinline__ int block_min_i32(int v, RL_LDS int *red) {
@@ -783,37 +822,8 @@ __device__ __forceinline__ int block_min_i32(int v, RL_LDS int *red) {
     if (lane_id() == 0) red[threadIdx.x / WAVE] = v;
     __syncthreads();
     int t = red[0];
-    for (uint32_t w = 1; w < FULL_WAVES; ++w) t = min(t, red[w]);
+    for (uint32_t w = 1; w < REPLAY_WAVES; ++w) t = min(t, red[w]);
     return t;
-}
-
-// Exclusive prefix of v over the block's threads in thread order; *total gets
-// the block's sum. Only used where every partial sum is exact, so the order of
-// the additions does not matter.
-__device__ __forceinline__ double block_exclusive_f64(double v, RL_LDS double *red, double *total) {
-    const uint32_t lane = lane_id(), wave = threadIdx.x / WAVE;
-    double incl = v;
-    for (uint32_t d = 1; d < WAVE; d <<= 1) {
-        const double o = __shfl_up(incl, d);
-        if (lane >= d) incl += o;
-    }
-    __syncthreads();
-    if (lane == WAVE - 1) red[wave] = incl;
-    __syncthreads();
-    double before = 0.0, all = 0.0;
-    for (uint32_t w = 0; w < FULL_WAVES; ++w) {
-        if (w < wave) before += red[w];
-        all += red[w];
-    }
-    *total = all;
-    return before + incl - v;
-}
-
-// Binary exponent of a finite nonzero f32 (subnormals count as -126): every
-// such value is a multiple of 2^(exponent - 23).
-__device__ __forceinline__ int f32_exponent(float p) {
-    const int e = (int)((__float_as_uint(p) >> 23) & 0xFFu);
-    return e == 0 ? -126 : e - 127;
 }
 
 // Walks src[0..n) in order on thread 0, one LDS-staged block at a time; the
@@ -823,7 +833,7 @@ __device__ __forceinline__ void staged_walk(const float *src, uint32_t n, RL_LDS
                                             RL_LDS uint32_t *stop, Body body) {
     for (uint32_t b = 0; b < n; b += STAGE) {
         const uint32_t cnt = min(STAGE, n - b);
-        for (uint32_t i = threadIdx.x; i < cnt; i += FULL_THREADS) stage[i] = ((const RL_GLB float *)src)[b + i];
+        for (uint32_t i = threadIdx.x; i < cnt; i += REPLAY_THREADS) stage[i] = ((const RL_GLB float *)src)[b + i];
         __syncthreads();
         if (threadIdx.x == 0) *stop = body(stage, b, cnt) ? 1u : 0u;
         __syncthreads();
@@ -831,27 +841,34 @@ __device__ __forceinline__ void staged_walk(const float *src, uint32_t n, RL_LDS
     }
 }
 
-// grid (slots), FULL_THREADS: the reference's tail over the whole candidate
-// list (sorted, or in id order when neither top-k nor top-p needs an order).
+struct NeverStop {
+    __device__ bool operator()(double) const { return false; }
+};
+
+// grid (slots), REPLAY_THREADS: the reference's tail (sample.rs:307-358) over
+// the whole candidate list (sorted, or in id order when neither top-k nor
+// top-p needs an order).
 //
-// The reference sums in candidate order in f64 (sample.rs:307-324, :342).
-// When every probability is a multiple of 2^(e_min - 23) and the total is below
-// 2^(29 + e_min), every partial sum is exactly representable in f64, so the
-// sequential sums equal sums in any order: the mass, the top-p cut and the
-// normalising total are then block reductions and scans. Otherwise they are
-// replayed in order on one thread. The draw (f32, sample.rs:349-356) is always
-// replayed in order.
-__global__ __launch_bounds__(FULL_THREADS) void k_full_replay(RowIO a, FullScratch f) {
+// The reference's sums are sequential in candidate order: the mass and the
+// top-p cumulative sum (f64, :307-324), the normalising total (f64, :342) and
+// the draw (f32, :349-356). seq_replay reproduces each one exactly with the
+// whole workgroup (rl_seqsum.h). Its premise is finite terms; a row with a NaN
+// or infinite probability (a NaN logit, a NaN temperature, or a normalising
+// total too small for 1/total to be finite) is walked in order by one thread
+// instead.
+__global__ __launch_bounds__(REPLAY_THREADS) void k_full_replay(RowIO a, FullScratch f) {
     __shared__ float stage_[STAGE];
-    __shared__ double red_d_[FULL_WAVES];
-    __shared__ int red_i_[FULL_WAVES];
-    __shared__ uint32_t wave_cnt_[FULL_WAVES];
+    __shared__ SeqLds<REPLAY_THREADS> seq;
+    __shared__ int red_i_[REPLAY_WAVES];
+    __shared__ uint32_t red_u_[REPLAY_WAVES];
+    __shared__ int64_t red_l_[REPLAY_WAVES];
     __shared__ uint32_t sh_m_, sh_stop_, sh_total_, sh_tok_;
-    __shared__ float sh_inv_;
-    __shared__ double sh_target_;
+    __shared__ double sh_d_;
+    __shared__ uint64_t exp_tab_[32];
     RL_LDS float *stage = (RL_LDS float *)stage_;
-    RL_LDS double *red_d = (RL_LDS double *)red_d_;
     RL_LDS int *red_i = (RL_LDS int *)red_i_;
+    RL_LDS uint32_t *red_u = (RL_LDS uint32_t *)red_u_;
+    RL_LDS int64_t *red_l = (RL_LDS int64_t *)red_l_;
     RL_LDS uint32_t *stop = (RL_LDS uint32_t *)&sh_stop_;
 
     const uint32_t slot = blockIdx.x;
@@ -870,64 +887,64 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_replay(RowIO a, FullScrat
     const uint32_t *keys = f.keyA + (uint64_t)slot * V;
     uint32_t *ids = f.idA + (uint64_t)slot * V;
     float *probs = f.probs + (uint64_t)slot * V;
+    const auto term = [probs](uint32_t j) { return ((const RL_GLB float *)probs)[j]; };
 
-    // exp (sample.rs:309), and what decides whether the f64 sums are exact.
-    int emin = 1 << 20;
+    // exp (sample.rs:309). Every loop over the candidates below loads UN
+    // elements per thread before it uses any, to keep loads in flight.
+    copy_exp_table((RL_LDS uint64_t *)exp_tab_);
+    const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab_};
     uint32_t bad = 0;
-    double part = 0.0;
-    for (uint32_t j = tid; j < k; j += FULL_THREADS) {
-        const float p = expf_libm((key_value(keys[j]) - M) / s.temperature);
-        probs[j] = p;
-        if (!(p <= 3.40282347e38f)) {
-            bad = 1;  // NaN or +inf
-        } else if (p > 0.0f) {
-            emin = min(emin, f32_exponent(p));
+    for (uint32_t b = 0; b < k; b += REPLAY_THREADS * UN) {
+        uint32_t kk[UN];
+#pragma unroll
+        for (uint32_t u = 0; u < UN; ++u) {
+            const uint32_t j = b + u * REPLAY_THREADS + tid;
+            kk[u] = j < k ? ((const RL_GLB uint32_t *)keys)[j] : 0u;
         }
-        part += (double)p;
+#pragma unroll
+        for (uint32_t u = 0; u < UN; ++u) {
+            const uint32_t j = b + u * REPLAY_THREADS + tid;
+            if (j < k) {
+                const float p = expf_libm_t((key_value(kk[u]) - M) / s.temperature, etab);
+                probs[j] = p;
+                if (!(p <= 3.40282347e38f)) bad = 1;  // NaN or +inf
+            }
+        }
     }
-    const double mass = block_sum_f64(part, red_d);
-    emin = block_min_i32(emin, red_i);
-    bad = (uint32_t)block_min_i32(bad ? 0 : 1, red_i) == 0 ? 1u : 0u;
-    const bool exact = !bad && (emin > 1000 || mass < ldexp(1.0, 29 + emin));
+    bad = block_min_i32(bad ? 0 : 1, red_i) == 0 ? 1u : 0u;
+    __syncthreads();
 
     uint32_t m = k;
+    // The sequential sum of the first m candidates, when a pass below has
+    // already produced it (-1 when not).
+    double sum_m = -1.0;
     if (s.top_p < 1.0f) {  // sample.rs:313-324
-        if (exact) {
-            const double target = (double)s.top_p * mass;
-            double base = 0.0;
-            for (uint32_t t0 = 0; t0 < k; t0 += FULL_THREADS * SCAN_ITEMS) {
-                const uint32_t j0 = t0 + tid * SCAN_ITEMS;
-                double mine = 0.0;
-                for (uint32_t i = 0; i < SCAN_ITEMS && j0 + i < k; ++i) mine += (double)probs[j0 + i];
-                double tile_total;
-                double c = base + block_exclusive_f64(mine, red_d, &tile_total);
-                int first = 0x7FFFFFFF;
-                for (uint32_t i = 0; i < SCAN_ITEMS && j0 + i < k; ++i) {
-                    c += (double)probs[j0 + i];
-                    if (c >= target) {
-                        first = (int)(j0 + i);
-                        break;
-                    }
-                }
-                first = block_min_i32(first, red_i);
-                if (first != 0x7FFFFFFF) {
-                    m = (uint32_t)first + 1;
-                    break;
-                }
-                base += tile_total;
-            }
+        double mass = 0.0;
+        if (!bad) {
+            seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, k, NeverStop{}, &seq, &mass);
+            sum_m = mass;
         } else {
-            double sum = 0.0;
             staged_walk(probs, k, stage, stop, [&](RL_LDS float *st, uint32_t, uint32_t cnt) {
-                for (uint32_t i = 0; i < cnt; ++i) sum += (double)st[i];
+                for (uint32_t i = 0; i < cnt; ++i) mass += (double)st[i];
                 return false;
             });
-            if (tid == 0) {
-                sh_target_ = (double)s.top_p * sum;
-                sh_m_ = k;
-            }
+            if (tid == 0) sh_d_ = mass;
             __syncthreads();
-            const double target = sh_target_;
+            mass = sh_d_;
+        }
+        const double target = (double)s.top_p * mass;
+        if (!bad) {
+            double at;
+            const uint32_t j =
+                seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, k, [target](double c) { return c >= target; }, &seq,
+                                                        &at);
+            if (j < k) {
+                m = j + 1;
+                sum_m = at;
+            }
+        } else {
+            if (tid == 0) sh_m_ = k;
+            __syncthreads();
             double cum = 0.0;
             staged_walk(probs, k, stage, stop, [&](RL_LDS float *st, uint32_t b, uint32_t cnt) {
                 for (uint32_t i = 0; i < cnt; ++i) {
@@ -944,99 +961,137 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_replay(RowIO a, FullScrat
         }
     }
     if (s.min_p > 0.0f) {  // sample.rs:326-340, a stable in-place compaction
-        if (tid == 0) sh_total_ = 0;
-        __syncthreads();
-        for (uint32_t b = 0; b < m; b += FULL_THREADS) {
-            const uint32_t j = b + tid;
-            const bool ok = j < m;
-            const float p = ok ? probs[j] : 0.0f;
-            const uint32_t id = ok ? ids[j] : 0u;
-            const bool surv = ok && p >= s.min_p;
-            const uint64_t bm = ballot(surv);
-            if (lane == 0) wave_cnt_[wave] = (uint32_t)__popcll(bm);
-            __syncthreads();
-            uint32_t before = sh_total_, all = 0;
-            for (uint32_t w = 0; w < FULL_WAVES; ++w) {
-                if (w < wave) before += wave_cnt_[w];
-                all += wave_cnt_[w];
-            }
-            __syncthreads();
-            if (surv) {
-                const uint32_t dst = before + lanes_below(bm);
-                ids[dst] = id;
-                probs[dst] = p;
-            }
-            if (tid == 0) sh_total_ += all;
-            __syncthreads();
-        }
-        m = sh_total_ > 1 ? sh_total_ : 1u;
-    }
-    // Normalise: f64 total in order, then f32 multiply (sample.rs:342-347).
-    double total;
-    if (exact) {
-        double t = 0.0;
-        for (uint32_t j = tid; j < m; j += FULL_THREADS) t += (double)probs[j];
-        total = block_sum_f64(t, red_d);
-    } else {
-        double t = 0.0;
-        staged_walk(probs, m, stage, stop, [&](RL_LDS float *st, uint32_t, uint32_t cnt) {
-            for (uint32_t i = 0; i < cnt; ++i) t += (double)st[i];
-            return false;
-        });
-        if (tid == 0) sh_target_ = t;
-        __syncthreads();
-        total = sh_target_;
-    }
-    const float inv = (float)(1.0 / total);
-    for (uint32_t j = tid; j < m; j += FULL_THREADS) {
-        const float q = probs[j] * inv;
-        probs[j] = q;
-        if (a.out_ids) {
-            a.out_ids[(uint64_t)row * a.cand_stride + j] = ids[j];
-            a.out_probs[(uint64_t)row * a.cand_stride + j] = q;
-        }
-    }
-    if (tid == 0) sh_tok_ = m - 1;  // f32 shortfall: the last candidate (sample.rs:357-358)
-    __syncthreads();
-    // The draw: f32 running sum against the host's uniform (sample.rs:349-356).
-    // q >= 0 (or NaN), so the running sum never decreases and a group of 16
-    // whose last sum is <= u holds no crossing; any other group (including one
-    // where a NaN entered) is scanned element by element.
-    const float u = a.uniforms[row];
-    float cum = 0.0f;
-    staged_walk(probs, m, stage, stop, [&](RL_LDS float *st, uint32_t b, uint32_t cnt) {
-        uint32_t i = 0;
-        for (; i + 16 <= cnt; i += 16) {
-            float c[16];
-            float x = cum;
+        // First whether the survivors are already a prefix (always so when
+        // the candidates are sorted, as p falls along the order): then the
+        // compaction moves nothing and only the count changes.
+        uint32_t first_out = 0xFFFFFFFFu, last_in = 0, count = 0;
+        for (uint32_t b = 0; b < m; b += REPLAY_THREADS * UN) {
+            float pp[UN];
 #pragma unroll
-            for (uint32_t t = 0; t < 16; ++t) {
-                x += st[i + t];
-                c[t] = x;
+            for (uint32_t u = 0; u < UN; ++u) {
+                const uint32_t j = b + u * REPLAY_THREADS + tid;
+                pp[u] = j < m ? ((const RL_GLB float *)probs)[j] : 0.0f;
             }
-            if (!(c[15] <= u)) {
 #pragma unroll
-                for (uint32_t t = 0; t < 16; ++t) {
-                    if (c[t] > u) {
-                        sh_tok_ = b + i + t;
-                        return true;
+            for (uint32_t u = 0; u < UN; ++u) {
+                const uint32_t j = b + u * REPLAY_THREADS + tid;
+                if (j < m) {
+                    if (pp[u] >= s.min_p) {
+                        ++count;
+                        last_in = j + 1;
+                    } else if (first_out == 0xFFFFFFFFu) {
+                        first_out = j;
                     }
                 }
             }
-            cum = x;
         }
-        for (; i < cnt; ++i) {
-            cum += st[i];
-            if (cum > u) {
-                sh_tok_ = b + i;
-                return true;
+        const uint32_t all_in = block_sum_u32(count, red_u);
+        const uint32_t lo_out = (uint32_t)-block_max_i64(-(int64_t)first_out, red_l);
+        const uint32_t hi_in = (uint32_t)block_max_i64((int64_t)last_in, red_l);
+        if (hi_in > lo_out) {
+            // Not a prefix: stable compaction, CI contiguous elements per
+            // thread per step.
+            uint32_t done = 0;
+            for (uint32_t b = 0; b < m; b += REPLAY_THREADS * CI) {
+                const uint32_t j0 = b + tid * CI;
+                float pv[CI];
+                uint32_t iv[CI];
+                uint32_t mine = 0;
+#pragma unroll
+                for (uint32_t i = 0; i < CI; ++i) {
+                    const bool ok = j0 + i < m;
+                    pv[i] = ok ? probs[j0 + i] : 0.0f;
+                    iv[i] = ok ? ids[j0 + i] : 0u;
+                    mine += (ok && pv[i] >= s.min_p) ? 1u : 0u;
+                }
+                uint32_t step_total;
+                const uint32_t before = block_exclusive_u32(mine, red_u, &step_total);
+                uint32_t dst = done + before;
+#pragma unroll
+                for (uint32_t i = 0; i < CI; ++i) {
+                    if (j0 + i < m && pv[i] >= s.min_p) {
+                        ids[dst] = iv[i];
+                        probs[dst] = pv[i];
+                        ++dst;
+                    }
+                }
+                done += step_total;
+                __syncthreads();
             }
         }
-        return false;
-    });
+        if (all_in != m) sum_m = -1.0;
+        m = all_in > 1 ? all_in : 1u;
+    }
+    // Normalise: f64 total in order, then f32 multiply (sample.rs:342-347).
+    double total = 0.0;
+    if (!bad && sum_m >= 0.0) {
+        total = sum_m;  // the same terms in the same order as the top-p pass
+    } else if (!bad) {
+        seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, m, NeverStop{}, &seq, &total);
+    } else {
+        staged_walk(probs, m, stage, stop, [&](RL_LDS float *st, uint32_t, uint32_t cnt) {
+            for (uint32_t i = 0; i < cnt; ++i) total += (double)st[i];
+            return false;
+        });
+        if (tid == 0) sh_d_ = total;
+        __syncthreads();
+        total = sh_d_;
+    }
+    const float inv = (float)(1.0 / total);
+    uint32_t qbad = 0;
+    for (uint32_t b = 0; b < m; b += REPLAY_THREADS * UN) {
+        float pp[UN];
+        uint32_t iv[UN];
+#pragma unroll
+        for (uint32_t u = 0; u < UN; ++u) {
+            const uint32_t j = b + u * REPLAY_THREADS + tid;
+            pp[u] = j < m ? ((const RL_GLB float *)probs)[j] : 0.0f;
+            iv[u] = (j < m && a.out_ids) ? ((const RL_GLB uint32_t *)ids)[j] : 0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < UN; ++u) {
+            const uint32_t j = b + u * REPLAY_THREADS + tid;
+            if (j < m) {
+                const float q = pp[u] * inv;
+                probs[j] = q;
+                if (!(q <= 3.40282347e38f)) qbad = 1;
+                if (a.out_ids) {
+                    a.out_ids[(uint64_t)row * a.cand_stride + j] = iv[u];
+                    a.out_probs[(uint64_t)row * a.cand_stride + j] = q;
+                }
+            }
+        }
+    }
+    qbad = block_min_i32(qbad ? 0 : 1, red_i) == 0 ? 1u : 0u;
     __syncthreads();
+    // The draw: f32 running sum against the host's uniform (sample.rs:349-356);
+    // a shortfall takes the last candidate (:357-358).
+    const float u = a.uniforms[row];
+    uint32_t pick;
+    if (!qbad) {
+        double unused;
+        const uint32_t j = seq_replay<24, REPLAY_THREADS, SEQ_ITEMS>(
+            term, m, [u](double c) { return c > (double)u; }, &seq, &unused);
+        pick = j < m ? j : m - 1;
+    } else {
+        if (tid == 0) sh_tok_ = m - 1;
+        __syncthreads();
+        float cum = 0.0f;
+        staged_walk(probs, m, stage, stop, [&](RL_LDS float *st, uint32_t b, uint32_t cnt) {
+            for (uint32_t i = 0; i < cnt; ++i) {
+                cum += st[i];
+                if (cum > u) {
+                    sh_tok_ = b + i;
+                    return true;
+                }
+            }
+            return false;
+        });
+        __syncthreads();
+        pick = sh_tok_;
+    }
     if (tid == 0) {
-        a.out_token[row] = ids[sh_tok_];
+        a.out_token[row] = ids[pick];
         a.out_kept[row] = m;
         a.out_used[row] = 1;
     }
@@ -1092,8 +1147,11 @@ __global__ void k_argmax_final(const uint64_t *part, uint32_t rows, uint32_t chu
 }
 
 __global__ void k_expf_range(uint32_t lo_bits, uint64_t count, float *out) {
+    __shared__ uint64_t tab[32];
+    copy_exp_table((RL_LDS uint64_t *)tab);
+    const LdsExpTable etab{(RL_LDS uint64_t *)tab};
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < count) out[i] = expf_libm(__uint_as_float(lo_bits + (uint32_t)i));
+    if (i < count) out[i] = expf_libm_t(__uint_as_float(lo_bits + (uint32_t)i), etab);
 }
 
 }  // namespace rl
