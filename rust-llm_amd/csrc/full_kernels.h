@@ -1,0 +1,945 @@
+// The FULL device path: rows with top_k == 0, top_k >= vocab or top_k > 64
+// (sample.rs:279-358 over the whole candidate list). Seven launches per group
+// of rows, alternating kernels that spread a row over many workgroups (the
+// HBM- and ALU-heavy steps) with one workgroup per row (the steps that follow
+// the reference's sequential order):
+//
+//   k_full_keys   (chunks x rows)  total-order keys in id order; the f32::max
+//                                  fold and argmax over the non-window ids
+//   k_full_sort   (rows)           the window's penalised values merged in
+//                                  (max, argmax, keys); the row sorted by the
+//                                  reference's order unless it keeps id order
+//   k_full_probs  (chunks x rows)  p = exp((l - max) / T) in candidate order,
+//                                  per-chunk sums, smallest exponent, min-p
+//                                  counts
+//   k_full_tail   (rows)           mass, top-p cut, min-p, normalising total
+//   k_full_norm   (chunks x rows)  q = p * (1 / total), the kept candidates
+//   k_full_draw   (rows)           the f32 draw against the host's uniform
+//
+// The sums are the reference's sequential sums, bit for bit: when every p is a
+// multiple of 2^(e_min - 23) and the mass is below 2^(30 + e_min), every partial
+// sum is exactly representable, so any order of addition gives the same bits
+// and the per-chunk sums serve; otherwise seq_replay (rl_seqsum.h) reproduces
+// the sequential rounding in parallel. Rows with a NaN or infinite p (NaN
+// logits, a NaN temperature, 1 / total overflowing) are walked in order by one
+// thread.
+#pragma once
+#include "sampler_kernels.h"
+
+namespace rl {
+
+struct FullRow {
+    float M;          // the f32::max fold of the penalised row
+    uint32_t am_tok;  // argmax of the penalised row
+    uint32_t done;    // the row is finished (no finite maximum)
+    uint32_t m;       // candidates kept (after top-p and min-p)
+    float inv;        // (1 / total) as f32
+    uint32_t qbad;    // a normalised probability is not finite
+    uint32_t pad[2];
+};
+
+struct FullScratch {
+    uint32_t *keyA, *idA, *keyB, *idB;  // [slot][vocab]
+    float *probs;                       // [slot][vocab]
+    float *part_max;                    // [slot][chunk] keys pass
+    uint64_t *part_am;                  // [slot][chunk]
+    double *psum;                       // [slot][chunk] probs pass
+    int *pemin;                         // [slot][chunk]
+    uint32_t *pcount;                   // [slot][chunk]
+    uint32_t *pbad;                     // [slot][chunk]
+    FullRow *row;                       // [slot]
+};
+
+__device__ __forceinline__ uint32_t full_k(const rl_sampling &s, uint32_t V) {
+    return s.top_k == 0 ? V : (s.top_k < V ? (uint32_t)s.top_k : V);  // sample.rs:289
+}
+__device__ __forceinline__ bool identity_order(const rl_sampling &s, uint32_t V) {
+    return full_k(s, V) == V && !(s.top_p < 1.0f);  // no select and no sort
+}
+
+// Chunk c of n items split into `chunks`: [chunk_lo(c), chunk_lo(c + 1)).
+__device__ __forceinline__ uint32_t chunk_lo(uint32_t n, uint32_t c, uint32_t chunks) {
+    return (uint32_t)((uint64_t)n * c / chunks);
+}
+
+// Binary exponent of a finite nonzero f32 (subnormals count as -126): every
+// such value is a multiple of 2^(exponent - 23).
+__device__ __forceinline__ int f32_exponent(float p) {
+    const int e = (int)((__float_as_uint(p) >> 23) & 0xFFu);
+    return e == 0 ? -126 : e - 127;
+}
+
+// ------------------------------------------------------------- keys ---
+// grid (chunks, slots), FULL_THREADS: the row's raw logits as total-order keys
+// in id order (the window ids' keys are rewritten by k_full_sort), and per
+// chunk the f32::max fold (NaN ignored) and the argmax composite over the ids
+// outside the window. A lane checks window membership only when an element
+// would raise its running maximum, so almost no element costs a lookup.
+template <bool VEC>
+__global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch f) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const WindowSet ws = window_set(smem, a.hash_bits);
+    __shared__ float red_max[FULL_THREADS / WAVE];
+    __shared__ uint64_t red_am[FULL_THREADS / WAVE];
+    const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
+    const uint32_t row = a.rows[slot];
+    const rl_sampling s = a.settings[row];
+    const uint32_t V = a.vocab;
+    const uint32_t wl = window_len(a, row);
+    const bool pen = penalises(s) && wl > 0;
+    const float *rowp = a.logits + (uint64_t)row * a.stride;
+    window_build(ws, a.windows + (uint64_t)row * a.wstride, wl, V, rowp, pen);
+    const uint32_t n4 = V / 4;
+    const uint32_t q0 = chunk_lo(n4, chunk, a.chunks), q1 = chunk_lo(n4, chunk + 1, a.chunks);
+    uint32_t *keys = f.keyA + (uint64_t)slot * V;
+    uint32_t *ids = f.idA + (uint64_t)slot * V;
+    const bool vstore = ((reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(ids)) & 15u) == 0;
+    float mx = -__builtin_inff();
+    uint64_t am = 0;
+    auto take = [&](float x, uint32_t id) {
+        const uint64_t c = composite(argmax_key(x), id);
+        const bool up_max = x > mx, up_am = c > am;
+        if ((up_max || up_am) && !(pen && window_contains(ws, id))) {
+            if (up_max) mx = x;
+            if (up_am) am = c;
+        }
+    };
+    for (uint32_t q = q0 + threadIdx.x; q < q1; q += FULL_THREADS) {
+        const f32x4 v = load4<VEC>(rowp, q);
+        const float x[4] = {v.x, v.y, v.z, v.w};
+        uint32_t kk[4];
+#pragma unroll
+        for (uint32_t c = 0; c < 4; ++c) {
+            kk[c] = total_key(x[c]);
+            take(x[c], 4 * q + c);
+        }
+        if (vstore) {
+            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+            *(RL_GLB u32x4 *)(keys + 4 * q) = u32x4{kk[0], kk[1], kk[2], kk[3]};
+            *(RL_GLB u32x4 *)(ids + 4 * q) = u32x4{4 * q, 4 * q + 1, 4 * q + 2, 4 * q + 3};
+        } else {
+#pragma unroll
+            for (uint32_t c = 0; c < 4; ++c) {
+                keys[4 * q + c] = kk[c];
+                ids[4 * q + c] = 4 * q + c;
+            }
+        }
+    }
+    if (chunk == a.chunks - 1) {  // the last vocab % 4 elements
+        const uint32_t e = 4 * n4 + threadIdx.x;
+        if (e < V) {
+            const float x = ((const RL_GLB float *)rowp)[e];
+            keys[e] = total_key(x);
+            ids[e] = e;
+            take(x, e);
+        }
+    }
+    mx = wave_maxnum_f32(mx);
+    am = wave_max_u64(am);
+    const uint32_t wave = threadIdx.x / WAVE;
+    if (lane_id() == 0) {
+        red_max[wave] = mx;
+        red_am[wave] = am;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t i = 1; i < FULL_THREADS / WAVE; ++i) {
+            mx = fmaxf(mx, red_max[i]);
+            am = red_am[i] > am ? red_am[i] : am;
+        }
+        f.part_max[slot * a.chunks + chunk] = mx;
+        f.part_am[slot * a.chunks + chunk] = am;
+    }
+}
+
+// ------------------------------------------------------------- sort ---
+// One wave's lanes with the same 8-bit digit (among the lanes where valid).
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
+    uint64_t m = ballot(valid);
+#pragma unroll
+    for (uint32_t b = 0; b < 8; ++b) {
+        const bool bit = (d >> b) & 1u;
+        const uint64_t bb = ballot(bit);
+        m &= bit ? bb : ~bb;
+    }
+    return m;
+}
+
+constexpr uint32_t SORT_ITEMS = 8;                          // elements per lane per tile
+constexpr uint32_t SORT_TILE = SORT_THREADS * SORT_ITEMS;    // elements per tile
+constexpr uint32_t WAVE_SEG = WAVE * SORT_ITEMS;             // a wave's contiguous share of a tile
+
+// grid (slots), SORT_THREADS.
+//
+// First the penalty's effect on the maximum, the argmax and the keys
+// (sample.rs:241-257, 267-277): the chunks' results cover the ids outside the
+// window; each distinct window id's penalised logit is merged in and its key
+// rewritten (from the raw logit, so a repeated id is rewritten to the same
+// value). A row without a finite maximum is answered here (argmax, no draw).
+//
+// Then a stable LSD radix sort of the row's (key, id) pairs by descending key,
+// 8 bits a pass; ids start in ascending order, so ties keep ascending ids (the
+// order of sample.rs:282-286). One read gives all four digits' histograms. A
+// pass is skipped when its digit is the same for every key of each sign (as
+// for logits on a bf16 grid, whose low 16 key bits follow the sign): keys that
+// agree above such a digit agree on it, so the pass could not change the final
+// order. Each tile gives every wave a contiguous segment, ranked item by item
+// with wave-local running counts per digit, so a tile of SORT_TILE elements
+// costs three barriers. The result ends in keyA/idA.
+__global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch f) {
+    __shared__ uint32_t hist[4][256];
+    __shared__ uint32_t offs[256];
+    __shared__ uint32_t cnt[SORT_WAVES][256];
+    __shared__ uint32_t pos[SORT_WAVES][256];
+    __shared__ uint32_t cls[4];  // OR and AND of the keys with the top bit clear, then set
+    __shared__ uint32_t tcount[256], tstart[256];
+    __shared__ uint32_t tile_k[SORT_TILE], tile_i[SORT_TILE];
+    __shared__ float red_max[SORT_WAVES];
+    __shared__ uint64_t red_am[SORT_WAVES];
+    const uint32_t slot = blockIdx.x;
+    const uint32_t row = a.rows[slot];
+    const rl_sampling s = a.settings[row];
+    const uint32_t V = a.vocab;
+    const uint32_t tid = threadIdx.x, wave = tid / WAVE, lane = lane_id();
+    const uint32_t wl = window_len(a, row);
+    const bool pen = penalises(s) && wl > 0;
+    const float *rowp = a.logits + (uint64_t)row * a.stride;
+    uint32_t *kin = f.keyA + (uint64_t)slot * V, *iin = f.idA + (uint64_t)slot * V;
+
+    float mx = -__builtin_inff();
+    uint64_t am = 0;
+    for (uint32_t c = tid; c < a.chunks; c += SORT_THREADS) {
+        mx = fmaxf(mx, f.part_max[slot * a.chunks + c]);
+        const uint64_t x = f.part_am[slot * a.chunks + c];
+        am = x > am ? x : am;
+    }
+    if (pen) {
+        const uint32_t *win = a.windows + (uint64_t)row * a.wstride;
+        for (uint32_t i = tid; i < wl; i += SORT_THREADS) {
+            const uint32_t id = win[i];
+            if (id >= V) continue;  // sample.rs:248
+            const float x = penalize(((const RL_GLB float *)rowp)[id], s.repeat_penalty);
+            kin[id] = total_key(x);
+            mx = fmaxf(mx, x);
+            const uint64_t c = composite(argmax_key(x), id);
+            am = c > am ? c : am;
+        }
+    }
+    mx = wave_maxnum_f32(mx);
+    am = wave_max_u64(am);
+    if (lane == 0) {
+        red_max[wave] = mx;
+        red_am[wave] = am;
+    }
+    __syncthreads();
+    for (uint32_t w = 0; w < SORT_WAVES; ++w) {
+        mx = fmaxf(mx, red_max[w]);
+        am = red_am[w] > am ? red_am[w] : am;
+    }
+    const uint32_t am_tok = comp_key(am) == 0 ? 0u : comp_id(am);
+    const bool finite = mx > -__builtin_inff() && mx < __builtin_inff();
+    if (tid == 0) {
+        FullRow st{};
+        st.M = mx;
+        st.am_tok = am_tok;
+        st.done = finite ? 0u : 1u;
+        f.row[slot] = st;
+        if (!finite) write_single(a, row, am_tok);  // sample.rs:270-277
+    }
+    if (!finite || identity_order(s, V)) return;
+
+    // Which passes run: per sign, the OR and the AND of its keys give the bits
+    // in which keys of that sign differ (OR ^ AND); over all keys, the bits in
+    // which any keys differ.
+    if (tid < 4) cls[tid] = (tid & 1) ? 0xFFFFFFFFu : 0u;
+    __syncthreads();  // also makes the rewritten window keys visible
+    {
+        uint32_t or0 = 0u, and0 = 0xFFFFFFFFu, or1 = 0u, and1 = 0xFFFFFFFFu;
+        for (uint32_t base = 0; base < V; base += SORT_THREADS * 4) {
+            uint32_t kk[4];
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+                const uint32_t j = base + u * SORT_THREADS + tid;
+                kk[u] = j < V ? ((const RL_GLB uint32_t *)kin)[j] : 0u;
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+                if (base + u * SORT_THREADS + tid < V) {
+                    if (kk[u] >> 31) {
+                        or1 |= kk[u];
+                        and1 &= kk[u];
+                    } else {
+                        or0 |= kk[u];
+                        and0 &= kk[u];
+                    }
+                }
+            }
+        }
+        for (int m = 32; m >= 1; m >>= 1) {
+            or0 |= (uint32_t)__shfl_xor((int)or0, m);
+            and0 &= (uint32_t)__shfl_xor((int)and0, m);
+            or1 |= (uint32_t)__shfl_xor((int)or1, m);
+            and1 &= (uint32_t)__shfl_xor((int)and1, m);
+        }
+        if (lane == 0) {
+            atomicOr(&cls[0], or0);
+            atomicAnd(&cls[1], and0);
+            atomicOr(&cls[2], or1);
+            atomicAnd(&cls[3], and1);
+        }
+    }
+    __syncthreads();
+    // An absent sign adds nothing: a key with the top bit clear clears it in
+    // the AND of that sign, one with it set sets it in the OR of its sign.
+    const bool has0 = cls[1] != 0xFFFFFFFFu, has1 = cls[2] != 0u;
+    const uint32_t vary_sign = (has0 ? (cls[0] ^ cls[1]) : 0u) | (has1 ? (cls[2] ^ cls[3]) : 0u);
+    const uint32_t all_or = (has0 ? cls[0] : 0u) | (has1 ? cls[2] : 0u);
+    const uint32_t all_and = (has0 ? cls[1] : 0xFFFFFFFFu) & (has1 ? cls[3] : 0xFFFFFFFFu);
+    // A lower digit's pass is skipped when the digit is the same for all keys
+    // of each sign; the top digit's when it is the same for all keys.
+    bool need[4];
+    for (uint32_t t = 0; t < 3; ++t) need[t] = ((vary_sign >> (8 * t)) & 255u) != 0;
+    need[3] = ((all_or ^ all_and) >> 24) != 0;
+
+    // Histograms of the digits that are sorted on (values flipped, 255 - d,
+    // for a descending order).
+    for (uint32_t i = tid; i < 4 * 256; i += SORT_THREADS) (&hist[0][0])[i] = 0;
+    __syncthreads();
+    if (need[0] || need[1] || need[2] || need[3]) {
+        for (uint32_t base = 0; base < V; base += SORT_THREADS * 4) {
+            uint32_t kk[4];
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+                const uint32_t j = base + u * SORT_THREADS + tid;
+                kk[u] = j < V ? ((const RL_GLB uint32_t *)kin)[j] : 0u;
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+                if (base + u * SORT_THREADS + tid < V) {
+#pragma unroll
+                    for (uint32_t t = 0; t < 4; ++t)
+                        if (need[t]) atomicAdd(&hist[t][255u - ((kk[u] >> (8 * t)) & 255u)], 1u);
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // The passes. Each tile is ranked per wave (a contiguous segment each),
+    // reordered by digit in LDS, and written out in runs, so that consecutive
+    // lanes write consecutive addresses.
+    uint32_t *kout = f.keyB + (uint64_t)slot * V, *iout = f.idB + (uint64_t)slot * V;
+    RL_LDS uint32_t *lk = (RL_LDS uint32_t *)tile_k, *li = (RL_LDS uint32_t *)tile_i;
+    for (uint32_t t = 0; t < 4; ++t) {
+        if (!need[t]) continue;
+        if (tid < WAVE) {  // offs = exclusive prefix of the histogram
+            uint32_t v[4], sum = 0;
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) {
+                v[q] = hist[t][4 * tid + q];
+                sum += v[q];
+            }
+            uint32_t incl = sum;
+            for (uint32_t d = 1; d < WAVE; d <<= 1) {
+                const uint32_t o = (uint32_t)__shfl_up((int)incl, d);
+                if (lane >= d) incl += o;
+            }
+            uint32_t run = incl - sum;
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) {
+                offs[4 * tid + q] = run;
+                run += v[q];
+            }
+        }
+        __syncthreads();
+        const uint32_t shift = 8 * t;
+        // The next tile's keys and ids load while this one is ranked.
+        uint32_t nk[SORT_ITEMS], ni[SORT_ITEMS];
+#pragma unroll
+        for (uint32_t i = 0; i < SORT_ITEMS; ++i) {
+            const uint32_t e = wave * WAVE_SEG + lane + i * WAVE;
+            nk[i] = e < V ? ((const RL_GLB uint32_t *)kin)[e] : 0u;
+            ni[i] = e < V ? ((const RL_GLB uint32_t *)iin)[e] : 0u;
+        }
+        for (uint32_t tb = 0; tb < V; tb += SORT_TILE) {
+            const uint32_t e0 = tb + wave * WAVE_SEG + lane;
+            const uint32_t tn = min(SORT_TILE, V - tb);
+            uint32_t kk[SORT_ITEMS], ii[SORT_ITEMS], rk[SORT_ITEMS];
+#pragma unroll
+            for (uint32_t i = 0; i < SORT_ITEMS; ++i) {
+                kk[i] = nk[i];
+                ii[i] = ni[i];
+                const uint32_t e = e0 + SORT_TILE + i * WAVE;
+                nk[i] = e < V ? ((const RL_GLB uint32_t *)kin)[e] : 0u;
+                ni[i] = e < V ? ((const RL_GLB uint32_t *)iin)[e] : 0u;
+            }
+            for (uint32_t d = lane; d < 256; d += WAVE) cnt[wave][d] = 0;
+            wave_lds_sync();
+#pragma unroll
+            for (uint32_t i = 0; i < SORT_ITEMS; ++i) {
+                const bool valid = e0 + i * WAVE < V;
+                const uint32_t d = 255u - ((kk[i] >> shift) & 255u);
+                const uint64_t peers = match_digit(d, valid);
+                const uint32_t before = valid ? cnt[wave][d] : 0u;
+                rk[i] = before + lanes_below(peers);
+                wave_lds_sync();
+                if (valid && lanes_below(peers) == 0) cnt[wave][d] = before + (uint32_t)__popcll(peers);
+                wave_lds_sync();
+            }
+            __syncthreads();
+            // Per digit: each wave's start within the digit's run of the tile,
+            // and the run's length.
+            if (tid < 256) {
+                uint32_t run = 0;
+                for (uint32_t w = 0; w < SORT_WAVES; ++w) {
+                    pos[w][tid] = run;
+                    run += cnt[w][tid];
+                }
+                tcount[tid] = run;
+            }
+            __syncthreads();
+            if (tid < WAVE) {  // tstart = exclusive prefix of the runs' lengths
+                uint32_t v[4], sum = 0;
+#pragma unroll
+                for (uint32_t q = 0; q < 4; ++q) {
+                    v[q] = tcount[4 * tid + q];
+                    sum += v[q];
+                }
+                uint32_t incl = sum;
+                for (uint32_t d = 1; d < WAVE; d <<= 1) {
+                    const uint32_t o = (uint32_t)__shfl_up((int)incl, d);
+                    if (lane >= d) incl += o;
+                }
+                uint32_t run = incl - sum;
+#pragma unroll
+                for (uint32_t q = 0; q < 4; ++q) {
+                    tstart[4 * tid + q] = run;
+                    run += v[q];
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (uint32_t i = 0; i < SORT_ITEMS; ++i) {
+                if (e0 + i * WAVE < V) {
+                    const uint32_t d = 255u - ((kk[i] >> shift) & 255u);
+                    const uint32_t at = tstart[d] + pos[wave][d] + rk[i];
+                    lk[at] = kk[i];
+                    li[at] = ii[i];
+                }
+            }
+            __syncthreads();
+            for (uint32_t j = tid; j < tn; j += SORT_THREADS) {
+                const uint32_t key = lk[j];
+                const uint32_t d = 255u - ((key >> shift) & 255u);
+                const uint32_t dst = offs[d] + (j - tstart[d]);
+                kout[dst] = key;
+                iout[dst] = li[j];
+            }
+            __syncthreads();
+            if (tid < 256) offs[tid] += tcount[tid];
+            __syncthreads();
+        }
+        uint32_t *tmp;
+        tmp = kin; kin = kout; kout = tmp;
+        tmp = iin; iin = iout; iout = tmp;
+    }
+    if (kin != f.keyA + (uint64_t)slot * V) {  // an odd number of passes ran
+        for (uint32_t j = tid; j < V; j += SORT_THREADS) {
+            kout[j] = kin[j];
+            iout[j] = iin[j];
+        }
+    }
+}
+
+// ------------------------------------------------------------ probs ---
+constexpr uint32_t UN = 4;  // elements per thread per step of the bulk loops
+
+// grid (chunks, slots), FULL_THREADS: p_j = exp((l_j - max) / T) for the
+// candidates of this chunk (sample.rs:309), and per chunk: their f64 sum,
+// the smallest binary exponent of a nonzero p, how many are >= min_p, and
+// whether one is NaN or infinite.
+__global__ __launch_bounds__(FULL_THREADS) void k_full_probs(RowIO a, FullScratch f) {
+    __shared__ uint64_t exp_tab[32];
+    __shared__ double red_d[FULL_THREADS / WAVE];
+    __shared__ int red_e[FULL_THREADS / WAVE];
+    __shared__ uint32_t red_c[FULL_THREADS / WAVE], red_b[FULL_THREADS / WAVE];
+    const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
+    const FullRow st = f.row[slot];
+    if (st.done) return;
+    const uint32_t row = a.rows[slot];
+    const rl_sampling s = a.settings[row];
+    const uint32_t V = a.vocab;
+    const uint32_t k = full_k(s, V);
+    const uint32_t j0 = chunk_lo(k, chunk, a.chunks), j1 = chunk_lo(k, chunk + 1, a.chunks);
+    const uint32_t *keys = f.keyA + (uint64_t)slot * V;
+    float *probs = f.probs + (uint64_t)slot * V;
+    copy_exp_table((RL_LDS uint64_t *)exp_tab);
+    const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab};
+    double sum = 0.0;
+    int emin = 1 << 20;
+    uint32_t count = 0, bad = 0;
+    for (uint32_t b = j0; b < j1; b += FULL_THREADS * UN) {
+        uint32_t kk[UN];
+#pragma unroll
+        for (uint32_t u = 0; u < UN; ++u) {
+            const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
+            kk[u] = j < j1 ? ((const RL_GLB uint32_t *)keys)[j] : 0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < UN; ++u) {
+            const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
+            if (j < j1) {
+                const float p = expf_libm_t((key_value(kk[u]) - st.M) / s.temperature, etab);
+                probs[j] = p;
+                if (!(p <= 3.40282347e38f)) {
+                    bad = 1;  // NaN or +inf
+                } else if (p > 0.0f) {
+                    emin = min(emin, f32_exponent(p));
+                }
+                sum += (double)p;
+                count += p >= s.min_p ? 1u : 0u;
+            }
+        }
+    }
+    for (int m = 32; m >= 1; m >>= 1) {
+        sum += __shfl_xor(sum, m);
+        emin = min(emin, __shfl_xor(emin, m));
+        count += (uint32_t)__shfl_xor((int)count, m);
+        bad |= (uint32_t)__shfl_xor((int)bad, m);
+    }
+    const uint32_t wave = threadIdx.x / WAVE;
+    if (lane_id() == 0) {
+        red_d[wave] = sum;
+        red_e[wave] = emin;
+        red_c[wave] = count;
+        red_b[wave] = bad;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < FULL_THREADS / WAVE; ++w) {
+            sum += red_d[w];
+            emin = min(emin, red_e[w]);
+            count += red_c[w];
+            bad |= red_b[w];
+        }
+        const uint32_t i = slot * a.chunks + chunk;
+        f.psum[i] = sum;
+        f.pemin[i] = emin;
+        f.pcount[i] = count;
+        f.pbad[i] = bad;
+    }
+}
+
+// ------------------------------------------------------------- tail ---
+constexpr uint32_t REPLAY_THREADS = 512;  // 8 waves: up to 256 VGPRs each, no spills
+constexpr uint32_t REPLAY_WAVES = REPLAY_THREADS / WAVE;
+constexpr uint32_t SEQ_ITEMS = 8;  // terms per thread per tile of the sum replay
+constexpr uint32_t CI = 8;         // contiguous elements per thread per step of a scan or compaction
+
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, RL_LDS uint32_t *red) {
+    for (int m = 32; m >= 1; m >>= 1) v += (uint32_t)__shfl_xor((int)v, m);
+    __syncthreads();
+    if (lane_id() == 0) red[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    uint32_t t = 0;
+    for (uint32_t w = 0; w < REPLAY_WAVES; ++w) t += red[w];
+    return t;
+}
+
+__device__ __forceinline__ int64_t block_max_i64(int64_t v, RL_LDS int64_t *red) {
+    for (int m = 32; m >= 1; m >>= 1) {
+        const int64_t o = (int64_t)shfl_xor_u64((uint64_t)v, m);
+        v = o > v ? o : v;
+    }
+    __syncthreads();
+    if (lane_id() == 0) red[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    int64_t t = red[0];
+    for (uint32_t w = 1; w < REPLAY_WAVES; ++w) t = red[w] > t ? red[w] : t;
+    return t;
+}
+
+// Exclusive prefix of v over the workgroup's threads in thread order; *total
+// gets the sum. For doubles it is only used where every partial sum is exact.
+template <class T>
+__device__ __forceinline__ T block_exclusive(T v, RL_LDS T *red, T *total) {
+    const uint32_t lane = lane_id(), wave = threadIdx.x / WAVE;
+    T incl = v;
+    for (uint32_t d = 1; d < WAVE; d <<= 1) {
+        const T o = __shfl_up(incl, d);
+        if (lane >= d) incl += o;
+    }
+    __syncthreads();
+    if (lane == WAVE - 1) red[wave] = incl;
+    __syncthreads();
+    T before = 0, all = 0;
+    for (uint32_t w = 0; w < REPLAY_WAVES; ++w) {
+        if (w < wave) before += red[w];
+        all += red[w];
+    }
+    *total = all;
+    return before + incl - v;
+}
+
+// Walks src[0..n) in order on thread 0, one LDS-staged block at a time; the
+// whole workgroup stages. body(stage, base, count) returns true to stop.
+template <class Body>
+__device__ __forceinline__ void staged_walk(const float *src, uint32_t n, RL_LDS float *stage,
+                                            RL_LDS uint32_t *stop, Body body) {
+    for (uint32_t b = 0; b < n; b += STAGE) {
+        const uint32_t cnt = min(STAGE, n - b);
+        for (uint32_t i = threadIdx.x; i < cnt; i += REPLAY_THREADS) stage[i] = ((const RL_GLB float *)src)[b + i];
+        __syncthreads();
+        if (threadIdx.x == 0) *stop = body(stage, b, cnt) ? 1u : 0u;
+        __syncthreads();
+        if (*stop) break;
+    }
+}
+
+struct NeverStop {
+    __device__ bool operator()(double) const { return false; }
+};
+
+// Where every partial sum of the probabilities is exact: the first j in
+// [lo, hi) with base + p[lo] + ... + p[j] >= target, and that sum in *at; or
+// hi, with the sum of them all in *at. Any order of addition gives these exact
+// sums, so a block scan serves. Whole workgroup.
+__device__ uint32_t exact_first_reaching(const float *probs, uint32_t lo, uint32_t hi, double base, double target,
+                                         RL_LDS double *red, RL_LDS uint32_t *hit, RL_LDS double *hit_sum,
+                                         double *at) {
+    for (uint32_t b = lo; b < hi; b += REPLAY_THREADS * CI) {
+        const uint32_t j0 = b + threadIdx.x * CI;
+        float pv[CI];
+        double mine = 0.0;
+#pragma unroll
+        for (uint32_t i = 0; i < CI; ++i) {
+            pv[i] = j0 + i < hi ? ((const RL_GLB float *)probs)[j0 + i] : 0.0f;
+            mine += (double)pv[i];
+        }
+        if (threadIdx.x == 0) *hit = 0xFFFFFFFFu;
+        double step_total;
+        double c = base + block_exclusive<double>(mine, red, &step_total);
+        uint32_t my_hit = 0xFFFFFFFFu;
+        double my_sum = 0.0;
+#pragma unroll
+        for (uint32_t i = 0; i < CI; ++i) {
+            if (my_hit == 0xFFFFFFFFu && j0 + i < hi) {
+                c += (double)pv[i];
+                if (c >= target) {
+                    my_hit = j0 + i;
+                    my_sum = c;
+                }
+            }
+        }
+        if (my_hit != 0xFFFFFFFFu) atomicMin((uint32_t *)hit, my_hit);
+        __syncthreads();
+        const uint32_t h = *hit;
+        if (h != 0xFFFFFFFFu) {
+            if (my_hit == h) *hit_sum = my_sum;
+            __syncthreads();
+            *at = *hit_sum;
+            __syncthreads();
+            return h;
+        }
+        base += step_total;
+        __syncthreads();
+    }
+    *at = base;
+    return hi;
+}
+
+// grid (slots), REPLAY_THREADS: the mass and the top-p cut (sample.rs:307-324),
+// min-p (:326-340) and the normalising total (:342-343). Leaves m and 1/total
+// in the row state.
+__global__ __launch_bounds__(REPLAY_THREADS) void k_full_tail(RowIO a, FullScratch f) {
+    __shared__ float stage_[STAGE];
+    __shared__ SeqLds<REPLAY_THREADS> seq;
+    __shared__ uint32_t red_u_[REPLAY_WAVES];
+    __shared__ int64_t red_l_[REPLAY_WAVES];
+    __shared__ double red_d_[REPLAY_WAVES];
+    __shared__ uint32_t sh_m_, sh_stop_, sh_hit_;
+    __shared__ double sh_d_, sh_hit_sum_;
+    __shared__ double chunk_sum_[MAX_CHUNKS];
+    RL_LDS double *chunk_sum = (RL_LDS double *)chunk_sum_;
+    RL_LDS float *stage = (RL_LDS float *)stage_;
+    RL_LDS uint32_t *red_u = (RL_LDS uint32_t *)red_u_;
+    RL_LDS int64_t *red_l = (RL_LDS int64_t *)red_l_;
+    RL_LDS double *red_d = (RL_LDS double *)red_d_;
+    RL_LDS uint32_t *stop = (RL_LDS uint32_t *)&sh_stop_;
+
+    const uint32_t slot = blockIdx.x;
+    if (f.row[slot].done) return;
+    const uint32_t row = a.rows[slot];
+    const rl_sampling s = a.settings[row];
+    const uint32_t V = a.vocab;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t k = full_k(s, V);
+    const uint32_t C = a.chunks;
+    uint32_t *ids = f.idA + (uint64_t)slot * V;
+    float *probs = f.probs + (uint64_t)slot * V;
+    const auto term = [probs](uint32_t j) { return ((const RL_GLB float *)probs)[j]; };
+
+    // The chunks' results, in chunk order (C <= MAX_CHUNKS).
+    if (tid < C) chunk_sum[tid] = f.psum[slot * C + tid];
+    __syncthreads();
+    bool bad = false;
+    int emin = 1 << 20;
+    uint32_t count = 0;
+    double tree_mass = 0.0;
+    for (uint32_t c = 0; c < C; ++c) {
+        const uint32_t i = slot * C + c;
+        bad |= f.pbad[i] != 0;
+        emin = min(emin, f.pemin[i]);
+        count += f.pcount[i];
+        tree_mass += chunk_sum[c];
+    }
+    // Every partial sum exact: all p are multiples of 2^(emin-23), the mass is
+    // below 2^53 of those steps. Then the chunk sums are the exact sums too.
+    const bool exact = !bad && (emin > 1000 || tree_mass < mul_pow2(1.0, 30 + emin));
+    // The exact sum of p[0..n), from the chunk sums and one partial chunk.
+    auto exact_prefix = [&](uint32_t n) {
+        double b = 0.0;
+        uint32_t c = 0;
+        while (c < C && chunk_lo(k, c + 1, C) <= n) b += chunk_sum[c++];
+        if (c == C || chunk_lo(k, c, C) == n) return b;
+        double at;
+        exact_first_reaching(probs, chunk_lo(k, c, C), n, b, __builtin_inf(), red_d, (RL_LDS uint32_t *)&sh_hit_, (RL_LDS double *)&sh_hit_sum_, &at);
+        return at;
+    };
+
+    uint32_t m = k;
+    bool have_sum_m = false;  // sum_m: the sequential sum of p[0..m)
+    double sum_m = 0.0;
+    if (s.top_p < 1.0f) {  // sample.rs:313-324
+        double mass = 0.0;
+        if (exact) {
+            mass = tree_mass;
+        } else if (!bad) {
+            seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, k, NeverStop{}, &seq, &mass);
+        } else {
+            staged_walk(probs, k, stage, stop, [&](RL_LDS float *st, uint32_t, uint32_t cnt) {
+                for (uint32_t i = 0; i < cnt; ++i) mass += (double)st[i];
+                return false;
+            });
+            if (tid == 0) sh_d_ = mass;
+            __syncthreads();
+            mass = sh_d_;
+        }
+        const double target = (double)s.top_p * mass;
+        if (exact) {
+            // The chunk where the running sum first reaches the target.
+            double b = 0.0;
+            uint32_t c = 0;
+            while (c < C && !(b + chunk_sum[c] >= target)) b += chunk_sum[c++];
+            if (c < C) {
+                double at;
+                const uint32_t j = exact_first_reaching(probs, chunk_lo(k, c, C), chunk_lo(k, c + 1, C), b, target,
+                                                        red_d, (RL_LDS uint32_t *)&sh_hit_, (RL_LDS double *)&sh_hit_sum_, &at);
+                m = j + 1;
+                have_sum_m = true;
+                sum_m = at;
+            } else {
+                have_sum_m = true;
+                sum_m = mass;
+            }
+        } else if (!bad) {
+            double at;
+            const uint32_t j = seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(
+                term, k, [target](double c) { return c >= target; }, &seq, &at);
+            have_sum_m = true;
+            if (j < k) {
+                m = j + 1;
+                sum_m = at;
+            } else {
+                sum_m = mass;
+            }
+        } else {
+            if (tid == 0) sh_m_ = k;
+            __syncthreads();
+            double cum = 0.0;
+            staged_walk(probs, k, stage, stop, [&](RL_LDS float *st, uint32_t b, uint32_t cnt) {
+                for (uint32_t i = 0; i < cnt; ++i) {
+                    cum += (double)st[i];
+                    if (cum >= target) {
+                        sh_m_ = b + i + 1;
+                        return true;
+                    }
+                }
+                return false;
+            });
+            __syncthreads();
+            m = sh_m_;
+        }
+    }
+    if (s.min_p > 0.0f) {  // sample.rs:326-340, a stable in-place compaction
+        uint32_t w;
+        if (!bad && !identity_order(s, V)) {
+            // Sorted candidates: p falls along the order, so the survivors
+            // are the first `count` of all k, and min(m, count) of the first m.
+            w = min(m, count);
+        } else {
+            // Survivors anywhere: count them, and compact unless they are
+            // already a prefix.
+            uint32_t first_out = 0xFFFFFFFFu, last_in = 0, cnt = 0;
+            for (uint32_t b = 0; b < m; b += REPLAY_THREADS) {
+                const uint32_t j = b + tid;
+                if (j < m) {
+                    if (((const RL_GLB float *)probs)[j] >= s.min_p) {
+                        ++cnt;
+                        last_in = j + 1;
+                    } else if (first_out == 0xFFFFFFFFu) {
+                        first_out = j;
+                    }
+                }
+            }
+            w = block_sum_u32(cnt, red_u);
+            const uint32_t lo_out = (uint32_t)-block_max_i64(-(int64_t)first_out, red_l);
+            const uint32_t hi_in = (uint32_t)block_max_i64((int64_t)last_in, red_l);
+            if (hi_in > lo_out) {
+                uint32_t done = 0;
+                for (uint32_t b = 0; b < m; b += REPLAY_THREADS * CI) {
+                    const uint32_t j0 = b + tid * CI;
+                    float pv[CI];
+                    uint32_t iv[CI];
+                    uint32_t mine = 0;
+#pragma unroll
+                    for (uint32_t i = 0; i < CI; ++i) {
+                        const bool ok = j0 + i < m;
+                        pv[i] = ok ? probs[j0 + i] : 0.0f;
+                        iv[i] = ok ? ids[j0 + i] : 0u;
+                        mine += (ok && pv[i] >= s.min_p) ? 1u : 0u;
+                    }
+                    uint32_t step_total;
+                    uint32_t dst = done + block_exclusive<uint32_t>(mine, red_u, &step_total);
+#pragma unroll
+                    for (uint32_t i = 0; i < CI; ++i) {
+                        if (j0 + i < m && pv[i] >= s.min_p) {
+                            ids[dst] = iv[i];
+                            probs[dst] = pv[i];
+                            ++dst;
+                        }
+                    }
+                    done += step_total;
+                    __syncthreads();
+                }
+            }
+        }
+        if (w != m) have_sum_m = false;
+        m = w > 1 ? w : 1u;
+    }
+    // Normalise: f64 total in order (sample.rs:342-343).
+    double total = 0.0;
+    if (have_sum_m) {
+        total = sum_m;  // the same terms in the same order as the top-p pass
+    } else if (exact && !identity_order(s, V)) {
+        total = exact_prefix(m);  // min-p moved nothing: the chunk sums still apply
+    } else if (exact) {
+        exact_first_reaching(probs, 0, m, 0.0, __builtin_inf(), red_d, (RL_LDS uint32_t *)&sh_hit_, (RL_LDS double *)&sh_hit_sum_, &total);
+    } else if (!bad) {
+        seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, m, NeverStop{}, &seq, &total);
+    } else {
+        staged_walk(probs, m, stage, stop, [&](RL_LDS float *st, uint32_t, uint32_t cnt) {
+            for (uint32_t i = 0; i < cnt; ++i) total += (double)st[i];
+            return false;
+        });
+        if (tid == 0) sh_d_ = total;
+        __syncthreads();
+        total = sh_d_;
+    }
+    if (tid == 0) {
+        f.row[slot].m = m;
+        f.row[slot].inv = (float)(1.0 / total);
+        f.row[slot].qbad = 0;
+    }
+}
+
+// ------------------------------------------------------------- norm ---
+// grid (chunks, slots), FULL_THREADS: q = p * (1 / total) for the kept
+// candidates (sample.rs:344-347), written to the outputs.
+__global__ __launch_bounds__(FULL_THREADS) void k_full_norm(RowIO a, FullScratch f) {
+    const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
+    const FullRow st = f.row[slot];
+    if (st.done) return;
+    const uint32_t row = a.rows[slot];
+    const uint32_t V = a.vocab;
+    const uint32_t m = st.m;
+    const uint32_t j0 = chunk_lo(m, chunk, a.chunks), j1 = chunk_lo(m, chunk + 1, a.chunks);
+    const uint32_t *ids = f.idA + (uint64_t)slot * V;
+    float *probs = f.probs + (uint64_t)slot * V;
+    uint32_t qbad = 0;
+    for (uint32_t b = j0; b < j1; b += FULL_THREADS * UN) {
+        float pp[UN];
+        uint32_t iv[UN];
+#pragma unroll
+        for (uint32_t u = 0; u < UN; ++u) {
+            const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
+            pp[u] = j < j1 ? ((const RL_GLB float *)probs)[j] : 0.0f;
+            iv[u] = (j < j1 && a.out_ids) ? ((const RL_GLB uint32_t *)ids)[j] : 0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < UN; ++u) {
+            const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
+            if (j < j1) {
+                const float q = pp[u] * st.inv;
+                probs[j] = q;
+                if (!(q <= 3.40282347e38f)) qbad = 1;
+                if (a.out_ids) {
+                    a.out_ids[(uint64_t)row * a.cand_stride + j] = iv[u];
+                    a.out_probs[(uint64_t)row * a.cand_stride + j] = q;
+                }
+            }
+        }
+    }
+    if (__ballot(qbad != 0) != 0 && lane_id() == 0) atomicOr(&f.row[slot].qbad, 1u);
+}
+
+// ------------------------------------------------------------- draw ---
+// grid (slots), REPLAY_THREADS: the f32 running sum against the host's uniform
+// (sample.rs:349-356); a shortfall takes the last candidate (:357-358).
+__global__ __launch_bounds__(REPLAY_THREADS) void k_full_draw(RowIO a, FullScratch f) {
+    __shared__ float stage_[STAGE];
+    __shared__ SeqLds<REPLAY_THREADS> seq;
+    __shared__ uint32_t sh_stop_, sh_tok_;
+    RL_LDS float *stage = (RL_LDS float *)stage_;
+    RL_LDS uint32_t *stop = (RL_LDS uint32_t *)&sh_stop_;
+    const uint32_t slot = blockIdx.x;
+    const FullRow st = f.row[slot];
+    if (st.done) return;
+    const uint32_t row = a.rows[slot];
+    const uint32_t V = a.vocab;
+    const uint32_t m = st.m;
+    const uint32_t *ids = f.idA + (uint64_t)slot * V;
+    const float *probs = f.probs + (uint64_t)slot * V;
+    const float u = a.uniforms[row];
+    uint32_t pick;
+    if (!st.qbad) {
+        double unused;
+        const uint32_t j = seq_replay<24, REPLAY_THREADS, SEQ_ITEMS>(
+            [probs](uint32_t j) { return ((const RL_GLB float *)probs)[j]; }, m,
+            [u](double c) { return c > (double)u; }, &seq, &unused);
+        pick = j < m ? j : m - 1;
+    } else {
+        if (threadIdx.x == 0) sh_tok_ = m - 1;
+        __syncthreads();
+        float cum = 0.0f;
+        staged_walk(probs, m, stage, stop, [&](RL_LDS float *sv, uint32_t b, uint32_t cnt) {
+            for (uint32_t i = 0; i < cnt; ++i) {
+                cum += sv[i];
+                if (cum > u) {
+                    sh_tok_ = b + i;
+                    return true;
+                }
+            }
+            return false;
+        });
+        __syncthreads();
+        pick = sh_tok_;
+    }
+    if (threadIdx.x == 0) {
+        a.out_token[row] = ids[pick];
+        a.out_kept[row] = m;
+        a.out_used[row] = 1;
+    }
+}
+
+}  // namespace rl

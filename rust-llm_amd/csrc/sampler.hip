@@ -10,7 +10,7 @@
 
 #include "rl_error.h"
 #include "rl_sampler.h"
-#include "sampler_kernels.h"
+#include "full_kernels.h"
 
 using namespace rl;
 
@@ -75,6 +75,10 @@ struct rl_sampler_ctx {
     float *d_probs = nullptr;
     float *d_part_max = nullptr;
     uint64_t *d_part_am = nullptr;
+    double *d_psum = nullptr;
+    int *d_pemin = nullptr;
+    uint32_t *d_pcount = nullptr, *d_pbad = nullptr;
+    FullRow *d_full_row = nullptr;
     uint64_t *d_argmax_part = nullptr;
     std::vector<void *> owned;
     // Host copy of the plan made by configure.
@@ -137,6 +141,11 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     if (e == hipSuccess) e = c->alloc(&c->d_probs, fg * V);
     if (e == hipSuccess) e = c->alloc(&c->d_part_max, fg * MAX_CHUNKS);
     if (e == hipSuccess) e = c->alloc(&c->d_part_am, fg * MAX_CHUNKS);
+    if (e == hipSuccess) e = c->alloc(&c->d_psum, fg * MAX_CHUNKS);
+    if (e == hipSuccess) e = c->alloc(&c->d_pemin, fg * MAX_CHUNKS);
+    if (e == hipSuccess) e = c->alloc(&c->d_pcount, fg * MAX_CHUNKS);
+    if (e == hipSuccess) e = c->alloc(&c->d_pbad, fg * MAX_CHUNKS);
+    if (e == hipSuccess) e = c->alloc(&c->d_full_row, fg);
     if (e == hipSuccess) e = c->alloc(&c->d_argmax_part, std::max<size_t>(CHUNK_SLOTS, max_rows));
     if (e != hipSuccess) {
         delete c;
@@ -263,12 +272,20 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
         f.rows = ctx->d_full_rows + g0;
         f.chunks = std::max(1u, std::min(MAX_CHUNKS, (TARGET_WGS + ng - 1) / ng));
         f.chunks = std::min(f.chunks, std::max(1u, vocab / 4096));
-        FullScratch fs{ctx->d_keyA, ctx->d_idA, ctx->d_keyB, ctx->d_idB, ctx->d_probs, ctx->d_part_max,
-                       ctx->d_part_am};
-        hipLaunchKernelGGL(k_full_keys, dim3(f.chunks, ng), dim3(FULL_THREADS),
-                           window_lds_bytes(ctx->hash_bits), st, f, fs);
+        FullScratch fs{ctx->d_keyA, ctx->d_idA,    ctx->d_keyB,   ctx->d_idB,  ctx->d_probs,     ctx->d_part_max,
+                       ctx->d_part_am, ctx->d_psum, ctx->d_pemin, ctx->d_pcount, ctx->d_pbad, ctx->d_full_row};
+        const dim3 cgrid(f.chunks, ng);
+        if (vec)
+            hipLaunchKernelGGL(k_full_keys<true>, cgrid, dim3(FULL_THREADS), window_lds_bytes(ctx->hash_bits), st,
+                               f, fs);
+        else
+            hipLaunchKernelGGL(k_full_keys<false>, cgrid, dim3(FULL_THREADS), window_lds_bytes(ctx->hash_bits), st,
+                               f, fs);
         hipLaunchKernelGGL(k_full_sort, dim3(ng), dim3(SORT_THREADS), 0, st, f, fs);
-        hipLaunchKernelGGL(k_full_replay, dim3(ng), dim3(REPLAY_THREADS), 0, st, f, fs);
+        hipLaunchKernelGGL(k_full_probs, cgrid, dim3(FULL_THREADS), 0, st, f, fs);
+        hipLaunchKernelGGL(k_full_tail, dim3(ng), dim3(REPLAY_THREADS), 0, st, f, fs);
+        hipLaunchKernelGGL(k_full_norm, cgrid, dim3(FULL_THREADS), 0, st, f, fs);
+        hipLaunchKernelGGL(k_full_draw, dim3(ng), dim3(REPLAY_THREADS), 0, st, f, fs);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return hip_fail(e, "full-path kernels");
     }

@@ -9,9 +9,8 @@
 //  and replays the reference's tail (sample.rs:267-358) on <= 64 candidates,
 //  one candidate per lane.
 //
-//  FULL (top_k == 0, top_k >= vocab, or top_k > 64): the reference's literal
-//  algorithm: total-order keys for the whole row, an LSD radix sort of the
-//  row, then the sequential sums and the draw over the sorted row.
+//  FULL (top_k == 0, top_k >= vocab, or top_k > 64): the whole candidate list,
+//  in full_kernels.h.
 #pragma once
 #include "rl_device.h"
 #include "rl_expf.h"
@@ -52,13 +51,6 @@ struct RowIO {
 struct FastScratch {
     uint64_t *chunk_cands;   // [slot][chunk][KMAX]
     uint32_t *chunk_counts;  // [slot][chunk]
-};
-
-struct FullScratch {
-    uint32_t *keyA, *idA, *keyB, *idB;  // [slot][vocab]
-    float *probs;                       // [slot][vocab]
-    float *part_max;                    // [slot][chunk]
-    uint64_t *part_am;                  // [slot][chunk]
 };
 
 __device__ __forceinline__ uint32_t window_len(const RowIO &a, uint32_t row) {
@@ -596,505 +588,6 @@ __global__ __launch_bounds__(WAVE) void k_stream_finalize(RowIO a, FastScratch s
     const uint32_t nL = total < k ? total : k;
     if (lane >= nL) top = 0;
     finalize_row(a, row, s, k, top, nL, ws, pen, rowp);
-}
-
-// ---------------------------------------------------------- FULL path ---
-
-__device__ __forceinline__ uint32_t full_k(const rl_sampling &s, uint32_t V) {
-    return s.top_k == 0 ? V : (s.top_k < V ? (uint32_t)s.top_k : V);  // sample.rs:289
-}
-__device__ __forceinline__ bool identity_order(const rl_sampling &s, uint32_t V) {
-    return full_k(s, V) == V && !(s.top_p < 1.0f);  // no select and no sort
-}
-
-// grid (chunks, slots), FULL_THREADS: the penalised row as total-order keys in
-// id order, plus per-chunk f32::max fold and argmax.
-__global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch f) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const WindowSet ws = window_set(smem, a.hash_bits);
-    __shared__ float red_max[FULL_THREADS / WAVE];
-    __shared__ uint64_t red_am[FULL_THREADS / WAVE];
-    const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
-    const uint32_t row = a.rows[slot];
-    const rl_sampling s = a.settings[row];
-    const uint32_t V = a.vocab;
-    const uint32_t wl = window_len(a, row);
-    const bool pen = penalises(s) && wl > 0;
-    const float *rowp = a.logits + (uint64_t)row * a.stride;
-    window_build(ws, a.windows + (uint64_t)row * a.wstride, wl, V, rowp, pen);
-    const uint32_t e0 = (uint32_t)((uint64_t)chunk * V / a.chunks);
-    const uint32_t e1 = (uint32_t)((uint64_t)(chunk + 1) * V / a.chunks);
-    uint32_t *keys = f.keyA + (uint64_t)slot * V;
-    uint32_t *ids = f.idA + (uint64_t)slot * V;
-    float mx = -__builtin_inff();
-    uint64_t am = 0;
-    for (uint32_t e = e0 + threadIdx.x; e < e1; e += FULL_THREADS) {
-        float x = rowp[e];
-        if (pen && window_contains(ws, e)) x = penalize(x, s.repeat_penalty);
-        keys[e] = total_key(x);
-        ids[e] = e;
-        mx = fmaxf(mx, x);
-        const uint64_t c = composite(argmax_key(x), e);
-        am = c > am ? c : am;
-    }
-    mx = wave_maxnum_f32(mx);
-    am = wave_max_u64(am);
-    const uint32_t wave = threadIdx.x / WAVE;
-    if (lane_id() == 0) {
-        red_max[wave] = mx;
-        red_am[wave] = am;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (uint32_t i = 1; i < FULL_THREADS / WAVE; ++i) {
-            mx = fmaxf(mx, red_max[i]);
-            am = red_am[i] > am ? red_am[i] : am;
-        }
-        f.part_max[slot * a.chunks + chunk] = mx;
-        f.part_am[slot * a.chunks + chunk] = am;
-    }
-}
-
-__device__ __forceinline__ void full_row_max(const RowIO &a, const FullScratch &f, uint32_t slot, float *M,
-                                             uint32_t *am_tok) {
-    float mx = -__builtin_inff();
-    uint64_t am = 0;
-    for (uint32_t c = 0; c < a.chunks; ++c) {
-        mx = fmaxf(mx, f.part_max[slot * a.chunks + c]);
-        const uint64_t x = f.part_am[slot * a.chunks + c];
-        am = x > am ? x : am;
-    }
-    *M = mx;
-    *am_tok = comp_key(am) == 0 ? 0u : comp_id(am);
-}
-
-// One wave's lanes with the same 8-bit digit (among the lanes where valid).
-__device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
-    uint64_t m = ballot(valid);
-#pragma unroll
-    for (uint32_t b = 0; b < 8; ++b) {
-        const bool bit = (d >> b) & 1u;
-        const uint64_t bb = ballot(bit);
-        m &= bit ? bb : ~bb;
-    }
-    return m;
-}
-
-// grid (slots), SORT_THREADS: stable LSD radix sort of the row's (key, id)
-// pairs, descending key, 8 bits a pass; ids were in ascending order, so ties
-// keep ascending ids (the order of sample.rs:282-286). Result ends in keyA/idA.
-__global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch f) {
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t offs[256];
-    __shared__ uint32_t cnt[SORT_WAVES][256];
-    __shared__ uint32_t pos[SORT_WAVES][256];
-    __shared__ uint32_t skip;
-    const uint32_t slot = blockIdx.x;
-    const uint32_t row = a.rows[slot];
-    const rl_sampling s = a.settings[row];
-    const uint32_t V = a.vocab;
-    float M;
-    uint32_t am_tok;
-    full_row_max(a, f, slot, &M, &am_tok);
-    if (!(M > -__builtin_inff() && M < __builtin_inff())) return;
-    if (identity_order(s, V)) return;
-    const uint32_t tid = threadIdx.x, wave = tid / WAVE;
-    uint32_t *kin = f.keyA + (uint64_t)slot * V, *iin = f.idA + (uint64_t)slot * V;
-    uint32_t *kout = f.keyB + (uint64_t)slot * V, *iout = f.idB + (uint64_t)slot * V;
-    for (uint32_t i = tid; i < SORT_WAVES * 256; i += SORT_THREADS) (&cnt[0][0])[i] = 0;
-    for (uint32_t shift = 0; shift < 32; shift += 8) {
-        if (tid < 256) hist[tid] = 0;
-        __syncthreads();
-        for (uint32_t base = 0; base < V; base += SORT_THREADS) {
-            const uint32_t j = base + tid;
-            const bool valid = j < V;
-            const uint32_t d = valid ? 255u - ((kin[j] >> shift) & 255u) : 0u;
-            const uint64_t peers = match_digit(d, valid);
-            if (valid && lanes_below(peers) == 0) atomicAdd(&hist[d], (uint32_t)__popcll(peers));
-        }
-        __syncthreads();
-        if (tid == 0) {
-            uint32_t run = 0, sk = 0;
-            for (uint32_t d = 0; d < 256; ++d) {
-                offs[d] = run;
-                if (hist[d] == V) sk = 1;
-                run += hist[d];
-            }
-            skip = sk;
-        }
-        __syncthreads();
-        if (skip) continue;  // every key has this digit: the pass would not move anything
-        for (uint32_t base = 0; base < V; base += SORT_THREADS) {
-            const uint32_t j = base + tid;
-            const bool valid = j < V;
-            const uint32_t key = valid ? kin[j] : 0u;
-            const uint32_t id = valid ? iin[j] : 0u;
-            const uint32_t d = 255u - ((key >> shift) & 255u);
-            const uint64_t peers = match_digit(d, valid);
-            const uint32_t rank = lanes_below(peers);
-            if (valid && rank == 0) cnt[wave][d] = (uint32_t)__popcll(peers);
-            __syncthreads();
-            if (tid < 256) {
-                uint32_t run = offs[tid];
-                for (uint32_t w = 0; w < SORT_WAVES; ++w) {
-                    const uint32_t c = cnt[w][tid];
-                    pos[w][tid] = run;
-                    run += c;
-                    cnt[w][tid] = 0;
-                }
-                offs[tid] = run;
-            }
-            __syncthreads();
-            if (valid) {
-                const uint32_t dst = pos[wave][d] + rank;
-                kout[dst] = key;
-                iout[dst] = id;
-            }
-        }
-        __syncthreads();
-        uint32_t *t;
-        t = kin; kin = kout; kout = t;
-        t = iin; iin = iout; iout = t;
-    }
-    if (kin != f.keyA + (uint64_t)slot * V) {  // an odd number of passes ran
-        for (uint32_t j = tid; j < V; j += SORT_THREADS) {
-            kout[j] = kin[j];
-            iout[j] = iin[j];
-        }
-    }
-}
-
-// ------------------------------------------------------ FULL-path tail ---
-constexpr uint32_t REPLAY_THREADS = 512;  // 8 waves: up to 256 VGPRs each, no spills
-constexpr uint32_t REPLAY_WAVES = REPLAY_THREADS / WAVE;
-constexpr uint32_t SEQ_ITEMS = 8;  // terms per thread per tile of the sum replay
-
-constexpr uint32_t UN = 4;  // elements per thread per step of the replay kernel's loops
-constexpr uint32_t CI = 8;  // contiguous elements per thread per step of the compaction
-
-__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, RL_LDS uint32_t *red) {
-    for (int m = 32; m >= 1; m >>= 1) v += (uint32_t)__shfl_xor((int)v, m);
-    __syncthreads();
-    if (lane_id() == 0) red[threadIdx.x / WAVE] = v;
-    __syncthreads();
-    uint32_t t = 0;
-    for (uint32_t w = 0; w < REPLAY_WAVES; ++w) t += red[w];
-    return t;
-}
-
-__device__ __forceinline__ int64_t block_max_i64(int64_t v, RL_LDS int64_t *red) {
-    for (int m = 32; m >= 1; m >>= 1) {
-        const int64_t o = (int64_t)shfl_xor_u64((uint64_t)v, m);
-        v = o > v ? o : v;
-    }
-    __syncthreads();
-    if (lane_id() == 0) red[threadIdx.x / WAVE] = v;
-    __syncthreads();
-    int64_t t = red[0];
-    for (uint32_t w = 1; w < REPLAY_WAVES; ++w) t = red[w] > t ? red[w] : t;
-    return t;
-}
-
-// Exclusive prefix of v over the workgroup's threads in thread order; *total
-// gets the sum.
-__device__ __forceinline__ uint32_t block_exclusive_u32(uint32_t v, RL_LDS uint32_t *red, uint32_t *total) {
-    const uint32_t lane = lane_id(), wave = threadIdx.x / WAVE;
-    uint32_t incl = v;
-    for (uint32_t d = 1; d < WAVE; d <<= 1) {
-        const uint32_t o = (uint32_t)__shfl_up((int)incl, d);
-        if (lane >= d) incl += o;
-    }
-    __syncthreads();
-    if (lane == WAVE - 1) red[wave] = incl;
-    __syncthreads();
-    uint32_t before = 0, all = 0;
-    for (uint32_t w = 0; w < REPLAY_WAVES; ++w) {
-        if (w < wave) before += red[w];
-        all += red[w];
-    }
-    *total = all;
-    return before + incl - v;
-}
-
-__device__ __forceinline__ int block_min_i32(int v, RL_LDS int *red) {
-    for (int m = 32; m >= 1; m >>= 1) v = min(v, __shfl_xor(v, m));
-    __syncthreads();
-    if (lane_id() == 0) red[threadIdx.x / WAVE] = v;
-    __syncthreads();
-    int t = red[0];
-    for (uint32_t w = 1; w < REPLAY_WAVES; ++w) t = min(t, red[w]);
-    return t;
-}
-
-// Walks src[0..n) in order on thread 0, one LDS-staged block at a time; the
-// whole workgroup stages. body(stage, base, count) returns true to stop.
-template <class Body>
-__device__ __forceinline__ void staged_walk(const float *src, uint32_t n, RL_LDS float *stage,
-                                            RL_LDS uint32_t *stop, Body body) {
-    for (uint32_t b = 0; b < n; b += STAGE) {
-        const uint32_t cnt = min(STAGE, n - b);
-        for (uint32_t i = threadIdx.x; i < cnt; i += REPLAY_THREADS) stage[i] = ((const RL_GLB float *)src)[b + i];
-        __syncthreads();
-        if (threadIdx.x == 0) *stop = body(stage, b, cnt) ? 1u : 0u;
-        __syncthreads();
-        if (*stop) break;
-    }
-}
-
-struct NeverStop {
-    __device__ bool operator()(double) const { return false; }
-};
-
-// grid (slots), REPLAY_THREADS: the reference's tail (sample.rs:307-358) over
-// the whole candidate list (sorted, or in id order when neither top-k nor
-// top-p needs an order).
-//
-// The reference's sums are sequential in candidate order: the mass and the
-// top-p cumulative sum (f64, :307-324), the normalising total (f64, :342) and
-// the draw (f32, :349-356). seq_replay reproduces each one exactly with the
-// whole workgroup (rl_seqsum.h). Its premise is finite terms; a row with a NaN
-// or infinite probability (a NaN logit, a NaN temperature, or a normalising
-// total too small for 1/total to be finite) is walked in order by one thread
-// instead.
-__global__ __launch_bounds__(REPLAY_THREADS) void k_full_replay(RowIO a, FullScratch f) {
-    __shared__ float stage_[STAGE];
-    __shared__ SeqLds<REPLAY_THREADS> seq;
-    __shared__ int red_i_[REPLAY_WAVES];
-    __shared__ uint32_t red_u_[REPLAY_WAVES];
-    __shared__ int64_t red_l_[REPLAY_WAVES];
-    __shared__ uint32_t sh_m_, sh_stop_, sh_total_, sh_tok_;
-    __shared__ double sh_d_;
-    __shared__ uint64_t exp_tab_[32];
-    RL_LDS float *stage = (RL_LDS float *)stage_;
-    RL_LDS int *red_i = (RL_LDS int *)red_i_;
-    RL_LDS uint32_t *red_u = (RL_LDS uint32_t *)red_u_;
-    RL_LDS int64_t *red_l = (RL_LDS int64_t *)red_l_;
-    RL_LDS uint32_t *stop = (RL_LDS uint32_t *)&sh_stop_;
-
-    const uint32_t slot = blockIdx.x;
-    const uint32_t row = a.rows[slot];
-    const rl_sampling s = a.settings[row];
-    const uint32_t V = a.vocab;
-    const uint32_t tid = threadIdx.x, wave = tid / WAVE, lane = lane_id();
-    float M;
-    uint32_t am_tok;
-    full_row_max(a, f, slot, &M, &am_tok);
-    if (!(M > -__builtin_inff() && M < __builtin_inff())) {  // sample.rs:270-277
-        if (tid == 0) write_single(a, row, am_tok);
-        return;
-    }
-    const uint32_t k = full_k(s, V);
-    const uint32_t *keys = f.keyA + (uint64_t)slot * V;
-    uint32_t *ids = f.idA + (uint64_t)slot * V;
-    float *probs = f.probs + (uint64_t)slot * V;
-    const auto term = [probs](uint32_t j) { return ((const RL_GLB float *)probs)[j]; };
-
-    // exp (sample.rs:309). Every loop over the candidates below loads UN
-    // elements per thread before it uses any, to keep loads in flight.
-    copy_exp_table((RL_LDS uint64_t *)exp_tab_);
-    const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab_};
-    uint32_t bad = 0;
-    for (uint32_t b = 0; b < k; b += REPLAY_THREADS * UN) {
-        uint32_t kk[UN];
-#pragma unroll
-        for (uint32_t u = 0; u < UN; ++u) {
-            const uint32_t j = b + u * REPLAY_THREADS + tid;
-            kk[u] = j < k ? ((const RL_GLB uint32_t *)keys)[j] : 0u;
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < UN; ++u) {
-            const uint32_t j = b + u * REPLAY_THREADS + tid;
-            if (j < k) {
-                const float p = expf_libm_t((key_value(kk[u]) - M) / s.temperature, etab);
-                probs[j] = p;
-                if (!(p <= 3.40282347e38f)) bad = 1;  // NaN or +inf
-            }
-        }
-    }
-    bad = block_min_i32(bad ? 0 : 1, red_i) == 0 ? 1u : 0u;
-    __syncthreads();
-
-    uint32_t m = k;
-    // The sequential sum of the first m candidates, when a pass below has
-    // already produced it (-1 when not).
-    double sum_m = -1.0;
-    if (s.top_p < 1.0f) {  // sample.rs:313-324
-        double mass = 0.0;
-        if (!bad) {
-            seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, k, NeverStop{}, &seq, &mass);
-            sum_m = mass;
-        } else {
-            staged_walk(probs, k, stage, stop, [&](RL_LDS float *st, uint32_t, uint32_t cnt) {
-                for (uint32_t i = 0; i < cnt; ++i) mass += (double)st[i];
-                return false;
-            });
-            if (tid == 0) sh_d_ = mass;
-            __syncthreads();
-            mass = sh_d_;
-        }
-        const double target = (double)s.top_p * mass;
-        if (!bad) {
-            double at;
-            const uint32_t j =
-                seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, k, [target](double c) { return c >= target; }, &seq,
-                                                        &at);
-            if (j < k) {
-                m = j + 1;
-                sum_m = at;
-            }
-        } else {
-            if (tid == 0) sh_m_ = k;
-            __syncthreads();
-            double cum = 0.0;
-            staged_walk(probs, k, stage, stop, [&](RL_LDS float *st, uint32_t b, uint32_t cnt) {
-                for (uint32_t i = 0; i < cnt; ++i) {
-                    cum += (double)st[i];
-                    if (cum >= target) {
-                        sh_m_ = b + i + 1;
-                        return true;
-                    }
-                }
-                return false;
-            });
-            __syncthreads();
-            m = sh_m_;
-        }
-    }
-    if (s.min_p > 0.0f) {  // sample.rs:326-340, a stable in-place compaction
-        // First whether the survivors are already a prefix (always so when
-        // the candidates are sorted, as p falls along the order): then the
-        // compaction moves nothing and only the count changes.
-        uint32_t first_out = 0xFFFFFFFFu, last_in = 0, count = 0;
-        for (uint32_t b = 0; b < m; b += REPLAY_THREADS * UN) {
-            float pp[UN];
-#pragma unroll
-            for (uint32_t u = 0; u < UN; ++u) {
-                const uint32_t j = b + u * REPLAY_THREADS + tid;
-                pp[u] = j < m ? ((const RL_GLB float *)probs)[j] : 0.0f;
-            }
-#pragma unroll
-            for (uint32_t u = 0; u < UN; ++u) {
-                const uint32_t j = b + u * REPLAY_THREADS + tid;
-                if (j < m) {
-                    if (pp[u] >= s.min_p) {
-                        ++count;
-                        last_in = j + 1;
-                    } else if (first_out == 0xFFFFFFFFu) {
-                        first_out = j;
-                    }
-                }
-            }
-        }
-        const uint32_t all_in = block_sum_u32(count, red_u);
-        const uint32_t lo_out = (uint32_t)-block_max_i64(-(int64_t)first_out, red_l);
-        const uint32_t hi_in = (uint32_t)block_max_i64((int64_t)last_in, red_l);
-        if (hi_in > lo_out) {
-            // Not a prefix: stable compaction, CI contiguous elements per
-            // thread per step.
-            uint32_t done = 0;
-            for (uint32_t b = 0; b < m; b += REPLAY_THREADS * CI) {
-                const uint32_t j0 = b + tid * CI;
-                float pv[CI];
-                uint32_t iv[CI];
-                uint32_t mine = 0;
-#pragma unroll
-                for (uint32_t i = 0; i < CI; ++i) {
-                    const bool ok = j0 + i < m;
-                    pv[i] = ok ? probs[j0 + i] : 0.0f;
-                    iv[i] = ok ? ids[j0 + i] : 0u;
-                    mine += (ok && pv[i] >= s.min_p) ? 1u : 0u;
-                }
-                uint32_t step_total;
-                const uint32_t before = block_exclusive_u32(mine, red_u, &step_total);
-                uint32_t dst = done + before;
-#pragma unroll
-                for (uint32_t i = 0; i < CI; ++i) {
-                    if (j0 + i < m && pv[i] >= s.min_p) {
-                        ids[dst] = iv[i];
-                        probs[dst] = pv[i];
-                        ++dst;
-                    }
-                }
-                done += step_total;
-                __syncthreads();
-            }
-        }
-        if (all_in != m) sum_m = -1.0;
-        m = all_in > 1 ? all_in : 1u;
-    }
-    // Normalise: f64 total in order, then f32 multiply (sample.rs:342-347).
-    double total = 0.0;
-    if (!bad && sum_m >= 0.0) {
-        total = sum_m;  // the same terms in the same order as the top-p pass
-    } else if (!bad) {
-        seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, m, NeverStop{}, &seq, &total);
-    } else {
-        staged_walk(probs, m, stage, stop, [&](RL_LDS float *st, uint32_t, uint32_t cnt) {
-            for (uint32_t i = 0; i < cnt; ++i) total += (double)st[i];
-            return false;
-        });
-        if (tid == 0) sh_d_ = total;
-        __syncthreads();
-        total = sh_d_;
-    }
-    const float inv = (float)(1.0 / total);
-    uint32_t qbad = 0;
-    for (uint32_t b = 0; b < m; b += REPLAY_THREADS * UN) {
-        float pp[UN];
-        uint32_t iv[UN];
-#pragma unroll
-        for (uint32_t u = 0; u < UN; ++u) {
-            const uint32_t j = b + u * REPLAY_THREADS + tid;
-            pp[u] = j < m ? ((const RL_GLB float *)probs)[j] : 0.0f;
-            iv[u] = (j < m && a.out_ids) ? ((const RL_GLB uint32_t *)ids)[j] : 0u;
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < UN; ++u) {
-            const uint32_t j = b + u * REPLAY_THREADS + tid;
-            if (j < m) {
-                const float q = pp[u] * inv;
-                probs[j] = q;
-                if (!(q <= 3.40282347e38f)) qbad = 1;
-                if (a.out_ids) {
-                    a.out_ids[(uint64_t)row * a.cand_stride + j] = iv[u];
-                    a.out_probs[(uint64_t)row * a.cand_stride + j] = q;
-                }
-            }
-        }
-    }
-    qbad = block_min_i32(qbad ? 0 : 1, red_i) == 0 ? 1u : 0u;
-    __syncthreads();
-    // The draw: f32 running sum against the host's uniform (sample.rs:349-356);
-    // a shortfall takes the last candidate (:357-358).
-    const float u = a.uniforms[row];
-    uint32_t pick;
-    if (!qbad) {
-        double unused;
-        const uint32_t j = seq_replay<24, REPLAY_THREADS, SEQ_ITEMS>(
-            term, m, [u](double c) { return c > (double)u; }, &seq, &unused);
-        pick = j < m ? j : m - 1;
-    } else {
-        if (tid == 0) sh_tok_ = m - 1;
-        __syncthreads();
-        float cum = 0.0f;
-        staged_walk(probs, m, stage, stop, [&](RL_LDS float *st, uint32_t b, uint32_t cnt) {
-            for (uint32_t i = 0; i < cnt; ++i) {
-                cum += st[i];
-                if (cum > u) {
-                    sh_tok_ = b + i;
-                    return true;
-                }
-            }
-            return false;
-        });
-        __syncthreads();
-        pick = sh_tok_;
-    }
-    if (tid == 0) {
-        a.out_token[row] = ids[pick];
-        a.out_kept[row] = m;
-        a.out_used[row] = 1;
-    }
 }
 
 // ------------------------------------------------------------ argmax ---
