@@ -29,14 +29,20 @@
 namespace rl {
 
 struct FullRow {
-    float M;          // the f32::max fold of the penalised row
-    uint32_t am_tok;  // argmax of the penalised row
-    uint32_t done;    // the row is finished (no finite maximum)
-    uint32_t m;       // candidates kept (after top-p and min-p)
-    float inv;        // (1 / total) as f32
-    uint32_t qbad;    // a normalised probability is not finite
-    uint32_t pad[2];
+    float M;           // the f32::max fold of the penalised row
+    uint32_t am_tok;   // argmax of the penalised row
+    uint32_t done;     // the row is finished (no finite maximum, or the min-p path)
+    uint32_t m;        // candidates kept (after top-p and min-p)
+    float inv;         // (1 / total) as f32
+    uint32_t qbad;     // a normalised probability is not finite
+    uint32_t small;    // the row tries the min-p path first
+    uint32_t nsurv;    // min-p survivors collected
+    uint32_t overflow; // more survivors than SURV_CAP
+    uint32_t ns_key;   // the largest key of an element below min-p (+1; 0 when none)
 };
+
+// Survivors the min-p path collects per row (their composites sort in LDS).
+constexpr uint32_t SURV_CAP = 4096;
 
 struct FullScratch {
     uint32_t *keyA, *idA, *keyB, *idB;  // [slot][vocab]
@@ -47,7 +53,20 @@ struct FullScratch {
     int *pemin;                         // [slot][chunk]
     uint32_t *pcount;                   // [slot][chunk]
     uint32_t *pbad;                     // [slot][chunk]
+    uint32_t *plast_in;                 // [slot][chunk] probs pass: last index + 1 with p >= min_p
+    uint32_t *pfirst_out;               // [slot][chunk] first index with p < min_p
+    uint64_t *surv;                     // [slot][SURV_CAP] min-p survivors (composites)
     FullRow *row;                       // [slot]
+};
+
+constexpr uint32_t UN = 4;                 // elements per thread per step of the bulk loops
+constexpr uint32_t REPLAY_THREADS = 512;   // per-row kernels: 8 waves, up to 256 VGPRs each, no spills
+constexpr uint32_t REPLAY_WAVES = REPLAY_THREADS / WAVE;
+constexpr uint32_t SEQ_ITEMS = 8;          // terms per thread per tile of the sum replay
+constexpr uint32_t CI = 8;                 // contiguous elements per thread per step of a scan or compaction
+
+struct NeverStop {
+    __device__ bool operator()(double) const { return false; }
 };
 
 __device__ __forceinline__ uint32_t full_k(const rl_sampling &s, uint32_t V) {
@@ -169,23 +188,83 @@ constexpr uint32_t SORT_ITEMS = 8;                          // elements per lane
 constexpr uint32_t SORT_TILE = SORT_THREADS * SORT_ITEMS;    // elements per tile
 constexpr uint32_t WAVE_SEG = WAVE * SORT_ITEMS;             // a wave's contiguous share of a tile
 
-// grid (slots), SORT_THREADS.
-//
-// First the penalty's effect on the maximum, the argmax and the keys
-// (sample.rs:241-257, 267-277): the chunks' results cover the ids outside the
-// window; each distinct window id's penalised logit is merged in and its key
-// rewritten (from the raw logit, so a repeated id is rewritten to the same
-// value). A row without a finite maximum is answered here (argmax, no draw).
-//
-// Then a stable LSD radix sort of the row's (key, id) pairs by descending key,
-// 8 bits a pass; ids start in ascending order, so ties keep ascending ids (the
-// order of sample.rs:282-286). One read gives all four digits' histograms. A
-// pass is skipped when its digit is the same for every key of each sign (as
-// for logits on a bf16 grid, whose low 16 key bits follow the sign): keys that
-// agree above such a digit agree on it, so the pass could not change the final
-// order. Each tile gives every wave a contiguous segment, ranked item by item
-// with wave-local running counts per digit, so a tile of SORT_TILE elements
-// costs three barriers. The result ends in keyA/idA.
+// Whether a row tries the min-p path: min-p on, the whole vocabulary as
+// candidates (top_k 0 or >= vocab), sampling (not greedy).
+__device__ __forceinline__ bool small_eligible(const rl_sampling &s, uint32_t V) {
+    return s.min_p > 0.0f && full_k(s, V) == V && s.temperature > 0.0f;
+}
+
+// grid (slots), FULL_THREADS: the penalty's effect on the maximum, the argmax
+// and the keys (sample.rs:241-257, 267-277). The chunks' results cover the ids
+// outside the window; each distinct window id's penalised logit is merged in
+// and its key rewritten (from the raw logit, so a repeated id is rewritten to
+// the same value). A row without a finite maximum is answered here (argmax,
+// no draw). Leaves the row state for the kernels that follow.
+__global__ __launch_bounds__(FULL_THREADS) void k_full_prep(RowIO a, FullScratch f) {
+    __shared__ float red_max[FULL_THREADS / WAVE];
+    __shared__ uint64_t red_am[FULL_THREADS / WAVE];
+    const uint32_t slot = blockIdx.x;
+    const uint32_t row = a.rows[slot];
+    const rl_sampling s = a.settings[row];
+    const uint32_t V = a.vocab;
+    const uint32_t tid = threadIdx.x, wave = tid / WAVE;
+    const uint32_t wl = window_len(a, row);
+    const bool pen = penalises(s) && wl > 0;
+    const float *rowp = a.logits + (uint64_t)row * a.stride;
+    uint32_t *keys = f.keyA + (uint64_t)slot * V;
+    float mx = -__builtin_inff();
+    uint64_t am = 0;
+    for (uint32_t c = tid; c < a.chunks; c += FULL_THREADS) {
+        mx = fmaxf(mx, f.part_max[slot * a.chunks + c]);
+        const uint64_t x = f.part_am[slot * a.chunks + c];
+        am = x > am ? x : am;
+    }
+    if (pen) {
+        const uint32_t *win = a.windows + (uint64_t)row * a.wstride;
+        for (uint32_t i = tid; i < wl; i += FULL_THREADS) {
+            const uint32_t id = win[i];
+            if (id >= V) continue;  // sample.rs:248
+            const float x = penalize(((const RL_GLB float *)rowp)[id], s.repeat_penalty);
+            keys[id] = total_key(x);
+            mx = fmaxf(mx, x);
+            const uint64_t c = composite(argmax_key(x), id);
+            am = c > am ? c : am;
+        }
+    }
+    mx = wave_maxnum_f32(mx);
+    am = wave_max_u64(am);
+    if (lane_id() == 0) {
+        red_max[wave] = mx;
+        red_am[wave] = am;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (uint32_t w = 0; w < FULL_THREADS / WAVE; ++w) {
+            mx = fmaxf(mx, red_max[w]);
+            am = red_am[w] > am ? red_am[w] : am;
+        }
+        const uint32_t am_tok = comp_key(am) == 0 ? 0u : comp_id(am);
+        const bool finite = mx > -__builtin_inff() && mx < __builtin_inff();
+        FullRow st{};
+        st.M = mx;
+        st.am_tok = am_tok;
+        st.done = finite ? 0u : 1u;
+        st.small = finite && small_eligible(s, V) ? 1u : 0u;
+        f.row[slot] = st;
+        if (!finite) write_single(a, row, am_tok);  // sample.rs:270-277
+    }
+}
+
+// grid (slots), SORT_THREADS: a stable LSD radix sort of the row's (key, id)
+// pairs by descending key, 8 bits a pass; ids start in ascending order, so
+// ties keep ascending ids (the order of sample.rs:282-286). One read decides
+// which passes run: a pass is skipped when its digit is the same for every key
+// of each sign (as for logits on a bf16 grid, whose low 16 key bits follow the
+// sign): keys that agree above such a digit agree on it, so the pass could not
+// change the final order. Each tile gives every wave a contiguous segment,
+// ranked item by item with wave-local running counts per digit, then
+// reordered by digit in LDS and written out in runs. The result ends in
+// keyA/idA.
 __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch f) {
     __shared__ uint32_t hist[4][256];
     __shared__ uint32_t offs[256];
@@ -194,65 +273,20 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
     __shared__ uint32_t cls[4];  // OR and AND of the keys with the top bit clear, then set
     __shared__ uint32_t tcount[256], tstart[256];
     __shared__ uint32_t tile_k[SORT_TILE], tile_i[SORT_TILE];
-    __shared__ float red_max[SORT_WAVES];
-    __shared__ uint64_t red_am[SORT_WAVES];
     const uint32_t slot = blockIdx.x;
+    if (f.row[slot].done) return;
     const uint32_t row = a.rows[slot];
     const rl_sampling s = a.settings[row];
     const uint32_t V = a.vocab;
+    if (identity_order(s, V)) return;
     const uint32_t tid = threadIdx.x, wave = tid / WAVE, lane = lane_id();
-    const uint32_t wl = window_len(a, row);
-    const bool pen = penalises(s) && wl > 0;
-    const float *rowp = a.logits + (uint64_t)row * a.stride;
     uint32_t *kin = f.keyA + (uint64_t)slot * V, *iin = f.idA + (uint64_t)slot * V;
-
-    float mx = -__builtin_inff();
-    uint64_t am = 0;
-    for (uint32_t c = tid; c < a.chunks; c += SORT_THREADS) {
-        mx = fmaxf(mx, f.part_max[slot * a.chunks + c]);
-        const uint64_t x = f.part_am[slot * a.chunks + c];
-        am = x > am ? x : am;
-    }
-    if (pen) {
-        const uint32_t *win = a.windows + (uint64_t)row * a.wstride;
-        for (uint32_t i = tid; i < wl; i += SORT_THREADS) {
-            const uint32_t id = win[i];
-            if (id >= V) continue;  // sample.rs:248
-            const float x = penalize(((const RL_GLB float *)rowp)[id], s.repeat_penalty);
-            kin[id] = total_key(x);
-            mx = fmaxf(mx, x);
-            const uint64_t c = composite(argmax_key(x), id);
-            am = c > am ? c : am;
-        }
-    }
-    mx = wave_maxnum_f32(mx);
-    am = wave_max_u64(am);
-    if (lane == 0) {
-        red_max[wave] = mx;
-        red_am[wave] = am;
-    }
-    __syncthreads();
-    for (uint32_t w = 0; w < SORT_WAVES; ++w) {
-        mx = fmaxf(mx, red_max[w]);
-        am = red_am[w] > am ? red_am[w] : am;
-    }
-    const uint32_t am_tok = comp_key(am) == 0 ? 0u : comp_id(am);
-    const bool finite = mx > -__builtin_inff() && mx < __builtin_inff();
-    if (tid == 0) {
-        FullRow st{};
-        st.M = mx;
-        st.am_tok = am_tok;
-        st.done = finite ? 0u : 1u;
-        f.row[slot] = st;
-        if (!finite) write_single(a, row, am_tok);  // sample.rs:270-277
-    }
-    if (!finite || identity_order(s, V)) return;
 
     // Which passes run: per sign, the OR and the AND of its keys give the bits
     // in which keys of that sign differ (OR ^ AND); over all keys, the bits in
     // which any keys differ.
     if (tid < 4) cls[tid] = (tid & 1) ? 0xFFFFFFFFu : 0u;
-    __syncthreads();  // also makes the rewritten window keys visible
+    __syncthreads();
     {
         uint32_t or0 = 0u, and0 = 0xFFFFFFFFu, or1 = 0u, and1 = 0xFFFFFFFFu;
         for (uint32_t base = 0; base < V; base += SORT_THREADS * 4) {
@@ -451,18 +485,220 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
     }
 }
 
-// ------------------------------------------------------------ probs ---
-constexpr uint32_t UN = 4;  // elements per thread per step of the bulk loops
+// ----------------------------------------------------------- min-p path ---
+// A row with min-p on and the whole vocabulary as candidates keeps only
+// candidates with p >= min_p (sample.rs:326-340), usually a few. Those are the
+// first candidates of the reference's order (p falls along the order; checked
+// below, not assumed), so the row needs only them sorted, plus the mass of the
+// whole row for the top-p cut (sample.rs:307-324). The mass's sequential f64
+// sum is not computed here: the sum in another order is within a proven
+// relative bound of it, and the cut is accepted only when no value in that
+// interval could move it. Anything else (too many survivors, a NaN, a cut
+// inside the interval) leaves the row to the sorting kernels.
 
+// grid (chunks, slots), FULL_THREADS: for rows on the min-p path, p of every
+// id in this chunk (keys in id order), the chunk's f64 sum of p, the
+// survivors as composites in the row's list, and the largest key of a
+// non-survivor.
+__global__ __launch_bounds__(FULL_THREADS) void k_full_collect(RowIO a, FullScratch f) {
+    __shared__ uint64_t exp_tab[32];
+    __shared__ double red_d[FULL_THREADS / WAVE];
+    const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
+    const FullRow st = f.row[slot];
+    if (st.done || !st.small) return;
+    const uint32_t row = a.rows[slot];
+    const rl_sampling s = a.settings[row];
+    const uint32_t V = a.vocab;
+    const uint32_t j0 = chunk_lo(V, chunk, a.chunks), j1 = chunk_lo(V, chunk + 1, a.chunks);
+    const uint32_t *keys = f.keyA + (uint64_t)slot * V;
+    uint64_t *list = f.surv + (uint64_t)slot * SURV_CAP;
+    FullRow *rs = f.row + slot;
+    copy_exp_table((RL_LDS uint64_t *)exp_tab);
+    const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab};
+    const uint32_t lane = lane_id();
+    double sum = 0.0;
+    uint32_t ns_key = 0;  // largest key + 1 of a non-survivor
+    bool stop = false;
+    for (uint32_t b = j0; b < j1 && !stop; b += FULL_THREADS * UN) {
+        uint32_t kk[UN];
+#pragma unroll
+        for (uint32_t u = 0; u < UN; ++u) {
+            const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
+            kk[u] = j < j1 ? ((const RL_GLB uint32_t *)keys)[j] : 0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < UN; ++u) {
+            const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
+            const bool ok = j < j1;
+            const float p = ok ? expf_libm_t((key_value(kk[u]) - st.M) / s.temperature, etab) : 0.0f;
+            const bool finite = p <= 3.40282347e38f;  // false for NaN
+            const bool surv = ok && finite && p >= s.min_p;
+            if (ok) sum += (double)p;
+            if (ok && finite && !surv) ns_key = max(ns_key, kk[u] + 1u);  // a finite p's key is below 0xFFFFFFFF
+            const uint64_t m = ballot(surv);
+            uint32_t base = 0;
+            if (m != 0 && lane == 0) base = atomicAdd(&rs->nsurv, (uint32_t)__popcll(m));
+            base = uniform_u32(__shfl((int)base, 0));
+            if (surv) {
+                const uint32_t at = base + lanes_below(m);
+                if (at < SURV_CAP) list[at] = composite(kk[u], j);
+            }
+            if ((m != 0 && base + (uint32_t)__popcll(m) > SURV_CAP) || ballot(ok && !finite) != 0) {
+                if (lane == 0) atomicOr(&rs->overflow, 1u);
+            }
+        }
+        stop = __hip_atomic_load(&rs->overflow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    }
+    for (int m = 32; m >= 1; m >>= 1) {
+        sum += __shfl_xor(sum, m);
+        ns_key = max(ns_key, (uint32_t)__shfl_xor((int)ns_key, m));
+    }
+    if (lane == 0 && ns_key != 0) atomicMax(&rs->ns_key, ns_key);
+    const uint32_t wave = threadIdx.x / WAVE;
+    if (lane == 0) red_d[wave] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < FULL_THREADS / WAVE; ++w) sum += red_d[w];
+        f.psum[slot * a.chunks + chunk] = sum;
+    }
+}
+
+// Sorts n2 (a power of two, <= SURV_CAP) composites in LDS, descending.
+__device__ __forceinline__ void lds_bitonic_desc(RL_LDS uint64_t *v, uint32_t n2, uint32_t nt) {
+    for (uint32_t size = 2; size <= n2; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t t = threadIdx.x; t < n2 / 2; t += nt) {
+                const uint32_t i = 2 * t - (t & (stride - 1)), j = i + stride;
+                const bool desc = (i & size) == 0;
+                const uint64_t x = v[i], y = v[j];
+                if ((x < y) == desc) {
+                    v[i] = y;
+                    v[j] = x;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// grid (slots), REPLAY_THREADS: finishes a min-p row from its survivors, or
+// leaves it (done stays 0) to the sorting kernels.
+__global__ __launch_bounds__(REPLAY_THREADS) void k_full_small(RowIO a, FullScratch f) {
+    __shared__ uint64_t sv_[SURV_CAP];
+    __shared__ float sp_[SURV_CAP];
+    __shared__ SeqLds<REPLAY_THREADS> seq;
+    __shared__ uint64_t exp_tab[32];
+    __shared__ uint32_t sh_bad;
+    RL_LDS uint64_t *sv = (RL_LDS uint64_t *)sv_;
+    RL_LDS float *sp = (RL_LDS float *)sp_;
+    const uint32_t slot = blockIdx.x;
+    const FullRow st = f.row[slot];
+    if (st.done || !st.small || st.overflow) return;
+    const uint32_t c = st.nsurv;
+    if (c == 0 || c > SURV_CAP) return;  // no survivor: the reference keeps its first candidate
+    const uint32_t row = a.rows[slot];
+    const rl_sampling s = a.settings[row];
+    const uint32_t V = a.vocab;
+    const uint32_t tid = threadIdx.x;
+    // With top-p off the reference keeps id order (no sort, sample.rs:290-305):
+    // the survivors are then sorted by ascending id, stored as
+    // (~id << 32 | key) so that the same descending sort serves.
+    const bool by_id = !(s.top_p < 1.0f);
+    uint32_t n2 = 1;
+    while (n2 < c) n2 <<= 1;
+    const uint64_t *list = f.surv + (uint64_t)slot * SURV_CAP;
+    for (uint32_t i = tid; i < n2; i += REPLAY_THREADS) {
+        uint64_t x = 0;
+        if (i < c) {
+            x = list[i];
+            if (by_id) x = ((uint64_t)(uint32_t)x << 32) | comp_key(x);  // ~id in the high half
+        }
+        sv[i] = x;
+    }
+    if (tid == 0) sh_bad = 0;
+    copy_exp_table((RL_LDS uint64_t *)exp_tab);
+    const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab};
+    lds_bitonic_desc(sv, n2, REPLAY_THREADS);
+    auto key_at = [&](uint32_t i) { return by_id ? (uint32_t)sv[i] : comp_key(sv[i]); };
+    auto id_at = [&](uint32_t i) { return by_id ? ~(uint32_t)(sv[i] >> 32) : comp_id(sv[i]); };
+    for (uint32_t i = tid; i < c; i += REPLAY_THREADS)
+        sp[i] = expf_libm_t((key_value(key_at(i)) - st.M) / s.temperature, etab);
+    __syncthreads();
+    const auto term = [sp](uint32_t j) { return sp[j]; };
+
+    uint32_t kept = c;
+    if (!by_id) {
+        // The survivors must be the first c candidates: every other key is
+        // below the smallest survivor key (equal keys have equal p).
+        if (st.ns_key != 0 && !(key_at(c - 1) >= st.ns_key)) return;
+        if (!(s.top_p > 0.0f)) {
+            kept = 1;  // a target <= 0 is met by the first candidate (sample.rs:315-323)
+        } else {
+            // The reference's mass (a sequential f64 sum of all V p's in
+            // candidate order) and S (this sum in chunk order) are each
+            // within gamma_(V-1) * mass of the exact sum, where
+            // gamma_n = n 2^-53 / (1 - n 2^-53); d bounds both, with margin.
+            double S = 0.0;
+            for (uint32_t ch = 0; ch < a.chunks; ++ch) S += f.psum[slot * a.chunks + ch];
+            const double d = 2.25 * ((double)V + 64.0) * 0x1p-53;
+            const double tp = (double)s.top_p;
+            const double t_lo = tp * (S * (1.0 - d)) * (1.0 - 0x1p-50);
+            const double t_hi = tp * (S * (1.0 + d)) * (1.0 + 0x1p-50);
+            double at;
+            const uint32_t j_lo =
+                seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, c, [t_lo](double v) { return v >= t_lo; }, &seq, &at);
+            if (j_lo < c) {
+                const uint32_t j_hi = seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(
+                    term, c, [t_hi](double v) { return v >= t_hi; }, &seq, &at);
+                if (j_hi != j_lo) return;  // the cut could fall on either side: sort the row
+                kept = j_lo + 1;
+            }
+        }
+    }
+    // Normalise over the kept candidates (sample.rs:342-347) and draw
+    // (:349-358), both in their order.
+    double total;
+    seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, kept, NeverStop{}, &seq, &total);
+    const float inv = (float)(1.0 / total);
+    for (uint32_t i = tid; i < kept; i += REPLAY_THREADS) {
+        const float q = sp[i] * inv;
+        if (!(q <= 3.40282347e38f)) sh_bad = 1;
+    }
+    __syncthreads();
+    if (sh_bad) return;  // a non-finite probability: the sorting kernels walk it in order
+    for (uint32_t i = tid; i < kept; i += REPLAY_THREADS) {
+        const float q = sp[i] * inv;
+        sp[i] = q;
+        if (a.out_ids) {
+            a.out_ids[(uint64_t)row * a.cand_stride + i] = id_at(i);
+            a.out_probs[(uint64_t)row * a.cand_stride + i] = q;
+        }
+    }
+    __syncthreads();
+    const float u = a.uniforms[row];
+    double unused;
+    const uint32_t j =
+        seq_replay<24, REPLAY_THREADS, SEQ_ITEMS>(term, kept, [u](double v) { return v > (double)u; }, &seq, &unused);
+    if (tid == 0) {
+        a.out_token[row] = id_at(j < kept ? j : kept - 1);
+        a.out_kept[row] = kept;
+        a.out_used[row] = 1;
+        f.row[slot].done = 1;
+    }
+}
+
+// ------------------------------------------------------------ probs ---
 // grid (chunks, slots), FULL_THREADS: p_j = exp((l_j - max) / T) for the
 // candidates of this chunk (sample.rs:309), and per chunk: their f64 sum,
-// the smallest binary exponent of a nonzero p, how many are >= min_p, and
-// whether one is NaN or infinite.
+// the smallest binary exponent of a nonzero p, how many are >= min_p, the
+// last index of one that is and the first of one that is not, and whether one
+// is NaN or infinite.
 __global__ __launch_bounds__(FULL_THREADS) void k_full_probs(RowIO a, FullScratch f) {
     __shared__ uint64_t exp_tab[32];
     __shared__ double red_d[FULL_THREADS / WAVE];
     __shared__ int red_e[FULL_THREADS / WAVE];
     __shared__ uint32_t red_c[FULL_THREADS / WAVE], red_b[FULL_THREADS / WAVE];
+    __shared__ uint32_t red_li[FULL_THREADS / WAVE], red_fo[FULL_THREADS / WAVE];
     const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
     const FullRow st = f.row[slot];
     if (st.done) return;
@@ -477,7 +713,7 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_probs(RowIO a, FullScratc
     const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab};
     double sum = 0.0;
     int emin = 1 << 20;
-    uint32_t count = 0, bad = 0;
+    uint32_t count = 0, bad = 0, last_in = 0, first_out = 0xFFFFFFFFu;
     for (uint32_t b = j0; b < j1; b += FULL_THREADS * UN) {
         uint32_t kk[UN];
 #pragma unroll
@@ -497,7 +733,12 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_probs(RowIO a, FullScratc
                     emin = min(emin, f32_exponent(p));
                 }
                 sum += (double)p;
-                count += p >= s.min_p ? 1u : 0u;
+                if (p >= s.min_p) {
+                    ++count;
+                    last_in = max(last_in, j + 1);
+                } else {
+                    first_out = min(first_out, j);
+                }
             }
         }
     }
@@ -506,6 +747,8 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_probs(RowIO a, FullScratc
         emin = min(emin, __shfl_xor(emin, m));
         count += (uint32_t)__shfl_xor((int)count, m);
         bad |= (uint32_t)__shfl_xor((int)bad, m);
+        last_in = max(last_in, (uint32_t)__shfl_xor((int)last_in, m));
+        first_out = min(first_out, (uint32_t)__shfl_xor((int)first_out, m));
     }
     const uint32_t wave = threadIdx.x / WAVE;
     if (lane_id() == 0) {
@@ -513,6 +756,8 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_probs(RowIO a, FullScratc
         red_e[wave] = emin;
         red_c[wave] = count;
         red_b[wave] = bad;
+        red_li[wave] = last_in;
+        red_fo[wave] = first_out;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -521,20 +766,20 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_probs(RowIO a, FullScratc
             emin = min(emin, red_e[w]);
             count += red_c[w];
             bad |= red_b[w];
+            last_in = max(last_in, red_li[w]);
+            first_out = min(first_out, red_fo[w]);
         }
         const uint32_t i = slot * a.chunks + chunk;
         f.psum[i] = sum;
         f.pemin[i] = emin;
         f.pcount[i] = count;
         f.pbad[i] = bad;
+        f.plast_in[i] = last_in;
+        f.pfirst_out[i] = first_out;
     }
 }
 
 // ------------------------------------------------------------- tail ---
-constexpr uint32_t REPLAY_THREADS = 512;  // 8 waves: up to 256 VGPRs each, no spills
-constexpr uint32_t REPLAY_WAVES = REPLAY_THREADS / WAVE;
-constexpr uint32_t SEQ_ITEMS = 8;  // terms per thread per tile of the sum replay
-constexpr uint32_t CI = 8;         // contiguous elements per thread per step of a scan or compaction
 
 __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, RL_LDS uint32_t *red) {
     for (int m = 32; m >= 1; m >>= 1) v += (uint32_t)__shfl_xor((int)v, m);
@@ -595,10 +840,6 @@ __device__ __forceinline__ void staged_walk(const float *src, uint32_t n, RL_LDS
         if (*stop) break;
     }
 }
-
-struct NeverStop {
-    __device__ bool operator()(double) const { return false; }
-};
 
 // Where every partial sum of the probabilities is exact: the first j in
 // [lo, hi) with base + p[lo] + ... + p[j] >= target, and that sum in *at; or
@@ -684,15 +925,19 @@ __global__ __launch_bounds__(REPLAY_THREADS) void k_full_tail(RowIO a, FullScrat
     __syncthreads();
     bool bad = false;
     int emin = 1 << 20;
-    uint32_t count = 0;
+    uint32_t count = 0, last_in = 0, first_out = 0xFFFFFFFFu;
     double tree_mass = 0.0;
     for (uint32_t c = 0; c < C; ++c) {
         const uint32_t i = slot * C + c;
         bad |= f.pbad[i] != 0;
         emin = min(emin, f.pemin[i]);
         count += f.pcount[i];
+        last_in = max(last_in, f.plast_in[i]);
+        first_out = min(first_out, f.pfirst_out[i]);
         tree_mass += chunk_sum[c];
     }
+    // The candidates with p >= min_p form a prefix of the list.
+    const bool surv_prefix = last_in <= first_out;
     // Every partial sum exact: all p are multiples of 2^(emin-23), the mass is
     // below 2^53 of those steps. Then the chunk sums are the exact sums too.
     const bool exact = !bad && (emin > 1000 || tree_mass < mul_pow2(1.0, 30 + emin));
@@ -773,9 +1018,10 @@ __global__ __launch_bounds__(REPLAY_THREADS) void k_full_tail(RowIO a, FullScrat
     }
     if (s.min_p > 0.0f) {  // sample.rs:326-340, a stable in-place compaction
         uint32_t w;
-        if (!bad && !identity_order(s, V)) {
-            // Sorted candidates: p falls along the order, so the survivors
-            // are the first `count` of all k, and min(m, count) of the first m.
+        if (!bad && surv_prefix) {
+            // The survivors are the first `count` of all k candidates (so it
+            // is with sorted candidates, where p falls along the order), and
+            // min(m, count) of the first m: nothing moves.
             w = min(m, count);
         } else {
             // Survivors anywhere: count them, and compact unless they are
@@ -831,7 +1077,7 @@ __global__ __launch_bounds__(REPLAY_THREADS) void k_full_tail(RowIO a, FullScrat
     double total = 0.0;
     if (have_sum_m) {
         total = sum_m;  // the same terms in the same order as the top-p pass
-    } else if (exact && !identity_order(s, V)) {
+    } else if (exact && (surv_prefix || !(s.min_p > 0.0f))) {
         total = exact_prefix(m);  // min-p moved nothing: the chunk sums still apply
     } else if (exact) {
         exact_first_reaching(probs, 0, m, 0.0, __builtin_inf(), red_d, (RL_LDS uint32_t *)&sh_hit_, (RL_LDS double *)&sh_hit_sum_, &total);

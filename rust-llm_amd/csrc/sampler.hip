@@ -77,7 +77,8 @@ struct rl_sampler_ctx {
     uint64_t *d_part_am = nullptr;
     double *d_psum = nullptr;
     int *d_pemin = nullptr;
-    uint32_t *d_pcount = nullptr, *d_pbad = nullptr;
+    uint32_t *d_pcount = nullptr, *d_pbad = nullptr, *d_plast_in = nullptr, *d_pfirst_out = nullptr;
+    uint64_t *d_surv = nullptr;
     FullRow *d_full_row = nullptr;
     uint64_t *d_argmax_part = nullptr;
     std::vector<void *> owned;
@@ -86,6 +87,7 @@ struct rl_sampler_ctx {
     std::vector<uint32_t> stream_rows, full_rows;  // ascending
     uint64_t cand_need = 0;
     bool any_drawing = false;
+    bool any_small = false;  // a full-path row may take the min-p path
 
     template <class T>
     hipError_t alloc(T **p, size_t count) {
@@ -145,6 +147,9 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     if (e == hipSuccess) e = c->alloc(&c->d_pemin, fg * MAX_CHUNKS);
     if (e == hipSuccess) e = c->alloc(&c->d_pcount, fg * MAX_CHUNKS);
     if (e == hipSuccess) e = c->alloc(&c->d_pbad, fg * MAX_CHUNKS);
+    if (e == hipSuccess) e = c->alloc(&c->d_plast_in, fg * MAX_CHUNKS);
+    if (e == hipSuccess) e = c->alloc(&c->d_pfirst_out, fg * MAX_CHUNKS);
+    if (e == hipSuccess) e = c->alloc(&c->d_surv, fg * SURV_CAP);
     if (e == hipSuccess) e = c->alloc(&c->d_full_row, fg);
     if (e == hipSuccess) e = c->alloc(&c->d_argmax_part, std::max<size_t>(CHUNK_SLOTS, max_rows));
     if (e != hipSuccess) {
@@ -170,11 +175,14 @@ int rl_sampler_configure(rl_sampler_ctx *ctx, const rl_sampling *settings, uint3
     if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select device");
     std::vector<uint32_t> sr, fr;
     uint64_t need = 0;
-    bool drawing = false;
+    bool drawing = false, small = false;
     for (uint32_t r = 0; r < rows; ++r) {
         (plan_row(settings[r], ctx->vocab) == Path::Stream ? sr : fr).push_back(r);
         need = std::max(need, row_cand_need(settings[r], ctx->vocab));
         drawing = drawing || !(settings[r].temperature <= 0.0f);
+        small = small || (plan_row(settings[r], ctx->vocab) == Path::Full && settings[r].min_p > 0.0f &&
+                          settings[r].temperature > 0.0f &&
+                          (settings[r].top_k == 0 || settings[r].top_k >= ctx->vocab));
     }
     hipError_t e = hipMemcpy(ctx->d_settings, settings, rows * sizeof(rl_sampling), hipMemcpyHostToDevice);
     if (e == hipSuccess && !sr.empty())
@@ -187,6 +195,7 @@ int rl_sampler_configure(rl_sampler_ctx *ctx, const rl_sampling *settings, uint3
     ctx->full_rows = std::move(fr);
     ctx->cand_need = need;
     ctx->any_drawing = drawing;
+    ctx->any_small = small;
     return RL_OK;
 }
 
@@ -272,8 +281,9 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
         f.rows = ctx->d_full_rows + g0;
         f.chunks = std::max(1u, std::min(MAX_CHUNKS, (TARGET_WGS + ng - 1) / ng));
         f.chunks = std::min(f.chunks, std::max(1u, vocab / 4096));
-        FullScratch fs{ctx->d_keyA, ctx->d_idA,    ctx->d_keyB,   ctx->d_idB,  ctx->d_probs,     ctx->d_part_max,
-                       ctx->d_part_am, ctx->d_psum, ctx->d_pemin, ctx->d_pcount, ctx->d_pbad, ctx->d_full_row};
+        FullScratch fs{ctx->d_keyA,     ctx->d_idA,      ctx->d_keyB,       ctx->d_idB,   ctx->d_probs,
+                       ctx->d_part_max, ctx->d_part_am,  ctx->d_psum,       ctx->d_pemin, ctx->d_pcount,
+                       ctx->d_pbad,     ctx->d_plast_in, ctx->d_pfirst_out, ctx->d_surv,  ctx->d_full_row};
         const dim3 cgrid(f.chunks, ng);
         if (vec)
             hipLaunchKernelGGL(k_full_keys<true>, cgrid, dim3(FULL_THREADS), window_lds_bytes(ctx->hash_bits), st,
@@ -281,6 +291,11 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
         else
             hipLaunchKernelGGL(k_full_keys<false>, cgrid, dim3(FULL_THREADS), window_lds_bytes(ctx->hash_bits), st,
                                f, fs);
+        hipLaunchKernelGGL(k_full_prep, dim3(ng), dim3(FULL_THREADS), 0, st, f, fs);
+        if (ctx->any_small) {
+            hipLaunchKernelGGL(k_full_collect, cgrid, dim3(FULL_THREADS), 0, st, f, fs);
+            hipLaunchKernelGGL(k_full_small, dim3(ng), dim3(REPLAY_THREADS), 0, st, f, fs);
+        }
         hipLaunchKernelGGL(k_full_sort, dim3(ng), dim3(SORT_THREADS), 0, st, f, fs);
         hipLaunchKernelGGL(k_full_probs, cgrid, dim3(FULL_THREADS), 0, st, f, fs);
         hipLaunchKernelGGL(k_full_tail, dim3(ng), dim3(REPLAY_THREADS), 0, st, f, fs);
