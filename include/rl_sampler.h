@@ -7,8 +7,8 @@
  * point below says which part of that API it replaces.
  *
  * Conventions:
- *   - Every pointer argument of rl_sampler_sample_rows and rl_argmax_rows is a
- *     DEVICE pointer (HBM). Logits are read, never written: the repetition
+ *   - Every pointer argument of rl_sampler_sample_rows, rl_argmax_rows and
+ *     rl_top_probability_rows is a DEVICE pointer (HBM). Logits are read, never written: the repetition
  *     penalty is applied virtually, so repeated calls on the same buffer are
  *     idempotent.
  *   - `stream` is a hipStream_t passed as void*; NULL is the default stream.
@@ -116,6 +116,16 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
  * max_rows of the context; independent of configure. */
 int rl_argmax_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t row_stride, uint32_t rows,
                    uint32_t vocab, uint32_t *out_token, void *stream);
+
+/* Per row: the argmax and its probability under a softmax over the whole row,
+ * 1 / sum_i exp(l_i - l_best) as f32, with the sum in f64 in id order exactly
+ * as the reference accumulates it (bit-identical). Replaces `top_probability`
+ * (crates/rust-llm/src/forward.rs:1671-1680, the MTP draft confidence tested
+ * against MTP_P_MIN at forward.rs:1014-1015), batched. A row holding a NaN, or
+ * nothing above -inf, or +inf, gives a NaN probability, as the reference's sum
+ * does. Device pointers; rows <= max_rows; independent of configure. */
+int rl_top_probability_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t row_stride, uint32_t rows,
+                            uint32_t vocab, uint32_t *out_token, float *out_prob, void *stream);
 
 /* Diagnostic: out[i] = the device's f32 exp of the float whose bit pattern is
  * lo_bits + i, for i < count (device pointer). This is the exp the sampler uses

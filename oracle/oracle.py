@@ -85,6 +85,10 @@ def lib():
         L.orc_naive.restype = ctypes.c_size_t
         L.orc_test_logits.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float]
         L.orc_alloc_test_logits.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_uint64]
+        L.orc_top_probability.argtypes = [_f32p, ctypes.c_size_t, _f32p]
+        L.orc_top_probability.restype = ctypes.c_uint32
+        L.orc_top_probability_rows.argtypes = [_f32p, ctypes.c_uint64, ctypes.c_size_t, ctypes.c_size_t, _u32p,
+                                               _f32p]
         L.orc_libm_expf.argtypes = [ctypes.c_float]
         L.orc_libm_expf.restype = ctypes.c_float
         L.orc_expf_compare.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint64, _u32p, ctypes.c_uint64]
@@ -245,6 +249,23 @@ def alloc_test_logits(n, seed):
     out = np.zeros(n, np.float32)
     lib().orc_alloc_test_logits(_ptr(out, _f32p), n, seed)
     return out
+
+
+def top_probability(logits):
+    """forward.rs:1671-1680: (argmax, 1 / sum exp(v - max)) of one row."""
+    a = np.ascontiguousarray(logits, dtype=np.float32)
+    p = ctypes.c_float()
+    t = lib().orc_top_probability(_ptr(a, _f32p), a.size, ctypes.byref(p))
+    return int(t), np.float32(p.value)
+
+
+def top_probability_rows(logits):
+    a = np.ascontiguousarray(logits, dtype=np.float32)
+    rows, n = a.shape
+    tok = np.zeros(rows, np.uint32)
+    prob = np.zeros(rows, np.float32)
+    lib().orc_top_probability_rows(_ptr(a, _f32p), n, rows, n, _ptr(tok, _u32p), _ptr(prob, _f32p))
+    return tok, prob
 
 
 def libm_expf(x):

@@ -24,6 +24,10 @@
  *   exp/sums/cut/draw pinned: the naive f64 reference (tests/sample.rs:16-83)
  *                    on 72 cases, edge counts tests/sample.rs:351-412, draw
  *                    frequencies tests/sample.rs:464-504.
+ *   orc_top_probability  pinned: known answers with exact results (equal
+ *                    logits: 1/n; one finite logit among -inf: 1), its NaN
+ *                    and infinity cases, and a step-by-step recomputation
+ *                    (Python float additions of this library's expf).
  *   One corner is parity unpinned: with top_p >= 1 and 0 < top_k < vocab the
  *   reference walks the candidates in the order Rust's select_nth_unstable_by
  *   leaves them (sample.rs:294, :349-356). That order is an implementation
@@ -570,6 +574,32 @@ void orc_alloc_test_logits(float *out, size_t n, uint64_t seed) {
         s ^= s << 17;
         out[i] = (float)(s >> 11) / (float)(1ull << 53) * 12.0f - 6.0f;
     }
+}
+
+/* ---------------------------------------------------- top probability ---- */
+/* forward.rs:1671-1680 `top_probability`: the argmax (IEEE '>', lowest id on a
+ * tie, starting from -inf and id 0) and (1 / sum) as f32, where sum is the f64
+ * sum, in id order, of exp(v - best) (f32 subtraction, libm expf). Rust's
+ * f64 Sum folds from -0.0, which gives the same bits as 0.0 for these terms
+ * (all >= +0 or NaN) and n >= 1. */
+uint32_t orc_top_probability(const float *l, size_t n, float *prob) {
+    size_t best = 0;
+    float best_v = -INFINITY;
+    for (size_t i = 0; i < n; i++) {
+        if (l[i] > best_v) {
+            best_v = l[i];
+            best = i;
+        }
+    }
+    double sum = -0.0;
+    for (size_t i = 0; i < n; i++) sum += (double)expf(l[i] - best_v);
+    *prob = (float)(1.0 / sum);
+    return (uint32_t)best;
+}
+
+void orc_top_probability_rows(const float *logits, uint64_t stride, size_t rows, size_t n, uint32_t *tok,
+                              float *prob) {
+    for (size_t r = 0; r < rows; r++) tok[r] = orc_top_probability(logits + r * stride, n, prob + r);
 }
 
 /* libm expf, the function Rust's f32::exp lowers to; exposed so the GPU's

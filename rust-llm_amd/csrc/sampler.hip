@@ -11,6 +11,7 @@
 #include "rl_error.h"
 #include "rl_sampler.h"
 #include "full_kernels.h"
+#include "top_probability.h"
 
 using namespace rl;
 
@@ -81,6 +82,8 @@ struct rl_sampler_ctx {
     uint64_t *d_surv = nullptr;
     FullRow *d_full_row = nullptr;
     uint64_t *d_argmax_part = nullptr;
+    uint32_t *d_tp_nan = nullptr;
+    double *d_tp_sum = nullptr;
     std::vector<void *> owned;
     // Host copy of the plan made by configure.
     uint32_t configured = 0;
@@ -152,6 +155,8 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     if (e == hipSuccess) e = c->alloc(&c->d_surv, fg * SURV_CAP);
     if (e == hipSuccess) e = c->alloc(&c->d_full_row, fg);
     if (e == hipSuccess) e = c->alloc(&c->d_argmax_part, std::max<size_t>(CHUNK_SLOTS, max_rows));
+    if (e == hipSuccess) e = c->alloc(&c->d_tp_nan, std::max<size_t>(CHUNK_SLOTS, max_rows));
+    if (e == hipSuccess) e = c->alloc(&c->d_tp_sum, std::max<size_t>(CHUNK_SLOTS, max_rows));
     if (e != hipSuccess) {
         delete c;
         return hip_fail(e, "hipMalloc");
@@ -334,6 +339,41 @@ int rl_argmax_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t row_stride
                        chunks, out_token);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "argmax kernels");
+    return RL_OK;
+}
+
+int rl_top_probability_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t row_stride, uint32_t rows,
+                            uint32_t vocab, uint32_t *out_token, float *out_prob, void *stream) {
+    if (!ctx) return fail(RL_ERR_ARGUMENT, "ctx is null");
+    if (vocab != ctx->vocab)
+        return fail(RL_ERR_VOCAB, "this sampler was built for a different vocabulary");
+    if (rows == 0) return RL_OK;
+    if (rows > ctx->max_rows) return fail(RL_ERR_CAPACITY, "more rows than max_rows");
+    if (!logits || !out_token || !out_prob) return fail(RL_ERR_ARGUMENT, "null logits or outputs");
+    if (rows > 1 && row_stride < vocab) return fail(RL_ERR_ARGUMENT, "row_stride below vocab");
+    DeviceGuard g(ctx->device);
+    if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select device");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const uint64_t stride = rows > 1 ? row_stride : vocab;
+    const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (stride % 4 == 0);
+    uint32_t chunks = std::min(MAX_CHUNKS, (TARGET_WGS + rows - 1) / rows);
+    chunks = std::max(1u, std::min(chunks, vocab / 4096));
+    dim3 grid(chunks, rows);
+    if (vec) {
+        hipLaunchKernelGGL(k_tp_max<true>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
+                           ctx->d_argmax_part, ctx->d_tp_nan);
+        hipLaunchKernelGGL(k_tp_sum<true>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
+                           ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum);
+    } else {
+        hipLaunchKernelGGL(k_tp_max<false>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
+                           ctx->d_argmax_part, ctx->d_tp_nan);
+        hipLaunchKernelGGL(k_tp_sum<false>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
+                           ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum);
+    }
+    hipLaunchKernelGGL(k_tp_final, dim3(rows), dim3(REPLAY_THREADS), 0, st, logits, stride, vocab, chunks,
+                       ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum, out_token, out_prob);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "top_probability kernels");
     return RL_OK;
 }
 

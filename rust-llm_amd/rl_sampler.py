@@ -85,6 +85,7 @@ def lib():
         L.rl_sampler_sample_rows.argtypes = [
             _vp, _vp, _u64, _u32, _u32, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u64, _vp]
         L.rl_argmax_rows.argtypes = [_vp, _vp, _u64, _u32, _u32, _vp, _vp]
+        L.rl_top_probability_rows.argtypes = [_vp, _vp, _u64, _u32, _u32, _vp, _vp, _vp]
         L.rl_sampler_last_error.restype = ctypes.c_char_p
         L.rl_sampler_expf_range.argtypes = [_u32, _u64, _vp, _vp]
         L.rl_rng_seeded.argtypes = [ctypes.POINTER(Rng), _u64]
@@ -203,6 +204,14 @@ class DeviceSampler:
         _check(lib().rl_argmax_rows(self.h, _ptr(logits), row_stride, rows,
                                     self.vocab if vocab is None else vocab, _ptr(out_token),
                                     current_stream() if stream is None else stream))
+
+
+    def top_probability_rows(self, logits, rows, row_stride, out_token, out_prob, vocab=None, stream=None):
+        """rl_top_probability_rows: argmax and 1 / sum exp(l - l_best) per row
+        (forward.rs:1671-1680)."""
+        _check(lib().rl_top_probability_rows(self.h, _ptr(logits), row_stride, rows,
+                                             self.vocab if vocab is None else vocab, _ptr(out_token),
+                                             _ptr(out_prob), current_stream() if stream is None else stream))
 
 
 class BatchResult:
