@@ -38,6 +38,9 @@ def parse():
                     help="budget for the CPU-baseline sample (0 skips it)")
     ap.add_argument("--no-candidates", action="store_true",
                     help="skip the candidate outputs (tokens only)")
+    ap.add_argument("--op", default="sample", choices=["sample", "top_probability", "argmax"],
+                    help="sample: rl_sampler_sample_rows (the benchmark); top_probability and argmax time "
+                         "rl_top_probability_rows and rl_argmax_rows on the same logits")
     ap.add_argument("--calibration-copy", type=int, default=0,
                     help="after the timed steps, run this many plain device copies of the logits "
                          "(known bytes) so profiler byte counters can be scaled")
@@ -116,10 +119,18 @@ def main():
     out_probs = torch.empty((wl.rows, cs), dtype=torch.float32, device=dev) if cs else None
     stream = torch.cuda.current_stream()
 
+    out_prob = torch.empty(wl.rows, dtype=torch.float32, device=dev)
+
     def step():
-        ctx.sample_rows(d_logits, wl.rows, d_logits.stride(0), out_tok, out_kept, out_used, windows=d_win,
-                        window_stride=W.WINDOW, window_len=d_wlen, uniforms=d_uni, out_ids=out_ids,
-                        out_probs=out_probs, cand_stride=cs, stream=stream.cuda_stream)
+        if args.op == "sample":
+            ctx.sample_rows(d_logits, wl.rows, d_logits.stride(0), out_tok, out_kept, out_used, windows=d_win,
+                            window_stride=W.WINDOW, window_len=d_wlen, uniforms=d_uni, out_ids=out_ids,
+                            out_probs=out_probs, cand_stride=cs, stream=stream.cuda_stream)
+        elif args.op == "top_probability":
+            ctx.top_probability_rows(d_logits, wl.rows, d_logits.stride(0), out_tok, out_prob,
+                                     stream=stream.cuda_stream)
+        else:
+            ctx.argmax_rows(d_logits, wl.rows, d_logits.stride(0), out_tok, stream=stream.cuda_stream)
 
     for _ in range(args.warmup):
         step()
@@ -138,7 +149,10 @@ def main():
     median_ms = per_call_ms[len(per_call_ms) // 2]
     ms_per_step = wall * 1e3 / args.steps
     rows_per_s = wl.rows / (ms_per_step / 1e3)
-    alg_bytes = wl.algorithmic_bytes() if cs else wl.algorithmic_bytes(kept_out=0)
+    if args.op == "sample":
+        alg_bytes = wl.algorithmic_bytes() if cs else wl.algorithmic_bytes(kept_out=0)
+    else:  # the logits once, and a token (and a probability) per row
+        alg_bytes = wl.rows * (wl.vocab * 4 + 4 + (4 if args.op == "top_probability" else 0))
     achieved = alg_bytes / (mean_ms / 1e3) / 1e9
     print("[bench] %s: wall %.3f ms/step, events mean %.3f median %.3f min %.3f max %.3f ms" % (
         name, ms_per_step, mean_ms, median_ms, per_call_ms[0], per_call_ms[-1]), file=sys.stderr, flush=True)
@@ -153,7 +167,7 @@ def main():
         del dst
 
     cpu = None
-    if args.cpu_seconds > 0:
+    if args.cpu_seconds > 0 and args.op == "sample":
         rate, n, el = cpu_baseline(wl, logits, windows, wlen, uniforms, settings, args.cpu_seconds)
         cpu = {"value": round(rate, 2), "unit": "rows/s", "cores": 1, "kind": "port",
                "sample": "%d rows of the same workload (%s) through the oracle on one host core in %.1f s"
@@ -162,7 +176,9 @@ def main():
 
     s0 = settings[0]
     line = {
-        "metric": "rows/s + achieved HBM GB/s, %dx%d fp32 logits, full sampling chain" % (wl.rows, wl.vocab),
+        "metric": ("rows/s + achieved HBM GB/s, %dx%d fp32 logits, full sampling chain" % (wl.rows, wl.vocab)
+                   if args.op == "sample" else
+                   "rows/s + achieved HBM GB/s, %dx%d fp32 logits, %s" % (wl.rows, wl.vocab, args.op)),
         "value": round(rows_per_s, 1),
         "unit": "rows/s",
         "n_gpus": 1,
@@ -188,7 +204,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic_bytes(name),
+            "traffic": traffic_bytes(name) if args.op == "sample" else None,
             "algorithmic_bytes_per_call": alg_bytes,
             "call_ms_mean": round(mean_ms, 5),
             "call_ms_median": round(median_ms, 5),
