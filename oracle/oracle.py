@@ -93,6 +93,13 @@ def lib():
         L.orc_libm_expf.restype = ctypes.c_float
         L.orc_expf_compare.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint64, _u32p, ctypes.c_uint64]
         L.orc_expf_compare.restype = ctypes.c_uint64
+        L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.orc_f16_to_f32.restype = ctypes.c_float
+        L.orc_quantize_rows.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_size_t, _f32p, _P(ctypes.c_int8),
+                                        _P(ctypes.c_int16)]
+        L.orc_q6k_matvec.argtypes = [_u8p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _f32p,
+                                     ctypes.c_size_t, _f32p]
+        L.orc_q6k_matvec.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -277,3 +284,48 @@ def expf_compare(got, lo_bits, report_max=16):
     rep = np.zeros(report_max, np.uint32)
     bad = lib().orc_expf_compare(_ptr(got, _f32p), lo_bits, got.size, _ptr(rep, _u32p), report_max)
     return bad, rep[: min(bad, report_max)]
+
+
+QK = 256
+Q6K_BYTES = 210
+
+
+def f16_to_f32(bits):
+    return np.float32(lib().orc_f16_to_f32(int(bits)))
+
+
+def quantize_rows(x):
+    """Activations::quantize_batch (quant.rs:337-375) of x [t][k]:
+    (d [t][nb] f32, qs [t][nb*256] i8, bsums [t][nb][16] i16)."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    if a.ndim == 1:
+        a = a[None, :]
+    t, k = a.shape
+    nb = -(-k // QK)
+    d = np.zeros((t, nb), np.float32)
+    qs = np.zeros((t, nb * QK), np.int8)
+    bs = np.zeros((t, nb, 16), np.int16)
+    lib().orc_quantize_rows(_ptr(a, _f32p), t, k, _ptr(d, _f32p), _ptr(qs, _P(ctypes.c_int8)),
+                            _ptr(bs, _P(ctypes.c_int16)))
+    return d, qs, bs
+
+
+def q6k_matvec(w, k, x, row_lo=0, row_hi=None):
+    """The head (forward.rs:932-937): logits [t][row_hi-row_lo] of the Q6_K
+    tensor w (bytes, [rows][ceil(k/256)*210]) times the rows of x [t][k]."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    if a.ndim == 1:
+        a = a[None, :]
+    t = a.shape[0]
+    assert a.shape[1] == k
+    row_bytes = -(-k // QK) * Q6K_BYTES
+    rows = w.size // row_bytes
+    if row_hi is None:
+        row_hi = rows
+    assert 0 <= row_lo <= row_hi <= rows
+    out = np.zeros((t, row_hi - row_lo), np.float32)
+    rc = lib().orc_q6k_matvec(_ptr(w, _u8p), k, row_lo, row_hi, _ptr(a, _f32p), t, _ptr(out, _f32p))
+    if rc != 0:
+        raise MemoryError("orc_q6k_matvec")
+    return out

@@ -1,0 +1,149 @@
+// C ABI of the gfx950 output head (include/rl_head.h): weight upload and
+// repack, activation quantization, and the head launches. Kernels are in
+// head_kernels.h.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <new>
+#include <string>
+
+#include "head_kernels.h"
+#include "rl_head.h"
+#include "rl_runtime.h"
+
+using namespace rl;
+
+namespace {
+
+// LDS one head pass may hold: activation blocks of every row of the pass.
+constexpr uint32_t HEAD_LDS_BYTES = 64 * 1024;
+constexpr uint32_t ACT_BLOCK_BYTES = ACT_WORDS * 4;
+
+uint32_t rows_per_pass(uint32_t nb) {
+    return std::min<uint32_t>(HEAD_TMAX, HEAD_LDS_BYTES / (nb * ACT_BLOCK_BYTES));
+}
+
+}  // namespace
+
+struct rl_head {
+    int device = 0;
+    uint32_t k = 0, rows = 0, nb = 0, groups = 0, max_batch = 0, per_pass = 0;
+    uint4 *wq = nullptr;
+    uint16_t *wd = nullptr;
+    uint32_t *act = nullptr;
+    ~rl_head() {
+        (void)hipFree(wq);
+        (void)hipFree(wd);
+        (void)hipFree(act);
+    }
+};
+
+namespace {
+
+template <int T>
+void launch_head(const rl_head *h, const uint32_t *act, uint32_t t, float *out, uint64_t stride, hipStream_t s) {
+    const uint32_t blocks = (h->groups + HEAD_WAVES - 1) / HEAD_WAVES;
+    const size_t lds = (size_t)t * h->nb * ACT_BLOCK_BYTES;
+    hipLaunchKernelGGL(k_head_q6k<T>, dim3(blocks), dim3(HEAD_THREADS), lds, s, h->wq, h->wd, act, t, h->nb,
+                       h->rows, h->groups, out, stride);
+}
+
+void launch_quantize(const float *x, uint32_t t, uint32_t k, uint32_t nb, uint32_t *act, float *d, int8_t *qs,
+                     int16_t *bs, hipStream_t s) {
+    const uint64_t waves = (uint64_t)t * nb;
+    const uint32_t blocks = (uint32_t)((waves + 3) / 4);
+    hipLaunchKernelGGL(k_quantize_rows, dim3(blocks), dim3(256), 0, s, x, t, k, nb, act, d, qs, bs);
+}
+
+}  // namespace
+
+extern "C" {
+
+int rl_head_create(int device, uint32_t k, uint32_t rows, uint32_t max_batch, const void *q6k, uint64_t q6k_bytes,
+                   rl_head **out) {
+    if (!out) return fail(RL_ERR_ARGUMENT, "out is null");
+    *out = nullptr;
+    if (!q6k) return fail(RL_ERR_ARGUMENT, "q6k is null");
+    if (k == 0 || rows == 0 || max_batch == 0) return fail(RL_ERR_ARGUMENT, "k, rows and max_batch must be positive");
+    const uint32_t nb = (k + QK - 1) / QK;
+    if (q6k_bytes != (uint64_t)rows * nb * Q6K_BLOCK_BYTES)
+        return fail(RL_ERR_ARGUMENT, "q6k_bytes is not rows * ceil(k/256) * 210");
+    if (rows_per_pass(nb) == 0)
+        return fail(RL_ERR_CAPACITY, "k above " + std::to_string(HEAD_LDS_BYTES / ACT_BLOCK_BYTES * QK));
+    DeviceGuard g(device);
+    if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select device " + std::to_string(device));
+    auto *h = new (std::nothrow) rl_head();
+    if (!h) return fail(RL_ERR_CAPACITY, "out of host memory");
+    h->device = device;
+    h->k = k;
+    h->rows = rows;
+    h->nb = nb;
+    h->groups = (rows + HEAD_LANES - 1) / HEAD_LANES;
+    h->max_batch = max_batch;
+    h->per_pass = rows_per_pass(nb);
+    const uint64_t gb = (uint64_t)h->groups * nb;
+    hipError_t e = hipMalloc(&h->wq, gb * HEAD_CHUNKS * HEAD_LANES * sizeof(uint4));
+    if (e == hipSuccess) e = hipMalloc(&h->wd, gb * HEAD_LANES * sizeof(uint16_t));
+    if (e == hipSuccess) e = hipMalloc(&h->act, (uint64_t)max_batch * nb * ACT_BLOCK_BYTES);
+    uint8_t *staging = nullptr;
+    if (e == hipSuccess) e = hipMalloc(&staging, q6k_bytes);
+    if (e == hipSuccess) e = hipMemcpy(staging, q6k, q6k_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        const uint64_t threads = gb * HEAD_LANES;
+        hipLaunchKernelGGL(k_q6k_repack, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, 0, staging, rows,
+                           nb, h->groups, h->wq, h->wd);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (staging) (void)hipFree(staging);
+    if (e != hipSuccess) {
+        delete h;
+        return hip_fail(e, "rl_head_create");
+    }
+    *out = h;
+    return RL_OK;
+}
+
+void rl_head_destroy(rl_head *head) {
+    if (!head) return;
+    DeviceGuard g(head->device);
+    delete head;
+}
+
+int rl_head_logits(rl_head *h, const float *x, uint32_t t, float *logits, uint64_t row_stride, void *stream) {
+    if (!h) return fail(RL_ERR_ARGUMENT, "head is null");
+    if (t == 0) return RL_OK;
+    if (!x || !logits) return fail(RL_ERR_ARGUMENT, "x and logits must be device pointers");
+    if (t > h->max_batch) return fail(RL_ERR_CAPACITY, "t above the head's max_batch");
+    if (row_stride < h->rows) return fail(RL_ERR_ARGUMENT, "row_stride below the vocabulary");
+    DeviceGuard g(h->device);
+    if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select the head's device");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    launch_quantize(x, t, h->k, h->nb, h->act, nullptr, nullptr, nullptr, s);
+    for (uint32_t t0 = 0; t0 < t; t0 += h->per_pass) {
+        const uint32_t n = std::min(h->per_pass, t - t0);
+        const uint32_t *act = h->act + (uint64_t)t0 * h->nb * ACT_WORDS;
+        float *out = logits + (uint64_t)t0 * row_stride;
+        if (n <= 1) launch_head<1>(h, act, n, out, row_stride, s);
+        else if (n <= 2) launch_head<2>(h, act, n, out, row_stride, s);
+        else if (n <= 4) launch_head<4>(h, act, n, out, row_stride, s);
+        else if (n <= 8) launch_head<8>(h, act, n, out, row_stride, s);
+        else if (n <= 16) launch_head<16>(h, act, n, out, row_stride, s);
+        else launch_head<32>(h, act, n, out, row_stride, s);
+    }
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? RL_OK : hip_fail(e, "rl_head_logits launch");
+}
+
+int rl_quantize_rows(const float *x, uint32_t t, uint32_t k, float *out_d, int8_t *out_qs, int16_t *out_bsums,
+                     void *stream) {
+    if (t == 0) return RL_OK;
+    if (!x || k == 0) return fail(RL_ERR_ARGUMENT, "x must be a device pointer and k positive");
+    const uint32_t nb = (k + QK - 1) / QK;
+    launch_quantize(x, t, k, nb, nullptr, out_d, out_qs, out_bsums, static_cast<hipStream_t>(stream));
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? RL_OK : hip_fail(e, "rl_quantize_rows launch");
+}
+
+}  // extern "C"

@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "rl_error.h"
+#include "rl_runtime.h"
 #include "rl_sampler.h"
 #include "full_kernels.h"
 #include "top_probability.h"
@@ -18,15 +19,6 @@ using namespace rl;
 namespace {
 
 thread_local std::string g_last_error;
-
-int fail(int code, const std::string &msg) {
-    rl::set_last_error(msg);
-    return code;
-}
-
-int hip_fail(hipError_t e, const char *what) {
-    return fail(RL_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
-}
 
 constexpr uint32_t MAX_WINDOW = 2048;
 constexpr uint32_t TARGET_WGS = 1024;  // enough workgroups to cover 256 CUs four deep
@@ -47,19 +39,6 @@ uint64_t row_cand_need(const rl_sampling &s, uint32_t vocab) {
     if (s.top_k == 0 || s.top_k >= vocab) return vocab;
     return s.top_k;
 }
-
-struct DeviceGuard {
-    int prev = -1;
-    bool ok = true;
-    explicit DeviceGuard(int dev) {
-        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-        if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
-    }
-    ~DeviceGuard() {
-        int cur = -1;
-        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-    }
-};
 
 }  // namespace
 

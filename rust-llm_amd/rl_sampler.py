@@ -1,7 +1,9 @@
-"""Python bindings (ctypes) for librl_sampler.so, the gfx950 token sampler.
+"""Python bindings (ctypes) for librl_sampler.so, the gfx950 token sampler and
+output head.
 
-The library's C ABI is include/rl_sampler.h (device batch entry points) and
-include/rl_sampler_host.h (the reference's Sampler API kept on the host). This
+The library's C ABI is include/rl_sampler.h (device batch entry points),
+include/rl_sampler_host.h (the reference's Sampler API kept on the host) and
+include/rl_head.h (the Q6_K output head that writes logits into HBM). This
 module only marshals arguments: every pick runs in the HIP library, and loading
 fails loudly when the library has not been built.
 
@@ -118,6 +120,11 @@ def lib():
         L.rl_host_sampler_verify.argtypes = [_vp, _vp, _u64, ctypes.c_size_t, _vp, _u32, _vp, _vp]
         L.rl_host_sampler_commit_verified.argtypes = [_vp, _u32, ctypes.POINTER(_u32)]
         L.rl_host_sample_batch.argtypes = [ctypes.POINTER(_vp), _u32, _vp, _u64, ctypes.c_size_t, _vp, _vp]
+        L.rl_head_create.argtypes = [ctypes.c_int, _u32, _u32, _u32, _vp, _u64, ctypes.POINTER(_vp)]
+        L.rl_head_destroy.argtypes = [_vp]
+        L.rl_head_destroy.restype = None
+        L.rl_head_logits.argtypes = [_vp, _vp, _u32, _vp, _u64, _vp]
+        L.rl_quantize_rows.argtypes = [_vp, _u32, _u32, _vp, _vp, _vp, _vp]
         _lib = L
     return _lib
 
@@ -354,3 +361,61 @@ def expf_range(lo_bits, out, stream=None):
 
 def entropy_seed():
     return lib().rl_entropy_seed()
+
+
+QK = 256
+Q6K_BYTES = 210
+
+
+class DeviceHead:
+    """rl_head_create / rl_head_logits: the tied Q6_K output head
+    (forward.rs:932-937) with its weights resident in HBM."""
+
+    def __init__(self, q6k, k, rows, max_batch=32, device=0):
+        import numpy as np
+        w = np.ascontiguousarray(q6k, dtype=np.uint8)
+        h = _vp()
+        _check(lib().rl_head_create(device, k, rows, max_batch, w.ctypes.data, w.nbytes, ctypes.byref(h)))
+        self.h = h
+        self.k, self.rows, self.max_batch, self.device = k, rows, max_batch, device
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().rl_head_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def logits_into(self, x, out, row_stride=None, stream=None):
+        """x: device f32 [t][k] (contiguous); out: device f32 with rows of
+        row_stride >= vocabulary entries."""
+        t = x.shape[0]
+        _check(lib().rl_head_logits(self.h, _ptr(x), t, _ptr(out),
+                                    self.rows if row_stride is None else row_stride,
+                                    current_stream() if stream is None else stream))
+
+    def logits(self, x):
+        import torch
+        assert x.dtype == torch.float32 and x.is_contiguous() and x.shape[1] == self.k
+        out = torch.empty((x.shape[0], self.rows), dtype=torch.float32, device=x.device)
+        self.logits_into(x, out)
+        return out
+
+
+def quantize_rows(x, stream=None):
+    """rl_quantize_rows (quant.rs:337-375) of a device f32 [t][k] tensor:
+    (d [t][nb], qs [t][nb*256] int8, bsums [t][nb][16] int16), device tensors."""
+    import torch
+    assert x.dtype == torch.float32 and x.is_contiguous()
+    t, k = x.shape
+    nb = -(-k // QK)
+    d = torch.empty((t, nb), dtype=torch.float32, device=x.device)
+    qs = torch.empty((t, nb * QK), dtype=torch.int8, device=x.device)
+    bs = torch.empty((t, nb, 16), dtype=torch.int16, device=x.device)
+    _check(lib().rl_quantize_rows(_ptr(x), t, k, _ptr(d), _ptr(qs), _ptr(bs),
+                                  current_stream() if stream is None else stream))
+    return d, qs, bs

@@ -15,7 +15,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def declared_functions():
     names = set()
-    for h in ("rl_sampler.h", "rl_sampler_host.h"):
+    for h in sorted(f for f in os.listdir(os.path.join(ROOT, "include")) if f.endswith(".h")):
         text = open(os.path.join(ROOT, "include", h)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names.update(re.findall(r"\b(rl_\w+)\s*\(", text))
@@ -41,6 +41,26 @@ def test_status_codes_without_a_device():
     assert lib.rl_sampler_sample_rows(None, None, 0, 1, 1, None, 0, None, None, None, None, None, None,
                                       None, 0, None) == R.RL_ERR_ARGUMENT
     lib.rl_sampler_destroy(None)  # accepted
+
+
+def test_head_status_codes_without_a_device():
+    lib = R.lib()
+    h = ctypes.c_void_p()
+    buf = (ctypes.c_uint8 * (2 * 210))()
+    assert lib.rl_head_create(0, 256, 2, 4, buf, 2 * 210, None) == R.RL_ERR_ARGUMENT
+    assert lib.rl_head_create(0, 256, 2, 4, None, 2 * 210, ctypes.byref(h)) == R.RL_ERR_ARGUMENT
+    assert lib.rl_head_create(0, 0, 2, 4, buf, 0, ctypes.byref(h)) == R.RL_ERR_ARGUMENT
+    assert lib.rl_head_create(0, 256, 2, 0, buf, 2 * 210, ctypes.byref(h)) == R.RL_ERR_ARGUMENT
+    # Two rows of one block are 420 bytes, not 419.
+    assert lib.rl_head_create(0, 256, 2, 4, buf, 419, ctypes.byref(h)) == R.RL_ERR_ARGUMENT
+    assert b"210" in lib.rl_sampler_last_error()
+    # k whose activation blocks would not fit one pass's LDS.
+    big = 200 * 256
+    assert lib.rl_head_create(0, big, 1, 1, buf, 200 * 210, ctypes.byref(h)) == R.RL_ERR_CAPACITY
+    assert lib.rl_head_logits(None, None, 1, None, 0, None) == R.RL_ERR_ARGUMENT
+    assert lib.rl_quantize_rows(None, 1, 256, None, None, None, None) == R.RL_ERR_ARGUMENT
+    assert lib.rl_quantize_rows(None, 0, 256, None, None, None, None) == R.RL_OK  # nothing to do
+    lib.rl_head_destroy(None)  # accepted
 
 
 @pytest.mark.skipif(os.path.exists("/dev/kfd") and os.access("/dev/kfd", os.R_OK),
