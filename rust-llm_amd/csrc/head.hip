@@ -14,46 +14,38 @@
 
 using namespace rl;
 
-namespace {
-
-// LDS one head pass may hold: activation blocks of every row of the pass.
-constexpr uint32_t HEAD_LDS_BYTES = 64 * 1024;
-constexpr uint32_t ACT_BLOCK_BYTES = ACT_WORDS * 4;
-
-uint32_t rows_per_pass(uint32_t nb) {
-    return std::min<uint32_t>(HEAD_TMAX, HEAD_LDS_BYTES / (nb * ACT_BLOCK_BYTES));
-}
-
-}  // namespace
-
 struct rl_head {
     int device = 0;
-    uint32_t k = 0, rows = 0, nb = 0, groups = 0, max_batch = 0, per_pass = 0;
+    uint32_t k = 0, rows = 0, nb = 0, groups = 0, max_batch = 0, tcap = 0;
     uint4 *wq = nullptr;
+    uint32_t *ws = nullptr;
     uint16_t *wd = nullptr;
-    uint32_t *act = nullptr;
+    int8_t *aq = nullptr;  // activation quants [tcap][nb][256]
+    float *ad = nullptr;   // activation scales [tcap][nb]
     ~rl_head() {
         (void)hipFree(wq);
+        (void)hipFree(ws);
         (void)hipFree(wd);
-        (void)hipFree(act);
+        (void)hipFree(aq);
+        (void)hipFree(ad);
     }
 };
 
 namespace {
 
-template <int T>
-void launch_head(const rl_head *h, const uint32_t *act, uint32_t t, float *out, uint64_t stride, hipStream_t s) {
+template <int NT>
+void launch_head(const rl_head *h, uint32_t t0, uint32_t n, float *out, uint64_t stride, hipStream_t s) {
     const uint32_t blocks = (h->groups + HEAD_WAVES - 1) / HEAD_WAVES;
-    const size_t lds = (size_t)t * h->nb * ACT_BLOCK_BYTES;
-    hipLaunchKernelGGL(k_head_q6k<T>, dim3(blocks), dim3(HEAD_THREADS), lds, s, h->wq, h->wd, act, t, h->nb,
-                       h->rows, h->groups, out, stride);
+    hipLaunchKernelGGL(k_head_q6k<NT>, dim3(blocks), dim3(HEAD_THREADS), 0, s, h->wq, h->ws, h->wd,
+                       h->aq + (uint64_t)t0 * h->nb * QK, h->ad + (uint64_t)t0 * h->nb, n, h->nb, h->rows,
+                       h->groups, out, stride);
 }
 
-void launch_quantize(const float *x, uint32_t t, uint32_t k, uint32_t nb, uint32_t *act, float *d, int8_t *qs,
-                     int16_t *bs, hipStream_t s) {
+void launch_quantize(const float *x, uint32_t t, uint32_t k, uint32_t nb, float *d, int8_t *qs, int16_t *bs,
+                     hipStream_t s) {
     const uint64_t waves = (uint64_t)t * nb;
     const uint32_t blocks = (uint32_t)((waves + 3) / 4);
-    hipLaunchKernelGGL(k_quantize_rows, dim3(blocks), dim3(256), 0, s, x, t, k, nb, act, d, qs, bs);
+    hipLaunchKernelGGL(k_quantize_rows, dim3(blocks), dim3(256), 0, s, x, t, k, nb, d, qs, bs);
 }
 
 }  // namespace
@@ -69,8 +61,6 @@ int rl_head_create(int device, uint32_t k, uint32_t rows, uint32_t max_batch, co
     const uint32_t nb = (k + QK - 1) / QK;
     if (q6k_bytes != (uint64_t)rows * nb * Q6K_BLOCK_BYTES)
         return fail(RL_ERR_ARGUMENT, "q6k_bytes is not rows * ceil(k/256) * 210");
-    if (rows_per_pass(nb) == 0)
-        return fail(RL_ERR_CAPACITY, "k above " + std::to_string(HEAD_LDS_BYTES / ACT_BLOCK_BYTES * QK));
     DeviceGuard g(device);
     if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select device " + std::to_string(device));
     auto *h = new (std::nothrow) rl_head();
@@ -79,20 +69,26 @@ int rl_head_create(int device, uint32_t k, uint32_t rows, uint32_t max_batch, co
     h->k = k;
     h->rows = rows;
     h->nb = nb;
-    h->groups = (rows + HEAD_LANES - 1) / HEAD_LANES;
+    h->groups = (rows + HEAD_GROUP - 1) / HEAD_GROUP;
     h->max_batch = max_batch;
-    h->per_pass = rows_per_pass(nb);
-    const uint64_t gb = (uint64_t)h->groups * nb;
-    hipError_t e = hipMalloc(&h->wq, gb * HEAD_CHUNKS * HEAD_LANES * sizeof(uint4));
-    if (e == hipSuccess) e = hipMalloc(&h->wd, gb * HEAD_LANES * sizeof(uint16_t));
-    if (e == hipSuccess) e = hipMalloc(&h->act, (uint64_t)max_batch * nb * ACT_BLOCK_BYTES);
+    h->tcap = (max_batch + HEAD_NTILE - 1) / HEAD_NTILE * HEAD_NTILE;
+    const uint64_t bgt = (uint64_t)nb * h->groups * HEAD_TILES;
+    hipError_t e = hipMalloc(&h->wq, bgt * HEAD_QCH * 64 * sizeof(uint4));
+    if (e == hipSuccess) e = hipMalloc(&h->ws, bgt * 64 * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&h->wd, bgt * HEAD_TILE * sizeof(uint16_t));
+    if (e == hipSuccess) e = hipMalloc(&h->aq, (uint64_t)h->tcap * nb * QK);
+    if (e == hipSuccess) e = hipMalloc(&h->ad, (uint64_t)h->tcap * nb * sizeof(float));
+    // Rows of a column tile past a call's t are read and their products
+    // discarded; start them at zero.
+    if (e == hipSuccess) e = hipMemset(h->aq, 0, (uint64_t)h->tcap * nb * QK);
+    if (e == hipSuccess) e = hipMemset(h->ad, 0, (uint64_t)h->tcap * nb * sizeof(float));
     uint8_t *staging = nullptr;
     if (e == hipSuccess) e = hipMalloc(&staging, q6k_bytes);
     if (e == hipSuccess) e = hipMemcpy(staging, q6k, q6k_bytes, hipMemcpyHostToDevice);
     if (e == hipSuccess) {
-        const uint64_t threads = gb * HEAD_LANES;
+        const uint64_t threads = bgt * 64;
         hipLaunchKernelGGL(k_q6k_repack, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, 0, staging, rows,
-                           nb, h->groups, h->wq, h->wd);
+                           nb, h->groups, h->wq, h->ws, h->wd);
         e = hipGetLastError();
     }
     if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -120,17 +116,13 @@ int rl_head_logits(rl_head *h, const float *x, uint32_t t, float *logits, uint64
     DeviceGuard g(h->device);
     if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select the head's device");
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    launch_quantize(x, t, h->k, h->nb, h->act, nullptr, nullptr, nullptr, s);
-    for (uint32_t t0 = 0; t0 < t; t0 += h->per_pass) {
-        const uint32_t n = std::min(h->per_pass, t - t0);
-        const uint32_t *act = h->act + (uint64_t)t0 * h->nb * ACT_WORDS;
+    launch_quantize(x, t, h->k, h->nb, h->ad, h->aq, nullptr, s);
+    const uint32_t per_pass = HEAD_MAX_NT * HEAD_NTILE;
+    for (uint32_t t0 = 0; t0 < t; t0 += per_pass) {
+        const uint32_t n = std::min(per_pass, t - t0);
         float *out = logits + (uint64_t)t0 * row_stride;
-        if (n <= 1) launch_head<1>(h, act, n, out, row_stride, s);
-        else if (n <= 2) launch_head<2>(h, act, n, out, row_stride, s);
-        else if (n <= 4) launch_head<4>(h, act, n, out, row_stride, s);
-        else if (n <= 8) launch_head<8>(h, act, n, out, row_stride, s);
-        else if (n <= 16) launch_head<16>(h, act, n, out, row_stride, s);
-        else launch_head<32>(h, act, n, out, row_stride, s);
+        if (n <= HEAD_NTILE) launch_head<1>(h, t0, n, out, row_stride, s);
+        else launch_head<2>(h, t0, n, out, row_stride, s);
     }
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? RL_OK : hip_fail(e, "rl_head_logits launch");
@@ -141,7 +133,7 @@ int rl_quantize_rows(const float *x, uint32_t t, uint32_t k, float *out_d, int8_
     if (t == 0) return RL_OK;
     if (!x || k == 0) return fail(RL_ERR_ARGUMENT, "x must be a device pointer and k positive");
     const uint32_t nb = (k + QK - 1) / QK;
-    launch_quantize(x, t, k, nb, nullptr, out_d, out_qs, out_bsums, static_cast<hipStream_t>(stream));
+    launch_quantize(x, t, k, nb, out_d, out_qs, out_bsums, static_cast<hipStream_t>(stream));
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? RL_OK : hip_fail(e, "rl_quantize_rows launch");
 }

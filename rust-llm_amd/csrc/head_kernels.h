@@ -7,40 +7,61 @@
 // blocks of 256 to int8 with one f32 scale per block (quant.rs:337-375), then
 // per (token, vocabulary row) sums, block by block from 0.0 in f32,
 //     (act.d * w.d) * (float)isum,   isum = sum_i s_{i/16} * (q_i - 32) * a_i,
-// where isum is an exact i32. Any order of the integer work gives the same
-// isum; the f32 line is kept as is, one lane per vocabulary row. So the device
-// result equals the reference's whatever the tiling, with no tolerance.
+// where isum is an exact i32. Any way of forming isum exactly gives the same
+// bits; the f32 line is kept as it is, in block order.
 //
-// Layouts in HBM (built once by k_q6k_repack from the GGUF bytes):
-//   wq  uint4 [groups][nb][13][64]: lane l of group g is vocabulary row
-//       g*64 + l. Per lane and block, 13 16-byte chunks: chunks 3p, 3p+1, 3p+2
-//       hold sub-blocks 4p..4p+3 as {L0,L1} pairs and their H words (below),
-//       chunk 12 holds the 16 signed sub-block scales. A wave's load of one
-//       chunk is 1 KiB contiguous.
-//   wd  u16 [groups][nb][64]: the block's f16 scale.
-//   Per sub-block of 16 unsigned 6-bit quants w_0..w_15 (ggml's value before
-//   the -32): L0 byte b = w_b & 15 | (w_{4+b} & 15) << 4, L1 byte b =
-//   w_{8+b} & 15 | (w_{12+b} & 15) << 4, H byte b = the high two bits of w_b,
-//   w_{4+b}, w_{8+b}, w_{12+b} at bits 0, 2, 4, 6. Unpacking gives the four
-//   dwords of bytes w_{4g..4g+3}, matching activation dword g of the sub-block.
-//   Total bytes equal the GGUF tensor's (208 + 2 per block and row).
-//   act u32 [t][nb][84]: per activation block, 64 dwords of int8 quants, 16
-//       words c_j = -32 * bsum_j (the constant -32 folded into the starting
-//       value of each sub-block's dot), the f32 scale, 3 words of padding.
+// How isum is formed here: on the matrix cores, in f16 with f32 accumulation,
+// exactly. Each sub-block scale s (an i8) is split as s = 16 * s_hi + s_lo with
+// s_lo in [0, 15] and s_hi in [-8, 7]. Two products are accumulated over the
+// block's 256 values with v_mfma_f32_16x16x32_f16:
+//     D_lo = sum s_lo * (q - 32) * a,   D_hi = sum s_hi * (q - 32) * a.
+// Every operand is an integer an f16 holds exactly (|s_lo (q-32)| <= 480,
+// |s_hi (q-32)| <= 256, |a| <= 127), every product is exact in f32, and every
+// partial sum is an integer below 2^24 (at most 256 * 480 * 127 < 15.7e6), so
+// the accumulation is exact in any order. Then isum = 16 * D_hi + D_lo in i32.
+//
+// Layouts in HBM (built once by k_q6k_repack from the GGUF bytes), for a
+// vocabulary of `groups` groups of 64 rows, each group four tiles of 16 rows:
+//   Lane l = 16 h + m of a tile holds row m and the quarter h of each block:
+//   values k = 64 h + 8 s + e (step s = 0..7, e = 0..7). The same k order is
+//   used for the activations, so the matrix-core sum runs over the block.
+//   wq  uint4 [nb][groups][4][3][64]: the lane's 64 unsigned 6-bit quants
+//       (ggml's value before the -32), 48 bytes in the packing below.
+//   ws  u32   [nb][groups][4][64]: the lane's four sub-block scales (i8),
+//       sub-blocks 4h .. 4h+3; step s uses byte s / 2.
+//   wd  u16   [nb][groups][4][16]: the f16 block scale of each row.
+//   Total bytes equal the GGUF tensor's: 210 per row and block.
+//   Packing of steps 2p and 2p+1 (values v0..v7 and v8..v15) in words
+//   P0, P1, P2 = words 3p .. 3p+2, as 16-bit halves (low, high):
+//     P0 = {v0 | v2 << 6 | (v12 & 15) << 12,  v1 | v3 << 6 | (v13 & 15) << 12}
+//     P1 = {v4 | v6 << 6 | (v14 & 15) << 12,  v5 | v7 << 6 | (v15 & 15) << 12}
+//     P2 = {v8 | v10 << 6 | (v12 >> 4) << 12 | (v14 >> 4) << 14,
+//           v9 | v11 << 6 | (v13 >> 4) << 12 | (v15 >> 4) << 14}
+//   so each f16 pair (v_2i, v_2i+1) comes out with a mask and an OR of the
+//   f16 exponent bits (0x6400 | q is the f16 1024 + q).
+//   Activations: int8 quants [Tcap][nb][256] and f32 scales [Tcap][nb], the
+//   reference's ActBlock fields.
 #pragma once
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace rl {
 
-constexpr int QK = 256;             // values per quantization block (quant.rs:12)
+constexpr int QK = 256;              // values per quantization block (quant.rs:12)
 constexpr int Q6K_BLOCK_BYTES = 210; // ql 128, qh 64, scales 16, d f16 (quant.rs:19)
-constexpr int HEAD_LANES = 64;       // vocabulary rows per group (one wave)
-constexpr int HEAD_CHUNKS = 13;      // 16-byte chunks per lane and block
-constexpr int ACT_WORDS = 84;        // u32 per activation block in the head's layout
-constexpr int HEAD_WAVES = 4;        // waves (groups) per workgroup
-constexpr int HEAD_THREADS = HEAD_WAVES * HEAD_LANES;
-constexpr int HEAD_TMAX = 32;        // activation rows one pass takes
+constexpr int HEAD_TILE = 16;        // vocabulary rows per matrix-core tile
+constexpr int HEAD_TILES = 4;        // tiles per wave
+constexpr int HEAD_GROUP = HEAD_TILE * HEAD_TILES;  // rows per wave
+constexpr int HEAD_QCH = 3;          // 16-byte quant chunks per lane, tile and block
+constexpr int HEAD_WAVES = 4;        // waves per workgroup
+constexpr int HEAD_THREADS = HEAD_WAVES * 64;
+constexpr int HEAD_NTILE = 16;       // activation rows per matrix-core column tile
+constexpr int HEAD_MAX_NT = 2;       // column tiles one pass takes (32 rows)
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------- repack
 
@@ -55,51 +76,46 @@ __device__ inline uint32_t q6k_quant_at(const uint8_t *b, int i) {
     return low | (high << 4);
 }
 
-// One thread per (group, block, lane); lanes are innermost so the 16-byte
-// stores of a wave are contiguous. Rows at or past `rows` are zero.
+// One thread per (block, group, tile, lane); lanes are innermost so the stores
+// of a wave are contiguous. Rows at or past `rows` are zero.
 __global__ void k_q6k_repack(const uint8_t *__restrict__ src, uint32_t rows, uint32_t nb, uint32_t groups,
-                             uint4 *__restrict__ wq, uint16_t *__restrict__ wd) {
+                             uint4 *__restrict__ wq, uint32_t *__restrict__ ws, uint16_t *__restrict__ wd) {
     const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const uint64_t total = (uint64_t)groups * nb * HEAD_LANES;
+    const uint64_t total = (uint64_t)nb * groups * HEAD_TILES * 64;
     if (idx >= total) return;
-    const uint32_t lane = (uint32_t)(idx % HEAD_LANES);
-    const uint64_t gb = idx / HEAD_LANES;  // g * nb + ib
-    const uint32_t ib = (uint32_t)(gb % nb);
-    const uint32_t g = (uint32_t)(gb / nb);
-    const uint32_t row = g * HEAD_LANES + lane;
-    uint4 *dst = wq + gb * HEAD_CHUNKS * HEAD_LANES + lane;
+    const uint32_t lane = (uint32_t)(idx & 63);
+    const uint64_t bgt = idx >> 6;  // (ib * groups + g) * 4 + tw
+    const uint32_t tw = (uint32_t)(bgt % HEAD_TILES);
+    const uint64_t bg = bgt / HEAD_TILES;
+    const uint32_t g = (uint32_t)(bg % groups);
+    const uint32_t ib = (uint32_t)(bg / groups);
+    const uint32_t m = lane & 15, h = lane >> 4;
+    const uint32_t row = g * HEAD_GROUP + tw * HEAD_TILE + m;
+    uint4 *dq = wq + bgt * HEAD_QCH * 64 + lane;
     if (row >= rows) {
-        for (int c = 0; c < HEAD_CHUNKS; ++c) dst[c * HEAD_LANES] = make_uint4(0, 0, 0, 0);
-        wd[gb * HEAD_LANES + lane] = 0;
+        for (int c = 0; c < HEAD_QCH; ++c) dq[c * 64] = make_uint4(0, 0, 0, 0);
+        ws[bgt * 64 + lane] = 0;
+        if (h == 0) wd[bgt * HEAD_TILE + m] = 0;
         return;
     }
     const uint8_t *b = src + ((uint64_t)row * nb + ib) * Q6K_BLOCK_BYTES;
-    uint32_t words[48];
-    for (int j = 0; j < 16; ++j) {
-        uint32_t l0 = 0, l1 = 0, hw = 0;
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t w0 = q6k_quant_at(b, 16 * j + e), w1 = q6k_quant_at(b, 16 * j + 4 + e);
-            const uint32_t w2 = q6k_quant_at(b, 16 * j + 8 + e), w3 = q6k_quant_at(b, 16 * j + 12 + e);
-            l0 |= ((w0 & 15) | ((w1 & 15) << 4)) << (8 * e);
-            l1 |= ((w2 & 15) | ((w3 & 15) << 4)) << (8 * e);
-            hw |= ((w0 >> 4) | ((w1 >> 4) << 2) | ((w2 >> 4) << 4) | ((w3 >> 4) << 6)) << (8 * e);
-        }
-        const int p = j >> 2, q = j & 3;
-        // chunk 3p: {L0,L1} of sub-blocks 4p, 4p+1; chunk 3p+1: of 4p+2, 4p+3;
-        // chunk 3p+2: H of 4p..4p+3.
-        const int pair_word = 4 * (3 * p + (q >> 1)) + 2 * (q & 1);
-        words[pair_word] = l0;
-        words[pair_word + 1] = l1;
-        words[4 * (3 * p + 2) + q] = hw;
+    uint32_t words[12];
+    for (int p = 0; p < 4; ++p) {
+        uint32_t v[16];
+        for (int i = 0; i < 16; ++i) v[i] = q6k_quant_at(b, 64 * h + 16 * p + i);
+        const uint32_t lo0 = v[0] | v[2] << 6 | (v[12] & 15) << 12, hi0 = v[1] | v[3] << 6 | (v[13] & 15) << 12;
+        const uint32_t lo1 = v[4] | v[6] << 6 | (v[14] & 15) << 12, hi1 = v[5] | v[7] << 6 | (v[15] & 15) << 12;
+        const uint32_t lo2 = v[8] | v[10] << 6 | (v[12] >> 4) << 12 | (v[14] >> 4) << 14;
+        const uint32_t hi2 = v[9] | v[11] << 6 | (v[13] >> 4) << 12 | (v[15] >> 4) << 14;
+        words[3 * p] = lo0 | hi0 << 16;
+        words[3 * p + 1] = lo1 | hi1 << 16;
+        words[3 * p + 2] = lo2 | hi2 << 16;
     }
-    for (int c = 0; c < 12; ++c)
-        dst[c * HEAD_LANES] = make_uint4(words[4 * c], words[4 * c + 1], words[4 * c + 2], words[4 * c + 3]);
-    uint32_t sc[4];
-    for (int w = 0; w < 4; ++w)
-        sc[w] = (uint32_t)b[192 + 4 * w] | ((uint32_t)b[193 + 4 * w] << 8) | ((uint32_t)b[194 + 4 * w] << 16) |
-                ((uint32_t)b[195 + 4 * w] << 24);
-    dst[12 * HEAD_LANES] = make_uint4(sc[0], sc[1], sc[2], sc[3]);
-    wd[gb * HEAD_LANES + lane] = (uint16_t)(b[208] | (b[209] << 8));
+    for (int c = 0; c < HEAD_QCH; ++c)
+        dq[c * 64] = make_uint4(words[4 * c], words[4 * c + 1], words[4 * c + 2], words[4 * c + 3]);
+    const uint8_t *sc = b + 192 + 4 * h;
+    ws[bgt * 64 + lane] = (uint32_t)sc[0] | (uint32_t)sc[1] << 8 | (uint32_t)sc[2] << 16 | (uint32_t)sc[3] << 24;
+    if (h == 0) wd[bgt * HEAD_TILE + m] = (uint16_t)(b[208] | (b[209] << 8));
 }
 
 // ------------------------------------------------------------ activations
@@ -117,12 +133,11 @@ __device__ inline int quant_one(float v, float id) {
 // lane l holds values 4l..4l+3 of the block (zero past k, which the reference
 // leaves out of the maximum and quantizes to 0). The maximum is order-free
 // (f32::max ignores NaN; fmaxf does too), so a wave reduction gives the
-// reference's amax. Writes the head's layout (`act`, may be null) and the
-// reference's ActBlock fields (`out_d`, `out_qs`, `out_bsums`, each may be
-// null).
+// reference's amax. Writes the reference's ActBlock fields; each output may be
+// null.
 __global__ __launch_bounds__(256) void k_quantize_rows(const float *__restrict__ x, uint32_t t, uint32_t k,
-                                                       uint32_t nb, uint32_t *__restrict__ act,
-                                                       float *__restrict__ out_d, int8_t *__restrict__ out_qs,
+                                                       uint32_t nb, float *__restrict__ out_d,
+                                                       int8_t *__restrict__ out_qs,
                                                        int16_t *__restrict__ out_bsums) {
     const uint32_t wave = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
     const uint32_t lane = threadIdx.x & 63;
@@ -147,13 +162,6 @@ __global__ __launch_bounds__(256) void k_quantize_rows(const float *__restrict__
     bsum += __shfl_xor(bsum, 1);
     bsum += __shfl_xor(bsum, 2);
     const uint64_t blk = (uint64_t)tt * nb + ib;
-    if (act) {
-        uint32_t *a = act + blk * ACT_WORDS;
-        a[lane] = packed;
-        if ((lane & 3) == 0) a[64 + lane / 4] = (uint32_t)(-32 * bsum);
-        if (lane == 0) a[80] = __float_as_uint(d);
-        if (lane >= 1 && lane <= 3) a[80 + lane] = 0;
-    }
     if (out_qs) reinterpret_cast<uint32_t *>(out_qs + blk * QK)[lane] = packed;
     if (out_bsums && (lane & 3) == 0) out_bsums[blk * 16 + lane / 4] = (int16_t)bsum;
     if (out_d && lane == 0) out_d[blk] = d;
@@ -161,99 +169,196 @@ __global__ __launch_bounds__(256) void k_quantize_rows(const float *__restrict__
 
 // ------------------------------------------------------------------- head
 
-// The four activation-ordered weight dwords of a sub-block from its L0, L1, H.
-__device__ inline void unpack_sub(uint32_t l0, uint32_t l1, uint32_t h, uint32_t &w0, uint32_t &w1, uint32_t &w2,
-                                  uint32_t &w3) {
-    w0 = (l0 & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
-    w1 = ((l0 >> 4) & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
-    w2 = (l1 & 0x0F0F0F0Fu) | (h & 0x30303030u);
-    w3 = ((l1 >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
+__device__ inline h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
+
+// The eight f16 pairs (1024 + q) of steps 2p and 2p+1 from P0, P1, P2.
+__device__ inline void unpack_steps(uint32_t p0, uint32_t p1, uint32_t p2, uint32_t x[8]) {
+    const uint32_t M6 = 0x003F003Fu, M4 = 0x000F000Fu, M2 = 0x00300030u, MAG = 0x64006400u;
+    x[0] = (p0 & M6) | MAG;
+    x[1] = ((p0 >> 6) & M6) | MAG;
+    x[2] = (p1 & M6) | MAG;
+    x[3] = ((p1 >> 6) & M6) | MAG;
+    x[4] = (p2 & M6) | MAG;
+    x[5] = ((p2 >> 6) & M6) | MAG;
+    x[6] = ((p0 >> 12) & M4) | ((p2 >> 8) & M2) | MAG;
+    x[7] = ((p1 >> 12) & M4) | ((p2 >> 10) & M2) | MAG;
 }
 
-// Sign-extended low 24 bits: tells the compiler the operand fits v_mad_i32_i24.
-// Every value passed here is within +/-2^17 (a sub-block dot).
-__device__ inline int fits24(int v) { return (v << 8) >> 8; }
+// Four signed int8 activations as two f16 pairs: bytes + 128 under the f16
+// exponent of 1024, minus 1152, exact.
+__device__ inline void act_pairs(uint32_t w, uint32_t &lo, uint32_t &hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    const h2_t bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    lo = __builtin_bit_cast(uint32_t, as_h2(a) + bias);
+    hi = __builtin_bit_cast(uint32_t, as_h2(b) + bias);
+}
 
-// One lane per vocabulary row, T activation rows per pass (t <= T active).
-// The activation blocks of the pass sit in LDS; every lane reads the same
-// words (broadcast). Per block: 13 coalesced 16-byte weight loads and the f16
-// scale, the integer dots with v_dot4_i32_i8 (unsigned 6-bit weights < 128 are
-// valid signed bytes; each sub-block's dot starts from -32 * bsum), then the
-// reference's f32 line per token.
-template <int T>
-__global__ __launch_bounds__(HEAD_THREADS) void k_head_q6k(const uint4 *__restrict__ wq,
-                                                            const uint16_t *__restrict__ wd,
-                                                            const uint32_t *__restrict__ act, uint32_t t,
-                                                            uint32_t nb, uint32_t rows, uint32_t groups,
-                                                            float *__restrict__ out, uint64_t out_stride) {
-    extern __shared__ uint4 sact4[];
-    const uint32_t words = t * nb * ACT_WORDS;
+// One tile's weights for one block: the lane's quant words, scale bytes and the
+// f16 scales of rows 4h .. 4h+3.
+struct HeadTile {
+    uint4 q[HEAD_QCH];
+    uint32_t sc;
+    uint2 dd;
+};
+
+__device__ inline HeadTile load_tile(const uint4 *__restrict__ wq, const uint32_t *__restrict__ ws,
+                                     const uint16_t *__restrict__ wd, uint64_t bgt, uint32_t lane, uint32_t h) {
+    HeadTile r;
+#pragma unroll
+    for (int c = 0; c < HEAD_QCH; ++c) r.q[c] = wq[(bgt * HEAD_QCH + c) * 64 + lane];
+    r.sc = ws[bgt * 64 + lane];
+    r.dd = reinterpret_cast<const uint2 *>(wd + bgt * HEAD_TILE)[h];
+    return r;
+}
+
+// The activation fragments of one block: row nt*16 + m, bytes 64h .. 64h+63.
+template <int NT>
+struct HeadAct {
+    uint4 raw[NT][4];
+    float d[NT];
+};
+
+template <int NT>
+__device__ inline HeadAct<NT> load_act(const int8_t *__restrict__ aq, const float *__restrict__ ad, uint32_t nb,
+                                       uint32_t ib, uint32_t m, uint32_t h) {
+    HeadAct<NT> r;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint64_t arow = (uint64_t)(nt * HEAD_NTILE + m) * nb + ib;
+        const uint4 *ap = reinterpret_cast<const uint4 *>(aq + arow * QK + 64 * h);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) r.raw[nt][c] = ap[c];
+        r.d[nt] = ad[arow];
+    }
+    return r;
+}
+
+// One wave per group of 64 vocabulary rows (four 16-row tiles); NT column
+// tiles of 16 activation rows. Per block: the activation fragments are
+// converted once and reused by the four tiles; per tile, 16 matrix-core
+// products (8 steps, s_lo and s_hi) and the reference's f32 line. The next
+// tile's weights (and, at the last tile, the next block's) are in flight while
+// a tile is computed. `stab` is the per-scale-byte table {s_lo, -1056 s_lo,
+// s_hi, -1056 s_hi} as f16 pairs, so (1024 + q) * s + c = (q - 32) * s exactly
+// in one packed FMA.
+template <int NT>
+__global__ __launch_bounds__(HEAD_THREADS) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4 : 2)))
+void k_head_q6k(const uint4 *__restrict__ wq,
+                                                               const uint32_t *__restrict__ ws,
+                                                               const uint16_t *__restrict__ wd,
+                                                               const int8_t *__restrict__ aq,
+                                                               const float *__restrict__ ad, uint32_t t,
+                                                               uint32_t nb, uint32_t rows, uint32_t groups,
+                                                               float *__restrict__ out, uint64_t out_stride) {
+    __shared__ uint4 stab[256];
     {
-        const uint4 *src = reinterpret_cast<const uint4 *>(act);
-        for (uint32_t i = threadIdx.x; i < words / 4; i += HEAD_THREADS) sact4[i] = src[i];
+        const int s = (int)(int8_t)threadIdx.x;  // HEAD_THREADS == 256 entries
+        const int slo = s & 15, shi = s >> 4;
+        const h2_t lo = {(_Float16)(float)slo, (_Float16)(float)slo};
+        const h2_t clo = {(_Float16)(float)(-1056 * slo), (_Float16)(float)(-1056 * slo)};
+        const h2_t hi = {(_Float16)(float)shi, (_Float16)(float)shi};
+        const h2_t chi = {(_Float16)(float)(-1056 * shi), (_Float16)(float)(-1056 * shi)};
+        stab[threadIdx.x & 255] = make_uint4(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, clo),
+                                             __builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, chi));
     }
     __syncthreads();
-    const uint32_t *sact = reinterpret_cast<const uint32_t *>(sact4);
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t g = blockIdx.x * HEAD_WAVES + threadIdx.x / 64;
     if (g >= groups) return;
-    const uint4 *wp = wq + (uint64_t)g * nb * HEAD_CHUNKS * HEAD_LANES + lane;
-    const uint16_t *dp = wd + (uint64_t)g * nb * HEAD_LANES + lane;
+    const uint32_t m = lane & 15, h = lane >> 4;
 
-    float sum[T];
+    f4_t sum[NT][HEAD_TILES];
 #pragma unroll
-    for (int tt = 0; tt < T; ++tt) sum[tt] = 0.0f;
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int tw = 0; tw < HEAD_TILES; ++tw) sum[nt][tw] = f4_t{0.f, 0.f, 0.f, 0.f};
 
+    HeadTile cur = load_tile(wq, ws, wd, (uint64_t)g * HEAD_TILES, lane, h);
     for (uint32_t ib = 0; ib < nb; ++ib) {
-        uint4 c[HEAD_CHUNKS];
+        const uint32_t nxt_ib = ib + 1 < nb ? ib + 1 : ib;  // the last block re-reads itself (a cache hit)
+        const HeadAct<NT> act = load_act<NT>(aq, ad, nb, ib, m, h);
+        h8_t bf[NT][8];
+        float adn[NT];
 #pragma unroll
-        for (int i = 0; i < HEAD_CHUNKS; ++i) c[i] = wp[((uint64_t)ib * HEAD_CHUNKS + i) * HEAD_LANES];
-        const float dw = __half2float(__ushort_as_half(dp[(uint64_t)ib * HEAD_LANES]));
-        int isum[T];
+        for (int nt = 0; nt < NT; ++nt) {
+            adn[nt] = act.d[nt];
 #pragma unroll
-        for (int tt = 0; tt < T; ++tt) isum[tt] = 0;
-        const uint32_t scw[4] = {c[12].x, c[12].y, c[12].z, c[12].w};
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t w4[4] = {act.raw[nt][c].x, act.raw[nt][c].y, act.raw[nt][c].z, act.raw[nt][c].w};
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const uint4 a = c[3 * p], b = c[3 * p + 1], hh = c[3 * p + 2];
-            const uint32_t l0s[4] = {a.x, a.z, b.x, b.z};
-            const uint32_t l1s[4] = {a.y, a.w, b.y, b.w};
-            const uint32_t hs[4] = {hh.x, hh.y, hh.z, hh.w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int j = 4 * p + q;
-                uint32_t w0, w1, w2, w3;
-                unpack_sub(l0s[q], l1s[q], hs[q], w0, w1, w2, w3);
-                const int sj = (int)(int8_t)(scw[p] >> (8 * q));
-#pragma unroll
-                for (int tt = 0; tt < T; ++tt) {
-                    if (tt < (int)t) {
-                        const uint32_t *ab = sact + ((uint64_t)tt * nb + ib) * ACT_WORDS;
-                        const uint4 av = *reinterpret_cast<const uint4 *>(ab + 4 * j);
-                        int dj = (int)ab[64 + j];
-                        dj = __builtin_amdgcn_sdot4((int)w0, (int)av.x, dj, false);
-                        dj = __builtin_amdgcn_sdot4((int)w1, (int)av.y, dj, false);
-                        dj = __builtin_amdgcn_sdot4((int)w2, (int)av.z, dj, false);
-                        dj = __builtin_amdgcn_sdot4((int)w3, (int)av.w, dj, false);
-                        isum[tt] += sj * fits24(dj);
-                    }
+                for (int j = 0; j < 2; ++j) {  // step 2c + j: bytes 8 (2c + j) .. +7
+                    uint32_t p0, p1, p2, p3;
+                    act_pairs(w4[2 * j], p0, p1);
+                    act_pairs(w4[2 * j + 1], p2, p3);
+                    const h2_t e0 = as_h2(p0), e1 = as_h2(p1), e2 = as_h2(p2), e3 = as_h2(p3);
+                    bf[nt][2 * c + j] = h8_t{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
                 }
             }
         }
 #pragma unroll
-        for (int tt = 0; tt < T; ++tt) {
-            if (tt < (int)t) {
-                const float ad = __uint_as_float(sact[((uint64_t)tt * nb + ib) * ACT_WORDS + 80]);
-                const float scale = ad * dw;
-                sum[tt] = sum[tt] + scale * (float)isum[tt];
+        for (int tw = 0; tw < HEAD_TILES; ++tw) {
+            const uint64_t nbgt = tw + 1 < HEAD_TILES ? ((uint64_t)ib * groups + g) * HEAD_TILES + tw + 1
+                                                      : ((uint64_t)nxt_ib * groups + g) * HEAD_TILES;
+            const HeadTile nxt = load_tile(wq, ws, wd, nbgt, lane, h);
+            const uint32_t w12[12] = {cur.q[0].x, cur.q[0].y, cur.q[0].z, cur.q[0].w, cur.q[1].x, cur.q[1].y,
+                                      cur.q[1].z, cur.q[1].w, cur.q[2].x, cur.q[2].y, cur.q[2].z, cur.q[2].w};
+            f4_t acc_lo[NT], acc_hi[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                acc_lo[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+                acc_hi[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
             }
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                uint32_t x[8];
+                unpack_steps(w12[3 * p], w12[3 * p + 1], w12[3 * p + 2], x);
+                const uint4 st = stab[(cur.sc >> (8 * p)) & 255];
+                const h2_t slo = as_h2(st.x), clo = as_h2(st.y), shi = as_h2(st.z), chi = as_h2(st.w);
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    h2_t lo[4], hi[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        lo[e] = __builtin_elementwise_fma(as_h2(x[4 * u + e]), slo, clo);
+                        hi[e] = __builtin_elementwise_fma(as_h2(x[4 * u + e]), shi, chi);
+                    }
+                    const h8_t alo = {lo[0][0], lo[0][1], lo[1][0], lo[1][1], lo[2][0], lo[2][1], lo[3][0], lo[3][1]};
+                    const h8_t ahi = {hi[0][0], hi[0][1], hi[1][0], hi[1][1], hi[2][0], hi[2][1], hi[3][0], hi[3][1]};
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) {
+                        acc_lo[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bf[nt][2 * p + u], acc_lo[nt], 0, 0, 0);
+                        acc_hi[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf[nt][2 * p + u], acc_hi[nt], 0, 0, 0);
+                    }
+                }
+            }
+            // Rows 4h + i of the tile, activation row nt*16 + m.
+            const uint32_t dw2[2] = {cur.dd.x, cur.dd.y};
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int isum = (int)acc_hi[nt][i] * 16 + (int)acc_lo[nt][i];
+                    const float dw = __half2float(__ushort_as_half((uint16_t)(dw2[i >> 1] >> (16 * (i & 1)))));
+                    const float scale = adn[nt] * dw;
+                    sum[nt][tw][i] = sum[nt][tw][i] + scale * (float)isum;
+                }
+            }
+            cur = nxt;
         }
     }
-    const uint32_t row = g * HEAD_LANES + lane;
-    if (row < rows) {
 #pragma unroll
-        for (int tt = 0; tt < T; ++tt)
-            if (tt < (int)t) out[(uint64_t)tt * out_stride + row] = sum[tt];
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t n = nt * HEAD_NTILE + m;
+        if (n >= t) continue;
+#pragma unroll
+        for (int tw = 0; tw < HEAD_TILES; ++tw)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t row = g * HEAD_GROUP + tw * HEAD_TILE + 4 * h + i;
+                if (row < rows) out[(uint64_t)n * out_stride + row] = sum[nt][tw][i];
+            }
     }
 }
 
