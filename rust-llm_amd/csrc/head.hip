@@ -20,32 +20,46 @@ struct rl_head {
     uint4 *wq = nullptr;
     uint32_t *ws = nullptr;
     uint16_t *wd = nullptr;
-    int8_t *aq = nullptr;  // activation quants [tcap][nb][256]
-    float *ad = nullptr;   // activation scales [tcap][nb]
+    int8_t *aq = nullptr;   // activation quants [tcap][nb][256]
+    float *ad = nullptr;    // activation scales [tcap][nb]
+    uint32_t *dq = nullptr; // the quants with bytes 1 and 2 of each word swapped [tcap][nb][64]
+    int32_t *dc = nullptr;  // -32 * bsum per sub-block [tcap][nb][16]
     ~rl_head() {
         (void)hipFree(wq);
         (void)hipFree(ws);
         (void)hipFree(wd);
         (void)hipFree(aq);
         (void)hipFree(ad);
+        (void)hipFree(dq);
+        (void)hipFree(dc);
     }
 };
 
 namespace {
 
-template <int NT>
+// Rows t0 .. t0 + n of the batch, n <= 32: the dot path for one or two rows
+// (memory-bound, least arithmetic per weight), the matrix cores for more.
 void launch_head(const rl_head *h, uint32_t t0, uint32_t n, float *out, uint64_t stride, hipStream_t s) {
     const uint32_t blocks = (h->groups + HEAD_WAVES - 1) / HEAD_WAVES;
-    hipLaunchKernelGGL(k_head_q6k<NT>, dim3(blocks), dim3(HEAD_THREADS), 0, s, h->wq, h->ws, h->wd,
-                       h->aq + (uint64_t)t0 * h->nb * QK, h->ad + (uint64_t)t0 * h->nb, n, h->nb, h->rows,
-                       h->groups, out, stride);
+    const uint64_t ao = (uint64_t)t0 * h->nb;
+    if (n <= 2) {
+        auto kern = n == 1 ? k_head_dot<1> : k_head_dot<2>;
+        hipLaunchKernelGGL(kern, dim3(blocks), dim3(HEAD_THREADS), 0, s, h->wq, h->ws, h->wd, h->dq + ao * 64,
+                           h->dc + ao * 16, h->ad + ao, n, h->nb, h->rows, h->groups, out, stride);
+    } else if (n <= HEAD_NTILE) {
+        hipLaunchKernelGGL(k_head_mfma_regs<1>, dim3(blocks), dim3(HEAD_THREADS), 0, s, h->wq, h->ws, h->wd,
+                           h->aq + ao * QK, h->ad + ao, n, h->nb, h->rows, h->groups, out, stride);
+    } else {
+        hipLaunchKernelGGL(k_head_mfma_lds<2>, dim3(blocks), dim3(HEAD_THREADS), 0, s, h->wq, h->ws, h->wd,
+                           h->aq + ao * QK, h->ad + ao, n, h->nb, h->rows, h->groups, out, stride);
+    }
 }
 
 void launch_quantize(const float *x, uint32_t t, uint32_t k, uint32_t nb, float *d, int8_t *qs, int16_t *bs,
-                     hipStream_t s) {
+                     uint32_t *dq, int32_t *dc, hipStream_t s) {
     const uint64_t waves = (uint64_t)t * nb;
     const uint32_t blocks = (uint32_t)((waves + 3) / 4);
-    hipLaunchKernelGGL(k_quantize_rows, dim3(blocks), dim3(256), 0, s, x, t, k, nb, d, qs, bs);
+    hipLaunchKernelGGL(k_quantize_rows, dim3(blocks), dim3(256), 0, s, x, t, k, nb, d, qs, bs, dq, dc);
 }
 
 }  // namespace
@@ -78,6 +92,8 @@ int rl_head_create(int device, uint32_t k, uint32_t rows, uint32_t max_batch, co
     if (e == hipSuccess) e = hipMalloc(&h->wd, bgt * HEAD_TILE * sizeof(uint16_t));
     if (e == hipSuccess) e = hipMalloc(&h->aq, (uint64_t)h->tcap * nb * QK);
     if (e == hipSuccess) e = hipMalloc(&h->ad, (uint64_t)h->tcap * nb * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&h->dq, (uint64_t)h->tcap * nb * QK);
+    if (e == hipSuccess) e = hipMalloc(&h->dc, (uint64_t)h->tcap * nb * 16 * sizeof(int32_t));
     // Rows of a column tile past a call's t are read and their products
     // discarded; start them at zero.
     if (e == hipSuccess) e = hipMemset(h->aq, 0, (uint64_t)h->tcap * nb * QK);
@@ -116,14 +132,10 @@ int rl_head_logits(rl_head *h, const float *x, uint32_t t, float *logits, uint64
     DeviceGuard g(h->device);
     if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select the head's device");
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    launch_quantize(x, t, h->k, h->nb, h->ad, h->aq, nullptr, s);
+    launch_quantize(x, t, h->k, h->nb, h->ad, h->aq, nullptr, h->dq, h->dc, s);
     const uint32_t per_pass = HEAD_MAX_NT * HEAD_NTILE;
-    for (uint32_t t0 = 0; t0 < t; t0 += per_pass) {
-        const uint32_t n = std::min(per_pass, t - t0);
-        float *out = logits + (uint64_t)t0 * row_stride;
-        if (n <= HEAD_NTILE) launch_head<1>(h, t0, n, out, row_stride, s);
-        else launch_head<2>(h, t0, n, out, row_stride, s);
-    }
+    for (uint32_t t0 = 0; t0 < t; t0 += per_pass)
+        launch_head(h, t0, std::min(per_pass, t - t0), logits + (uint64_t)t0 * row_stride, row_stride, s);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? RL_OK : hip_fail(e, "rl_head_logits launch");
 }
@@ -133,7 +145,7 @@ int rl_quantize_rows(const float *x, uint32_t t, uint32_t k, float *out_d, int8_
     if (t == 0) return RL_OK;
     if (!x || k == 0) return fail(RL_ERR_ARGUMENT, "x must be a device pointer and k positive");
     const uint32_t nb = (k + QK - 1) / QK;
-    launch_quantize(x, t, k, nb, out_d, out_qs, out_bsums, static_cast<hipStream_t>(stream));
+    launch_quantize(x, t, k, nb, out_d, out_qs, out_bsums, nullptr, nullptr, static_cast<hipStream_t>(stream));
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? RL_OK : hip_fail(e, "rl_quantize_rows launch");
 }

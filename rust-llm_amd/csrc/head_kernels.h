@@ -135,10 +135,16 @@ __device__ inline int quant_one(float v, float id) {
 // (f32::max ignores NaN; fmaxf does too), so a wave reduction gives the
 // reference's amax. Writes the reference's ActBlock fields; each output may be
 // null.
+//
+// For the head's dot path it can also write `dot_qs` (the quants with bytes 1
+// and 2 of every word swapped, the byte order the unpacked weights come out in)
+// and `dot_c` (-32 * bsum per sub-block, i32: the start of each sub-block's dot
+// product with unsigned 6-bit weights).
 __global__ __launch_bounds__(256) void k_quantize_rows(const float *__restrict__ x, uint32_t t, uint32_t k,
                                                        uint32_t nb, float *__restrict__ out_d,
                                                        int8_t *__restrict__ out_qs,
-                                                       int16_t *__restrict__ out_bsums) {
+                                                       int16_t *__restrict__ out_bsums,
+                                                       uint32_t *__restrict__ dot_qs, int32_t *__restrict__ dot_c) {
     const uint32_t wave = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
     const uint32_t lane = threadIdx.x & 63;
     if (wave >= t * nb) return;
@@ -165,23 +171,44 @@ __global__ __launch_bounds__(256) void k_quantize_rows(const float *__restrict__
     if (out_qs) reinterpret_cast<uint32_t *>(out_qs + blk * QK)[lane] = packed;
     if (out_bsums && (lane & 3) == 0) out_bsums[blk * 16 + lane / 4] = (int16_t)bsum;
     if (out_d && lane == 0) out_d[blk] = d;
+    if (dot_qs) dot_qs[blk * 64 + lane] = __builtin_amdgcn_perm(packed, packed, 0x03010200u);
+    if (dot_c && (lane & 3) == 0) dot_c[blk * 16 + lane / 4] = -32 * bsum;
 }
 
 // ------------------------------------------------------------------- head
 
+// Sign-extended low 24 bits: tells the compiler the operand fits v_mad_i32_i24.
+// Every value passed here is within +/-2^17 (a sub-block dot).
+__device__ inline int fits24(int v) { return (v << 8) >> 8; }
+
+
 __device__ inline h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
 
+// The masks of the unpacking, held in registers: gfx9 VOP3 takes no literal,
+// so with the constants in registers each field is one v_and_or_b32.
+struct UnpackConsts {
+    uint32_t m6, m4, m2, mag;
+};
+
+__device__ inline UnpackConsts unpack_consts() {
+    UnpackConsts c;
+    asm volatile("v_mov_b32 %0, 0x003F003F" : "=v"(c.m6));
+    asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(c.m4));
+    asm volatile("v_mov_b32 %0, 0x00300030" : "=v"(c.m2));
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(c.mag));
+    return c;
+}
+
 // The eight f16 pairs (1024 + q) of steps 2p and 2p+1 from P0, P1, P2.
-__device__ inline void unpack_steps(uint32_t p0, uint32_t p1, uint32_t p2, uint32_t x[8]) {
-    const uint32_t M6 = 0x003F003Fu, M4 = 0x000F000Fu, M2 = 0x00300030u, MAG = 0x64006400u;
-    x[0] = (p0 & M6) | MAG;
-    x[1] = ((p0 >> 6) & M6) | MAG;
-    x[2] = (p1 & M6) | MAG;
-    x[3] = ((p1 >> 6) & M6) | MAG;
-    x[4] = (p2 & M6) | MAG;
-    x[5] = ((p2 >> 6) & M6) | MAG;
-    x[6] = ((p0 >> 12) & M4) | ((p2 >> 8) & M2) | MAG;
-    x[7] = ((p1 >> 12) & M4) | ((p2 >> 10) & M2) | MAG;
+__device__ inline void unpack_steps(uint32_t p0, uint32_t p1, uint32_t p2, uint32_t x[8], const UnpackConsts &k) {
+    x[0] = (p0 & k.m6) | k.mag;
+    x[1] = ((p0 >> 6) & k.m6) | k.mag;
+    x[2] = (p1 & k.m6) | k.mag;
+    x[3] = ((p1 >> 6) & k.m6) | k.mag;
+    x[4] = (p2 & k.m6) | k.mag;
+    x[5] = ((p2 >> 6) & k.m6) | k.mag;
+    x[6] = ((p0 >> 12) & k.m4) | (((p2 >> 8) & k.m2) | k.mag);
+    x[7] = ((p1 >> 12) & k.m4) | (((p2 >> 10) & k.m2) | k.mag);
 }
 
 // Four signed int8 activations as two f16 pairs: bytes + 128 under the f16
@@ -235,6 +262,146 @@ __device__ inline HeadAct<NT> load_act(const int8_t *__restrict__ aq, const floa
     return r;
 }
 
+// Builds one block's activation fragments in LDS, cooperatively: entry
+// (nt, step s, lane 16h + m) is the f16 fragment of activation row nt*16 + m,
+// values k = 64h + 8s .. +7, as the matrix core's B operand wants it; plus the
+// block scale of each activation row.
+template <int NT>
+__device__ inline void fill_act(uint4 *__restrict__ frag, float *__restrict__ fd, const int8_t *__restrict__ aq,
+                                const float *__restrict__ ad, uint32_t nb, uint32_t ib) {
+    for (uint32_t e = threadIdx.x; e < NT * 8 * 64; e += HEAD_THREADS) {
+        const uint32_t nt = e / 512, s = (e / 64) % 8, l = e % 64;
+        const uint32_t n = nt * HEAD_NTILE + (l & 15), hq = l >> 4;
+        const uint2 raw = *reinterpret_cast<const uint2 *>(aq + ((uint64_t)n * nb + ib) * QK + 64 * hq + 8 * s);
+        uint32_t p0, p1, p2, p3;
+        act_pairs(raw.x, p0, p1);
+        act_pairs(raw.y, p2, p3);
+        frag[e] = make_uint4(p0, p1, p2, p3);
+    }
+    if (threadIdx.x < NT * HEAD_NTILE) fd[threadIdx.x] = ad[(uint64_t)threadIdx.x * nb + ib];
+}
+
+// One wave per group of 64 vocabulary rows (four 16-row tiles); NT column
+// tiles of 16 activation rows. The workgroup walks the blocks in step (one
+// barrier per block): the activation fragments of block ib + 1 are built in
+// LDS while block ib is computed. Each tile takes 16 matrix-core products
+// (8 steps, s_lo and s_hi) and then the reference's f32 line. Weights are
+// fetched two tiles ahead. `stab` is the per-scale-byte table {s_lo,
+// -1056 s_lo, s_hi, -1056 s_hi} as f16 pairs, so (1024 + q) * s + c =
+// (q - 32) * s exactly in one packed FMA.
+template <int NT>
+__global__ __launch_bounds__(HEAD_THREADS) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4 : 2)))
+void k_head_mfma_lds(const uint4 *__restrict__ wq, const uint32_t *__restrict__ ws, const uint16_t *__restrict__ wd,
+                const int8_t *__restrict__ aq, const float *__restrict__ ad, uint32_t t, uint32_t nb,
+                uint32_t rows, uint32_t groups, float *__restrict__ out, uint64_t out_stride) {
+    __shared__ uint4 stab[256];
+    __shared__ uint4 frag[2][NT * 8 * 64];
+    __shared__ float fd[2][NT * HEAD_NTILE];
+    {
+        const int s = (int)(int8_t)threadIdx.x;  // HEAD_THREADS == 256 entries
+        const int slo = s & 15, shi = s >> 4;
+        const h2_t lo = {(_Float16)(float)slo, (_Float16)(float)slo};
+        const h2_t clo = {(_Float16)(float)(-1056 * slo), (_Float16)(float)(-1056 * slo)};
+        const h2_t hi = {(_Float16)(float)shi, (_Float16)(float)shi};
+        const h2_t chi = {(_Float16)(float)(-1056 * shi), (_Float16)(float)(-1056 * shi)};
+        stab[threadIdx.x & 255] = make_uint4(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, clo),
+                                             __builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, chi));
+    }
+    fill_act<NT>(frag[0], fd[0], aq, ad, nb, 0);
+    const uint32_t lane = threadIdx.x & 63;
+    // Wave-uniform, so weight addresses are a scalar base plus the lane offset.
+    const uint32_t g = __builtin_amdgcn_readfirstlane(blockIdx.x * HEAD_WAVES + threadIdx.x / 64);
+    // A wave past the vocabulary still takes part in the barriers.
+    const bool active = g < groups;
+    const uint32_t gg = active ? g : groups - 1;
+    const uint32_t m = lane & 15, h = lane >> 4;
+    const UnpackConsts uk = unpack_consts();
+
+    f4_t sum[NT][HEAD_TILES];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int tw = 0; tw < HEAD_TILES; ++tw) sum[nt][tw] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+    HeadTile cur = load_tile(wq, ws, wd, (uint64_t)gg * HEAD_TILES, lane, h);
+    HeadTile nx1 = load_tile(wq, ws, wd, (uint64_t)gg * HEAD_TILES + 1, lane, h);
+    for (uint32_t ib = 0; ib < nb; ++ib) {
+        __syncthreads();  // block ib's fragments are built; block ib - 1's buffer is free
+        if (ib + 1 < nb) fill_act<NT>(frag[(ib + 1) & 1], fd[(ib + 1) & 1], aq, ad, nb, ib + 1);
+        const uint4 *bfr = frag[ib & 1];
+        float adn[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) adn[nt] = fd[ib & 1][nt * HEAD_NTILE + m];
+        const uint32_t nxt_ib = ib + 1 < nb ? ib + 1 : ib;  // past the end: re-read (a cache hit)
+#pragma unroll
+        for (int tw = 0; tw < HEAD_TILES; ++tw) {
+            // Two tiles ahead: tile tw + 2 of this block, or of the next.
+            const uint64_t nbgt = tw + 2 < HEAD_TILES ? ((uint64_t)ib * groups + gg) * HEAD_TILES + tw + 2
+                                                      : ((uint64_t)nxt_ib * groups + gg) * HEAD_TILES + tw + 2 - HEAD_TILES;
+            const HeadTile nx2 = load_tile(wq, ws, wd, nbgt, lane, h);
+            const uint32_t w12[12] = {cur.q[0].x, cur.q[0].y, cur.q[0].z, cur.q[0].w, cur.q[1].x, cur.q[1].y,
+                                      cur.q[1].z, cur.q[1].w, cur.q[2].x, cur.q[2].y, cur.q[2].z, cur.q[2].w};
+            f4_t acc_lo[NT], acc_hi[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                acc_lo[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+                acc_hi[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                uint32_t x[8];
+                unpack_steps(w12[3 * p], w12[3 * p + 1], w12[3 * p + 2], x, uk);
+                const uint4 st = stab[(cur.sc >> (8 * p)) & 255];
+                const h2_t slo = as_h2(st.x), clo = as_h2(st.y), shi = as_h2(st.z), chi = as_h2(st.w);
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    h2_t lo[4], hi[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        lo[e] = __builtin_elementwise_fma(as_h2(x[4 * u + e]), slo, clo);
+                        hi[e] = __builtin_elementwise_fma(as_h2(x[4 * u + e]), shi, chi);
+                    }
+                    const h8_t alo = {lo[0][0], lo[0][1], lo[1][0], lo[1][1], lo[2][0], lo[2][1], lo[3][0], lo[3][1]};
+                    const h8_t ahi = {hi[0][0], hi[0][1], hi[1][0], hi[1][1], hi[2][0], hi[2][1], hi[3][0], hi[3][1]};
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) {
+                        const h8_t b = __builtin_bit_cast(h8_t, bfr[(nt * 8 + 2 * p + u) * 64 + lane]);
+                        acc_lo[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, acc_lo[nt], 0, 0, 0);
+                        acc_hi[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, acc_hi[nt], 0, 0, 0);
+                    }
+                }
+            }
+            // Rows 4h + i of the tile, activation row nt*16 + m.
+            const uint32_t dw2[2] = {cur.dd.x, cur.dd.y};
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int isum = (int)acc_hi[nt][i] * 16 + (int)acc_lo[nt][i];
+                    const float dw = __half2float(__ushort_as_half((uint16_t)(dw2[i >> 1] >> (16 * (i & 1)))));
+                    const float scale = adn[nt] * dw;
+                    sum[nt][tw][i] = sum[nt][tw][i] + scale * (float)isum;
+                }
+            }
+            cur = nx1;
+            nx1 = nx2;
+        }
+    }
+    if (!active) return;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t n = nt * HEAD_NTILE + m;
+        if (n >= t) continue;
+#pragma unroll
+        for (int tw = 0; tw < HEAD_TILES; ++tw)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t row = g * HEAD_GROUP + tw * HEAD_TILE + 4 * h + i;
+                if (row < rows) out[(uint64_t)n * out_stride + row] = sum[nt][tw][i];
+            }
+    }
+}
+
 // One wave per group of 64 vocabulary rows (four 16-row tiles); NT column
 // tiles of 16 activation rows. Per block: the activation fragments are
 // converted once and reused by the four tiles; per tile, 16 matrix-core
@@ -245,7 +412,7 @@ __device__ inline HeadAct<NT> load_act(const int8_t *__restrict__ aq, const floa
 // in one packed FMA.
 template <int NT>
 __global__ __launch_bounds__(HEAD_THREADS) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4 : 2)))
-void k_head_q6k(const uint4 *__restrict__ wq,
+void k_head_mfma_regs(const uint4 *__restrict__ wq,
                                                                const uint32_t *__restrict__ ws,
                                                                const uint16_t *__restrict__ wd,
                                                                const int8_t *__restrict__ aq,
@@ -265,9 +432,10 @@ void k_head_q6k(const uint4 *__restrict__ wq,
     }
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63;
-    const uint32_t g = blockIdx.x * HEAD_WAVES + threadIdx.x / 64;
+    const uint32_t g = __builtin_amdgcn_readfirstlane(blockIdx.x * HEAD_WAVES + threadIdx.x / 64);
     if (g >= groups) return;
     const uint32_t m = lane & 15, h = lane >> 4;
+    const UnpackConsts uk = unpack_consts();
 
     f4_t sum[NT][HEAD_TILES];
 #pragma unroll
@@ -313,7 +481,7 @@ void k_head_q6k(const uint4 *__restrict__ wq,
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
                 uint32_t x[8];
-                unpack_steps(w12[3 * p], w12[3 * p + 1], w12[3 * p + 2], x);
+                unpack_steps(w12[3 * p], w12[3 * p + 1], w12[3 * p + 2], x, uk);
                 const uint4 st = stab[(cur.sc >> (8 * p)) & 255];
                 const h2_t slo = as_h2(st.x), clo = as_h2(st.y), shi = as_h2(st.z), chi = as_h2(st.w);
 #pragma unroll
@@ -359,6 +527,105 @@ void k_head_q6k(const uint4 *__restrict__ wq,
                 const uint32_t row = g * HEAD_GROUP + tw * HEAD_TILE + 4 * h + i;
                 if (row < rows) out[(uint64_t)n * out_stride + row] = sum[nt][tw][i];
             }
+    }
+}
+
+// The dot path, for one or two activation rows: v_dot4_i32_i8 on the same
+// layout. Lane (m, h) unpacks its quarter-block to bytes (unsigned 6-bit
+// weights, which are valid signed bytes) in the order [v0 v2 v1 v3] per word,
+// dots them with the activation words stored in that order (bytes 1 and 2
+// swapped) starting from -32 * bsum of the sub-block, scales by the sub-block
+// scale, and the four lanes of a row add their exact partial sums with two
+// lane shuffles. Then the reference's f32 line; lane (m, h) stores activation
+// row h.
+template <int T>
+__global__ __launch_bounds__(HEAD_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
+void k_head_dot(const uint4 *__restrict__ wq, const uint32_t *__restrict__ ws, const uint16_t *__restrict__ wd,
+                const uint32_t *__restrict__ dq, const int32_t *__restrict__ dc, const float *__restrict__ ad,
+                uint32_t t, uint32_t nb, uint32_t rows, uint32_t groups, float *__restrict__ out,
+                uint64_t out_stride) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t g = __builtin_amdgcn_readfirstlane(blockIdx.x * HEAD_WAVES + threadIdx.x / 64);
+    if (g >= groups) return;
+    const uint32_t m = lane & 15, h = lane >> 4;
+    const uint32_t M6 = 0x003F003Fu, M6S = 0x3F003F00u, M4 = 0x000F000Fu, M2 = 0x00300030u, M4S = 0x0F000F00u,
+                   M2S = 0x30003000u;
+
+    float sum[HEAD_TILES][T];
+#pragma unroll
+    for (int tw = 0; tw < HEAD_TILES; ++tw)
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt) sum[tw][tt] = 0.0f;
+
+    const uint64_t tile0 = (uint64_t)g * HEAD_TILES;
+    HeadTile cur = load_tile(wq, ws, wd, tile0, lane, h);
+    uint16_t curd = wd[tile0 * HEAD_TILE + m];
+    for (uint32_t ib = 0; ib < nb; ++ib) {
+        const uint32_t nxt_ib = ib + 1 < nb ? ib + 1 : ib;  // past the end: re-read (a cache hit)
+        uint4 a[T][4];
+        uint4 cv[T];
+        float adv[T];
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt) {
+            const uint64_t blk = (uint64_t)(tt < (int)t ? tt : 0) * nb + ib;
+            const uint4 *ap = reinterpret_cast<const uint4 *>(dq + blk * 64 + 16 * h);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) a[tt][c] = ap[c];
+            cv[tt] = reinterpret_cast<const uint4 *>(dc + blk * 16)[h];
+            adv[tt] = ad[blk];
+        }
+#pragma unroll
+        for (int tw = 0; tw < HEAD_TILES; ++tw) {
+            const uint64_t nbgt = tw + 1 < HEAD_TILES ? ((uint64_t)ib * groups + g) * HEAD_TILES + tw + 1
+                                                      : ((uint64_t)nxt_ib * groups + g) * HEAD_TILES;
+            const HeadTile nxt = load_tile(wq, ws, wd, nbgt, lane, h);
+            const uint16_t nxtd = wd[nbgt * HEAD_TILE + m];
+            const uint32_t w12[12] = {cur.q[0].x, cur.q[0].y, cur.q[0].z, cur.q[0].w, cur.q[1].x, cur.q[1].y,
+                                      cur.q[1].z, cur.q[1].w, cur.q[2].x, cur.q[2].y, cur.q[2].z, cur.q[2].w};
+            int isum[T];
+#pragma unroll
+            for (int tt = 0; tt < T; ++tt) isum[tt] = 0;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const uint32_t p0 = w12[3 * p], p1 = w12[3 * p + 1], p2 = w12[3 * p + 2];
+                const uint32_t b0 = (p0 & M6) | ((p0 << 2) & M6S);
+                const uint32_t b1 = (p1 & M6) | ((p1 << 2) & M6S);
+                const uint32_t b2 = (p2 & M6) | ((p2 << 2) & M6S);
+                const uint32_t b3 = ((p0 >> 12) & M4) | ((p2 >> 8) & M2) | ((p1 >> 4) & M4S) | ((p2 >> 2) & M2S);
+                const int sj = (int)(int8_t)(cur.sc >> (8 * p));
+#pragma unroll
+                for (int tt = 0; tt < T; ++tt) {
+                    const uint32_t av[4] = {a[tt][p].x, a[tt][p].y, a[tt][p].z, a[tt][p].w};
+                    const uint32_t cw[4] = {cv[tt].x, cv[tt].y, cv[tt].z, cv[tt].w};
+                    int d = (int)cw[p];
+                    d = __builtin_amdgcn_sdot4((int)b0, (int)av[0], d, false);
+                    d = __builtin_amdgcn_sdot4((int)b1, (int)av[1], d, false);
+                    d = __builtin_amdgcn_sdot4((int)b2, (int)av[2], d, false);
+                    d = __builtin_amdgcn_sdot4((int)b3, (int)av[3], d, false);
+                    isum[tt] += sj * fits24(d);
+                }
+            }
+            const float dw = __half2float(__ushort_as_half(curd));
+#pragma unroll
+            for (int tt = 0; tt < T; ++tt) {
+                int v = isum[tt];
+                v += __shfl_xor(v, 16);
+                v += __shfl_xor(v, 32);
+                const float scale = adv[tt] * dw;
+                sum[tw][tt] = sum[tw][tt] + scale * (float)v;
+            }
+            cur = nxt;
+            curd = nxtd;
+        }
+    }
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt) {
+        if (tt >= (int)t || h != (uint32_t)tt) continue;
+#pragma unroll
+        for (int tw = 0; tw < HEAD_TILES; ++tw) {
+            const uint32_t row = g * HEAD_GROUP + tw * HEAD_TILE + m;
+            if (row < rows) out[(uint64_t)tt * out_stride + row] = sum[tw][tt];
+        }
     }
 }
 
