@@ -10,6 +10,11 @@ row in [8, 14); T 0.6, top-k 20, top-p 0.95, min-p 0, repeat penalty 1.2 over
 64-id windows. Other workload shapes are parity cases (tests/) and can be timed
 with --workload.
 
+--op head times the output head instead (rl_head_logits: t normed hidden rows
+times the tied Q6_K embedding [2560, 248320], logits into HBM); --op head_sample
+times the head followed by sampling its logits, the device path from hidden
+state to token.
+
 Prints one JSON line. `roofline.achieved` is the workload's algorithmic bytes
 per call divided by the average duration of a call, timed with HIP events on
 the stream the kernels run on. `cpu_baseline` times the oracle (the C
@@ -38,9 +43,12 @@ def parse():
                     help="budget for the CPU-baseline sample (0 skips it)")
     ap.add_argument("--no-candidates", action="store_true",
                     help="skip the candidate outputs (tokens only)")
-    ap.add_argument("--op", default="sample", choices=["sample", "top_probability", "argmax"],
+    ap.add_argument("--op", default="sample", choices=["sample", "top_probability", "argmax", "head", "head_sample"],
                     help="sample: rl_sampler_sample_rows (the benchmark); top_probability and argmax time "
-                         "rl_top_probability_rows and rl_argmax_rows on the same logits")
+                         "rl_top_probability_rows and rl_argmax_rows on the same logits; head times "
+                         "rl_head_logits, head_sample the head followed by sampling its logits")
+    ap.add_argument("--head-rows", type=int, default=1,
+                    help="activation rows per head call (1 = a decode step, 9 or 17 = a verify batch)")
     ap.add_argument("--calibration-copy", type=int, default=0,
                     help="after the timed steps, run this many plain device copies of the logits "
                          "(known bytes) so profiler byte counters can be scaled")
@@ -83,6 +91,136 @@ def cpu_baseline(wl, logits, windows, wlen, uniforms, settings, budget_s):
     return done / el, done, el
 
 
+def head_cpu_baseline(w, x, budget_s):
+    """The oracle head on one host core over slices of the vocabulary, until
+    the time budget is spent. Returns full-vocabulary head calls/s."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    import workloads as W
+    rows = W.HEAD_ROWS
+    chunk = 2048
+    done = 0
+    lo = 0
+    t0 = time.perf_counter()
+    while True:
+        hi = min(rows, lo + chunk)
+        oracle.q6k_matvec(w, W.HEAD_K, x, lo, hi)
+        done += hi - lo
+        lo = 0 if hi == rows else hi
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return done / rows / el, done, el
+
+
+def bench_head(args):
+    """--op head / head_sample: the output head, and the head then sampling."""
+    import numpy as np
+    import torch
+
+    import rl_sampler as R
+    import workloads as W
+
+    t = args.head_rows
+    dev = torch.device("cuda:0")
+    t0 = time.time()
+    w = W.head_weights()
+    x = W.head_inputs(t)
+    head = R.DeviceHead(w, W.HEAD_K, W.HEAD_ROWS, max_batch=max(t, 1))
+    print("[bench] head weights generated and uploaded in %.1fs" % (time.time() - t0), file=sys.stderr, flush=True)
+    d_x = torch.from_numpy(x).to(dev)
+    d_logits = torch.empty((t, W.HEAD_ROWS), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream()
+    sample = args.op == "head_sample"
+    if sample:
+        # The verify batch's settings (penalty 1.3 over 64-id windows, T 0.6,
+        # top-k 20, top-p 0.95), one stream of uniforms in row order.
+        settings = [R.sampling(0.6, 20, 0.95, 0.0, 1.3, 64, 0) for _ in range(t)]
+        g = np.random.default_rng(5)
+        d_win = torch.from_numpy(g.integers(0, W.HEAD_ROWS, (t, W.WINDOW)).astype(np.int32)).to(dev)
+        d_wlen = torch.full((t,), W.WINDOW, dtype=torch.int32, device=dev)
+        d_uni = torch.from_numpy(g.random(t).astype(np.float32)).to(dev)
+        ctx = R.DeviceSampler(t, W.HEAD_ROWS, max_window=W.WINDOW)
+        ctx.configure(settings)
+        cs = ctx.required_cand_stride()
+        out_tok = torch.empty(t, dtype=torch.int32, device=dev)
+        out_kept = torch.empty(t, dtype=torch.int32, device=dev)
+        out_used = torch.empty(t, dtype=torch.uint8, device=dev)
+        out_ids = torch.empty((t, cs), dtype=torch.int32, device=dev)
+        out_probs = torch.empty((t, cs), dtype=torch.float32, device=dev)
+
+    def step():
+        head.logits_into(d_x, d_logits, stream=stream.cuda_stream)
+        if sample:
+            ctx.sample_rows(d_logits, t, d_logits.stride(0), out_tok, out_kept, out_used, windows=d_win,
+                            window_stride=W.WINDOW, window_len=d_wlen, uniforms=d_uni, out_ids=out_ids,
+                            out_probs=out_probs, cand_stride=cs, stream=stream.cuda_stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    t_wall = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    per_call_ms = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    mean_ms = sum(per_call_ms) / len(per_call_ms)
+    median_ms = per_call_ms[len(per_call_ms) // 2]
+    ms_per_step = wall * 1e3 / args.steps
+    weight_bytes = W.HEAD_ROWS * (-(-W.HEAD_K // 256)) * W.Q6K_BLOCK_BYTES
+    # Weights once, the hidden rows, the logits written; sampling re-reads the
+    # logits and writes (token, kept, used, 20 candidates) per row.
+    alg_bytes = weight_bytes + t * W.HEAD_K * 4 + t * W.HEAD_ROWS * 4
+    if sample:
+        alg_bytes += t * (W.HEAD_ROWS * 4 + W.WINDOW * 4 + 4 + 4 + 4 + 1 + 20 * 8)
+    achieved = alg_bytes / (mean_ms / 1e3) / 1e9
+    print("[bench] head t=%d%s: wall %.3f ms/step, events mean %.3f median %.3f min %.3f max %.3f ms" % (
+        t, " + sample" if sample else "", ms_per_step, mean_ms, median_ms, per_call_ms[0], per_call_ms[-1]),
+        file=sys.stderr, flush=True)
+    cpu = None
+    if args.cpu_seconds > 0:
+        rate, n, el = head_cpu_baseline(w, x, args.cpu_seconds)
+        cpu = {"value": round(rate, 4), "unit": "head calls/s", "cores": 1, "kind": "port",
+               "sample": "%d vocabulary rows x %d activation rows through the oracle's scalar Q6_K head on "
+                         "one host core in %.1f s, scaled to full-vocabulary calls" % (n, t, el)}
+        print("[bench] cpu baseline %.4f head calls/s" % rate, file=sys.stderr, flush=True)
+    line = {
+        "metric": "head calls/s + achieved HBM GB/s, Q6_K [%d, %d] output head, %d activation row%s%s" % (
+            W.HEAD_K, W.HEAD_ROWS, t, "" if t == 1 else "s", ", then sampling" if sample else ""),
+        "value": round(1e3 / ms_per_step, 2),
+        "unit": "head calls/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q6_k x int8 (exact integer sums, f32 scaling)",
+        "data": "synthetic (seeded Q6_K weights and hidden rows, rust-llm_amd/workloads.py)",
+        "config": {"workload": "head: token_embd [%d, %d] Q6_K, %d rows" % (W.HEAD_K, W.HEAD_ROWS, t),
+                   "rows": t, "vocab": W.HEAD_ROWS, "k": W.HEAD_K, "sampling": sample},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_call": alg_bytes,
+            "call_ms_mean": round(mean_ms, 5),
+            "call_ms_median": round(median_ms, 5),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -90,6 +228,9 @@ def main():
               "independent, so a multi-GPU run is not part of this build (asked for --gpus %d)" % args.gpus,
               file=sys.stderr)
         sys.exit(2)
+    if args.op in ("head", "head_sample"):
+        bench_head(args)
+        return
     import numpy as np
     import torch
 

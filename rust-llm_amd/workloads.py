@@ -144,3 +144,27 @@ WORKLOADS = {
 }
 
 BENCH_WORKLOAD = "spikes"
+
+
+# The output head's workload: the tied embedding token_embd [2560, 248320]
+# Q6_K of the reference's model (docs/models.md:107) with synthetic weights.
+HEAD_K = 2560
+HEAD_ROWS = V2
+Q6K_BLOCK_BYTES = 210
+
+
+def head_weights(seed=0x7E4D, rows=HEAD_ROWS, k=HEAD_K):
+    """A Q6_K tensor of `rows` rows of `k` values as the GGUF stores it: random
+    quant and scale bytes (every bit pattern is a valid block) and block scales
+    d uniform in [-0.01, 0.01) as f16, drawn from numpy's PCG64 with `seed`."""
+    nb = -(-k // 256)
+    g = np.random.default_rng(seed)
+    w = g.integers(0, 256, size=(rows * nb, Q6K_BLOCK_BYTES), dtype=np.uint8)
+    d = (g.random(rows * nb, dtype=np.float32) * 2 - 1) * np.float32(0.01)
+    w[:, 208:210] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    return w.reshape(-1)
+
+
+def head_inputs(t, seed=0x4EAD, k=HEAD_K):
+    """t normed hidden rows, N(0, 1.5^2) f32."""
+    return (np.random.default_rng(seed).standard_normal((t, k)) * 1.5).astype(np.float32)
