@@ -22,30 +22,34 @@ struct rl_head {
     uint16_t *wd = nullptr;
     int8_t *aq = nullptr;   // activation quants [tcap][nb][256]
     float *ad = nullptr;    // activation scales [tcap][nb]
-    uint32_t *dq = nullptr; // the quants with bytes 1 and 2 of each word swapped [tcap][nb][64]
-    int32_t *dc = nullptr;  // -32 * bsum per sub-block [tcap][nb][16]
     ~rl_head() {
         (void)hipFree(wq);
         (void)hipFree(ws);
         (void)hipFree(wd);
         (void)hipFree(aq);
         (void)hipFree(ad);
-        (void)hipFree(dq);
-        (void)hipFree(dc);
     }
 };
 
 namespace {
 
+// LDS the dot path's own quantization takes for `t` rows of `nb` blocks.
+size_t dot_lds_bytes(uint32_t t, uint32_t nb) { return (size_t)t * nb * DOT_ACT_WORDS * 4; }
+constexpr size_t DOT_LDS_MAX = 48 * 1024;
+
+// Whether rows t0 .. t0 + n take the dot path (which quantizes them itself).
+bool dot_path(const rl_head *h, uint32_t n) { return n <= 2 && dot_lds_bytes(n, h->nb) <= DOT_LDS_MAX; }
+
 // Rows t0 .. t0 + n of the batch, n <= 32: the dot path for one or two rows
 // (memory-bound, least arithmetic per weight), the matrix cores for more.
-void launch_head(const rl_head *h, uint32_t t0, uint32_t n, float *out, uint64_t stride, hipStream_t s) {
+void launch_head(const rl_head *h, const float *x, uint32_t t0, uint32_t n, float *out, uint64_t stride,
+                 hipStream_t s) {
     const uint32_t blocks = (h->groups + HEAD_WAVES - 1) / HEAD_WAVES;
     const uint64_t ao = (uint64_t)t0 * h->nb;
-    if (n <= 2) {
+    if (dot_path(h, n)) {
         auto kern = n == 1 ? k_head_dot<1> : k_head_dot<2>;
-        hipLaunchKernelGGL(kern, dim3(blocks), dim3(HEAD_THREADS), 0, s, h->wq, h->ws, h->wd, h->dq + ao * 64,
-                           h->dc + ao * 16, h->ad + ao, n, h->nb, h->rows, h->groups, out, stride);
+        hipLaunchKernelGGL(kern, dim3(blocks), dim3(HEAD_THREADS), dot_lds_bytes(n, h->nb), s, h->wq, h->ws,
+                           h->wd, x + (uint64_t)t0 * h->k, h->k, h->nb, h->rows, h->groups, out, stride);
     } else if (n <= HEAD_NTILE) {
         hipLaunchKernelGGL(k_head_mfma_regs<1>, dim3(blocks), dim3(HEAD_THREADS), 0, s, h->wq, h->ws, h->wd,
                            h->aq + ao * QK, h->ad + ao, n, h->nb, h->rows, h->groups, out, stride);
@@ -56,10 +60,10 @@ void launch_head(const rl_head *h, uint32_t t0, uint32_t n, float *out, uint64_t
 }
 
 void launch_quantize(const float *x, uint32_t t, uint32_t k, uint32_t nb, float *d, int8_t *qs, int16_t *bs,
-                     uint32_t *dq, int32_t *dc, hipStream_t s) {
+                     hipStream_t s) {
     const uint64_t waves = (uint64_t)t * nb;
     const uint32_t blocks = (uint32_t)((waves + 3) / 4);
-    hipLaunchKernelGGL(k_quantize_rows, dim3(blocks), dim3(256), 0, s, x, t, k, nb, d, qs, bs, dq, dc);
+    hipLaunchKernelGGL(k_quantize_rows, dim3(blocks), dim3(256), 0, s, x, t, k, nb, d, qs, bs);
 }
 
 }  // namespace
@@ -92,8 +96,6 @@ int rl_head_create(int device, uint32_t k, uint32_t rows, uint32_t max_batch, co
     if (e == hipSuccess) e = hipMalloc(&h->wd, bgt * HEAD_TILE * sizeof(uint16_t));
     if (e == hipSuccess) e = hipMalloc(&h->aq, (uint64_t)h->tcap * nb * QK);
     if (e == hipSuccess) e = hipMalloc(&h->ad, (uint64_t)h->tcap * nb * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc(&h->dq, (uint64_t)h->tcap * nb * QK);
-    if (e == hipSuccess) e = hipMalloc(&h->dc, (uint64_t)h->tcap * nb * 16 * sizeof(int32_t));
     // Rows of a column tile past a call's t are read and their products
     // discarded; start them at zero.
     if (e == hipSuccess) e = hipMemset(h->aq, 0, (uint64_t)h->tcap * nb * QK);
@@ -132,10 +134,11 @@ int rl_head_logits(rl_head *h, const float *x, uint32_t t, float *logits, uint64
     DeviceGuard g(h->device);
     if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select the head's device");
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    launch_quantize(x, t, h->k, h->nb, h->ad, h->aq, nullptr, h->dq, h->dc, s);
     const uint32_t per_pass = HEAD_MAX_NT * HEAD_NTILE;
+    // The matrix-core passes read the quantized rows; the dot path quantizes its own.
+    if (!dot_path(h, t)) launch_quantize(x, t, h->k, h->nb, h->ad, h->aq, nullptr, s);
     for (uint32_t t0 = 0; t0 < t; t0 += per_pass)
-        launch_head(h, t0, std::min(per_pass, t - t0), logits + (uint64_t)t0 * row_stride, row_stride, s);
+        launch_head(h, x, t0, std::min(per_pass, t - t0), logits + (uint64_t)t0 * row_stride, row_stride, s);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? RL_OK : hip_fail(e, "rl_head_logits launch");
 }
@@ -145,7 +148,7 @@ int rl_quantize_rows(const float *x, uint32_t t, uint32_t k, float *out_d, int8_
     if (t == 0) return RL_OK;
     if (!x || k == 0) return fail(RL_ERR_ARGUMENT, "x must be a device pointer and k positive");
     const uint32_t nb = (k + QK - 1) / QK;
-    launch_quantize(x, t, k, nb, out_d, out_qs, out_bsums, nullptr, nullptr, static_cast<hipStream_t>(stream));
+    launch_quantize(x, t, k, nb, out_d, out_qs, out_bsums, static_cast<hipStream_t>(stream));
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? RL_OK : hip_fail(e, "rl_quantize_rows launch");
 }

@@ -129,50 +129,55 @@ __device__ inline int quant_one(float v, float id) {
     return c == c ? (int)c : 0;
 }
 
-// Activations::quantize_batch (quant.rs:337-375). One wave per (row, block);
-// lane l holds values 4l..4l+3 of the block (zero past k, which the reference
-// leaves out of the maximum and quantizes to 0). The maximum is order-free
-// (f32::max ignores NaN; fmaxf does too), so a wave reduction gives the
-// reference's amax. Writes the reference's ActBlock fields; each output may be
-// null.
-//
-// For the head's dot path it can also write `dot_qs` (the quants with bytes 1
-// and 2 of every word swapped, the byte order the unpacked weights come out in)
-// and `dot_c` (-32 * bsum per sub-block, i32: the start of each sub-block's dot
-// product with unsigned 6-bit weights).
-__global__ __launch_bounds__(256) void k_quantize_rows(const float *__restrict__ x, uint32_t t, uint32_t k,
-                                                       uint32_t nb, float *__restrict__ out_d,
-                                                       int8_t *__restrict__ out_qs,
-                                                       int16_t *__restrict__ out_bsums,
-                                                       uint32_t *__restrict__ dot_qs, int32_t *__restrict__ dot_c) {
-    const uint32_t wave = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
-    const uint32_t lane = threadIdx.x & 63;
-    if (wave >= t * nb) return;
-    const uint32_t tt = wave / nb, ib = wave % nb;
-    const float *src = x + (uint64_t)tt * k + (uint64_t)ib * QK;
-    const uint32_t base = ib * QK + 4 * lane;
+// One activation block quantized by one wave (quant.rs:360-374): lane l holds
+// values 4l..4l+3 (zero past `valid`, which the reference leaves out of the
+// maximum and quantizes to 0). The maximum is order-free (f32::max ignores
+// NaN; fmaxf does too), so a wave reduction gives the reference's amax.
+// Returns the block scale, the lane's four quants packed little-endian, and
+// the sum of the 16 quants of the lane's sub-block (in every lane of it).
+__device__ inline float quantize_block_wave(const float *__restrict__ src, uint32_t valid, uint32_t lane,
+                                            uint32_t &packed, int &bsum) {
     float v[4];
-    for (int e = 0; e < 4; ++e) v[e] = base + e < k ? src[4 * lane + e] : 0.0f;
+    for (int e = 0; e < 4; ++e) v[e] = 4 * lane + e < valid ? src[4 * lane + e] : 0.0f;
     float amax = 0.0f;
     for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(v[e]));
     for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
     const float d = amax / 127.0f;
     const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
     int q[4];
-    uint32_t packed = 0;
+    packed = 0;
     for (int e = 0; e < 4; ++e) {
         q[e] = quant_one(v[e], id);
         packed |= ((uint32_t)q[e] & 0xFF) << (8 * e);
     }
-    int bsum = q[0] + q[1] + q[2] + q[3];
+    bsum = q[0] + q[1] + q[2] + q[3];
     bsum += __shfl_xor(bsum, 1);
     bsum += __shfl_xor(bsum, 2);
+    return d;
+}
+
+// The dot path's byte order: bytes 1 and 2 of every word swapped, the order
+// the unpacked weights come out in.
+__device__ inline uint32_t dot_order(uint32_t packed) { return __builtin_amdgcn_perm(packed, packed, 0x03010200u); }
+
+// Activations::quantize_batch (quant.rs:337-375). One wave per (row, block).
+// Writes the reference's ActBlock fields; each output may be null.
+__global__ __launch_bounds__(256) void k_quantize_rows(const float *__restrict__ x, uint32_t t, uint32_t k,
+                                                       uint32_t nb, float *__restrict__ out_d,
+                                                       int8_t *__restrict__ out_qs,
+                                                       int16_t *__restrict__ out_bsums) {
+    const uint32_t wave = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    const uint32_t lane = threadIdx.x & 63;
+    if (wave >= t * nb) return;
+    const uint32_t tt = wave / nb, ib = wave % nb;
+    const uint32_t valid = k - ib * QK < QK ? k - ib * QK : QK;
+    uint32_t packed;
+    int bsum;
+    const float d = quantize_block_wave(x + (uint64_t)tt * k + (uint64_t)ib * QK, valid, lane, packed, bsum);
     const uint64_t blk = (uint64_t)tt * nb + ib;
     if (out_qs) reinterpret_cast<uint32_t *>(out_qs + blk * QK)[lane] = packed;
     if (out_bsums && (lane & 3) == 0) out_bsums[blk * 16 + lane / 4] = (int16_t)bsum;
     if (out_d && lane == 0) out_d[blk] = d;
-    if (dot_qs) dot_qs[blk * 64 + lane] = __builtin_amdgcn_perm(packed, packed, 0x03010200u);
-    if (dot_c && (lane & 3) == 0) dot_c[blk * 16 + lane / 4] = -32 * bsum;
 }
 
 // ------------------------------------------------------------------- head
@@ -531,25 +536,48 @@ void k_head_mfma_regs(const uint4 *__restrict__ wq,
 }
 
 // The dot path, for one or two activation rows: v_dot4_i32_i8 on the same
-// layout. Lane (m, h) unpacks its quarter-block to bytes (unsigned 6-bit
-// weights, which are valid signed bytes) in the order [v0 v2 v1 v3] per word,
-// dots them with the activation words stored in that order (bytes 1 and 2
-// swapped) starting from -32 * bsum of the sub-block, scales by the sub-block
-// scale, and the four lanes of a row add their exact partial sums with two
-// lane shuffles. Then the reference's f32 line; lane (m, h) stores activation
-// row h.
+// layout, with the activation rows quantized by the workgroup itself into LDS
+// (the same arithmetic as k_quantize_rows). Lane (m, h) unpacks its
+// quarter-block to bytes (unsigned 6-bit weights, which are valid signed
+// bytes) in the order [v0 v2 v1 v3] per word, dots them with the activation
+// words in that order starting from -32 * bsum of the sub-block, scales by the
+// sub-block scale, and the four lanes of a row add their exact partial sums
+// with two lane shuffles. Then the reference's f32 line; lane (m, h) stores
+// activation row h. LDS per activation block: 64 words of quants, 16 words of
+// -32 * bsum, the f32 scale, 3 words of padding.
+constexpr int DOT_ACT_WORDS = 84;
+
 template <int T>
 __global__ __launch_bounds__(HEAD_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
 void k_head_dot(const uint4 *__restrict__ wq, const uint32_t *__restrict__ ws, const uint16_t *__restrict__ wd,
-                const uint32_t *__restrict__ dq, const int32_t *__restrict__ dc, const float *__restrict__ ad,
-                uint32_t t, uint32_t nb, uint32_t rows, uint32_t groups, float *__restrict__ out,
-                uint64_t out_stride) {
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t g = __builtin_amdgcn_readfirstlane(blockIdx.x * HEAD_WAVES + threadIdx.x / 64);
-    if (g >= groups) return;
+                const float *__restrict__ x, uint32_t k, uint32_t nb, uint32_t rows, uint32_t groups,
+                float *__restrict__ out, uint64_t out_stride) {
+    extern __shared__ uint4 sact4[];
+    uint32_t *sact = reinterpret_cast<uint32_t *>(sact4);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x / 64;
+    const uint32_t g = __builtin_amdgcn_readfirstlane(blockIdx.x * HEAD_WAVES + wave);
+    const uint32_t gg = g < groups ? g : groups - 1;
     const uint32_t m = lane & 15, h = lane >> 4;
     const uint32_t M6 = 0x003F003Fu, M6S = 0x3F003F00u, M4 = 0x000F000Fu, M2 = 0x00300030u, M4S = 0x0F000F00u,
                    M2S = 0x30003000u;
+
+    // The first tile's weights are in flight while the activations are quantized.
+    const uint64_t tile0 = (uint64_t)gg * HEAD_TILES;
+    HeadTile cur = load_tile(wq, ws, wd, tile0, lane, h);
+    uint16_t curd = wd[tile0 * HEAD_TILE + m];
+    for (uint32_t w = wave; w < T * nb; w += HEAD_WAVES) {
+        const uint32_t tt = w / nb, ib = w % nb;
+        const uint32_t valid = k - ib * QK < QK ? k - ib * QK : QK;
+        uint32_t packed;
+        int bsum;
+        const float d = quantize_block_wave(x + (uint64_t)tt * k + (uint64_t)ib * QK, valid, lane, packed, bsum);
+        uint32_t *a = sact + (uint64_t)w * DOT_ACT_WORDS;
+        a[lane] = dot_order(packed);
+        if ((lane & 3) == 0) a[64 + lane / 4] = (uint32_t)(-32 * bsum);
+        if (lane == 0) a[80] = __float_as_uint(d);
+    }
+    __syncthreads();
+    if (g >= groups) return;
 
     float sum[HEAD_TILES][T];
 #pragma unroll
@@ -557,9 +585,6 @@ void k_head_dot(const uint4 *__restrict__ wq, const uint32_t *__restrict__ ws, c
 #pragma unroll
         for (int tt = 0; tt < T; ++tt) sum[tw][tt] = 0.0f;
 
-    const uint64_t tile0 = (uint64_t)g * HEAD_TILES;
-    HeadTile cur = load_tile(wq, ws, wd, tile0, lane, h);
-    uint16_t curd = wd[tile0 * HEAD_TILE + m];
     for (uint32_t ib = 0; ib < nb; ++ib) {
         const uint32_t nxt_ib = ib + 1 < nb ? ib + 1 : ib;  // past the end: re-read (a cache hit)
         uint4 a[T][4];
@@ -567,12 +592,11 @@ void k_head_dot(const uint4 *__restrict__ wq, const uint32_t *__restrict__ ws, c
         float adv[T];
 #pragma unroll
         for (int tt = 0; tt < T; ++tt) {
-            const uint64_t blk = (uint64_t)(tt < (int)t ? tt : 0) * nb + ib;
-            const uint4 *ap = reinterpret_cast<const uint4 *>(dq + blk * 64 + 16 * h);
+            const uint32_t *ab = sact + ((uint64_t)tt * nb + ib) * DOT_ACT_WORDS;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) a[tt][c] = ap[c];
-            cv[tt] = reinterpret_cast<const uint4 *>(dc + blk * 16)[h];
-            adv[tt] = ad[blk];
+            for (int c = 0; c < 4; ++c) a[tt][c] = reinterpret_cast<const uint4 *>(ab + 16 * h)[c];
+            cv[tt] = reinterpret_cast<const uint4 *>(ab + 64)[h];
+            adv[tt] = __uint_as_float(ab[80]);
         }
 #pragma unroll
         for (int tw = 0; tw < HEAD_TILES; ++tw) {
@@ -597,12 +621,12 @@ void k_head_dot(const uint4 *__restrict__ wq, const uint32_t *__restrict__ ws, c
                 for (int tt = 0; tt < T; ++tt) {
                     const uint32_t av[4] = {a[tt][p].x, a[tt][p].y, a[tt][p].z, a[tt][p].w};
                     const uint32_t cw[4] = {cv[tt].x, cv[tt].y, cv[tt].z, cv[tt].w};
-                    int d = (int)cw[p];
-                    d = __builtin_amdgcn_sdot4((int)b0, (int)av[0], d, false);
-                    d = __builtin_amdgcn_sdot4((int)b1, (int)av[1], d, false);
-                    d = __builtin_amdgcn_sdot4((int)b2, (int)av[2], d, false);
-                    d = __builtin_amdgcn_sdot4((int)b3, (int)av[3], d, false);
-                    isum[tt] += sj * fits24(d);
+                    int dsum = (int)cw[p];
+                    dsum = __builtin_amdgcn_sdot4((int)b0, (int)av[0], dsum, false);
+                    dsum = __builtin_amdgcn_sdot4((int)b1, (int)av[1], dsum, false);
+                    dsum = __builtin_amdgcn_sdot4((int)b2, (int)av[2], dsum, false);
+                    dsum = __builtin_amdgcn_sdot4((int)b3, (int)av[3], dsum, false);
+                    isum[tt] += sj * fits24(dsum);
                 }
             }
             const float dw = __half2float(__ushort_as_half(curd));
@@ -620,7 +644,7 @@ void k_head_dot(const uint4 *__restrict__ wq, const uint32_t *__restrict__ ws, c
     }
 #pragma unroll
     for (int tt = 0; tt < T; ++tt) {
-        if (tt >= (int)t || h != (uint32_t)tt) continue;
+        if (h != (uint32_t)tt) continue;
 #pragma unroll
         for (int tw = 0; tw < HEAD_TILES; ++tw) {
             const uint32_t row = g * HEAD_GROUP + tw * HEAD_TILE + m;
