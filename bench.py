@@ -182,6 +182,15 @@ def bench_head(args):
     print("[bench] head t=%d%s: wall %.3f ms/step, events mean %.3f median %.3f min %.3f max %.3f ms" % (
         t, " + sample" if sample else "", ms_per_step, mean_ms, median_ms, per_call_ms[0], per_call_ms[-1]),
         file=sys.stderr, flush=True)
+    if args.calibration_copy > 0:
+        src = torch.zeros(weight_bytes // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.calibration_copy):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print("[bench] calibration: %d copies of %d bytes" % (args.calibration_copy, weight_bytes),
+              file=sys.stderr, flush=True)
+        del src, dst
     cpu = None
     if args.cpu_seconds > 0:
         rate, n, el = head_cpu_baseline(w, x, args.cpu_seconds)
@@ -211,7 +220,7 @@ def bench_head(args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": None if sample else traffic_bytes("head_t%d" % t),
             "algorithmic_bytes_per_call": alg_bytes,
             "call_ms_mean": round(mean_ms, 5),
             "call_ms_median": round(median_ms, 5),
