@@ -51,6 +51,7 @@ struct rl_sampler_ctx {
     uint32_t *d_stream_rows = nullptr, *d_full_rows = nullptr;
     uint64_t *d_chunk_cands = nullptr;
     uint32_t *d_chunk_counts = nullptr;
+    uint32_t *d_arrive = nullptr;
     uint32_t *d_keyA = nullptr, *d_idA = nullptr, *d_keyB = nullptr, *d_idB = nullptr;
     float *d_probs = nullptr;
     float *d_part_max = nullptr;
@@ -118,6 +119,9 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     // chunks <= ceil(TARGET_WGS / rows), so rows * chunks < 2 * TARGET_WGS.
     if (e == hipSuccess) e = c->alloc(&c->d_chunk_cands, (size_t)CHUNK_SLOTS * KMAX);
     if (e == hipSuccess) e = c->alloc(&c->d_chunk_counts, (size_t)CHUNK_SLOTS);
+    if (e == hipSuccess) e = c->alloc(&c->d_arrive, (size_t)max_rows);
+    // Arrival counters return to zero at the end of every call.
+    if (e == hipSuccess) e = hipMemset(c->d_arrive, 0, (size_t)max_rows * sizeof(uint32_t));
     if (e == hipSuccess) e = c->alloc(&c->d_keyA, fg * V);
     if (e == hipSuccess) e = c->alloc(&c->d_idA, fg * V);
     if (e == hipSuccess) e = c->alloc(&c->d_keyB, fg * V);
@@ -247,15 +251,13 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
         chunks = std::min(chunks, MAX_CHUNKS);
         chunks = std::min(chunks, std::max(1u, n4 / (FAST_THREADS * UNROLL)));
         s.chunks = std::max(chunks, 1u);
-        FastScratch sc{ctx->d_chunk_cands, ctx->d_chunk_counts};
+        FastScratch sc{ctx->d_chunk_cands, ctx->d_chunk_counts, ctx->d_arrive};
         const size_t lds = window_lds_bytes(ctx->hash_bits);
         dim3 grid(s.chunks, ns);
         if (vec)
             hipLaunchKernelGGL(k_stream<true>, grid, dim3(FAST_THREADS), lds, st, s, sc);
         else
             hipLaunchKernelGGL(k_stream<false>, grid, dim3(FAST_THREADS), lds, st, s, sc);
-        if (s.chunks > 1)
-            hipLaunchKernelGGL(k_stream_finalize, dim3(ns), dim3(WAVE), window_lds_bytes(ctx->hash_bits), st, s, sc);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return hip_fail(e, "stream kernels");
     }

@@ -51,6 +51,7 @@ struct RowIO {
 struct FastScratch {
     uint64_t *chunk_cands;   // [slot][chunk][KMAX]
     uint32_t *chunk_counts;  // [slot][chunk]
+    uint32_t *arrive;        // [slot]: chunks of the row done; zero between calls
 };
 
 __device__ __forceinline__ uint32_t window_len(const RowIO &a, uint32_t row) {
@@ -433,7 +434,8 @@ __device__ __forceinline__ uint64_t ascending_from(const uint64_t *list, uint32_
 }
 
 // grid (chunks, rows on this path), FAST_THREADS threads. Dynamic LDS: the
-// window set.
+// window set. A row split into chunks is finished by whichever of its chunks
+// publishes its list last (a per-row arrival counter), so no second launch.
 template <bool VEC>
 __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc) {
     __shared__ uint64_t s_buf[FAST_WAVES * CBUF];
@@ -538,53 +540,78 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
     compact(w);
     if (lane == 0) s_cnt[wave] = w.cnt;
     __syncthreads();
-    if (wave != 0) return;
-    // Merge the four sorted lists: lane i of list j is candidate i of wave j.
-    const uint64_t *lb = (const uint64_t *)s_buf;
-    uint64_t top = lane < s_cnt[0] ? lb[lane] : 0ull;
-    uint32_t total = s_cnt[0];
+    __shared__ uint32_t s_last;
+    if (wave == 0) {
+        // Merge the four sorted lists: lane i of list j is candidate i of wave j.
+        const uint64_t *lb = (const uint64_t *)s_buf;
+        uint64_t top = lane < s_cnt[0] ? lb[lane] : 0ull;
+        uint32_t total = s_cnt[0];
 #pragma unroll
-    for (uint32_t j = 1; j < FAST_WAVES; ++j) {
-        top = wave_merge64(top, ascending_from(lb + j * CBUF, s_cnt[j]));
-        total += s_cnt[j];
+        for (uint32_t j = 1; j < FAST_WAVES; ++j) {
+            top = wave_merge64(top, ascending_from(lb + j * CBUF, s_cnt[j]));
+            total += s_cnt[j];
+        }
+        // The window's ids with their penalised values, once per row.
+        if (pen && chunk == 0)
+            total += merge_window(top, ws, s.repeat_penalty, greedy, total >= k ? read_lane_u64(top, k - 1) : 0ull);
+        const uint32_t nL = total < k ? total : k;
+        if (lane >= nL) top = 0;
+        if (a.chunks == 1) {
+            finalize_row(a, row, s, k, top, nL, ws, pen, rowp);
+        } else {
+            // Publish this chunk's list; the row's last chunk to arrive finishes it.
+            uint64_t *dst = sc.chunk_cands + ((uint64_t)slot * a.chunks + chunk) * KMAX;
+            if (lane < nL) dst[lane] = top;
+            if (lane == 0) sc.chunk_counts[slot * a.chunks + chunk] = nL;
+            __threadfence();  // release: the list before the arrival
+            uint32_t old = 0;
+            if (lane == 0) old = atomicAdd(&sc.arrive[slot], 1u);
+            old = read_lane_u32(old, 0);
+            if (lane == 0) s_last = old == a.chunks - 1 ? 1u : 0u;
+        }
     }
-    // The window's ids with their penalised values, once per row.
-    if (pen && chunk == 0)
-        total += merge_window(top, ws, s.repeat_penalty, greedy, total >= k ? read_lane_u64(top, k - 1) : 0ull);
-    const uint32_t nL = total < k ? total : k;
-    if (lane >= nL) top = 0;
-    if (a.chunks == 1) {
-        finalize_row(a, row, s, k, top, nL, ws, pen, rowp);
-    } else {
-        uint64_t *dst = sc.chunk_cands + ((uint64_t)slot * a.chunks + chunk) * KMAX;
-        if (lane < nL) dst[lane] = top;
-        if (lane == 0) sc.chunk_counts[slot * a.chunks + chunk] = nL;
-    }
-}
-
-// grid (rows on this path), one wave: merges the chunks' lists and finishes.
-__global__ __launch_bounds__(WAVE) void k_stream_finalize(RowIO a, FastScratch sc) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const WindowSet ws = window_set(smem, a.hash_bits);
-    const uint32_t slot = blockIdx.x;
-    const uint32_t row = a.rows[slot];
-    const rl_sampling s = a.settings[row];
-    const bool greedy = s.temperature <= 0.0f;
-    const uint32_t k = greedy ? 1u : (uint32_t)s.top_k;
-    const uint32_t wl = window_len(a, row);
-    const bool pen = penalises(s) && wl > 0;
-    const float *rowp = a.logits + (uint64_t)row * a.stride;
-    const uint32_t lane = lane_id();
-    window_build(ws, a.windows + (uint64_t)row * a.wstride, wl, a.vocab, rowp, pen);
+    if (a.chunks == 1) return;
+    __syncthreads();
+    if (!s_last) return;
+    // The last chunk of the row: every chunk's list is published. Each wave
+    // merges the lists j = wave (mod FAST_WAVES), all loaded at once, then wave
+    // 0 merges the four results and runs the tail.
+    __threadfence();  // acquire: the other chunks' lists after their arrivals
     const uint64_t *lists = sc.chunk_cands + (uint64_t)slot * a.chunks * KMAX;
     const uint32_t *counts = sc.chunk_counts + slot * a.chunks;
+    constexpr uint32_t PER = MAX_CHUNKS / FAST_WAVES;
+    uint64_t v[PER];
+    uint32_t n[PER];
+#pragma unroll
+    for (uint32_t i = 0; i < PER; ++i) {
+        const uint32_t j = wave + FAST_WAVES * i;
+        const bool ok = j < a.chunks;
+        n[i] = ok ? __hip_atomic_load(counts + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+        v[i] = ok ? __hip_atomic_load(lists + (uint64_t)j * KMAX + (WAVE - 1 - lane), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT)
+                  : 0ull;
+    }
     uint64_t top = 0;
     uint32_t total = 0;
-    for (uint32_t j = 0; j < a.chunks; ++j) {
-        const uint32_t n = counts[j];
-        top = wave_merge64(top, ascending_from(lists + (uint64_t)j * KMAX, n));
-        total += n;
+#pragma unroll
+    for (uint32_t i = 0; i < PER; ++i) {
+        if (wave + FAST_WAVES * i >= a.chunks) break;
+        top = wave_merge64(top, WAVE - 1 - lane < n[i] ? v[i] : 0ull);  // lane i: list[63 - i], ascending
+        total += n[i];
     }
+    uint64_t *part = (uint64_t *)s_buf;
+    __syncthreads();  // the candidate buffers are free
+    part[wave * WAVE + lane] = top;
+    if (lane == 0) s_cnt[wave] = total;
+    __syncthreads();
+    if (wave != 0) return;
+    total = s_cnt[0];
+#pragma unroll
+    for (uint32_t j = 1; j < FAST_WAVES; ++j) {
+        top = wave_merge64(top, part[j * WAVE + (WAVE - 1 - lane)]);
+        total += s_cnt[j];
+    }
+    if (lane == 0) sc.arrive[slot] = 0;  // ready for the next call
     const uint32_t nL = total < k ? total : k;
     if (lane >= nL) top = 0;
     finalize_row(a, row, s, k, top, nL, ws, pen, rowp);
