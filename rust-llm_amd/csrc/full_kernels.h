@@ -59,7 +59,7 @@ struct FullScratch {
     FullRow *row;                       // [slot]
 };
 
-constexpr uint32_t UN = 4;                 // elements per thread per step of the bulk loops
+constexpr uint32_t UN = 16;                // elements per thread per step of the bulk loops (loads in flight)
 constexpr uint32_t REPLAY_THREADS = 512;   // per-row kernels: 8 waves, up to 256 VGPRs each, no spills
 constexpr uint32_t REPLAY_WAVES = REPLAY_THREADS / WAVE;
 constexpr uint32_t SEQ_ITEMS = 8;          // terms per thread per tile of the sum replay
@@ -92,12 +92,19 @@ __device__ __forceinline__ int f32_exponent(float p) {
 // grid (chunks, slots), FULL_THREADS: the row's raw logits as total-order keys
 // in id order (the window ids' keys are rewritten by k_full_sort), and per
 // chunk the f32::max fold (NaN ignored) and the argmax composite over the ids
-// outside the window. A lane checks window membership only when an element
-// would raise its running maximum, so almost no element costs a lookup.
+// outside the window. Dynamic LDS: a bitmap of the chunk's window ids
+// (k_full_keys_lds_bytes).
+// LDS bytes of k_full_keys's bitmap: one bit per element of the largest chunk.
+__host__ __device__ inline size_t k_full_keys_lds_bytes(uint32_t vocab, uint32_t chunks) {
+    const uint32_t n4 = vocab / 4;
+    const uint32_t most = 4 * ((n4 + chunks - 1) / chunks) + 3;
+    return ((size_t)(most + 31) / 32) * 4;
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch f) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const WindowSet ws = window_set(smem, a.hash_bits);
+    RL_LDS uint32_t *bm = (RL_LDS uint32_t *)smem;  // window ids in this chunk, one bit per element
     __shared__ float red_max[FULL_THREADS / WAVE];
     __shared__ uint64_t red_am[FULL_THREADS / WAVE];
     const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
@@ -107,9 +114,25 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch
     const uint32_t wl = window_len(a, row);
     const bool pen = penalises(s) && wl > 0;
     const float *rowp = a.logits + (uint64_t)row * a.stride;
-    window_build(ws, a.windows + (uint64_t)row * a.wstride, wl, V, rowp, pen);
     const uint32_t n4 = V / 4;
     const uint32_t q0 = chunk_lo(n4, chunk, a.chunks), q1 = chunk_lo(n4, chunk + 1, a.chunks);
+    // The chunk's elements [e0, e1) (the last chunk also takes the vocab % 4
+    // tail). A bitmap of the window ids among them makes the membership test
+    // one LDS read with no probing loop: the test runs whenever a lane's
+    // running maximum rises, which on a random row is nearly every step for
+    // some lane of the wave.
+    const uint32_t e0 = 4 * q0, e1 = chunk == a.chunks - 1 ? V : 4 * q1;
+    const uint32_t nwords = (e1 - e0 + 31) / 32;
+    if (pen) {
+        for (uint32_t i = threadIdx.x; i < nwords; i += FULL_THREADS) bm[i] = 0;
+        __syncthreads();
+        const uint32_t *win = a.windows + (uint64_t)row * a.wstride;
+        for (uint32_t i = threadIdx.x; i < wl; i += FULL_THREADS) {
+            const uint32_t id = win[i];
+            if (id >= e0 && id < e1) atomicOr((uint32_t *)&bm[(id - e0) >> 5], 1u << ((id - e0) & 31));
+        }
+        __syncthreads();
+    }
     uint32_t *keys = f.keyA + (uint64_t)slot * V;
     uint32_t *ids = f.idA + (uint64_t)slot * V;
     const bool vstore = ((reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(ids)) & 15u) == 0;
@@ -118,29 +141,42 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch
     auto take = [&](float x, uint32_t id) {
         const uint64_t c = composite(argmax_key(x), id);
         const bool up_max = x > mx, up_am = c > am;
-        if ((up_max || up_am) && !(pen && window_contains(ws, id))) {
+        if ((up_max || up_am) && !(pen && ((bm[(id - e0) >> 5] >> ((id - e0) & 31)) & 1u))) {
             if (up_max) mx = x;
             if (up_am) am = c;
         }
     };
-    for (uint32_t q = q0 + threadIdx.x; q < q1; q += FULL_THREADS) {
-        const f32x4 v = load4<VEC>(rowp, q);
-        const float x[4] = {v.x, v.y, v.z, v.w};
-        uint32_t kk[4];
+    // Four 16-byte loads in flight per thread; indices past the chunk are
+    // clamped to its last element (a cache hit) and their results dropped.
+    constexpr uint32_t KU = 4;
+    for (uint32_t q = q0 + threadIdx.x; q < q1; q += FULL_THREADS * KU) {
+        f32x4 v[KU];
 #pragma unroll
-        for (uint32_t c = 0; c < 4; ++c) {
-            kk[c] = total_key(x[c]);
-            take(x[c], 4 * q + c);
+        for (uint32_t u = 0; u < KU; ++u) {
+            const uint32_t qq = q + u * FULL_THREADS;
+            v[u] = load4<VEC>(rowp, qq < q1 ? qq : q1 - 1);
         }
-        if (vstore) {
-            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-            *(RL_GLB u32x4 *)(keys + 4 * q) = u32x4{kk[0], kk[1], kk[2], kk[3]};
-            *(RL_GLB u32x4 *)(ids + 4 * q) = u32x4{4 * q, 4 * q + 1, 4 * q + 2, 4 * q + 3};
-        } else {
+#pragma unroll
+        for (uint32_t u = 0; u < KU; ++u) {
+            const uint32_t qq = q + u * FULL_THREADS;
+            if (qq >= q1) break;
+            const float x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+            uint32_t kk[4];
 #pragma unroll
             for (uint32_t c = 0; c < 4; ++c) {
-                keys[4 * q + c] = kk[c];
-                ids[4 * q + c] = 4 * q + c;
+                kk[c] = total_key(x[c]);
+                take(x[c], 4 * qq + c);
+            }
+            if (vstore) {
+                typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+                *(RL_GLB u32x4 *)(keys + 4 * qq) = u32x4{kk[0], kk[1], kk[2], kk[3]};
+                *(RL_GLB u32x4 *)(ids + 4 * qq) = u32x4{4 * qq, 4 * qq + 1, 4 * qq + 2, 4 * qq + 3};
+            } else {
+#pragma unroll
+                for (uint32_t c = 0; c < 4; ++c) {
+                    keys[4 * qq + c] = kk[c];
+                    ids[4 * qq + c] = 4 * qq + c;
+                }
             }
         }
     }
@@ -524,7 +560,7 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_collect(RowIO a, FullScra
 #pragma unroll
         for (uint32_t u = 0; u < UN; ++u) {
             const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
-            kk[u] = j < j1 ? ((const RL_GLB uint32_t *)keys)[j] : 0u;
+            kk[u] = ((const RL_GLB uint32_t *)keys)[j < j1 ? j : j1 - 1];  // clamped: no branch around the load
         }
 #pragma unroll
         for (uint32_t u = 0; u < UN; ++u) {
@@ -719,7 +755,7 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_probs(RowIO a, FullScratc
 #pragma unroll
         for (uint32_t u = 0; u < UN; ++u) {
             const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
-            kk[u] = j < j1 ? ((const RL_GLB uint32_t *)keys)[j] : 0u;
+            kk[u] = ((const RL_GLB uint32_t *)keys)[j < j1 ? j : j1 - 1];  // clamped: no branch around the load
         }
 #pragma unroll
         for (uint32_t u = 0; u < UN; ++u) {
@@ -1119,8 +1155,9 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_norm(RowIO a, FullScratch
 #pragma unroll
         for (uint32_t u = 0; u < UN; ++u) {
             const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
-            pp[u] = j < j1 ? ((const RL_GLB float *)probs)[j] : 0.0f;
-            iv[u] = (j < j1 && a.out_ids) ? ((const RL_GLB uint32_t *)ids)[j] : 0u;
+            const uint32_t jc = j < j1 ? j : j1 - 1;  // clamped: no branch around the loads
+            pp[u] = ((const RL_GLB float *)probs)[jc];
+            iv[u] = ((const RL_GLB uint32_t *)ids)[jc];
         }
 #pragma unroll
         for (uint32_t u = 0; u < UN; ++u) {

@@ -271,12 +271,11 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
                        ctx->d_part_max, ctx->d_part_am,  ctx->d_psum,       ctx->d_pemin, ctx->d_pcount,
                        ctx->d_pbad,     ctx->d_plast_in, ctx->d_pfirst_out, ctx->d_surv,  ctx->d_full_row};
         const dim3 cgrid(f.chunks, ng);
+        const size_t keys_lds = k_full_keys_lds_bytes(vocab, f.chunks);
         if (vec)
-            hipLaunchKernelGGL(k_full_keys<true>, cgrid, dim3(FULL_THREADS), window_lds_bytes(ctx->hash_bits), st,
-                               f, fs);
+            hipLaunchKernelGGL(k_full_keys<true>, cgrid, dim3(FULL_THREADS), keys_lds, st, f, fs);
         else
-            hipLaunchKernelGGL(k_full_keys<false>, cgrid, dim3(FULL_THREADS), window_lds_bytes(ctx->hash_bits), st,
-                               f, fs);
+            hipLaunchKernelGGL(k_full_keys<false>, cgrid, dim3(FULL_THREADS), keys_lds, st, f, fs);
         hipLaunchKernelGGL(k_full_prep, dim3(ng), dim3(FULL_THREADS), 0, st, f, fs);
         if (ctx->any_small) {
             hipLaunchKernelGGL(k_full_collect, cgrid, dim3(FULL_THREADS), 0, st, f, fs);
