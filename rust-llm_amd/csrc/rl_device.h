@@ -263,22 +263,6 @@ __device__ __forceinline__ void window_store(const WindowSet &w, uint32_t slot, 
     __hip_atomic_fetch_max(w.top, composite(k0 > k1 ? k0 : k1, id), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Whole-workgroup: clears the set and inserts window[0..len), ids only (no
-// raw values, `top` stays 0): for membership tests, without the gather of
-// logits at random ids (each a likely TLB miss). Ends with a barrier.
-__device__ __forceinline__ void window_build_ids(const WindowSet &w, const uint32_t *window, uint32_t len,
-                                                 uint32_t vocab, bool active) {
-    window_clear(w);
-    __syncthreads();
-    if (active) {
-        for (uint32_t i = threadIdx.x; i < len; i += blockDim.x) {
-            const uint32_t id = window[i];
-            if (id < vocab) (void)window_insert(w, id);
-        }
-    }
-    __syncthreads();
-}
-
 // Whole-workgroup: clears the set, inserts window[0..len), and gathers each
 // distinct id's raw logit from `row`. Ends with a barrier.
 __device__ __forceinline__ void window_build(const WindowSet &w, const uint32_t *window, uint32_t len,
