@@ -10,6 +10,9 @@ row in [8, 14); T 0.6, top-k 20, top-p 0.95, min-p 0, repeat penalty 1.2 over
 64-id windows. Other workload shapes are parity cases (tests/) and can be timed
 with --workload.
 
+--op embed times the embedding lookup from the same resident tensor
+(rl_head_embed_rows: --tokens rows of 2560 f32 each).
+
 --op head times the output head instead (rl_head_logits: t normed hidden rows
 times the tied Q6_K embedding [2560, 248320], logits into HBM); --op head_sample
 times the head followed by sampling its logits, the device path from hidden
@@ -43,10 +46,14 @@ def parse():
                     help="budget for the CPU-baseline sample (0 skips it)")
     ap.add_argument("--no-candidates", action="store_true",
                     help="skip the candidate outputs (tokens only)")
-    ap.add_argument("--op", default="sample", choices=["sample", "top_probability", "argmax", "head", "head_sample"],
+    ap.add_argument("--op", default="sample",
+                    choices=["sample", "top_probability", "argmax", "head", "head_sample", "embed"],
                     help="sample: rl_sampler_sample_rows (the benchmark); top_probability and argmax time "
                          "rl_top_probability_rows and rl_argmax_rows on the same logits; head times "
-                         "rl_head_logits, head_sample the head followed by sampling its logits")
+                         "rl_head_logits, head_sample the head followed by sampling its logits; embed times "
+                         "rl_head_embed_rows, the embedding lookup from the same tensor")
+    ap.add_argument("--tokens", type=int, default=1,
+                    help="tokens per embedding lookup (1 = a decode step, more = a prompt)")
     ap.add_argument("--head-rows", type=int, default=1,
                     help="activation rows per head call (1 = a decode step, 9 or 17 = a verify batch)")
     ap.add_argument("--calibration-copy", type=int, default=0,
@@ -113,6 +120,100 @@ def head_cpu_baseline(w, x, budget_s):
     return done / rows / el, done, el
 
 
+def time_calls(step, args, stream):
+    """args.warmup untimed calls, then args.steps timed ones: (wall ms per
+    step, sorted per-call HIP-event ms on `stream`)."""
+    import torch
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    t_wall = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    return wall * 1e3 / args.steps, sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
+
+
+def bench_embed(args):
+    """--op embed: the embedding lookup of --tokens tokens from the resident
+    Q6_K tensor."""
+    import numpy as np
+    import torch
+
+    import rl_sampler as R
+    import workloads as W
+
+    n = args.tokens
+    dev = torch.device("cuda:0")
+    t0 = time.time()
+    w = W.head_weights()
+    head = R.DeviceHead(w, W.HEAD_K, W.HEAD_ROWS, max_batch=1)
+    print("[bench] head weights generated and uploaded in %.1fs" % (time.time() - t0), file=sys.stderr, flush=True)
+    tokens = np.random.default_rng(6).integers(0, W.HEAD_ROWS, n).astype(np.int32)
+    d_tok = torch.from_numpy(tokens).to(dev)
+    d_out = torch.empty((n, W.HEAD_K), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def step():
+        head.embed_into(d_tok, d_out, stream=stream.cuda_stream)
+
+    ms_per_step, per_call_ms = time_calls(step, args, stream)
+    mean_ms = sum(per_call_ms) / len(per_call_ms)
+    median_ms = per_call_ms[len(per_call_ms) // 2]
+    nb = -(-W.HEAD_K // 256)
+    # Per token: the id, its row's blocks, the f32 row written.
+    alg_bytes = n * (4 + nb * W.Q6K_BLOCK_BYTES + W.HEAD_K * 4)
+    achieved = alg_bytes / (mean_ms / 1e3) / 1e9
+    print("[bench] embed %d tokens: wall %.4f ms/step, events mean %.4f median %.4f min %.4f max %.4f ms" % (
+        n, ms_per_step, mean_ms, median_ms, per_call_ms[0], per_call_ms[-1]), file=sys.stderr, flush=True)
+    cpu = None
+    if args.cpu_seconds > 0:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+        done, t_cpu = 0, time.perf_counter()
+        while time.perf_counter() - t_cpu < min(args.cpu_seconds, 3.0):
+            oracle.embed_rows(w, W.HEAD_K, tokens)
+            done += n
+        el = time.perf_counter() - t_cpu
+        cpu = {"value": round(done / el, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": "%d lookups through the oracle's dequantize_row on one host core in %.1f s" % (done, el)}
+    line = {
+        "metric": "tokens/s + achieved HBM GB/s, embedding lookup from Q6_K [%d, %d], %d token%s" % (
+            W.HEAD_K, W.HEAD_ROWS, n, "" if n == 1 else "s"),
+        "value": round(n * 1e3 / ms_per_step, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q6_k -> f32",
+        "data": "synthetic (seeded Q6_K weights and token ids, rust-llm_amd/workloads.py)",
+        "config": {"workload": "embed: token_embd [%d, %d] Q6_K, %d tokens" % (W.HEAD_K, W.HEAD_ROWS, n),
+                   "tokens": n, "k": W.HEAD_K},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_call": alg_bytes,
+            "call_ms_mean": round(mean_ms, 5),
+            "call_ms_median": round(median_ms, 5),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def bench_head(args):
     """--op head / head_sample: the output head, and the head then sampling."""
     import numpy as np
@@ -156,22 +257,9 @@ def bench_head(args):
                             window_stride=W.WINDOW, window_len=d_wlen, uniforms=d_uni, out_ids=out_ids,
                             out_probs=out_probs, cand_stride=cs, stream=stream.cuda_stream)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    t_wall = time.perf_counter()
-    for i in range(args.steps):
-        starts[i].record(stream)
-        step()
-        ends[i].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_wall
-    per_call_ms = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    ms_per_step, per_call_ms = time_calls(step, args, stream)
     mean_ms = sum(per_call_ms) / len(per_call_ms)
     median_ms = per_call_ms[len(per_call_ms) // 2]
-    ms_per_step = wall * 1e3 / args.steps
     weight_bytes = W.HEAD_ROWS * (-(-W.HEAD_K // 256)) * W.Q6K_BLOCK_BYTES
     # Weights once, the hidden rows, the logits written; sampling re-reads the
     # logits and writes (token, kept, used, 20 candidates) per row.
@@ -237,6 +325,9 @@ def main():
               "independent, so a multi-GPU run is not part of this build (asked for --gpus %d)" % args.gpus,
               file=sys.stderr)
         sys.exit(2)
+    if args.op == "embed":
+        bench_embed(args)
+        return
     if args.op in ("head", "head_sample"):
         bench_head(args)
         return

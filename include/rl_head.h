@@ -50,6 +50,18 @@ void rl_head_destroy(rl_head *head);
 int rl_head_logits(rl_head *head, const float *x, uint32_t t, float *logits, uint64_t row_stride,
                    void *stream);
 
+/* The embedding lookup from the same resident tensor (the tied `token_embd`):
+ * out[i * row_stride + j] = row tokens[i] of the tensor expanded to f32, for
+ * i < t and j < k, the same bits as the reference's Exec::embed
+ * (crates/rust-llm/src/forward.rs:1127-1138), which is dequantize_row's Q6_K
+ * arm (crates/llm-core/src/quant.rs:177-203). tokens [t] u32 and out are device
+ * pointers, so a token the sampler drew in HBM feeds the next step without a
+ * host round trip; row_stride >= k. The reference asserts a token is below
+ * `rows`; a device kernel cannot stop, so such a token's row is written as NaN.
+ * Columns past k in a padded row are not written. */
+int rl_head_embed_rows(rl_head *head, const uint32_t *tokens, uint32_t t, float *out, uint64_t row_stride,
+                       void *stream);
+
 /* Activations::quantize_batch (quant.rs:337-375) on the device, for any k:
  * x [t][k] f32 into nb = ceil(k/256) blocks per row, written as the reference's
  * ActBlock fields (quant.rs:233-237): out_d [t][nb] f32, out_qs [t][nb*256]

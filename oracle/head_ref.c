@@ -23,6 +23,12 @@
  *                      zero rows give d = 0 and all-zero quants; NaN ignored by
  *                      the maximum and quantized to 0; halves round away from
  *                      zero), and a numpy restatement on random rows.
+ *   orc_dequantize_row pinned: the reference tests' own check against a
+ *                      dequantization written out again in the test, within
+ *                      1e-6 relative (crates/llm-core/tests/kernels.rs:633-668);
+ *                      exact known answers (d = 1 gives the integers s*(q-32),
+ *                      a power-of-two d scales them exactly); elements past k
+ *                      untouched.
  *   orc_q6k_matvec     pinned: the reference tests' own check, an f64 dot of
  *                      the dequantized ggml layout within 1e-5 of the absolute
  *                      terms (crates/llm-core/tests/kernels.rs:130-200); exact
@@ -176,4 +182,36 @@ int orc_q6k_matvec(const uint8_t *w, size_t k, size_t row_lo, size_t row_hi, con
     free(qs);
     free(bs);
     return 0;
+}
+
+/* dequantize_row's Q6_K arm (crates/llm-core/src/quant.rs:177-203): the
+ * embedding lookup (crates/rust-llm/src/forward.rs:1127-1138) of one row of k
+ * values: out[i] = d * (float)(s * (q - 32)), the integer product exact and
+ * one f32 multiply. Elements past k are not written. */
+void orc_dequantize_row(const uint8_t *w, size_t k, float *out)
+{
+    size_t nb = (k + QK - 1) / QK;
+    for (size_t ib = 0; ib < nb; ib++) {
+        const uint8_t *b = w + ib * Q6K_BYTES;
+        const uint8_t *ql = b, *qh = b + 128, *sc = b + 192;
+        float d = f16_to_f32((uint16_t)(b[208] | (b[209] << 8)));
+        for (int h = 0; h < 2; h++) {
+            const uint8_t *qlh = ql + h * 64, *qhh = qh + h * 32;
+            for (int g = 0; g < 4; g++) {
+                for (int l = 0; l < 32; l++) {
+                    int low;
+                    switch (g) {
+                    case 0: low = qlh[l] & 0xF; break;
+                    case 1: low = qlh[32 + l] & 0xF; break;
+                    case 2: low = qlh[l] >> 4; break;
+                    default: low = qlh[32 + l] >> 4; break;
+                    }
+                    int q = (low | (((qhh[l] >> (2 * g)) & 3) << 4)) - 32;
+                    int s = (int8_t)sc[h * 8 + 2 * g + l / 16];
+                    size_t at = ib * QK + (size_t)(h * 128 + g * 32 + l);
+                    if (at < k) out[at] = d * (float)(s * q);
+                }
+            }
+        }
+    }
 }

@@ -100,6 +100,8 @@ def lib():
         L.orc_q6k_matvec.argtypes = [_u8p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _f32p,
                                      ctypes.c_size_t, _f32p]
         L.orc_q6k_matvec.restype = ctypes.c_int
+        L.orc_dequantize_row.argtypes = [_u8p, ctypes.c_size_t, _f32p]
+        L.orc_dequantize_row.restype = None
         _lib = L
     return _lib
 
@@ -328,4 +330,15 @@ def q6k_matvec(w, k, x, row_lo=0, row_hi=None):
     rc = lib().orc_q6k_matvec(_ptr(w, _u8p), k, row_lo, row_hi, _ptr(a, _f32p), t, _ptr(out, _f32p))
     if rc != 0:
         raise MemoryError("orc_q6k_matvec")
+    return out
+
+
+def embed_rows(w, k, tokens):
+    """The embedding lookup (forward.rs:1127-1138) of each token: [len][k] f32."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    row_bytes = -(-k // QK) * Q6K_BYTES
+    out = np.zeros((len(tokens), k), np.float32)
+    for i, t in enumerate(tokens):
+        r = np.ascontiguousarray(w[int(t) * row_bytes:(int(t) + 1) * row_bytes])
+        lib().orc_dequantize_row(_ptr(r, _u8p), k, _ptr(out[i], _f32p))
     return out

@@ -143,6 +143,23 @@ int rl_head_logits(rl_head *h, const float *x, uint32_t t, float *logits, uint64
     return e == hipSuccess ? RL_OK : hip_fail(e, "rl_head_logits launch");
 }
 
+int rl_head_embed_rows(rl_head *h, const uint32_t *tokens, uint32_t t, float *out, uint64_t row_stride,
+                       void *stream) {
+    if (!h) return fail(RL_ERR_ARGUMENT, "head is null");
+    if (t == 0) return RL_OK;
+    if (!tokens || !out) return fail(RL_ERR_ARGUMENT, "tokens and out must be device pointers");
+    if (row_stride < h->k) return fail(RL_ERR_ARGUMENT, "row_stride below k");
+    const uint64_t threads = (uint64_t)t * h->nb * 16;
+    const uint64_t blocks = (threads + EMBED_THREADS - 1) / EMBED_THREADS;
+    if (blocks > 0xFFFFFFFFull) return fail(RL_ERR_CAPACITY, "too many tokens for one launch");
+    DeviceGuard g(h->device);
+    if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select the head's device");
+    hipLaunchKernelGGL(k_embed_rows, dim3((uint32_t)blocks), dim3(EMBED_THREADS), 0, static_cast<hipStream_t>(stream),
+                       h->wq, h->ws, h->wd, tokens, t, h->k, h->nb, h->rows, h->groups, out, row_stride);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? RL_OK : hip_fail(e, "rl_head_embed_rows launch");
+}
+
 int rl_quantize_rows(const float *x, uint32_t t, uint32_t k, float *out_d, int8_t *out_qs, int16_t *out_bsums,
                      void *stream) {
     if (t == 0) return RL_OK;

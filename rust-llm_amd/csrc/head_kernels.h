@@ -653,4 +653,71 @@ void k_head_dot(const uint4 *__restrict__ wq, const uint32_t *__restrict__ ws, c
     }
 }
 
+// ------------------------------------------------------------ embedding lookup
+
+// The reference's embedding lookup (forward.rs:1127-1138), dequantize_row's
+// Q6_K arm (quant.rs:177-203), from the repacked tensor: value i of a row is
+// d * (float)(s * (q - 32)), the integer product exact and one f32 multiply,
+// as the reference forms it. One thread per (token, block, quarter h, step
+// pair p): the row's 16 values 64 h + 16 p .. + 15 of the block, all of
+// sub-block 4 h + p, from words 3p .. 3p+2 of lane 16 h + m's quant chunks (the
+// packing above). A token at or past `rows` gives a row of NaN: the reference
+// asserts (forward.rs:1130-1134), which a kernel cannot.
+constexpr int EMBED_THREADS = 256;
+
+__global__ __launch_bounds__(EMBED_THREADS) void k_embed_rows(const uint4 *__restrict__ wq,
+                                                              const uint32_t *__restrict__ ws,
+                                                              const uint16_t *__restrict__ wd,
+                                                              const uint32_t *__restrict__ tokens, uint32_t t,
+                                                              uint32_t k, uint32_t nb, uint32_t rows, uint32_t groups,
+                                                              float *__restrict__ out, uint64_t out_stride) {
+    const uint64_t idx = (uint64_t)blockIdx.x * EMBED_THREADS + threadIdx.x;
+    if (idx >= (uint64_t)t * nb * 16) return;
+    const uint32_t p = (uint32_t)(idx & 3), h = (uint32_t)((idx >> 2) & 3);
+    const uint64_t tb = idx >> 4;
+    const uint32_t ib = (uint32_t)(tb % nb), ti = (uint32_t)(tb / nb);
+    const uint32_t k0 = ib * QK + 64 * h + 16 * p;
+    if (k0 >= k) return;
+    const uint32_t n = k - k0 < 16 ? k - k0 : 16;
+    float *o = out + (uint64_t)ti * out_stride + k0;
+    const uint32_t tok = tokens[ti];
+    float v[16];
+    if (tok >= rows) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = __builtin_nanf("");
+    } else {
+        const uint32_t g = tok / HEAD_GROUP, tw = (tok / HEAD_TILE) % HEAD_TILES, m = tok % HEAD_TILE;
+        const uint64_t bgt = ((uint64_t)ib * groups + g) * HEAD_TILES + tw;
+        const uint32_t lane = 16 * h + m;
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(wq + bgt * HEAD_QCH * 64 + lane);
+        uint32_t pw[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const uint32_t wi = 3 * p + j;
+            pw[j] = q[(wi / 4) * 64 * 4 + wi % 4];
+        }
+        const int s = (int)(int8_t)(ws[bgt * 64 + lane] >> (8 * p));
+        const float d = __half2float(__ushort_as_half(wd[bgt * HEAD_TILE + m]));
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            const uint32_t a = pw[0] >> (16 * x), b = pw[1] >> (16 * x), c = pw[2] >> (16 * x);
+            const uint32_t u[8] = {a & 63, (a >> 6) & 63, b & 63, (b >> 6) & 63,
+                                   c & 63, (c >> 6) & 63, ((a >> 12) & 15) | ((c >> 12) & 3) << 4,
+                                   ((b >> 12) & 15) | ((c >> 14) & 3) << 4};
+            // u[j] is value 2 j + x of the sixteen.
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[2 * j + x] = d * (float)(s * ((int)u[j] - 32));
+        }
+    }
+    if (n == 16 && (reinterpret_cast<uintptr_t>(o) & 15) == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            reinterpret_cast<float4 *>(o)[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if ((uint32_t)i < n) o[i] = v[i];
+    }
+}
+
 }  // namespace rl

@@ -124,6 +124,7 @@ def lib():
         L.rl_head_destroy.argtypes = [_vp]
         L.rl_head_destroy.restype = None
         L.rl_head_logits.argtypes = [_vp, _vp, _u32, _vp, _u64, _vp]
+        L.rl_head_embed_rows.argtypes = [_vp, _vp, _u32, _vp, _u64, _vp]
         L.rl_quantize_rows.argtypes = [_vp, _u32, _u32, _vp, _vp, _vp, _vp]
         _lib = L
     return _lib
@@ -403,6 +404,23 @@ class DeviceHead:
         assert x.dtype == torch.float32 and x.is_contiguous() and x.shape[1] == self.k
         out = torch.empty((x.shape[0], self.rows), dtype=torch.float32, device=x.device)
         self.logits_into(x, out)
+        return out
+
+    def embed_into(self, tokens, out, row_stride=None, stream=None):
+        """rl_head_embed_rows (forward.rs:1127-1138): tokens device int32/uint32
+        [t]; out device f32 with rows of row_stride >= k entries."""
+        t = tokens.shape[0]
+        _check(lib().rl_head_embed_rows(self.h, _ptr(tokens), t, _ptr(out),
+                                        self.k if row_stride is None else row_stride,
+                                        current_stream() if stream is None else stream))
+
+    def embed(self, tokens):
+        """The embedding rows of device tokens [t] (int32 holding u32 ids), as a
+        device f32 [t][k] tensor."""
+        import torch
+        assert tokens.dtype == torch.int32 and tokens.is_contiguous() and tokens.dim() == 1
+        out = torch.empty((tokens.shape[0], self.k), dtype=torch.float32, device=tokens.device)
+        self.embed_into(tokens, out)
         return out
 
 

@@ -55,6 +55,7 @@ def test_head_status_codes_without_a_device():
     assert lib.rl_head_create(0, 256, 2, 4, buf, 419, ctypes.byref(h)) == R.RL_ERR_ARGUMENT
     assert b"210" in lib.rl_sampler_last_error()
     assert lib.rl_head_logits(None, None, 1, None, 0, None) == R.RL_ERR_ARGUMENT
+    assert lib.rl_head_embed_rows(None, None, 1, None, 0, None) == R.RL_ERR_ARGUMENT
     assert lib.rl_quantize_rows(None, 1, 256, None, None, None, None) == R.RL_ERR_ARGUMENT
     assert lib.rl_quantize_rows(None, 0, 256, None, None, None, None) == R.RL_OK  # nothing to do
     lib.rl_head_destroy(None)  # accepted
