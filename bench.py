@@ -171,6 +171,14 @@ def bench_embed(args):
     achieved = alg_bytes / (mean_ms / 1e3) / 1e9
     print("[bench] embed %d tokens: wall %.4f ms/step, events mean %.4f median %.4f min %.4f max %.4f ms" % (
         n, ms_per_step, mean_ms, median_ms, per_call_ms[0], per_call_ms[-1]), file=sys.stderr, flush=True)
+    if args.calibration_copy > 0:
+        dst = torch.empty_like(d_out)
+        for _ in range(args.calibration_copy):
+            dst.copy_(d_out)
+        torch.cuda.synchronize()
+        print("[bench] calibration: %d copies of %d bytes" % (args.calibration_copy, d_out.numel() * 4),
+              file=sys.stderr, flush=True)
+        del dst
     cpu = None
     if args.cpu_seconds > 0:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -204,7 +212,7 @@ def bench_embed(args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic_bytes("embed_n%d" % n),
             "algorithmic_bytes_per_call": alg_bytes,
             "call_ms_mean": round(mean_ms, 5),
             "call_ms_median": round(median_ms, 5),
