@@ -289,13 +289,16 @@ __device__ inline void fill_act(uint4 *__restrict__ frag, float *__restrict__ fd
 // One wave per group of 64 vocabulary rows (four 16-row tiles); NT column
 // tiles of 16 activation rows. The workgroup walks the blocks in step (one
 // barrier per block): the activation fragments of block ib + 1 are built in
-// LDS while block ib is computed. Each tile takes 16 matrix-core products
-// (8 steps, s_lo and s_hi) and then the reference's f32 line. Weights are
-// fetched two tiles ahead. `stab` is the per-scale-byte table {s_lo,
+// LDS while block ib is computed. Each tile takes 16 matrix-core products per
+// column tile (8 steps, s_lo and s_hi) and then the reference's f32 line; the
+// next tile's weights are in flight meanwhile. Four waves per SIMD: the
+// fragments are read from LDS step by step, and a scheduling barrier per step
+// pair keeps the compiler from hoisting every step's reads (which costs the
+// registers of a fourth wave). `stab` is the per-scale-byte table {s_lo,
 // -1056 s_lo, s_hi, -1056 s_hi} as f16 pairs, so (1024 + q) * s + c =
 // (q - 32) * s exactly in one packed FMA.
 template <int NT>
-__global__ __launch_bounds__(HEAD_THREADS) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4 : 2)))
+__global__ __launch_bounds__(HEAD_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
 void k_head_mfma_lds(const uint4 *__restrict__ wq, const uint32_t *__restrict__ ws, const uint16_t *__restrict__ wd,
                 const int8_t *__restrict__ aq, const float *__restrict__ ad, uint32_t t, uint32_t nb,
                 uint32_t rows, uint32_t groups, float *__restrict__ out, uint64_t out_stride) {
@@ -329,7 +332,6 @@ void k_head_mfma_lds(const uint4 *__restrict__ wq, const uint32_t *__restrict__ 
         for (int tw = 0; tw < HEAD_TILES; ++tw) sum[nt][tw] = f4_t{0.f, 0.f, 0.f, 0.f};
 
     HeadTile cur = load_tile(wq, ws, wd, (uint64_t)gg * HEAD_TILES, lane, h);
-    HeadTile nx1 = load_tile(wq, ws, wd, (uint64_t)gg * HEAD_TILES + 1, lane, h);
     for (uint32_t ib = 0; ib < nb; ++ib) {
         __syncthreads();  // block ib's fragments are built; block ib - 1's buffer is free
         if (ib + 1 < nb) fill_act<NT>(frag[(ib + 1) & 1], fd[(ib + 1) & 1], aq, ad, nb, ib + 1);
@@ -340,10 +342,10 @@ void k_head_mfma_lds(const uint4 *__restrict__ wq, const uint32_t *__restrict__ 
         const uint32_t nxt_ib = ib + 1 < nb ? ib + 1 : ib;  // past the end: re-read (a cache hit)
 #pragma unroll
         for (int tw = 0; tw < HEAD_TILES; ++tw) {
-            // Two tiles ahead: tile tw + 2 of this block, or of the next.
-            const uint64_t nbgt = tw + 2 < HEAD_TILES ? ((uint64_t)ib * groups + gg) * HEAD_TILES + tw + 2
-                                                      : ((uint64_t)nxt_ib * groups + gg) * HEAD_TILES + tw + 2 - HEAD_TILES;
-            const HeadTile nx2 = load_tile(wq, ws, wd, nbgt, lane, h);
+            // The next tile: tile tw + 1 of this block, or the first of the next.
+            const uint64_t nbgt = tw + 1 < HEAD_TILES ? ((uint64_t)ib * groups + gg) * HEAD_TILES + tw + 1
+                                                      : ((uint64_t)nxt_ib * groups + gg) * HEAD_TILES;
+            const HeadTile nxt = load_tile(wq, ws, wd, nbgt, lane, h);
             const uint32_t w12[12] = {cur.q[0].x, cur.q[0].y, cur.q[0].z, cur.q[0].w, cur.q[1].x, cur.q[1].y,
                                       cur.q[1].z, cur.q[1].w, cur.q[2].x, cur.q[2].y, cur.q[2].z, cur.q[2].w};
             f4_t acc_lo[NT], acc_hi[NT];
@@ -354,6 +356,7 @@ void k_head_mfma_lds(const uint4 *__restrict__ wq, const uint32_t *__restrict__ 
             }
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
+                __builtin_amdgcn_sched_barrier(0);
                 uint32_t x[8];
                 unpack_steps(w12[3 * p], w12[3 * p + 1], w12[3 * p + 2], x, uk);
                 const uint4 st = stab[(cur.sc >> (8 * p)) & 255];
@@ -388,8 +391,7 @@ void k_head_mfma_lds(const uint4 *__restrict__ wq, const uint32_t *__restrict__ 
                     sum[nt][tw][i] = sum[nt][tw][i] + scale * (float)isum;
                 }
             }
-            cur = nx1;
-            nx1 = nx2;
+            cur = nxt;
         }
     }
     if (!active) return;
