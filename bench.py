@@ -98,6 +98,56 @@ def cpu_baseline(wl, logits, windows, wlen, uniforms, settings, budget_s):
     return done / el, done, el
 
 
+def host_threads():
+    """Host threads a CPU baseline may use: the affinity mask, the cgroup CPU
+    quota where one is set, at most 16 (one GPU's share of a box's cores)."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return max(1, min(n, 16))
+
+
+def cpu_baseline_threads(wl, logits, windows, wlen, uniforms, settings, budget_s, threads):
+    """The oracle on `threads` host threads (rows split over them, each thread
+    cycling over its own slice; the oracle's C calls run without the GIL),
+    until the time budget is spent. Returns rows/s and the sample size."""
+    import threading
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    osets = [oracle.Sampling(s.temperature, s.top_p, s.min_p, s.repeat_penalty, s.top_k, s.repeat_last_n, s.seed)
+             for s in settings]
+    rows = logits.shape[0]
+    per = max(1, rows // threads)
+    batch = min(per, 16)
+    counts = [0] * threads
+    t0 = time.perf_counter()
+
+    def work(i):
+        lo = (i * per) % rows
+        hi = min(rows, lo + per)
+        r0 = lo
+        while time.perf_counter() - t0 < budget_s:
+            r1 = min(hi, r0 + batch)
+            sl = slice(r0, r1)
+            oracle.pick_rows(logits[sl], osets[sl], windows[sl], wlen[sl], uniforms[sl], cand_cap=1)
+            counts[i] += r1 - r0
+            r0 = r1 if r1 < hi else lo
+
+    ts = [threading.Thread(target=work, args=(i,)) for i in range(threads)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    el = time.perf_counter() - t0
+    return sum(counts) / el, sum(counts), el
+
+
 def head_cpu_baseline(w, x, budget_s):
     """The oracle head on one host core over slices of the vocabulary, until
     the time budget is spent. Returns full-vocabulary head calls/s."""
@@ -416,12 +466,22 @@ def main():
         del dst
 
     cpu = None
+    cpu_n = None
     if args.cpu_seconds > 0 and args.op == "sample":
         rate, n, el = cpu_baseline(wl, logits, windows, wlen, uniforms, settings, args.cpu_seconds)
         cpu = {"value": round(rate, 2), "unit": "rows/s", "cores": 1, "kind": "port",
                "sample": "%d rows of the same workload (%s) through the oracle on one host core in %.1f s"
                          % (n, name, el)}
         print("[bench] cpu baseline %.1f rows/s over %d rows" % (rate, n), file=sys.stderr, flush=True)
+        nt = host_threads()
+        if nt > 1:
+            rate_n, n_n, el_n = cpu_baseline_threads(wl, logits, windows, wlen, uniforms, settings,
+                                                     args.cpu_seconds / 2, nt)
+            cpu_n = {"value": round(rate_n, 2), "unit": "rows/s", "cores": nt, "kind": "port",
+                     "sample": "%d rows of the same workload (%s) through the oracle on %d host threads, rows "
+                               "split over them, in %.1f s" % (n_n, name, nt, el_n)}
+            print("[bench] cpu baseline, %d threads: %.1f rows/s over %d rows" % (nt, rate_n, n_n),
+                  file=sys.stderr, flush=True)
 
     s0 = settings[0]
     line = {
@@ -459,6 +519,7 @@ def main():
             "call_ms_median": round(median_ms, 5),
         },
         "cpu_baseline": cpu,
+        "cpu_baseline_threads": cpu_n,
     }
     print(json.dumps(line), flush=True)
 
