@@ -18,6 +18,9 @@
 
 namespace rl {
 
+// s_waitcnt immediate for vmcnt(0) (gfx9 encoding; expcnt and lgkmcnt left at
+// their maximum, so only vector memory operations are waited for).
+constexpr int WAITCNT_VM0 = 0x0F70;
 constexpr uint32_t FAST_THREADS = 256;
 constexpr uint32_t FAST_WAVES = FAST_THREADS / WAVE;
 constexpr uint32_t KMAX = 64;     // largest top_k the stream path takes (one per lane)
@@ -559,11 +562,18 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
         if (a.chunks == 1) {
             finalize_row(a, row, s, k, top, nL, ws, pen, rowp);
         } else {
-            // Publish this chunk's list; the row's last chunk to arrive finishes it.
+            // Publish this chunk's list; the row's last chunk to arrive finishes
+            // it. The list is written with device-scope stores, which write
+            // through this XCD's L2, and the arrival waits until they have
+            // completed: the list is then visible to every XCD, with no
+            // writeback of the whole L2 (what a device-scope fence costs,
+            // serialised per XCD).
             uint64_t *dst = sc.chunk_cands + ((uint64_t)slot * a.chunks + chunk) * KMAX;
-            if (lane < nL) dst[lane] = top;
-            if (lane == 0) sc.chunk_counts[slot * a.chunks + chunk] = nL;
-            __threadfence();  // release: the list before the arrival
+            if (lane < nL) __hip_atomic_store(dst + lane, top, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0)
+                __hip_atomic_store(sc.chunk_counts + slot * a.chunks + chunk, nL, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);  // the stores have completed
             uint32_t old = 0;
             if (lane == 0) old = atomicAdd(&sc.arrive[slot], 1u);
             old = read_lane_u32(old, 0);
@@ -575,8 +585,9 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
     if (!s_last) return;
     // The last chunk of the row: every chunk's list is published. Each wave
     // merges the lists j = wave (mod FAST_WAVES), all loaded at once, then wave
-    // 0 merges the four results and runs the tail.
-    __threadfence();  // acquire: the other chunks' lists after their arrivals
+    // 0 merges the four results and runs the tail. The lists are read with
+    // device-scope loads, which bypass this XCD's L2, issued after the
+    // arrival that saw every other chunk's.
     const uint64_t *lists = sc.chunk_cands + (uint64_t)slot * a.chunks * KMAX;
     const uint32_t *counts = sc.chunk_counts + slot * a.chunks;
     constexpr uint32_t PER = MAX_CHUNKS / FAST_WAVES;
