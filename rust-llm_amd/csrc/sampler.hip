@@ -245,11 +245,17 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
                                    ctx->full_rows.begin());
     if (ns > 0) {
         RowIO s = io;
-        s.rows = ctx->d_stream_rows;
+        // The stream rows are ascending and distinct: they are 0 .. ns-1
+        // exactly when the last is ns - 1, and the kernel then needs no list.
+        s.rows = ctx->stream_rows[ns - 1] == ns - 1 ? nullptr : ctx->d_stream_rows;
         const uint32_t n4 = vocab / 4;
+        // Few rows are split into chunks; as many as fill the GPU, but no more
+        // than it takes for every chunk to fit in one tile (a chunk a little
+        // over one tile pays a second round trip to memory for its rest).
+        constexpr uint32_t STEP4 = FAST_THREADS * UNROLL;
         uint32_t chunks = (TARGET_WGS + ns - 1) / ns;
         chunks = std::min(chunks, MAX_CHUNKS);
-        chunks = std::min(chunks, std::max(1u, n4 / (FAST_THREADS * UNROLL)));
+        chunks = std::min(chunks, std::max(1u, (n4 + STEP4 - 1) / STEP4));
         s.chunks = std::max(chunks, 1u);
         FastScratch sc{ctx->d_chunk_cands, ctx->d_chunk_counts, ctx->d_arrive};
         const size_t lds = window_lds_bytes(ctx->hash_bits);

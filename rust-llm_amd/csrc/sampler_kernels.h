@@ -36,7 +36,7 @@ struct RowIO {
     uint64_t stride;
     uint32_t vocab;
     const rl_sampling *settings;  // indexed by row
-    const uint32_t *rows;         // this path's rows: rows[slot] = row index
+    const uint32_t *rows;         // this path's rows: rows[slot] = row index (k_stream: null = slot)
     const uint32_t *windows;
     uint32_t wstride;
     const uint32_t *wlen;
@@ -234,8 +234,11 @@ __device__ __forceinline__ void process_tile(Stream &w, const f32x4 *T, uint32_t
 // (window ids excluded), then the k-th best t of those 64 lane maxima. At
 // least k distinct elements are >= t, so nothing below t is among the row's k
 // best; the threshold is t - 1 because the k elements >= t are not in any
-// buffer yet and must still pass the strict test composite > T.
-__device__ __forceinline__ void bootstrap(Stream &w, const f32x4 *A, uint32_t base) {
+// buffer yet and must still pass the strict test composite > T. Loads at or
+// past `end` were clamped (duplicates of the chunk's last element under other
+// ids) and are left out; a lane with none contributes nothing, and with fewer
+// than k contributing lanes t is 0 (no threshold).
+__device__ __forceinline__ void bootstrap(Stream &w, const f32x4 *A, uint32_t base, uint32_t end) {
     const uint32_t tid = threadIdx.x;
     uint64_t bound = ~0ull, best = 0;
     for (uint32_t attempt = 0; attempt < 4; ++attempt) {
@@ -243,10 +246,11 @@ __device__ __forceinline__ void bootstrap(Stream &w, const f32x4 *A, uint32_t ba
 #pragma unroll
         for (uint32_t u = 0; u < UNROLL; ++u) {
             const float x[4] = {A[u].x, A[u].y, A[u].z, A[u].w};
-            const uint32_t id0 = 4 * (base + u * FAST_THREADS + tid);
+            const uint32_t f = base + u * FAST_THREADS + tid;
+            const uint32_t id0 = 4 * f;
 #pragma unroll
             for (uint32_t c = 0; c < 4; ++c) {
-                const bool ok = !w.greedy || x[c] >= -3.40282347e38f;
+                const bool ok = f < end && (!w.greedy || x[c] >= -3.40282347e38f);
                 const uint64_t comp = composite(stream_key(w, x[c]), id0 + c);
                 if (ok && comp < bound && comp > best) best = comp;
             }
@@ -447,7 +451,9 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
     extern __shared__ __align__(16) uint8_t smem[];
     const WindowSet ws = window_set(smem, a.hash_bits);
     const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
-    const uint32_t row = a.rows[slot];
+    // The common case, every row on this path, needs no lookup before the
+    // row's address is known.
+    const uint32_t row = a.rows ? a.rows[slot] : slot;
     const rl_sampling s = a.settings[row];
     const bool greedy = s.temperature <= 0.0f;
     const uint32_t k = uniform_u32(greedy ? 1u : (uint32_t)s.top_k);
@@ -476,7 +482,7 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
     const uint32_t *wrow = a.windows + (uint64_t)row * a.wstride;
     const bool small_win = pen && wl <= FAST_THREADS;
     if (pen && !small_win) window_build(ws, wrow, wl, V, rowp, true);
-    const uint32_t *idp = small_win ? wrow + (tid < wl ? tid : wl - 1) : a.rows + slot;
+    const uint32_t *idp = small_win ? wrow + (tid < wl ? tid : wl - 1) : reinterpret_cast<const uint32_t *>(a.settings + row);
     const uint32_t id_loaded = *(const RL_GLB uint32_t *)idp;  // unconditional, see load_tile_clamped
     // The first tile. A row of fewer than 4 logits has no tile; it loads 16
     // bytes of its own settings instead, so that this load needs no branch
@@ -509,7 +515,7 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
 
     // Wave priority falls as the row progresses (see set_progress_priority).
     __builtin_amdgcn_s_setprio(3);
-    if (nfull > 0) bootstrap(w, A, q0);
+    if (ntiles > 0) bootstrap(w, A, q0, q1);
     if (my_slot != EMPTY_ID) window_store(ws, my_slot, my_id, my_raw);
     __syncthreads();
     w.wtop = window_top(ws);
