@@ -444,7 +444,7 @@ __device__ __forceinline__ uint64_t ascending_from(const uint64_t *list, uint32_
 // window set. A row split into chunks is finished by whichever of its chunks
 // publishes its list last (a per-row arrival counter), so no second launch.
 template <bool VEC>
-__global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc) {
+__global__ __launch_bounds__(FAST_THREADS) __attribute__((amdgpu_waves_per_eu(4))) void k_stream(RowIO a, FastScratch sc) {
     __shared__ uint64_t s_buf[FAST_WAVES * CBUF];
     __shared__ uint64_t s_T;
     __shared__ uint32_t s_cnt[FAST_WAVES];
@@ -516,26 +516,41 @@ __global__ __launch_bounds__(FAST_THREADS) void k_stream(RowIO a, FastScratch sc
     // Wave priority falls as the row progresses (see set_progress_priority).
     __builtin_amdgcn_s_setprio(3);
     if (ntiles > 0) bootstrap(w, A, q0, q1);
-    if (my_slot != EMPTY_ID) window_store(ws, my_slot, my_id, my_raw);
-    __syncthreads();
-    w.wtop = window_top(ws);
-    // Double-buffered: tile t+1 is in flight while tile t is filtered. Loads
-    // past the chunk are clamped (they cost one cache line per wave), so the
-    // last, partial tile runs through the same loop.
-    for (uint32_t t = 0; t < ntiles; t += 2) {
-        const uint32_t b0 = q0 + t * STEP, b1 = b0 + STEP;
-        load_tile_clamped<VEC>(B, rowp, b1, q1);
-        if (t < nfull)
-            process_tile<false>(w, A, b0, q1);
-        else
-            process_tile<true>(w, A, b0, q1);
-        load_tile_clamped<VEC>(A, rowp, b1 + STEP, q1);
-        if (t + 1 < nfull)
-            process_tile<false>(w, B, b1, q1);
-        else if (t + 1 < ntiles)
-            process_tile<true>(w, B, b1, q1);
-        raise_threshold(w, load_shared_T(lT));
-        set_progress_priority(t + 2, ntiles);
+    if (ntiles <= 1) {
+        // One tile or none (a chunk of a split row): nothing more to load.
+        // The window's raw logits were loaded behind the tile, so they are
+        // stored after it is filtered (wtop stays ~0 meanwhile: compaction
+        // checks every candidate against the window set); merge_window reads
+        // them at the end.
+        if (nfull == 1)
+            process_tile<false>(w, A, q0, q1);
+        else if (ntiles == 1)
+            process_tile<true>(w, A, q0, q1);
+        if (my_slot != EMPTY_ID) window_store(ws, my_slot, my_id, my_raw);
+        __syncthreads();
+        w.wtop = window_top(ws);
+    } else {
+        if (my_slot != EMPTY_ID) window_store(ws, my_slot, my_id, my_raw);
+        __syncthreads();
+        w.wtop = window_top(ws);
+        // Double-buffered: tile t+1 is in flight while tile t is filtered.
+        // Loads past the chunk are clamped (they cost one cache line per
+        // wave), so the last, partial tile runs through the same loop.
+        for (uint32_t t = 0; t < ntiles; t += 2) {
+            const uint32_t b0 = q0 + t * STEP, b1 = b0 + STEP;
+            load_tile_clamped<VEC>(B, rowp, b1, q1);
+            if (t < nfull)
+                process_tile<false>(w, A, b0, q1);
+            else
+                process_tile<true>(w, A, b0, q1);
+            load_tile_clamped<VEC>(A, rowp, b1 + STEP, q1);
+            if (t + 1 < nfull)
+                process_tile<false>(w, B, b1, q1);
+            else if (t + 1 < ntiles)
+                process_tile<true>(w, B, b1, q1);
+            raise_threshold(w, load_shared_T(lT));
+            set_progress_priority(t + 2, ntiles);
+        }
     }
     __builtin_amdgcn_s_setprio(0);
     // The row's last vocab % 4 elements.
