@@ -220,9 +220,12 @@ __device__ __forceinline__ uint64_t wave_scan_sum(uint64_t v) {
     return v;
 }
 
-// Replays s = fl_P(s + x_j) for j = 0, 1, ... over the n terms load(j) (finite,
-// >= 0), in order, with the whole workgroup (NT threads, ITEMS consecutive
-// terms per thread per tile). Returns the first j whose partial sum satisfies
+// Replays s = fl_P(s + x_j) for j = 0, 1, ... over the n terms
+// x_j = term(fetch(j)) (finite, >= 0), in order, with the whole workgroup (NT
+// threads, ITEMS consecutive terms per thread per tile). fetch(j) returns the
+// raw 32 bits a term is made from and term turns them into the f32 term, so
+// the next tile's fetches stay in flight while the current tile is reduced
+// (a term computed at fetch time would wait for its load there). Returns the first j whose partial sum satisfies
 // pred (a predicate that stays true once true as the sum grows), or n; when
 // it returns n, *sum is the sequential sum of all n terms, and otherwise the
 // partial sum at the returned index. Every thread of the workgroup must call
@@ -236,8 +239,8 @@ __device__ __forceinline__ uint64_t wave_scan_sum(uint64_t v) {
 // tells whether the sum leaves its segment or meets pred inside the tile, and
 // only then is a block scan needed to find where. A tile holding a tie goes
 // through the parity-carrying term maps instead.
-template <int P, uint32_t NT, uint32_t ITEMS, class Load, class Pred>
-__device__ uint32_t seq_replay(Load load, uint32_t n, Pred pred, SeqLds<NT> *L, double *sum) {
+template <int P, uint32_t NT, uint32_t ITEMS, class Fetch, class Term, class Pred>
+__device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t n, Pred pred, SeqLds<NT> *L, double *sum) {
     constexpr uint32_t TILE = NT * ITEMS;
     constexpr uint32_t NW = NT / 64;
     const uint32_t tid = threadIdx.x, lane = __lane_id(), wave = tid / 64;
@@ -246,10 +249,10 @@ __device__ uint32_t seq_replay(Load load, uint32_t n, Pred pred, SeqLds<NT> *L, 
     SumSeg g{0, 0, 0};
     uint32_t pos = 0;  // the next term to add
     uint32_t cur = 0xFFFFFFFFu, nxt = 0xFFFFFFFFu;  // bases of the tiles in xb and nb
-    uint32_t xb[ITEMS], nb[ITEMS];
+    uint32_t xb[ITEMS], nb[ITEMS];  // terms of the current tile, raw bits of the next
     if (n > 0 && pred(0.0)) {
         // A predicate that +0 already meets is met by the first term's sum.
-        *sum = add_p<P>(0.0, load(0));
+        *sum = add_p<P>(0.0, term(fetch(0)));
         return 0;
     }
     while (pos < n) {
@@ -258,17 +261,17 @@ __device__ uint32_t seq_replay(Load load, uint32_t n, Pred pred, SeqLds<NT> *L, 
         if (base != cur) {
             if (base == nxt) {
 #pragma unroll
-                for (uint32_t i = 0; i < ITEMS; ++i) xb[i] = nb[i];
+                for (uint32_t i = 0; i < ITEMS; ++i) xb[i] = j0 + i < n ? __float_as_uint(term(nb[i])) : 0u;
             } else {
 #pragma unroll
-                for (uint32_t i = 0; i < ITEMS; ++i) xb[i] = j0 + i < n ? __float_as_uint(load(j0 + i)) : 0u;
+                for (uint32_t i = 0; i < ITEMS; ++i) xb[i] = j0 + i < n ? __float_as_uint(term(fetch(j0 + i))) : 0u;
             }
             cur = base;
             nxt = base + TILE;
 #pragma unroll
             for (uint32_t i = 0; i < ITEMS; ++i) {
                 const uint32_t j = nxt + tid * ITEMS + i;
-                nb[i] = j < n ? __float_as_uint(load(j)) : 0u;
+                nb[i] = fetch(j < n ? j : n - 1);  // clamped: no branch around the load
             }
         }
         // This tile's terms from pos on (the others count as +0).
@@ -436,6 +439,12 @@ __device__ uint32_t seq_replay(Load load, uint32_t n, Pred pred, SeqLds<NT> *L, 
     }
     *sum = s;
     return n;
+}
+// The same over terms that need no transformation: load(j) is the f32 term.
+template <int P, uint32_t NT, uint32_t ITEMS, class Load, class Pred>
+__device__ __forceinline__ uint32_t seq_replay(Load load, uint32_t n, Pred pred, SeqLds<NT> *L, double *sum) {
+    return seq_replay<P, NT, ITEMS>([load](uint32_t j) { return __float_as_uint(load(j)); },
+                                    [](uint32_t bits) { return __uint_as_float(bits); }, n, pred, L, sum);
 }
 #endif  // __HIPCC__
 

@@ -155,8 +155,9 @@ __global__ __launch_bounds__(REPLAY_THREADS) void k_tp_final(const float *logits
         const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab};
         double sum;
         seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(
-            [rowp, best, etab](uint32_t j) { return expf_libm_t(((const RL_GLB float *)rowp)[j] - best, etab); },
-            vocab, NeverStop{}, &seq, &sum);
+            [rowp](uint32_t j) { return ((const RL_GLB uint32_t *)rowp)[j]; },
+            [best, etab](uint32_t bits) { return expf_libm_t(__uint_as_float(bits) - best, etab); }, vocab,
+            NeverStop{}, &seq, &sum);
         prob = (float)(1.0 / sum);
     }
     if (threadIdx.x == 0) {
