@@ -29,14 +29,27 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_max(const float *logits, ui
     const uint32_t q0 = chunk_lo(n4, chunk, chunks), q1 = chunk_lo(n4, chunk + 1, chunks);
     uint64_t best = 0;
     uint32_t nan = 0;
-    for (uint32_t q = q0 + threadIdx.x; q < q1; q += FAST_THREADS) {
-        const f32x4 v = load4<VEC>(rowp, q);
-        const float x[4] = {v.x, v.y, v.z, v.w};
+    // Tiles of UNROLL float4 per thread, the next in flight while one is
+    // scanned; loads past the chunk are clamped and their values skipped.
+    constexpr uint32_t STEP = FAST_THREADS * UNROLL;
+    if (q1 > q0) {
+        f32x4 A[UNROLL], B[UNROLL];
+        load_tile_clamped<VEC>(A, rowp, q0, q1);
+        for (uint32_t b = q0; b < q1; b += STEP) {
+            load_tile_clamped<VEC>(B, rowp, b + STEP, q1);
 #pragma unroll
-        for (uint32_t c = 0; c < 4; ++c) {
-            const uint64_t cc = composite(argmax_key(x[c]), 4 * q + c);
-            best = cc > best ? cc : best;
-            nan |= x[c] != x[c] ? 1u : 0u;
+            for (uint32_t u = 0; u < UNROLL; ++u) {
+                const uint32_t q = b + u * FAST_THREADS + threadIdx.x;
+                const float x[4] = {A[u].x, A[u].y, A[u].z, A[u].w};
+#pragma unroll
+                for (uint32_t c = 0; c < 4; ++c) {
+                    const uint64_t cc = q < q1 ? composite(argmax_key(x[c]), 4 * q + c) : 0ull;
+                    best = cc > best ? cc : best;
+                    nan |= (q < q1 && x[c] != x[c]) ? 1u : 0u;
+                }
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < UNROLL; ++u) A[u] = B[u];
         }
     }
     if (chunk == chunks - 1) {
@@ -101,12 +114,25 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
     const uint32_t n4 = vocab / 4;
     const uint32_t q0 = chunk_lo(n4, chunk, chunks), q1 = chunk_lo(n4, chunk + 1, chunks);
     double sum = 0.0;
-    for (uint32_t q = q0 + threadIdx.x; q < q1; q += FAST_THREADS) {
-        const f32x4 v = load4<VEC>(rowp, q);
-        sum += (double)expf_libm_t(v.x - best, etab);
-        sum += (double)expf_libm_t(v.y - best, etab);
-        sum += (double)expf_libm_t(v.z - best, etab);
-        sum += (double)expf_libm_t(v.w - best, etab);
+    // Tiles as in k_tp_max: the next tile's loads overlap this tile's exps.
+    constexpr uint32_t STEP = FAST_THREADS * UNROLL;
+    if (q1 > q0) {
+        f32x4 A[UNROLL], B[UNROLL];
+        load_tile_clamped<VEC>(A, rowp, q0, q1);
+        for (uint32_t b = q0; b < q1; b += STEP) {
+            load_tile_clamped<VEC>(B, rowp, b + STEP, q1);
+#pragma unroll
+            for (uint32_t u = 0; u < UNROLL; ++u) {
+                if (b + u * FAST_THREADS + threadIdx.x < q1) {
+                    sum += (double)expf_libm_t(A[u].x - best, etab);
+                    sum += (double)expf_libm_t(A[u].y - best, etab);
+                    sum += (double)expf_libm_t(A[u].z - best, etab);
+                    sum += (double)expf_libm_t(A[u].w - best, etab);
+                }
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < UNROLL; ++u) A[u] = B[u];
+        }
     }
     if (chunk == chunks - 1) {
         const uint32_t e = 4 * n4 + threadIdx.x;
