@@ -662,13 +662,26 @@ __global__ __launch_bounds__(FAST_THREADS) void k_argmax_part(const float *logit
     const uint32_t q0 = (uint32_t)((uint64_t)chunk * n4 / chunks);
     const uint32_t q1 = (uint32_t)((uint64_t)(chunk + 1) * n4 / chunks);
     uint64_t best = 0;
-    for (uint32_t f = q0 + threadIdx.x; f < q1; f += FAST_THREADS) {
-        const f32x4 v = load4<VEC>(rowp, f);
-        const float x[4] = {v.x, v.y, v.z, v.w};
+    // Double-buffered tiles of UNROLL float4 per thread; loads past the chunk
+    // are clamped and their values skipped.
+    constexpr uint32_t STEP = FAST_THREADS * UNROLL;
+    if (q1 > q0) {
+        f32x4 A[UNROLL], B[UNROLL];
+        load_tile_clamped<VEC>(A, rowp, q0, q1);
+        for (uint32_t b = q0; b < q1; b += STEP) {
+            load_tile_clamped<VEC>(B, rowp, b + STEP, q1);
 #pragma unroll
-        for (uint32_t c = 0; c < 4; ++c) {
-            const uint64_t cc = composite(argmax_key(x[c]), 4 * f + c);
-            best = cc > best ? cc : best;
+            for (uint32_t u = 0; u < UNROLL; ++u) {
+                const uint32_t f = b + u * FAST_THREADS + threadIdx.x;
+                const float x[4] = {A[u].x, A[u].y, A[u].z, A[u].w};
+#pragma unroll
+                for (uint32_t c = 0; c < 4; ++c) {
+                    const uint64_t cc = f < q1 ? composite(argmax_key(x[c]), 4 * f + c) : 0ull;
+                    best = cc > best ? cc : best;
+                }
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < UNROLL; ++u) A[u] = B[u];
         }
     }
     if (chunk == chunks - 1) {
