@@ -663,12 +663,16 @@ __global__ __launch_bounds__(REPLAY_THREADS) void k_full_small(RowIO a, FullScra
     const auto term = [sp](uint32_t j) { return sp[j]; };
 
     uint32_t kept = c;
+    double total = 0.0;
+    bool have_total = false;  // the normalising sum already known from the cut's replay
     if (!by_id) {
         // The survivors must be the first c candidates: every other key is
         // below the smallest survivor key (equal keys have equal p).
         if (st.ns_key != 0 && !(key_at(c - 1) >= st.ns_key)) return;
         if (!(s.top_p > 0.0f)) {
             kept = 1;  // a target <= 0 is met by the first candidate (sample.rs:315-323)
+            total = (double)sp[0];
+            have_total = true;
         } else {
             // The reference's mass (a sequential f64 sum of all V p's in
             // candidate order) and S (this sum in chunk order) are each
@@ -684,17 +688,28 @@ __global__ __launch_bounds__(REPLAY_THREADS) void k_full_small(RowIO a, FullScra
             const uint32_t j_lo =
                 seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, c, [t_lo](double v) { return v >= t_lo; }, &seq, &at);
             if (j_lo < c) {
-                const uint32_t j_hi = seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(
-                    term, c, [t_hi](double v) { return v >= t_hi; }, &seq, &at);
-                if (j_hi != j_lo) return;  // the cut could fall on either side: sort the row
+                // Partial sums never decrease and the one before j_lo is below
+                // t_lo <= t_hi, so when the sum at j_lo reaches t_hi too, j_lo
+                // is also the first index to reach t_hi.
+                if (!(at >= t_hi)) {
+                    double unused;
+                    const uint32_t j_hi = seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(
+                        term, c, [t_hi](double v) { return v >= t_hi; }, &seq, &unused);
+                    if (j_hi != j_lo) return;  // the cut could fall on either side: sort the row
+                }
                 kept = j_lo + 1;
             }
+            // The normalising total (sample.rs:342) is the same f64 sum of
+            // the same terms in the same order, up to the last kept one: the
+            // partial sum the cut's replay stopped at (all c of them when no
+            // cut). Min-p removes none of them: every survivor is >= min_p.
+            total = at;
+            have_total = true;
         }
     }
     // Normalise over the kept candidates (sample.rs:342-347) and draw
     // (:349-358), both in their order.
-    double total;
-    seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, kept, NeverStop{}, &seq, &total);
+    if (!have_total) seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, kept, NeverStop{}, &seq, &total);
     const float inv = (float)(1.0 / total);
     for (uint32_t i = tid; i < kept; i += REPLAY_THREADS) {
         const float q = sp[i] * inv;
