@@ -562,6 +562,11 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_collect(RowIO a, FullScra
             const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
             kk[u] = ((const RL_GLB uint32_t *)keys)[j < j1 ? j : j1 - 1];  // clamped: no branch around the load
         }
+        // The survivors of all UN steps take their list slots with one
+        // atomic per wave (the wave waits for its result).
+        uint64_t sm[UN];
+        uint32_t wtotal = 0;
+        bool nonfinite = false;
 #pragma unroll
         for (uint32_t u = 0; u < UN; ++u) {
             const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
@@ -571,18 +576,25 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_collect(RowIO a, FullScra
             const bool surv = ok && finite && p >= s.min_p;
             if (ok) sum += (double)p;
             if (ok && finite && !surv) ns_key = max(ns_key, kk[u] + 1u);  // a finite p's key is below 0xFFFFFFFF
-            const uint64_t m = ballot(surv);
-            uint32_t base = 0;
-            if (m != 0 && lane == 0) base = atomicAdd(&rs->nsurv, (uint32_t)__popcll(m));
-            base = uniform_u32(__shfl((int)base, 0));
-            if (surv) {
-                const uint32_t at = base + lanes_below(m);
-                if (at < SURV_CAP) list[at] = composite(kk[u], j);
-            }
-            if ((m != 0 && base + (uint32_t)__popcll(m) > SURV_CAP) || ballot(ok && !finite) != 0) {
-                if (lane == 0) atomicOr(&rs->overflow, 1u);
-            }
+            nonfinite |= ok && !finite;
+            sm[u] = ballot(surv);
+            wtotal += (uint32_t)__popcll(sm[u]);
         }
+        if (wtotal != 0) {
+            uint32_t base = 0;
+            if (lane == 0) base = atomicAdd(&rs->nsurv, wtotal);
+            base = uniform_u32(__shfl((int)base, 0));
+#pragma unroll
+            for (uint32_t u = 0; u < UN; ++u) {
+                if ((sm[u] >> lane) & 1ull) {
+                    const uint32_t at = base + lanes_below(sm[u]);
+                    if (at < SURV_CAP) list[at] = composite(kk[u], b + u * FULL_THREADS + threadIdx.x);
+                }
+                base += (uint32_t)__popcll(sm[u]);
+            }
+            if (base > SURV_CAP && lane == 0) atomicOr(&rs->overflow, 1u);
+        }
+        if (ballot(nonfinite) != 0 && lane == 0) atomicOr(&rs->overflow, 1u);
         stop = __hip_atomic_load(&rs->overflow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
     }
     for (int m = 32; m >= 1; m >>= 1) {
