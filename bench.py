@@ -19,10 +19,11 @@ times the head followed by sampling its logits, the device path from hidden
 state to token.
 
 Prints one JSON line. `roofline.achieved` is the workload's algorithmic bytes
-per call divided by the average duration of a call, timed with HIP events on
-the stream the kernels run on. `cpu_baseline` times the oracle (the C
-restatement of the reference sampler) on one host core over a bounded sample
-of the same rows.
+per call divided by the average duration of a call: the timed calls run back
+to back between one pair of HIP events on the stream the kernels run on, and
+the region's time is divided by the number of calls. `cpu_baseline` times the
+oracle (the C restatement of the reference sampler) on one host core over a
+bounded sample of the same rows, `cpu_baseline_threads` on the host's threads.
 """
 import argparse
 import json
@@ -171,22 +172,34 @@ def head_cpu_baseline(w, x, budget_s):
 
 
 def time_calls(step, args, stream):
-    """args.warmup untimed calls, then args.steps timed ones: (wall ms per
-    step, sorted per-call HIP-event ms on `stream`)."""
+    """args.warmup untimed calls, then args.steps timed ones, back to back,
+    bracketed by one HIP-event pair on `stream` (an event recorded between two
+    calls delays the next launch by several microseconds, so none is). Returns
+    (wall ms per step, HIP-event ms per call over the timed region, sorted
+    per-call HIP-event ms from a separate, untimed pass of args.steps calls
+    each between its own events: the spread, not the throughput)."""
     import torch
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    t_start.record(stream)
+    for _ in range(args.steps):
+        step()
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    region_ms = t_start.elapsed_time(t_end) / args.steps
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    t_wall = time.perf_counter()
     for i in range(args.steps):
         starts[i].record(stream)
         step()
         ends[i].record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t_wall
-    return wall * 1e3 / args.steps, sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
+    return wall * 1e3 / args.steps, region_ms, sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
 
 
 def bench_embed(args):
@@ -212,14 +225,13 @@ def bench_embed(args):
     def step():
         head.embed_into(d_tok, d_out, stream=stream.cuda_stream)
 
-    ms_per_step, per_call_ms = time_calls(step, args, stream)
-    mean_ms = sum(per_call_ms) / len(per_call_ms)
+    ms_per_step, mean_ms, per_call_ms = time_calls(step, args, stream)
     median_ms = per_call_ms[len(per_call_ms) // 2]
     nb = -(-W.HEAD_K // 256)
     # Per token: the id, its row's blocks, the f32 row written.
     alg_bytes = n * (4 + nb * W.Q6K_BLOCK_BYTES + W.HEAD_K * 4)
     achieved = alg_bytes / (mean_ms / 1e3) / 1e9
-    print("[bench] embed %d tokens: wall %.4f ms/step, events mean %.4f median %.4f min %.4f max %.4f ms" % (
+    print("[bench] embed %d tokens: wall %.4f ms/step, events %.4f ms per call over the timed region; alone: median %.4f min %.4f max %.4f ms" % (
         n, ms_per_step, mean_ms, median_ms, per_call_ms[0], per_call_ms[-1]), file=sys.stderr, flush=True)
     if args.calibration_copy > 0:
         dst = torch.empty_like(d_out)
@@ -265,7 +277,7 @@ def bench_embed(args):
             "traffic": traffic_bytes("embed_n%d" % n),
             "algorithmic_bytes_per_call": alg_bytes,
             "call_ms_mean": round(mean_ms, 5),
-            "call_ms_median": round(median_ms, 5),
+            "call_ms_median_alone": round(median_ms, 5),
         },
         "cpu_baseline": cpu,
     }
@@ -315,8 +327,7 @@ def bench_head(args):
                             window_stride=W.WINDOW, window_len=d_wlen, uniforms=d_uni, out_ids=out_ids,
                             out_probs=out_probs, cand_stride=cs, stream=stream.cuda_stream)
 
-    ms_per_step, per_call_ms = time_calls(step, args, stream)
-    mean_ms = sum(per_call_ms) / len(per_call_ms)
+    ms_per_step, mean_ms, per_call_ms = time_calls(step, args, stream)
     median_ms = per_call_ms[len(per_call_ms) // 2]
     weight_bytes = W.HEAD_ROWS * (-(-W.HEAD_K // 256)) * W.Q6K_BLOCK_BYTES
     # Weights once, the hidden rows, the logits written; sampling re-reads the
@@ -325,7 +336,7 @@ def bench_head(args):
     if sample:
         alg_bytes += t * (W.HEAD_ROWS * 4 + W.WINDOW * 4 + 4 + 4 + 4 + 1 + 20 * 8)
     achieved = alg_bytes / (mean_ms / 1e3) / 1e9
-    print("[bench] head t=%d%s: wall %.3f ms/step, events mean %.3f median %.3f min %.3f max %.3f ms" % (
+    print("[bench] head t=%d%s: wall %.3f ms/step, events %.3f ms per call over the timed region; alone: median %.3f min %.3f max %.3f ms" % (
         t, " + sample" if sample else "", ms_per_step, mean_ms, median_ms, per_call_ms[0], per_call_ms[-1]),
         file=sys.stderr, flush=True)
     if args.calibration_copy > 0:
@@ -369,7 +380,7 @@ def bench_head(args):
             "traffic": None if sample else traffic_bytes("head_t%d" % t),
             "algorithmic_bytes_per_call": alg_bytes,
             "call_ms_mean": round(mean_ms, 5),
-            "call_ms_median": round(median_ms, 5),
+            "call_ms_median_alone": round(median_ms, 5),
         },
         "cpu_baseline": cpu,
     }
@@ -431,29 +442,15 @@ def main():
         else:
             ctx.argmax_rows(d_logits, wl.rows, d_logits.stride(0), out_tok, stream=stream.cuda_stream)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    t_wall = time.perf_counter()
-    for i in range(args.steps):
-        starts[i].record(stream)
-        step()
-        ends[i].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_wall
-    per_call_ms = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
-    mean_ms = sum(per_call_ms) / len(per_call_ms)
+    ms_per_step, mean_ms, per_call_ms = time_calls(step, args, stream)
     median_ms = per_call_ms[len(per_call_ms) // 2]
-    ms_per_step = wall * 1e3 / args.steps
     rows_per_s = wl.rows / (ms_per_step / 1e3)
     if args.op == "sample":
         alg_bytes = wl.algorithmic_bytes() if cs else wl.algorithmic_bytes(kept_out=0)
     else:  # the logits once, and a token (and a probability) per row
         alg_bytes = wl.rows * (wl.vocab * 4 + 4 + (4 if args.op == "top_probability" else 0))
     achieved = alg_bytes / (mean_ms / 1e3) / 1e9
-    print("[bench] %s: wall %.3f ms/step, events mean %.3f median %.3f min %.3f max %.3f ms" % (
+    print("[bench] %s: wall %.3f ms/step, events %.3f ms per call over the timed region; alone: median %.3f min %.3f max %.3f ms" % (
         name, ms_per_step, mean_ms, median_ms, per_call_ms[0], per_call_ms[-1]), file=sys.stderr, flush=True)
 
     if args.calibration_copy > 0:
@@ -516,7 +513,7 @@ def main():
             "traffic": traffic_bytes(name) if args.op == "sample" else None,
             "algorithmic_bytes_per_call": alg_bytes,
             "call_ms_mean": round(mean_ms, 5),
-            "call_ms_median": round(median_ms, 5),
+            "call_ms_median_alone": round(median_ms, 5),
         },
         "cpu_baseline": cpu,
         "cpu_baseline_threads": cpu_n,
