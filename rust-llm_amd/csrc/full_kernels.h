@@ -221,6 +221,7 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
 }
 
 constexpr uint32_t SORT_ITEMS = 8;                          // elements per lane per tile
+constexpr uint32_t SORT_UN = 8;                             // loads in flight per thread in the key scans
 constexpr uint32_t SORT_TILE = SORT_THREADS * SORT_ITEMS;    // elements per tile
 constexpr uint32_t WAVE_SEG = WAVE * SORT_ITEMS;             // a wave's contiguous share of a tile
 
@@ -325,15 +326,17 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
     __syncthreads();
     {
         uint32_t or0 = 0u, and0 = 0xFFFFFFFFu, or1 = 0u, and1 = 0xFFFFFFFFu;
-        for (uint32_t base = 0; base < V; base += SORT_THREADS * 4) {
-            uint32_t kk[4];
+        for (uint32_t base = 0; base < V; base += SORT_THREADS * SORT_UN) {
+            // Clamped, unconditional loads: a branch around each load would
+            // make the loop wait for every load before the first use.
+            uint32_t kk[SORT_UN];
 #pragma unroll
-            for (uint32_t u = 0; u < 4; ++u) {
+            for (uint32_t u = 0; u < SORT_UN; ++u) {
                 const uint32_t j = base + u * SORT_THREADS + tid;
-                kk[u] = j < V ? ((const RL_GLB uint32_t *)kin)[j] : 0u;
+                kk[u] = ((const RL_GLB uint32_t *)kin)[j < V ? j : V - 1];
             }
 #pragma unroll
-            for (uint32_t u = 0; u < 4; ++u) {
+            for (uint32_t u = 0; u < SORT_UN; ++u) {
                 if (base + u * SORT_THREADS + tid < V) {
                     if (kk[u] >> 31) {
                         or1 |= kk[u];
@@ -376,15 +379,15 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
     for (uint32_t i = tid; i < 4 * 256; i += SORT_THREADS) (&hist[0][0])[i] = 0;
     __syncthreads();
     if (need[0] || need[1] || need[2] || need[3]) {
-        for (uint32_t base = 0; base < V; base += SORT_THREADS * 4) {
-            uint32_t kk[4];
+        for (uint32_t base = 0; base < V; base += SORT_THREADS * SORT_UN) {
+            uint32_t kk[SORT_UN];
 #pragma unroll
-            for (uint32_t u = 0; u < 4; ++u) {
+            for (uint32_t u = 0; u < SORT_UN; ++u) {
                 const uint32_t j = base + u * SORT_THREADS + tid;
-                kk[u] = j < V ? ((const RL_GLB uint32_t *)kin)[j] : 0u;
+                kk[u] = ((const RL_GLB uint32_t *)kin)[j < V ? j : V - 1];
             }
 #pragma unroll
-            for (uint32_t u = 0; u < 4; ++u) {
+            for (uint32_t u = 0; u < SORT_UN; ++u) {
                 if (base + u * SORT_THREADS + tid < V) {
 #pragma unroll
                     for (uint32_t t = 0; t < 4; ++t)
@@ -428,8 +431,8 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
 #pragma unroll
         for (uint32_t i = 0; i < SORT_ITEMS; ++i) {
             const uint32_t e = wave * WAVE_SEG + lane + i * WAVE;
-            nk[i] = e < V ? ((const RL_GLB uint32_t *)kin)[e] : 0u;
-            ni[i] = e < V ? ((const RL_GLB uint32_t *)iin)[e] : 0u;
+            nk[i] = ((const RL_GLB uint32_t *)kin)[e < V ? e : V - 1];  // clamped; past V unused
+            ni[i] = ((const RL_GLB uint32_t *)iin)[e < V ? e : V - 1];
         }
         for (uint32_t tb = 0; tb < V; tb += SORT_TILE) {
             const uint32_t e0 = tb + wave * WAVE_SEG + lane;
@@ -440,8 +443,8 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
                 kk[i] = nk[i];
                 ii[i] = ni[i];
                 const uint32_t e = e0 + SORT_TILE + i * WAVE;
-                nk[i] = e < V ? ((const RL_GLB uint32_t *)kin)[e] : 0u;
-                ni[i] = e < V ? ((const RL_GLB uint32_t *)iin)[e] : 0u;
+                nk[i] = ((const RL_GLB uint32_t *)kin)[e < V ? e : V - 1];
+                ni[i] = ((const RL_GLB uint32_t *)iin)[e < V ? e : V - 1];
             }
             for (uint32_t d = lane; d < 256; d += WAVE) cnt[wave][d] = 0;
             wave_lds_sync();
