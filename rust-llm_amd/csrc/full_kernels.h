@@ -309,7 +309,10 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
     __shared__ uint32_t pos[SORT_WAVES][256];
     __shared__ uint32_t cls[4];  // OR and AND of the keys with the top bit clear, then set
     __shared__ uint32_t tcount[256], tstart[256];
-    __shared__ uint32_t tile_k[SORT_TILE], tile_i[SORT_TILE];
+    // The tile's keys and ids during the passes; before them, each wave's
+    // private digit histograms ([wave][digit position][256], the same size).
+    __shared__ uint32_t tile_ki[2 * SORT_TILE];
+    static_assert(SORT_WAVES * 4 * 256 <= 2 * SORT_TILE, "private histograms fit the tile buffers");
     const uint32_t slot = blockIdx.x;
     if (f.row[slot].done) return;
     const uint32_t row = a.rows[slot];
@@ -375,10 +378,14 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
     need[3] = ((all_or ^ all_and) >> 24) != 0;
 
     // Histograms of the digits that are sorted on (values flipped, 255 - d,
-    // for a descending order).
-    for (uint32_t i = tid; i < 4 * 256; i += SORT_THREADS) (&hist[0][0])[i] = 0;
+    // for a descending order). Each wave counts into its own histograms, so
+    // only lanes of one instruction contend for a counter (many equal keys
+    // would otherwise serialise every wave on it); they are summed after.
+    RL_LDS uint32_t *ph = (RL_LDS uint32_t *)tile_ki;
+    for (uint32_t i = tid; i < SORT_WAVES * 4 * 256; i += SORT_THREADS) ph[i] = 0;
     __syncthreads();
     if (need[0] || need[1] || need[2] || need[3]) {
+        uint32_t hot[4] = {256u, 256u, 256u, 256u};  // wave-uniform; 256: none yet
         for (uint32_t base = 0; base < V; base += SORT_THREADS * SORT_UN) {
             uint32_t kk[SORT_UN];
 #pragma unroll
@@ -388,13 +395,35 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
             }
 #pragma unroll
             for (uint32_t u = 0; u < SORT_UN; ++u) {
-                if (base + u * SORT_THREADS + tid < V) {
+                const bool valid = base + u * SORT_THREADS + tid < V;
 #pragma unroll
-                    for (uint32_t t = 0; t < 4; ++t)
-                        if (need[t]) atomicAdd(&hist[t][255u - ((kk[u] >> (8 * t)) & 255u)], 1u);
+                for (uint32_t t = 0; t < 4; ++t) {
+                    if (!need[t]) continue;
+                    const uint32_t d = 255u - ((kk[u] >> (8 * t)) & 255u);
+                    // The lanes holding the wave's hot digit add once, through
+                    // their first lane; the others one by one.
+                    const uint64_t hm = ballot(valid && d == hot[t]);
+                    if (hm != 0 && lanes_below(hm) == 0 && ((hm >> lane) & 1ull))
+                        atomicAdd(&tile_ki[(wave * 4 + t) * 256 + hot[t]], (uint32_t)__popcll(hm));
+                    if (valid && d != hot[t]) atomicAdd(&tile_ki[(wave * 4 + t) * 256 + d], 1u);
+                    // The hot digit follows the most frequent one seen: the
+                    // first other lane's digit replaces it when it is held by
+                    // more lanes of this step.
+                    const uint64_t rest = ballot(valid) & ~hm;
+                    if (rest != 0) {
+                        const uint32_t c = uniform_u32(
+                            (uint32_t)__builtin_amdgcn_readlane((int)d, (int)__builtin_ctzll(rest)));
+                        if (__popcll(ballot(valid && d == c)) > __popcll(hm)) hot[t] = c;
+                    }
                 }
             }
         }
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < 4 * 256; i += SORT_THREADS) {  // i = t * 256 + d
+        uint32_t c = 0;
+        for (uint32_t w = 0; w < SORT_WAVES; ++w) c += ph[w * 4 * 256 + i];
+        (&hist[0][0])[i] = c;
     }
     __syncthreads();
 
@@ -402,7 +431,7 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
     // reordered by digit in LDS, and written out in runs, so that consecutive
     // lanes write consecutive addresses.
     uint32_t *kout = f.keyB + (uint64_t)slot * V, *iout = f.idB + (uint64_t)slot * V;
-    RL_LDS uint32_t *lk = (RL_LDS uint32_t *)tile_k, *li = (RL_LDS uint32_t *)tile_i;
+    RL_LDS uint32_t *lk = (RL_LDS uint32_t *)tile_ki, *li = (RL_LDS uint32_t *)tile_ki + SORT_TILE;
     for (uint32_t t = 0; t < 4; ++t) {
         if (!need[t]) continue;
         if (tid < WAVE) {  // offs = exclusive prefix of the histogram
