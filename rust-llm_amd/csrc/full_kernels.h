@@ -1223,11 +1223,14 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_norm(RowIO a, FullScratch
             const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
             if (j < j1) {
                 const float q = pp[u] * st.inv;
-                probs[j] = q;
                 if (!(q <= 3.40282347e38f)) qbad = 1;
+                // The draw reads the normalised list from the caller's
+                // candidate output when there is one, else from probs.
                 if (a.out_ids) {
                     a.out_ids[(uint64_t)row * a.cand_stride + j] = iv[u];
                     a.out_probs[(uint64_t)row * a.cand_stride + j] = q;
+                } else {
+                    probs[j] = q;
                 }
             }
         }
@@ -1251,7 +1254,9 @@ __global__ __launch_bounds__(REPLAY_THREADS) void k_full_draw(RowIO a, FullScrat
     const uint32_t V = a.vocab;
     const uint32_t m = st.m;
     const uint32_t *ids = f.idA + (uint64_t)slot * V;
-    const float *probs = f.probs + (uint64_t)slot * V;
+    // The normalised list k_full_norm wrote (the caller's candidates when
+    // requested).
+    const float *probs = a.out_probs ? a.out_probs + (uint64_t)row * a.cand_stride : f.probs + (uint64_t)slot * V;
     const float u = a.uniforms[row];
     uint32_t pick;
     if (!st.qbad) {
