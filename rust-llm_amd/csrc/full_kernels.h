@@ -136,6 +136,9 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch
     uint32_t *keys = f.keyA + (uint64_t)slot * V;
     uint32_t *ids = f.idA + (uint64_t)slot * V;
     const bool vstore = ((reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(ids)) & 15u) == 0;
+    // The ids in id order are written only for a row that keeps that order
+    // (no sort); the sort's first pass makes them from positions.
+    const bool write_ids = identity_order(s, V);
     float mx = -__builtin_inff();
     uint64_t am = 0;
     auto take = [&](float x, uint32_t id) {
@@ -170,12 +173,12 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch
             if (vstore) {
                 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
                 *(RL_GLB u32x4 *)(keys + 4 * qq) = u32x4{kk[0], kk[1], kk[2], kk[3]};
-                *(RL_GLB u32x4 *)(ids + 4 * qq) = u32x4{4 * qq, 4 * qq + 1, 4 * qq + 2, 4 * qq + 3};
+                if (write_ids) *(RL_GLB u32x4 *)(ids + 4 * qq) = u32x4{4 * qq, 4 * qq + 1, 4 * qq + 2, 4 * qq + 3};
             } else {
 #pragma unroll
                 for (uint32_t c = 0; c < 4; ++c) {
                     keys[4 * qq + c] = kk[c];
-                    ids[4 * qq + c] = 4 * qq + c;
+                    if (write_ids) ids[4 * qq + c] = 4 * qq + c;
                 }
             }
         }
@@ -185,7 +188,7 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch
         if (e < V) {
             const float x = ((const RL_GLB float *)rowp)[e];
             keys[e] = total_key(x);
-            ids[e] = e;
+            if (write_ids) ids[e] = e;
             take(x, e);
         }
     }
@@ -431,6 +434,9 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
     // reordered by digit in LDS, and written out in runs, so that consecutive
     // lanes write consecutive addresses.
     uint32_t *kout = f.keyB + (uint64_t)slot * V, *iout = f.idB + (uint64_t)slot * V;
+    // k_full_keys leaves the ids unwritten for a row that is sorted: the
+    // first pass takes each element's position as its id.
+    bool first = true;
     RL_LDS uint32_t *lk = (RL_LDS uint32_t *)tile_ki, *li = (RL_LDS uint32_t *)tile_ki + SORT_TILE;
     for (uint32_t t = 0; t < 4; ++t) {
         if (!need[t]) continue;
@@ -461,7 +467,7 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
         for (uint32_t i = 0; i < SORT_ITEMS; ++i) {
             const uint32_t e = wave * WAVE_SEG + lane + i * WAVE;
             nk[i] = ((const RL_GLB uint32_t *)kin)[e < V ? e : V - 1];  // clamped; past V unused
-            ni[i] = ((const RL_GLB uint32_t *)iin)[e < V ? e : V - 1];
+            ni[i] = first ? e : ((const RL_GLB uint32_t *)iin)[e < V ? e : V - 1];
         }
         for (uint32_t tb = 0; tb < V; tb += SORT_TILE) {
             const uint32_t e0 = tb + wave * WAVE_SEG + lane;
@@ -473,7 +479,7 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
                 ii[i] = ni[i];
                 const uint32_t e = e0 + SORT_TILE + i * WAVE;
                 nk[i] = ((const RL_GLB uint32_t *)kin)[e < V ? e : V - 1];
-                ni[i] = ((const RL_GLB uint32_t *)iin)[e < V ? e : V - 1];
+                ni[i] = first ? e : ((const RL_GLB uint32_t *)iin)[e < V ? e : V - 1];
             }
             for (uint32_t d = lane; d < 256; d += WAVE) cnt[wave][d] = 0;
             wave_lds_sync();
@@ -541,6 +547,7 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
             if (tid < 256) offs[tid] += tcount[tid];
             __syncthreads();
         }
+        first = false;
         uint32_t *tmp;
         tmp = kin; kin = kout; kout = tmp;
         tmp = iin; iin = iout; iout = tmp;
@@ -550,6 +557,8 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
             kout[j] = kin[j];
             iout[j] = iin[j];
         }
+    } else if (first) {  // no pass ran (every key alike): the ids in id order
+        for (uint32_t j = tid; j < V; j += SORT_THREADS) iin[j] = j;
     }
 }
 
