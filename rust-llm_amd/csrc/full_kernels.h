@@ -818,12 +818,23 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_probs(RowIO a, FullScratc
     double sum = 0.0;
     int emin = 1 << 20;
     uint32_t count = 0, bad = 0, last_in = 0, first_out = 0xFFFFFFFFu;
+    // The next step's keys load while this step's exps are computed (clamped
+    // loads: no branch around them).
+    uint32_t nk[UN];
+    if (j0 < j1) {
+#pragma unroll
+        for (uint32_t u = 0; u < UN; ++u) {
+            const uint32_t j = j0 + u * FULL_THREADS + threadIdx.x;
+            nk[u] = ((const RL_GLB uint32_t *)keys)[j < j1 ? j : j1 - 1];
+        }
+    }
     for (uint32_t b = j0; b < j1; b += FULL_THREADS * UN) {
         uint32_t kk[UN];
 #pragma unroll
         for (uint32_t u = 0; u < UN; ++u) {
-            const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
-            kk[u] = ((const RL_GLB uint32_t *)keys)[j < j1 ? j : j1 - 1];  // clamped: no branch around the load
+            kk[u] = nk[u];
+            const uint32_t j = b + FULL_THREADS * UN + u * FULL_THREADS + threadIdx.x;
+            nk[u] = ((const RL_GLB uint32_t *)keys)[j < j1 ? j : j1 - 1];
         }
 #pragma unroll
         for (uint32_t u = 0; u < UN; ++u) {
