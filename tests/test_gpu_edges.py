@@ -197,3 +197,31 @@ def test_errors_are_status_codes(device):
     torch.cuda.synchronize()
     assert o.cpu().tolist() == [37, 37, 37, 37]
     assert kept.cpu().tolist() == [1, 1, 1, 1]
+
+
+def test_full_path_rows_of_equal_keys(device):
+    # Rows whose keys agree in every digit the sort would rank on (a constant
+    # row, all -0.0), or in all but the sign bit (a mix of +0.0 and -0.0), sent
+    # down the full path (top-k 0): the kept candidates are the ties in
+    # ascending id order (sample.rs:282-286), whatever passes the sort skips.
+    V, rows = 3000, 8
+    rng = np.random.default_rng(77)
+    logits = np.empty((rows, V), np.float32)
+    logits[0] = 1.25
+    logits[1] = -3.0
+    logits[2] = -0.0
+    logits[3] = rng.choice(np.array([0.0, -0.0], np.float32), V)
+    logits[4] = 7.5
+    logits[5] = -np.inf
+    logits[6] = 0.5
+    logits[7] = rng.choice(np.array([0.0, -0.0], np.float32), V)
+    topp = [0.5, 0.9, 0.999, 0.3, 0.01, 0.9, 1.0, 0.75]
+    settings = [R.sampling(1.0 if r % 2 else 0.6, 0, topp[r], 0.0, 1.0, 0, r) for r in range(rows)]
+    windows = np.zeros((rows, 1), np.uint32)
+    wlen = np.zeros(rows, np.uint32)
+    uniforms = rng.random(rows).astype(np.float32)
+    got, want = run_both(device, logits, settings, windows, wlen, uniforms)
+    assert_match("equal keys", got, want, settings)
+    for r in (0, 1, 2, 4):
+        k = int(want["kept"][r])
+        assert np.array_equal(want["ids"][r, :k], np.arange(k, dtype=np.uint32)), r
