@@ -137,6 +137,17 @@ __device__ __forceinline__ uint64_t lane_xor64(uint64_t v) {
     return ((uint64_t)lane_xor<S>((uint32_t)(v >> 32)) << 32) | lane_xor<S>((uint32_t)v);
 }
 
+// The wave's total of v in every lane (butterfly over the lane exchanges).
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+    v += lane_xor<1>(v);
+    v += lane_xor<2>(v);
+    v += lane_xor<4>(v);
+    v += lane_xor<8>(v);
+    v += lane_xor<16>(v);
+    v += lane_xor<32>(v);
+    return v;
+}
+
 // One compare-exchange stage of a bitonic network across the wave: lanes i
 // and i^STRIDE, blocks of SIZE lanes alternately descending and ascending
 // (the final SIZE = 64 block runs in the direction DESC).

@@ -3,23 +3,36 @@
 //
 // The reference accumulates in a fixed order: the probability mass and the
 // top-p cumulative sum in f64 (sample.rs:307-324), the normalising total in
-// f64 (:342) and the draw's cumulative sum in f32 (:349-356). Each partial sum
-// is rounded to the precision P of its type (53 or 24 bits), so a different
-// order or a tree reduction gives different bits. This header reproduces the
-// sequential bits without a sequential loop.
+// f64 (:342) and the draw's cumulative sum in f32 (:349-356); top_probability
+// sums in f64 (forward.rs:1678). Each partial sum is rounded to the precision
+// P of its type (53 or 24 bits), so a different order or a tree reduction
+// gives different bits. This header reproduces the sequential bits without a
+// sequential loop.
 //
 // While the running sum s stays inside one binade [2^E, 2^(E+1)), every value
 // it takes is a multiple of u = 2^(E-P+1), and adding a term x rounds to that
 // grid: s + x -> s + u * rnd(x / u). rnd rounds to nearest; only an exact tie
 // (x / u = q + 1/2) depends on s, through the parity of s / u (ties go to the
 // even significand), and a tie always leaves the significand even. So within a
-// segment each term is a map  parity -> (increment, new parity),  maps compose
-// associatively, and a parallel scan of them gives every partial sum exactly.
-// A term whose exact sum leaves the binade (s + x >= 2^(E+1)) is added with
-// the hardware's own IEEE addition, which starts a new segment; there are at
-// most as many segments as binades the sum passes through.
+// segment each term is a map  parity -> (increment, new parity),  and maps
+// compose associatively. A term whose exact sum leaves the binade
+// (s + x >= 2^(E+1)) is added with the hardware's own IEEE addition, which
+// starts a new segment.
 //
-// The core (grid, term maps, composition) is plain C++ usable on the host,
+// Because a tie fixes the parity, a run of terms needs no general map: it adds
+// `base` steps plus, at its first tie, one step that depends on the parity
+// entering the run, and leaves a parity that is fixed once the run holds a
+// tie (StepRun). Across the 64 lanes of a wave, the parity entering each lane
+// follows from two ballots: the lanes holding a tie and the lanes leaving an
+// odd parity (parity_in).
+//
+// A stretch of terms in which no addition can round needs no segments at all:
+// when s and every term are multiples of the grid of a binade that lies above
+// the stretch's end sum, every partial sum is exactly representable, the
+// sequential sum is the exact sum, and any summation order (an f64 tree)
+// computes it exactly, however many binades the sum crosses on the way.
+//
+// The core (grid, term maps, runs, parities) is plain C++ usable on the host,
 // where a test checks it against sequential loops; the workgroup-wide replay
 // is device code.
 #pragma once
@@ -27,6 +40,7 @@
 #include <string.h>
 
 #if defined(__HIPCC__)
+#include "rl_device.h"
 #define RL_HD __host__ __device__
 #else
 #define RL_HD
@@ -165,57 +179,153 @@ RL_HD inline double add_p(double s, float x) {
     return s + (double)x;
 }
 
+RL_HD inline uint32_t popc64(uint64_t v) { return (uint32_t)__builtin_popcountll(v); }
+
+// Steps of one term are capped at STEP_CAP (above any segment's room, which is
+// at most 2^53), and so is a run's total: sums of a workgroup's capped steps do
+// not wrap around, and a capped sum still reads as leaving the segment.
+constexpr uint64_t STEP_CAP = 1ull << 54;
+
+// A run of consecutive terms on the grid of one segment, as a function of the
+// parity p entering it: it adds base + (tie ? (p ^ c) & 1 : 0) steps, and
+// leaves parity p ^ par without a tie, par with one.
+struct StepRun {
+    uint64_t base;
+    uint32_t tie, c, par;
+};
+
+RL_HD inline StepRun run_identity() { return StepRun{0, 0, 0, 0}; }
+
+// Appends the f32 term with bits xb (finite, >= 0) on the grid 2^uexp.
+RL_HD inline void run_add(StepRun &r, uint32_t xb, int uexp) {
+    bool t;
+    uint64_t q = inc_of(xb, uexp, &t);  // a tie's increment rounded down
+    q = q < STEP_CAP ? q : STEP_CAP;
+    if (!t) {
+        r.base += q;
+        r.par ^= (uint32_t)(q & 1);
+    } else if (!r.tie) {
+        // The parity before this tie is p ^ par; it rounds up iff that plus q is odd.
+        r.tie = 1;
+        r.c = r.par ^ (uint32_t)(q & 1);
+        r.base += q;
+        r.par = 0;
+    } else {
+        r.base += q + ((r.par ^ q) & 1);
+        r.par = 0;
+    }
+}
+
+// Runs 0, 1, ... in order: T has bit i set when run i holds a tie, O when run
+// i's par is 1. The parity entering run i (0 <= i <= 64; 64 means after the
+// last run) is p0 ^ k when *dep is set (p0 enters run 0), and k otherwise.
+RL_HD inline uint32_t parity_in(uint64_t T, uint64_t O, uint32_t i, uint32_t *dep) {
+    const uint64_t below = i ? (~0ull >> (64 - i)) : 0ull;
+    const uint64_t tb = T & below;
+    if (tb == 0) {
+        *dep = 1;
+        return popc64(O & below) & 1u;
+    }
+    *dep = 0;
+    const uint32_t t = 63u - (uint32_t)__builtin_clzll(tb);  // the last run with a tie before i
+    const uint64_t after = below & ~((2ull << t) - 1ull);     // runs t+1 .. i-1, none with a tie
+    return (uint32_t)((O >> t) & 1u) ^ (popc64(O & after) & 1u);
+}
+
+// The exponent of the lowest set bit of a nonzero finite f32 term's value.
+RL_HD inline int low_bit_exp(uint32_t xb) {
+    uint32_t m = xb & 0x7FFFFFu;
+    const int ex = (int)((xb >> 23) & 0xFFu);
+    if (ex != 0) return ex - 150 + __builtin_ctz(m | 0x800000u);
+    return -149 + __builtin_ctz(m);
+}
+
+// The grid exponent of precision-P values in the binade of `up` (> 0, normal):
+// the finest grid on which every P-bit value below 2^(E+1) lies, E = the
+// binade of up.
+template <int P>
+RL_HD inline int grid_exp_of(double up) {
+    const int E = (int)((f64_bits(up) >> 52) & 0x7FF) - 1023;
+    const int gx = E - (P - 1);
+    return (P == 24 && gx < -149) ? -149 : gx;
+}
+
+// Whether the segment's sum g.n * 2^g.uexp (n > 0) is a multiple of 2^gx.
+RL_HD inline bool seg_multiple(const SumSeg &g, int gx) {
+    return g.uexp >= gx || (int)__builtin_ctzll(g.n) >= gx - g.uexp;
+}
+
 #if defined(__HIPCC__)
 // ------------------------------------------------------------- device ---
-// LDS a workgroup of NT threads needs for seq_replay.
+// LDS a workgroup of NT threads needs for seq_replay. The per-wave records
+// alternate between two sets from one pass to the next, so that a pass needs
+// one barrier: a wave writes a set only after every wave has passed the
+// barrier behind which the set was last read.
 template <uint32_t NT>
 struct SeqLds {
-    TermMap wave_map[NT / 64];
-    uint64_t wave_sum[NT / 64];
-    uint32_t wave_tie[NT / 64];
+    uint64_t wave_base[2][NT / 64];  // steps, every tie resolved but the wave's first (capped)
+    double wave_fsum[2][NT / 64];    // f64 sum of the wave's terms
+    uint32_t wave_bits[2][NT / 64];  // bit 0: a tie; bit 1: the first tie's constant; bit 2: par
+    int32_t wave_low[2][NT / 64];    // lowest bit exponent of the wave's nonzero terms
     uint32_t cross, hit, nonzero;
     double s_new;
 };
 
-__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
-    return ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(v >> 32), src) << 32) | (uint32_t)__shfl((int)(uint32_t)v, src);
-}
 __device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v, int d) {
     return ((uint64_t)(uint32_t)__shfl_up((int)(uint32_t)(v >> 32), d) << 32) |
            (uint32_t)__shfl_up((int)(uint32_t)v, d);
 }
-__device__ __forceinline__ uint64_t shfl_xor_sat_sum(uint64_t v) {
-    for (int m = 32; m >= 1; m >>= 1) {
-        const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m) << 32) |
-                           (uint32_t)__shfl_xor((int)(uint32_t)v, m);
-        v = sat_add(v, o);
-    }
+
+// Butterfly totals across the wave with DPP and permlane exchanges (VALU
+// operations, no LDS round trip); every lane gets the same total (the f64
+// additions are commutative, so both lanes of a pair compute the same sum).
+__device__ __forceinline__ uint64_t wave_total_u64(uint64_t v) {
+    v += lane_xor64<1>(v);
+    v += lane_xor64<2>(v);
+    v += lane_xor64<4>(v);
+    v += lane_xor64<8>(v);
+    v += lane_xor64<16>(v);
+    v += lane_xor64<32>(v);
+    return v;
+}
+template <uint32_t S>
+__device__ __forceinline__ double lane_xor_f64(double v) {
+    return f64_from_bits(lane_xor64<S>(f64_bits(v)));
+}
+__device__ __forceinline__ double wave_total_f64(double v) {
+    v += lane_xor_f64<1>(v);
+    v += lane_xor_f64<2>(v);
+    v += lane_xor_f64<4>(v);
+    v += lane_xor_f64<8>(v);
+    v += lane_xor_f64<16>(v);
+    v += lane_xor_f64<32>(v);
+    return v;
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+    v = min(v, (int)lane_xor<1>((uint32_t)v));
+    v = min(v, (int)lane_xor<2>((uint32_t)v));
+    v = min(v, (int)lane_xor<4>((uint32_t)v));
+    v = min(v, (int)lane_xor<8>((uint32_t)v));
+    v = min(v, (int)lane_xor<16>((uint32_t)v));
+    v = min(v, (int)lane_xor<32>((uint32_t)v));
     return v;
 }
 
-__device__ __forceinline__ TermMap shfl_up_map(const TermMap &v, int d) {
-    TermMap o;
-    o.i0 = shfl_up_u64(v.i0, d);
-    o.i1 = shfl_up_u64(v.i1, d);
-    o.p0 = (uint32_t)__shfl_up((int)v.p0, d);
-    o.p1 = (uint32_t)__shfl_up((int)v.p1, d);
-    return o;
-}
-
-// Inclusive scans across the wave: lane i gets lanes 0..i combined in order.
-__device__ __forceinline__ TermMap wave_scan_map(TermMap v) {
-    const uint32_t lane = __lane_id();
-    for (int d = 1; d < 64; d <<= 1) {
-        const TermMap o = shfl_up_map(v, d);
-        if (lane >= (uint32_t)d) v = map_then(o, v);
-    }
-    return v;
-}
-__device__ __forceinline__ uint64_t wave_scan_sum(uint64_t v) {
+// Inclusive scans across the wave (lane i gets lanes 0..i), for the passes
+// that locate an event.
+__device__ __forceinline__ uint64_t wave_incl_u64(uint64_t v) {
     const uint32_t lane = __lane_id();
     for (int d = 1; d < 64; d <<= 1) {
         const uint64_t o = shfl_up_u64(v, d);
-        if (lane >= (uint32_t)d) v = sat_add(o, v);
+        if (lane >= (uint32_t)d) v += o;
+    }
+    return v;
+}
+__device__ __forceinline__ double wave_incl_f64(double v) {
+    const uint32_t lane = __lane_id();
+    for (int d = 1; d < 64; d <<= 1) {
+        const double o = f64_from_bits(shfl_up_u64(f64_bits(v), d));
+        if (lane >= (uint32_t)d) v += o;
     }
     return v;
 }
@@ -225,20 +335,23 @@ __device__ __forceinline__ uint64_t wave_scan_sum(uint64_t v) {
 // threads, ITEMS consecutive terms per thread per tile). fetch(j) returns the
 // raw 32 bits a term is made from and term turns them into the f32 term, so
 // the next tile's fetches stay in flight while the current tile is reduced
-// (a term computed at fetch time would wait for its load there). Returns the first j whose partial sum satisfies
-// pred (a predicate that stays true once true as the sum grows), or n; when
-// it returns n, *sum is the sequential sum of all n terms, and otherwise the
-// partial sum at the returned index. Every thread of the workgroup must call
-// it with the same arguments; it contains barriers.
+// (a term computed at fetch time would wait for its load there). Returns the
+// first j whose partial sum satisfies pred (a predicate that stays true once
+// true as the sum grows), or n; when it returns n, *sum is the sequential sum
+// of all n terms, and otherwise the partial sum at the returned index. Every
+// thread of the workgroup must call it with the same arguments; it contains
+// barriers.
 //
 // Tiles are aligned to NT * ITEMS terms and the next tile is loaded while the
-// current one is reduced. When the sum leaves its segment inside a tile, the
-// rest of the tile is processed again from registers under the new segment.
-// Per pass over a tile: when no remaining term of the tile is an exact rounding
-// tie, every term's increment is independent of the sum, so a block reduction
-// tells whether the sum leaves its segment or meets pred inside the tile, and
-// only then is a block scan needed to find where. A tile holding a tie goes
-// through the parity-carrying term maps instead.
+// current one is reduced. A pass over (the rest of) a tile reduces, per wave,
+// the terms' f64 sum, their lowest bit and their steps on the current
+// segment's grid with the ties resolved (StepRun, parity_in), and the waves'
+// records are combined in order behind one barrier. If no addition in the
+// tile can round, the sum moves to the exact end sum, across binades; else if
+// the steps stay in the segment and pred stays false, the sum moves by them.
+// Otherwise a scan locates the event: the first term whose sum meets pred, or
+// leaves the segment (added with the IEEE addition; the rest of the tile is
+// then processed again from registers under the new segment).
 template <int P, uint32_t NT, uint32_t ITEMS, class Fetch, class Term, class Pred>
 __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t n, Pred pred, SeqLds<NT> *L, double *sum) {
     constexpr uint32_t TILE = NT * ITEMS;
@@ -248,6 +361,7 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
     bool zero = true;
     SumSeg g{0, 0, 0};
     uint32_t pos = 0;  // the next term to add
+    uint32_t set = 0;  // the LDS record set this pass writes
     uint32_t cur = 0xFFFFFFFFu, nxt = 0xFFFFFFFFu;  // bases of the tiles in xb and nb
     uint32_t xb[ITEMS], nb[ITEMS];  // terms of the current tile, raw bits of the next
     if (n > 0 && pred(0.0)) {
@@ -311,74 +425,121 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
             pos = jz + 1;
             continue;
         }
-        const uint32_t par0 = (uint32_t)(g.n & 1);
-        const uint64_t room = g.lim - g.n;
-        uint64_t mine = 0;
-        bool tie = false;
+        // This thread's terms: a run on the segment's grid, their f64 sum and
+        // their lowest bit.
+        StepRun r = run_identity();
+        double fs = 0.0;
+        int low = 0x7FFFFFFF;
 #pragma unroll
         for (uint32_t i = 0; i < ITEMS; ++i) {
-            bool t;
-            mine = sat_add(mine, inc_of(xv[i], g.uexp, &t));
-            tie |= t;
+            run_add(r, xv[i], g.uexp);
+            fs += (double)__uint_as_float(xv[i]);
+            if (xv[i] & 0x7FFFFFFFu) low = min(low, low_bit_exp(xv[i]));
         }
-        const uint64_t wsum = shfl_xor_sat_sum(mine);
-        const bool wtie = __ballot(tie) != 0;
+        r.base = r.base < STEP_CAP ? r.base : STEP_CAP;
+        const uint64_t T = __ballot(r.tie != 0), O = __ballot((r.par & 1u) != 0);
+        uint32_t dep;
+        const uint32_t k = parity_in(T, O, lane, &dep);
+        // The wave's steps with every tie resolved but its first, whose step
+        // depends on the parity entering the wave.
+        const uint64_t wb = wave_total_u64(r.base + ((r.tie && !dep) ? ((k ^ r.c) & 1u) : 0u));
+        const double wf = wave_total_f64(fs);
+        const int wl = wave_min_i32(low);
+        uint32_t bits;
+        if (T != 0) {
+            const uint32_t ft = (uint32_t)__builtin_ctzll(T);
+            const uint32_t cf = (uint32_t)__builtin_amdgcn_readlane((int)r.c, (int)ft);
+            uint32_t d0, d1;
+            const uint32_t kf = parity_in(T, O, ft, &d0);
+            const uint32_t po = parity_in(T, O, 64, &d1);
+            bits = 1u | (((kf ^ cf) & 1u) << 1) | (po << 2);
+        } else {
+            bits = (popc64(O) & 1u) << 2;
+        }
         if (lane == 0) {
-            L->wave_sum[wave] = wsum;
-            L->wave_tie[wave] = wtie ? 1u : 0u;
+            L->wave_base[set][wave] = wb < STEP_CAP ? wb : STEP_CAP;
+            L->wave_fsum[set][wave] = wf;
+            L->wave_bits[set][wave] = bits;
+            L->wave_low[set][wave] = wl;
         }
         if (tid == 0) {
             L->cross = 0xFFFFFFFFu;
             L->hit = 0xFFFFFFFFu;
         }
         __syncthreads();
-        uint64_t total = 0;
-        uint32_t anytie = 0;
+        // The waves in order, from the segment's parity: the tile's steps, the
+        // parity entering this wave and the steps and f64 sum before it.
+        uint32_t p = (uint32_t)(g.n & 1u), pw = 0;
+        uint64_t tot = 0, tot_before = 0;
+        double fsum = 0.0, f_before = 0.0;
+        int lowest = 0x7FFFFFFF;
+#pragma unroll
         for (uint32_t w = 0; w < NW; ++w) {
-            total = sat_add(total, L->wave_sum[w]);
-            anytie |= L->wave_tie[w];
+            if (w == wave) {
+                tot_before = tot;
+                pw = p;
+                f_before = fsum;
+            }
+            const uint32_t b = L->wave_bits[set][w];
+            tot += L->wave_base[set][w] + ((b & 1u) ? ((p ^ (b >> 1)) & 1u) : 0u);
+            p = (b & 1u) ? ((b >> 2) & 1u) : (p ^ ((b >> 2) & 1u));
+            fsum += L->wave_fsum[set][w];
+            lowest = min(lowest, L->wave_low[set][w]);
         }
-        if (!anytie && total < room && !pred(scaled(g.n + total, g.uexp))) {
+        set ^= 1u;
+        // No addition in the rest of the tile rounds when s and every term are
+        // multiples of the grid of a binade above the end sum (the f64 sum
+        // est is within far less than 2^-30 of the exact one, and exact when
+        // this holds: every subset sum is then representable).
+        const double est = s + fsum;
+        const int gx = grid_exp_of<P>(est * (1.0 + 0x1p-30));
+        if (lowest >= gx && seg_multiple(g, gx)) {
+            if (!pred(est)) {
+                s = est;
+                g = seg_of<P>(s);
+                pos = base + TILE;
+                continue;
+            }
+            // Every partial sum is exact: the first that meets pred.
+            const double incl = wave_incl_f64(fs);
+            double run = (s + f_before) + (incl - fs);
+            uint32_t my_hit = 0xFFFFFFFFu;
+            double v_hit = 0.0;
+#pragma unroll
+            for (uint32_t i = 0; i < ITEMS; ++i) {
+                const uint32_t j = j0 + i;
+                if (j >= n || my_hit != 0xFFFFFFFFu) break;
+                if (j < pos) continue;
+                run += (double)__uint_as_float(xv[i]);
+                if (pred(run)) {
+                    my_hit = j;
+                    v_hit = run;
+                }
+            }
+            if (my_hit != 0xFFFFFFFFu) atomicMin(&L->hit, my_hit);
+            __syncthreads();
+            const uint32_t hit = L->hit;
+            if (my_hit == hit) L->s_new = v_hit;
+            __syncthreads();
+            *sum = L->s_new;
+            __syncthreads();
+            return hit;
+        }
+        const uint64_t room = g.lim - g.n;
+        if (tot < room && !pred(scaled(g.n + tot, g.uexp))) {
             // Nothing happens in the rest of this tile.
-            g.n += total;
+            g.n += tot;
             s = scaled(g.n, g.uexp);
             pos = base + TILE;
-            __syncthreads();
             continue;
         }
-        // Something happens here: the exclusive prefix of this thread's terms.
-        uint64_t I;
-        uint32_t par;
-        if (!anytie) {
-            const uint64_t incl = wave_scan_sum(mine);
-            __syncthreads();
-            if (lane == 63) L->wave_sum[wave] = incl;
-            __syncthreads();
-            uint64_t before = 0;
-            for (uint32_t w = 0; w < wave; ++w) before = sat_add(before, L->wave_sum[w]);
-            uint64_t prev = shfl_up_u64(incl, 1);
-            if (lane == 0) prev = 0;
-            I = sat_add(before, prev);
-            par = 0;  // unused without ties
-        } else {
-            TermMap agg = map_identity();
-#pragma unroll
-            for (uint32_t i = 0; i < ITEMS; ++i) agg = map_then(agg, map_of(xv[i], g.uexp));
-            const TermMap incl = wave_scan_map(agg);
-            if (lane == 63) L->wave_map[wave] = incl;
-            __syncthreads();
-            TermMap before = map_identity(), all = map_identity();
-            for (uint32_t w = 0; w < NW; ++w) {
-                if (w < wave) before = map_then(before, L->wave_map[w]);
-                all = map_then(all, L->wave_map[w]);
-            }
-            total = map_inc(all, par0);  // the increment of the rest of the tile, ties included
-            TermMap prev = shfl_up_map(incl, 1);
-            if (lane == 0) prev = map_identity();
-            const TermMap excl = map_then(before, prev);
-            I = map_inc(excl, par0);
-            par = map_parity(excl, par0);
-        }
+        // Something happens here: the parity entering this thread's terms and
+        // the steps before them, then its terms one by one.
+        const uint32_t pl = dep ? (pw ^ k) : k;
+        const uint64_t mine = r.base + (r.tie ? ((pl ^ r.c) & 1u) : 0u);
+        const uint64_t incl = wave_incl_u64(mine);
+        uint64_t I = tot_before + (incl - mine);
+        uint32_t par = pl;
         uint32_t my_cross = 0xFFFFFFFFu, my_hit = 0xFFFFFFFFu, x_cross = 0;
         uint64_t I_cross = 0, I_hit = 0;
 #pragma unroll
@@ -386,16 +547,12 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
             const uint32_t j = j0 + i;
             if (j >= n || my_cross != 0xFFFFFFFFu || my_hit != 0xFFFFFFFFu) break;
             if (j < pos) continue;
-            uint64_t step;
-            if (!anytie) {
-                bool t;
-                step = inc_of(xv[i], g.uexp, &t);
-            } else {
-                const TermMap e = map_of(xv[i], g.uexp);
-                step = map_inc(e, par);
-                par = map_parity(e, par);
-            }
-            const uint64_t In = sat_add(I, step);
+            bool t;
+            uint64_t q = inc_of(xv[i], g.uexp, &t);
+            q = q < STEP_CAP ? q : STEP_CAP;
+            const uint64_t step = t ? q + ((par ^ q) & 1u) : q;
+            par = t ? 0u : (par ^ (uint32_t)(q & 1u));
+            const uint64_t In = I + step;
             if (In >= room) {  // this term's sum leaves the segment
                 my_cross = j;
                 I_cross = I;
@@ -418,24 +575,25 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
             __syncthreads();
             return hit;
         }
-        if (cross != 0xFFFFFFFFu) {
-            if (my_cross == cross) L->s_new = add_p<P>(scaled(g.n + I_cross, g.uexp), __uint_as_float(x_cross));
-            __syncthreads();
-            s = L->s_new;
-            __syncthreads();
-            if (pred(s)) {
-                *sum = s;
-                return cross;
-            }
-            g = seg_of<P>(s);
-            pos = cross + 1;  // the rest of this tile is redone from registers
+        if (cross == 0xFFFFFFFFu) {
+            // Not reached: a step total at or past the room, or pred met at
+            // the end, has its event in this tile. Kept so that every path
+            // moves pos forward.
+            g.n += tot;
+            s = scaled(g.n, g.uexp);
+            pos = base + TILE;
             continue;
         }
-        // Only a tie tile can get here without an event.
-        g.n += total;
-        s = scaled(g.n, g.uexp);
-        pos = base + TILE;
+        if (my_cross == cross) L->s_new = add_p<P>(scaled(g.n + I_cross, g.uexp), __uint_as_float(x_cross));
         __syncthreads();
+        s = L->s_new;
+        __syncthreads();
+        if (pred(s)) {
+            *sum = s;
+            return cross;
+        }
+        g = seg_of<P>(s);
+        pos = cross + 1;  // the rest of this tile is redone from registers
     }
     *sum = s;
     return n;

@@ -64,6 +64,7 @@ struct rl_sampler_ctx {
     uint64_t *d_argmax_part = nullptr;
     uint32_t *d_tp_nan = nullptr;
     double *d_tp_sum = nullptr;
+    uint32_t *d_tp_small = nullptr;  // per chunk: nonzero terms below 2^-26
     std::vector<void *> owned;
     // Host copy of the plan made by configure.
     uint32_t configured = 0;
@@ -140,6 +141,7 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     if (e == hipSuccess) e = c->alloc(&c->d_argmax_part, std::max<size_t>(CHUNK_SLOTS, max_rows));
     if (e == hipSuccess) e = c->alloc(&c->d_tp_nan, std::max<size_t>(CHUNK_SLOTS, max_rows));
     if (e == hipSuccess) e = c->alloc(&c->d_tp_sum, std::max<size_t>(CHUNK_SLOTS, max_rows));
+    if (e == hipSuccess) e = c->alloc(&c->d_tp_small, std::max<size_t>(CHUNK_SLOTS, max_rows));
     if (e != hipSuccess) {
         delete c;
         return hip_fail(e, "hipMalloc");
@@ -349,15 +351,15 @@ int rl_top_probability_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t r
         hipLaunchKernelGGL(k_tp_max<true>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
                            ctx->d_argmax_part, ctx->d_tp_nan);
         hipLaunchKernelGGL(k_tp_sum<true>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
-                           ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum);
+                           ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum, ctx->d_tp_small);
     } else {
         hipLaunchKernelGGL(k_tp_max<false>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
                            ctx->d_argmax_part, ctx->d_tp_nan);
         hipLaunchKernelGGL(k_tp_sum<false>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
-                           ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum);
+                           ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum, ctx->d_tp_small);
     }
     hipLaunchKernelGGL(k_tp_final, dim3(rows), dim3(REPLAY_THREADS), 0, st, logits, stride, vocab, chunks,
-                       ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum, out_token, out_prob);
+                       ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum, ctx->d_tp_small, out_token, out_prob);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "top_probability kernels");
     return RL_OK;

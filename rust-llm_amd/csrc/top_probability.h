@@ -4,12 +4,29 @@
 // (forward.rs:341, :1014-1015), so the bits matter.
 //
 // Three launches: the argmax per chunk (and whether a NaN occurs), the f64
-// sum of the terms per chunk in any order, then per row a certificate: the
-// reference's sequential sum and the chunked one are each within
-// gamma_(V-1) * sum of the exact sum, and (float)(1.0 / s) is monotone in s,
-// so when both ends of that interval round to the same f32 that is the answer.
-// Otherwise (about one row in a few hundred) the row's sequential sum is
-// replayed exactly (rl_seqsum.h).
+// sum of the terms per chunk in any order, then per row a certificate: an
+// interval that holds both the chunked sum's exact value and the reference's
+// sequential sum; (float)(1.0 / s) is monotone in s, so when both ends of the
+// interval give the same f32 that is the answer. Otherwise the row's
+// sequential sum is replayed exactly (rl_seqsum.h).
+//
+// The interval. Every term is at most 1 (exp of a value <= 0) and the best
+// one is exactly 1, so the sum S is at least 1; let E >= 0 be its binade and
+// G = 2^(E-52) the grid of f64 values there. A step s + x of the sequential
+// sum rounds only if x is not a multiple of the grid of the new partial sum
+// (at most G), or if the partial sum enters a new binade. An f32 term
+// x >= 2^(E-29) has its lowest bit at or above 2^(E-52) = G, so only terms
+// below 2^(E-29) can round outside binade changes, and there are at most
+// E + 150 binade changes above the smallest f32. Each rounding is at most
+// G / 2: the sequential sum is within (small + 200) * G / 2 of the exact sum,
+// where small counts the nonzero terms below 2^(E-29). The sum pass counts
+// those below 2^-26, which serves every E <= 3; a larger E falls back to the
+// general bound gamma_(V-1) * S. The chunked sum adds every term
+// into a 32-term sum, those in order per thread, then a tree and the chunks in
+// order: its relative error is at most the depth of that summation times
+// 2^-53. For the rows of a peaked distribution this interval is about a
+// thousand times narrower than gamma_(V-1) * S, and a row almost never needs
+// the replay.
 #pragma once
 #include "full_kernels.h"
 
@@ -96,14 +113,30 @@ __device__ __forceinline__ bool tp_row(const uint64_t *part_am, const uint32_t *
     return nan != 0 || key == 0 || key_value(key) == __builtin_inff();
 }
 
+// Terms counted by the sum pass: nonzero and below 2^-26 (bits 0x32800000).
+constexpr uint32_t TP_SMALL = 0x32800000u;
+
+// The depth of k_tp_sum's summation (the additions any term's value passes
+// through): 32 within a tile, one per tile of the thread, the tail element,
+// six across the wave and three across its waves, then the chunks in
+// k_tp_final.
+__host__ __device__ inline uint32_t tp_sum_depth(uint32_t vocab, uint32_t chunks) {
+    const uint32_t n4 = vocab / 4;
+    const uint32_t per = (n4 + chunks - 1) / chunks;
+    const uint32_t tiles = (per + FAST_THREADS * UNROLL - 1) / (FAST_THREADS * UNROLL);
+    return 32 + tiles + 1 + 6 + (FAST_WAVES - 1) + chunks;
+}
+
 // grid (chunks, rows), FAST_THREADS: per chunk the f64 sum of exp(l_i - best)
-// (forward.rs:1678), in any order.
+// (forward.rs:1678), in any order, and how many terms are small (above).
 template <bool VEC>
 __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, uint64_t stride, uint32_t vocab,
                                                          uint32_t chunks, const uint64_t *part_am,
-                                                         const uint32_t *part_nan, double *part_sum) {
+                                                         const uint32_t *part_nan, double *part_sum,
+                                                         uint32_t *part_small) {
     __shared__ uint64_t exp_tab[32];
     __shared__ double red[FAST_WAVES];
+    __shared__ uint32_t red_c[FAST_WAVES];
     const uint32_t row = blockIdx.y, chunk = blockIdx.x;
     uint64_t am;
     if (tp_row(part_am, part_nan, row, chunks, &am)) return;
@@ -114,37 +147,56 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
     const uint32_t n4 = vocab / 4;
     const uint32_t q0 = chunk_lo(n4, chunk, chunks), q1 = chunk_lo(n4, chunk + 1, chunks);
     double sum = 0.0;
+    uint32_t small = 0;
+    auto add = [&](double &acc, float x) {
+        const float t = expf_libm_t(x - best, etab);
+        acc += (double)t;
+        small += __float_as_uint(t) - 1u < TP_SMALL - 1u ? 1u : 0u;  // +0 wraps round and is not counted
+    };
     // Tiles as in k_tp_max: the next tile's loads overlap this tile's exps.
+    // Each tile's terms are summed on their own, then added to the thread's
+    // sum, which bounds the depth of the summation (tp_sum_depth).
     constexpr uint32_t STEP = FAST_THREADS * UNROLL;
     if (q1 > q0) {
         f32x4 A[UNROLL], B[UNROLL];
         load_tile_clamped<VEC>(A, rowp, q0, q1);
         for (uint32_t b = q0; b < q1; b += STEP) {
             load_tile_clamped<VEC>(B, rowp, b + STEP, q1);
+            double ts = 0.0;
 #pragma unroll
             for (uint32_t u = 0; u < UNROLL; ++u) {
                 if (b + u * FAST_THREADS + threadIdx.x < q1) {
-                    sum += (double)expf_libm_t(A[u].x - best, etab);
-                    sum += (double)expf_libm_t(A[u].y - best, etab);
-                    sum += (double)expf_libm_t(A[u].z - best, etab);
-                    sum += (double)expf_libm_t(A[u].w - best, etab);
+                    add(ts, A[u].x);
+                    add(ts, A[u].y);
+                    add(ts, A[u].z);
+                    add(ts, A[u].w);
                 }
             }
+            sum += ts;
 #pragma unroll
             for (uint32_t u = 0; u < UNROLL; ++u) A[u] = B[u];
         }
     }
     if (chunk == chunks - 1) {
         const uint32_t e = 4 * n4 + threadIdx.x;
-        if (e < vocab) sum += (double)expf_libm_t(((const RL_GLB float *)rowp)[e] - best, etab);
+        if (e < vocab) add(sum, ((const RL_GLB float *)rowp)[e]);
     }
     for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m);
+    small = wave_sum_u32(small);
     const uint32_t wave = threadIdx.x / WAVE;
-    if (lane_id() == 0) red[wave] = sum;
+    if (lane_id() == 0) {
+        red[wave] = sum;
+        red_c[wave] = small;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (uint32_t w = 1; w < FAST_WAVES; ++w) sum += red[w];
-        part_sum[(uint64_t)row * chunks + chunk] = sum;
+        for (uint32_t w = 1; w < FAST_WAVES; ++w) {
+            sum += red[w];
+            small += red_c[w];
+        }
+        const uint64_t at = (uint64_t)row * chunks + chunk;
+        part_sum[at] = sum;
+        part_small[at] = small;
     }
 }
 
@@ -153,7 +205,8 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
 __global__ __launch_bounds__(REPLAY_THREADS) void k_tp_final(const float *logits, uint64_t stride, uint32_t vocab,
                                                              uint32_t chunks, const uint64_t *part_am,
                                                              const uint32_t *part_nan, const double *part_sum,
-                                                             uint32_t *out_token, float *out_prob) {
+                                                             const uint32_t *part_small, uint32_t *out_token,
+                                                             float *out_prob) {
     __shared__ SeqLds<REPLAY_THREADS> seq;
     __shared__ uint64_t exp_tab[32];
     const uint32_t row = blockIdx.x;
@@ -168,11 +221,26 @@ __global__ __launch_bounds__(REPLAY_THREADS) void k_tp_final(const float *logits
         return;
     }
     double S = 0.0;
-    for (uint32_t c = 0; c < chunks; ++c) S += part_sum[(uint64_t)row * chunks + c];
-    // Both the sequential sum and S are within gamma_(V-1) of the exact sum
-    // (gamma_n = n 2^-53 / (1 - n 2^-53)); d bounds their distance, with margin.
-    const double d = 2.25 * ((double)vocab + 64.0) * 0x1p-53;
-    const float lo = (float)(1.0 / (S * (1.0 + d))), hi = (float)(1.0 / (S * (1.0 - d)));
+    uint32_t small = 0;
+    for (uint32_t c = 0; c < chunks; ++c) {
+        const uint64_t at = (uint64_t)row * chunks + c;
+        S += part_sum[at];
+        small += part_small[at];
+    }
+    // The interval (the file's header): S is within dS of the exact sum, the
+    // sequential sum within dq of it.
+    const double dS = 2.0 * (double)tp_sum_depth(vocab, chunks) * 0x1p-53 * S;
+    const double S_up = S * (1.0 + 4.0 * ((double)vocab + 64.0) * 0x1p-53);  // above both sums
+    const int E = (int)((f64_bits(S_up) >> 52) & 0x7FF) - 1023;
+    double dq;
+    if (E <= 3) {
+        dq = ((double)small + 200.0) * mul_pow2(1.0, E - 53);
+    } else {
+        dq = 2.0 * ((double)vocab + 64.0) * 0x1p-53 * S_up;  // gamma_(V-1) * S, with margin
+    }
+    const double D = dS + dq;
+    const double s_lo = (S - D) * (1.0 - 0x1p-50), s_hi = (S + D) * (1.0 + 0x1p-50);
+    const float lo = (float)(1.0 / s_hi), hi = (float)(1.0 / s_lo);
     float prob = lo;
     if (lo != hi) {
         const float *rowp = logits + (uint64_t)row * stride;

@@ -4,11 +4,15 @@
 // For each case: an array of non-negative f32 terms; the plain loop
 // s = fl_P(s + x_j) (P = 24: f32, P = 53: f64) gives every partial sum. The
 // replay walks the same array in tiles of `tile` terms the way the device
-// does: per tile, the composition of the term maps of the current segment,
-// the first term whose partial sum leaves the segment (added with the IEEE
-// addition instead), and the first term whose partial sum meets a monotone
-// predicate. Both the final sums and the predicate indices must agree, bit for
-// bit, for every threshold tried.
+// does: per tile, the exact path when no addition in it can round (the sum
+// moves to the exact end sum, across binades), else the composition of the
+// term maps of the current segment, the first term whose partial sum leaves
+// the segment (added with the IEEE addition instead), and the first term whose
+// partial sum meets a monotone predicate. Both the final sums and the
+// predicate indices must agree, bit for bit, for every threshold tried. It
+// also checks that the device's per-thread runs and ballot parities compose
+// to the same steps and parities as the term maps, and that the term maps
+// compose associatively.
 //
 // Output: one line "ok <cases>" or the first mismatch; exit status 0 on
 // success.
@@ -63,6 +67,9 @@ static void plain(const std::vector<float> &x, std::vector<double> &partial) {
     }
 }
 
+static int failures = 0;
+static long exact_tiles = 0;
+
 // The device algorithm, run serially: returns the first j whose partial sum
 // is >= thr (or > thr when strict), or n; *sum gets the partial sum there, or
 // the final sum when none.
@@ -105,10 +112,44 @@ static uint32_t replay(const std::vector<float> &x, uint32_t tile, double thr, b
             pos = jz + 1;
             continue;
         }
+        // As on the device: when s and every term left in the tile are
+        // multiples of the grid of a binade above the end sum, no addition
+        // rounds, and the f64 sum is the exact sum.
+        {
+            double fsum = 0.0;
+            int lowest = 0x7FFFFFFF;
+            for (uint32_t j = base; j < end; ++j) {
+                fsum += (double)from_bits(term(j));
+                if (term(j) & 0x7FFFFFFFu) lowest = std::min(lowest, low_bit_exp(term(j)));
+            }
+            const double est = s + fsum;
+            const int gx = grid_exp_of<P>(est * (1.0 + 0x1p-30));
+            if (lowest >= gx && seg_multiple(g, gx)) {
+                ++exact_tiles;
+                if (!pred(est)) {
+                    s = est;
+                    g = seg_of<P>(s);
+                    pos = base + tile;
+                    continue;
+                }
+                double run = s;
+                for (uint32_t j = pos; j < end; ++j) {
+                    run += (double)x[j];
+                    if (pred(run)) {
+                        *sum = run;
+                        return j;
+                    }
+                }
+                printf("FAIL exact tile: pred met at the end but not on the way\n");
+                ++failures;
+                return n;
+            }
+        }
         const uint32_t par0 = (uint32_t)(g.n & 1);
         const uint64_t room = g.lim - g.n;
-        // As on the device: a tile without an exact tie uses the plain
-        // increments, a tile with one the parity-carrying maps.
+        // The segment's steps: a tile without an exact tie uses the plain
+        // increments, a tile with one the parity-carrying maps (the device's
+        // runs and parities compose to the same, check_runs).
         bool anytie = false;
         for (uint32_t j = base; j < end; ++j) {
             bool t;
@@ -162,8 +203,6 @@ static uint32_t replay(const std::vector<float> &x, uint32_t tile, double thr, b
     *sum = s;
     return n;
 }
-
-static int failures = 0;
 
 template <int P>
 static void check(const std::vector<float> &x, const char *what, uint32_t tile) {
@@ -222,6 +261,104 @@ static void check_assoc() {
     }
 }
 
+// The workgroup's step arithmetic (StepRun per thread, parity_in across the
+// 64 lanes of a wave from the tie and odd-parity masks, the waves' records
+// combined in order) against the composition of the term maps: the tile's
+// total steps and final parity, and every thread's entering parity and steps
+// before it, from both starting parities. Terms are drawn tie-heavy on a
+// random grid.
+static void check_runs() {
+    for (int rep = 0; rep < 3000; ++rep) {
+        const int uexp = -60 + (int)(rnd() % 30);
+        const uint32_t items = 1 + (uint32_t)(rnd() % 8), nw = 1 + (uint32_t)(rnd() % 4);
+        const uint32_t tie_pct = (uint32_t)(rnd() % 101);
+        const uint32_t n = items * 64 * nw;
+        std::vector<uint32_t> x(n);
+        for (uint32_t i = 0; i < n; ++i) {
+            const uint64_t q = rnd() % 1024;
+            const uint32_t kind = (uint32_t)(rnd() % 100);
+            float v;
+            if (kind < tie_pct)
+                v = ldexpf((float)(2 * q + 1), uexp - 1);  // an exact tie on the grid
+            else if (kind % 4 == 0)
+                v = 0.0f;
+            else if (kind % 4 == 1)
+                v = ldexpf((float)q, uexp);  // a multiple of the step
+            else
+                v = ldexpf((float)(rnd() % (1u << 20)), uexp - 10);  // anything in between
+            x[i] = fbits(v);
+        }
+        for (uint32_t p0 = 0; p0 < 2; ++p0) {
+            // Per thread and per wave, as the device computes them.
+            std::vector<StepRun> run(64 * nw);
+            std::vector<uint32_t> k(64 * nw), dep(64 * nw);
+            std::vector<uint64_t> wbase(nw);
+            std::vector<uint32_t> wbits(nw);
+            for (uint32_t w = 0; w < nw; ++w) {
+                uint64_t T = 0, O = 0;
+                for (uint32_t l = 0; l < 64; ++l) {
+                    StepRun r = run_identity();
+                    for (uint32_t i = 0; i < items; ++i) run_add(r, x[((w * 64 + l) * items) + i], uexp);
+                    run[w * 64 + l] = r;
+                    if (r.tie) T |= 1ull << l;
+                    if (r.par & 1) O |= 1ull << l;
+                }
+                uint64_t wb = 0;
+                for (uint32_t l = 0; l < 64; ++l) {
+                    const StepRun &r = run[w * 64 + l];
+                    k[w * 64 + l] = parity_in(T, O, l, &dep[w * 64 + l]);
+                    wb += r.base + ((r.tie && !dep[w * 64 + l]) ? ((k[w * 64 + l] ^ r.c) & 1u) : 0u);
+                }
+                uint32_t bits;
+                if (T) {
+                    const uint32_t ft = (uint32_t)__builtin_ctzll(T);
+                    uint32_t d0, d1;
+                    const uint32_t kf = parity_in(T, O, ft, &d0);
+                    const uint32_t po = parity_in(T, O, 64, &d1);
+                    bits = 1u | (((kf ^ run[w * 64 + ft].c) & 1u) << 1) | (po << 2);
+                } else {
+                    bits = (popc64(O) & 1u) << 2;
+                }
+                wbase[w] = wb;
+                wbits[w] = bits;
+            }
+            uint32_t p = p0;
+            uint64_t tot = 0;
+            std::vector<uint64_t> before(nw);
+            std::vector<uint32_t> pin(nw);
+            for (uint32_t w = 0; w < nw; ++w) {
+                before[w] = tot;
+                pin[w] = p;
+                const uint32_t b = wbits[w];
+                tot += wbase[w] + ((b & 1u) ? ((p ^ (b >> 1)) & 1u) : 0u);
+                p = (b & 1u) ? ((b >> 2) & 1u) : (p ^ ((b >> 2) & 1u));
+            }
+            // The maps, term by term.
+            TermMap acc = map_identity();
+            for (uint32_t w = 0; w < nw; ++w) {
+                uint64_t I = before[w];
+                for (uint32_t l = 0; l < 64; ++l) {
+                    const uint32_t t = w * 64 + l;
+                    const uint32_t pl = dep[t] ? (pin[w] ^ k[t]) : k[t];
+                    if (map_inc(acc, p0) != I || map_parity(acc, p0) != pl) {
+                        if (failures++ < 5)
+                            printf("FAIL runs: thread %u of %u, items %u, p0 %u: steps %llu/%llu parity %u/%u\n", t,
+                                   64 * nw, items, p0, (unsigned long long)I,
+                                   (unsigned long long)map_inc(acc, p0), pl, map_parity(acc, p0));
+                        return;
+                    }
+                    I += run[t].base + (run[t].tie ? ((pl ^ run[t].c) & 1u) : 0u);
+                    for (uint32_t i = 0; i < items; ++i) acc = map_then(acc, map_of(x[t * items + i], uexp));
+                }
+            }
+            if (map_inc(acc, p0) != tot || map_parity(acc, p0) != p) {
+                if (failures++ < 5) printf("FAIL runs: tile total, items %u, p0 %u\n", items, p0);
+                return;
+            }
+        }
+    }
+}
+
 template <int P>
 static void run_all(int &cases) {
     const uint32_t tiles[] = {1, 7, 64, 2048};
@@ -265,10 +402,15 @@ static void run_all(int &cases) {
 int main() {
     int cases = 0;
     check_assoc();
+    check_runs();
     run_all<24>(cases);
     run_all<53>(cases);
     if (failures) {
         printf("%d failures\n", failures);
+        return 1;
+    }
+    if (exact_tiles == 0) {
+        printf("FAIL no tile took the exact path\n");
         return 1;
     }
     printf("ok %d\n", cases);

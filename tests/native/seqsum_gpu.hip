@@ -1,0 +1,65 @@
+// Test harness (not part of the library): runs the device replay of
+// sequential sums (rust-llm_amd/csrc/rl_seqsum.h) on arbitrary term arrays,
+// one workgroup per case, with the library's own workgroup shape and with a
+// second one, so that tests/test_gpu_seqsum.py can compare every result with
+// plain sequential loops on the host.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "full_kernels.h"
+
+namespace {
+
+// mode 0: never stops; 1: stops at the first partial sum >= thr; 2: > thr.
+struct CasePred {
+    double thr;
+    uint32_t mode;
+    __device__ bool operator()(double v) const { return mode == 1 ? v >= thr : (mode == 2 ? v > thr : false); }
+};
+
+template <int P, uint32_t NT, uint32_t ITEMS>
+__global__ __launch_bounds__(NT) void k_seqsum_cases(const float *terms, const uint64_t *off, const uint32_t *n,
+                                                     const double *thr, const uint32_t *mode, uint32_t *out_idx,
+                                                     double *out_sum) {
+    __shared__ rl::SeqLds<NT> seq;
+    const uint32_t c = blockIdx.x;
+    const float *x = terms + off[c];
+    const CasePred pred{thr[c], mode[c]};
+    double sum = -1.0;
+    const uint32_t idx = rl::seq_replay<P, NT, ITEMS>(
+        [x](uint32_t j) { return ((const RL_GLB float *)x)[j]; }, n[c], pred, &seq, &sum);
+    if (threadIdx.x == 0) {
+        out_idx[c] = idx;
+        out_sum[c] = sum;
+    }
+}
+
+template <int P, uint32_t NT, uint32_t ITEMS>
+int launch(const float *terms, const uint64_t *off, const uint32_t *n, const double *thr, const uint32_t *mode,
+           uint32_t cases, uint32_t *out_idx, double *out_sum, hipStream_t st) {
+    hipLaunchKernelGGL((k_seqsum_cases<P, NT, ITEMS>), dim3(cases), dim3(NT), 0, st, terms, off, n, thr, mode, out_idx,
+                       out_sum);
+    return (int)hipGetLastError();
+}
+
+}  // namespace
+
+// shape 0: the library's (REPLAY_THREADS threads, SEQ_ITEMS terms each);
+// shape 1: 128 threads, 3 terms each. Every pointer is device memory; a
+// case's terms are terms[off[c] .. off[c] + n[c]).
+extern "C" int seqsum_gpu_run(int precision, int shape, const float *terms, const uint64_t *off, const uint32_t *n,
+                              const double *thr, const uint32_t *mode, uint32_t cases, uint32_t *out_idx,
+                              double *out_sum, void *stream) {
+    if (cases == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    if (shape == 0) {
+        if (precision == 24)
+            return launch<24, rl::REPLAY_THREADS, rl::SEQ_ITEMS>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
+        if (precision == 53)
+            return launch<53, rl::REPLAY_THREADS, rl::SEQ_ITEMS>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
+    } else if (shape == 1) {
+        if (precision == 24) return launch<24, 128, 3>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
+        if (precision == 53) return launch<53, 128, 3>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
+    }
+    return -1;
+}

@@ -1,0 +1,157 @@
+"""The device replay of sequential sums (rust-llm_amd/csrc/rl_seqsum.h) on the
+GPU, against plain sequential loops on the host, bit for bit.
+
+The reference's sums are sequential: f64 for the probability mass, the top-p
+cumulative sum and the normalising total (sample.rs:307-324, :342) and for
+top_probability (forward.rs:1678), f32 for the draw (sample.rs:349-356). The
+harness tests/native/seqsum_gpu.hip runs the device replay on arbitrary term
+arrays, one workgroup per case, with the library's workgroup shape and a
+second one (128 threads of 3 terms). Each case asks for the whole sum or for
+the first partial sum >= or > a threshold (every partial sum, its neighbours,
+0 and -1); numpy's cumulative sums (sequential, in the terms' precision) give
+the expected index and value.
+
+Cases: uniform, wide and very wide ranges, narrow values whose sums stay
+exact across binades, subnormals, mostly zeros, two values, short
+significands, values near 1, runs of exact rounding ties in f32 and in f64,
+constant runs, the exp terms of a 248 320-wide top_probability row, sorted
+and unsorted, lengths 0 to 248 320.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(ROOT, "tests", "native", "libseqsum_gpu.so")
+
+
+def harness():
+    if not os.path.exists(LIB):
+        raise RuntimeError("%s is not built (make -C tests/native)" % LIB)
+    lib = ctypes.CDLL(LIB)
+    lib.seqsum_gpu_run.argtypes = [ctypes.c_int, ctypes.c_int] + [ctypes.c_void_p] * 5 + [ctypes.c_uint32] + \
+        [ctypes.c_void_p] * 3
+    lib.seqsum_gpu_run.restype = ctypes.c_int
+    return lib
+
+
+def term_arrays(seed):
+    g = np.random.default_rng(seed)
+    out = []
+    for rep in range(160):
+        n = int(g.integers(1, 300 if rep < 80 else 5000))
+        kind = rep % 13
+        u = g.random(n)
+        if kind == 0:
+            x = u.astype(np.float32)
+        elif kind == 1:
+            x = np.exp(-40.0 * u).astype(np.float32)
+        elif kind == 2:
+            x = (1.0 + u * 1e-3).astype(np.float32)
+        elif kind == 3:
+            x = g.integers(0, 0x00800000, n, dtype=np.uint32).view(np.float32)
+        elif kind == 4:
+            x = np.where(g.integers(0, 4, n) == 0, u, 0.0).astype(np.float32)
+        elif kind == 5:
+            x = np.where(g.integers(0, 2, n) == 1, np.float32(0.75), np.float32(1.0 / 3.0)).astype(np.float32)
+        elif kind == 6:
+            x = np.ldexp(1.0 + g.integers(0, 8, n) / 8.0, -g.integers(0, 60, n)).astype(np.float32)
+        elif kind == 7:
+            x = (np.uint32(0x3F800000) + g.integers(0, 4, n, dtype=np.uint32)).view(np.float32)
+        elif kind == 8:
+            x = np.exp(-100.0 * u).astype(np.float32)
+        elif kind == 9:
+            x = (u * u * u).astype(np.float32)
+        elif kind == 10:
+            # f32 sums in [1, 2): every odd multiple of 2^-24 is an exact tie.
+            x = np.ldexp(2.0 * g.integers(0, 64, n) + 1.0, -24).astype(np.float32)
+            x[0] = 1.0
+        elif kind == 11:
+            # f64 sums in [1, 2): odd multiples of 2^-53 are exact ties.
+            x = np.ldexp(2.0 * g.integers(0, 1 << 20, n) + 1.0, -53).astype(np.float32)
+            x[0] = 1.0
+        else:
+            x = np.full(n, np.ldexp(float(g.integers(1, 256)), -int(g.integers(8, 28))), np.float32)
+        if rep % 3 == 0:
+            x = np.sort(x)[::-1].copy()
+        out.append(x)
+    out.append(np.zeros(0, np.float32))
+    out.append(np.zeros(700, np.float32))
+    # A top_probability row's terms: exp(l - max) of 248 320 logits N(0, 2^2)
+    # with spikes in [8, 14) (numpy's f32 exp: any f32 terms will do here).
+    lg = (g.standard_normal(248320) * 2.0).astype(np.float32)
+    lg[g.choice(248320, 16, replace=False)] = g.uniform(8.0, 14.0, 16).astype(np.float32)
+    out.append(np.exp(lg - lg.max()).astype(np.float32))
+    # Ties-heavy rows long enough for many tiles, and a long constant run.
+    out.append(np.ldexp(2.0 * g.integers(0, 64, 60000) + 1.0, -24).astype(np.float32))
+    out.append(np.full(100000, np.float32(3.0 / 1024.0)))
+    return out
+
+
+def expected(x, precision, thr, mode):
+    n = x.size
+    p = np.cumsum(x) if precision == 24 else np.cumsum(x.astype(np.float64))
+    p = p.astype(np.float64)
+    if mode == 0:
+        return n, (float(p[-1]) if n else 0.0)
+    hit = p >= thr if mode == 1 else p > thr
+    i = int(np.argmax(hit)) if n and hit.any() else n
+    return i, (float(p[i]) if i < n else (float(p[-1]) if n else 0.0))
+
+
+def run_cases(device, precision, shape, seed):
+    import torch
+    arrays = term_arrays(seed)
+    g = np.random.default_rng(seed + 1)
+    offs, ns, thrs, modes, want = [], [], [], [], []
+    flat, at = [], 0
+    for x in arrays:
+        flat.append(x)
+        p = np.cumsum(x) if precision == 24 else np.cumsum(x.astype(np.float64))
+        p = p.astype(np.float64)
+        picks = [(0.0, 0)]
+        for t in range(4):
+            if x.size == 0:
+                break
+            v = float(p[int(g.integers(0, x.size))])
+            w = int(g.integers(-1, 2))
+            if w:
+                v = float(np.nextafter(v, np.inf if w > 0 else -np.inf))
+            picks.append((v, 1 + (t % 2)))
+        picks += [(0.0, 1), (-1.0, 2), (float(p[-1]) if x.size else 0.0, 2)]
+        for thr, mode in picks:
+            offs.append(at)
+            ns.append(x.size)
+            thrs.append(thr)
+            modes.append(mode)
+            want.append(expected(x, precision, thr, mode))
+        at += x.size
+    terms = torch.from_numpy(np.concatenate(flat)).to(device)
+    d = lambda a, dt: torch.from_numpy(np.asarray(a, dt)).to(device)
+    d_off, d_n = d(offs, np.int64), d(np.asarray(ns, np.uint32).view(np.int32), np.int32)
+    d_thr, d_mode = d(thrs, np.float64), d(np.asarray(modes, np.uint32).view(np.int32), np.int32)
+    cases = len(offs)
+    out_idx = torch.empty(cases, dtype=torch.int32, device=device)
+    out_sum = torch.empty(cases, dtype=torch.float64, device=device)
+    print("seqsum P=%d shape=%d: %d cases, %d terms" % (precision, shape, cases, at), flush=True)
+    rc = harness().seqsum_gpu_run(precision, shape, terms.data_ptr(), d_off.data_ptr(), d_n.data_ptr(),
+                                  d_thr.data_ptr(), d_mode.data_ptr(), cases, out_idx.data_ptr(),
+                                  out_sum.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    gi = out_idx.cpu().numpy().view(np.uint32)
+    gs = out_sum.cpu().numpy()
+    bad = [c for c in range(cases) if gi[c] != want[c][0] or gs[c].tobytes() != np.float64(want[c][1]).tobytes()]
+    assert not bad, "P=%d shape=%d: %d of %d cases differ, first %s: got (%d, %r) want %r (n=%d thr=%r mode=%d)" % (
+        precision, shape, len(bad), cases, bad[0], gi[bad[0]], gs[bad[0]], want[bad[0]], ns[bad[0]], thrs[bad[0]],
+        modes[bad[0]])
+
+
+@pytest.mark.parametrize("precision", [24, 53])
+@pytest.mark.parametrize("shape", [0, 1])
+def test_replay_matches_sequential_loops(device, precision, shape):
+    run_cases(device, precision, shape, seed=1000 + precision + shape)

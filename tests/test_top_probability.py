@@ -8,7 +8,10 @@ The reference returns the argmax (IEEE '>' from -inf, lowest id on a tie) and
 give 1 / (1 + e^(b-a)) in exact f64 terms), the NaN cases of the reference's
 arithmetic, a sum long enough that f32 accumulation would be visibly wrong,
 and a step-by-step recomputation (Python float additions of libm expf
-values) on random rows.
+values) on random rows. The device's certificate (an interval around its own
+f64 sum that holds the sequential sum) is pinned against exact sums (fsum):
+its bound on the sequential sum's error holds on rows built so that every
+addition rounds the same way, and on random rows.
 """
 import math
 
@@ -87,6 +90,63 @@ def test_step_by_step_recomputation():
         for v in x:
             s += float(O.libm_expf(f32(f32(v) - f32(bv))))
         assert O.top_probability(x) == (best, f32(1.0 / s)), n
+
+
+def seq_error_bound(terms):
+    """The device certificate's bound on the sequential sum's distance from the
+    exact sum (rust-llm_amd/csrc/top_probability.h): terms <= 1 with one term
+    exactly 1, E the binade of the sum, (small + 200) * 2^(E-53), small the
+    nonzero terms below 2^-26; None for E > 3."""
+    t = np.asarray(terms, np.float32)
+    S = math.fsum(t.astype(np.float64)) * (1.0 + 1e-12)
+    E = math.frexp(S)[1] - 1
+    if E > 3:
+        return None
+    small = int(np.count_nonzero((t > 0) & (t < 2.0 ** -26)))
+    return (small + 200) * 2.0 ** (E - 53)
+
+
+def test_sequential_sum_error_bound_holds_where_the_rounding_errors_add_up():
+    # 1 followed by k halves of the f64 grid at 1: every addition is an exact
+    # tie and rounds to the even significand, 1.0, so the error grows by
+    # 2^-53 a step; the same with the grid at 2, 4 and 8. A bound that
+    # counted too few terms (a threshold too low, a wrong binade) fails here.
+    # The terms (1 + 2^-23) * 2^(E-30), just below 2^(E-29), also tie at
+    # every step (their lowest bit is half the grid): the largest terms that
+    # can round.
+    for E, lead in ((0, [1.0]), (1, [1.0, 1.0]), (2, [1.0] * 4), (3, [1.0] * 8)):
+        for k, x in ((300, 2.0 ** (E - 53)), (5000, 2.0 ** (E - 53)), (40000, 2.0 ** (E - 53)),
+                     (3000, (1.0 + 2.0 ** -23) * 2.0 ** (E - 30))):
+            terms = np.array(lead + [x] * k, np.float32)
+            seq = 0.0
+            for x in terms:
+                seq += float(x)
+            exact = math.fsum(terms.astype(np.float64))
+            err = abs(seq - exact) + math.ulp(exact)
+            assert err >= k * 2.0 ** (E - 53) * 0.99, (E, k)  # the errors do add up
+            assert err <= seq_error_bound(terms), (E, k)
+
+
+def test_sequential_sum_error_bound_on_random_rows():
+    g = np.random.default_rng(31)
+    for rep in range(60):
+        n = int(g.integers(1000, 30000))
+        kind = rep % 4
+        if kind == 0:
+            x = np.exp(-np.abs(g.standard_normal(n) * 12.0)).astype(np.float32)   # peaked
+        elif kind == 1:
+            x = np.exp(-g.uniform(0.0, 60.0, n)).astype(np.float32)                # many tiny terms
+        elif kind == 2:
+            x = (g.uniform(0.5, 1.0, n) * 2.0 ** g.integers(-40, -20, n)).astype(np.float32)
+        else:
+            x = np.where(g.random(n) < 0.5, 0.0, np.exp(-g.uniform(20.0, 40.0, n))).astype(np.float32)
+        x[int(g.integers(0, n))] = 1.0
+        bound = seq_error_bound(x)
+        if bound is None:
+            continue
+        seq = float(np.cumsum(x.astype(np.float64))[-1])
+        exact = math.fsum(x.astype(np.float64))
+        assert abs(seq - exact) + math.ulp(exact) <= bound, rep
 
 
 # ------------------------------------------------------------------ GPU --
