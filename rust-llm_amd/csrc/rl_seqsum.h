@@ -181,43 +181,72 @@ RL_HD inline double add_p(double s, float x) {
 
 RL_HD inline uint32_t popc64(uint64_t v) { return (uint32_t)__builtin_popcountll(v); }
 
-// Steps of one term are capped at STEP_CAP (above any segment's room, which is
-// at most 2^53), and so is a run's total: sums of a workgroup's capped steps do
-// not wrap around, and a capped sum still reads as leaving the segment.
-constexpr uint64_t STEP_CAP = 1ull << 54;
+// Grid steps are counted in f64: every count below 2^53 is exact, and a term
+// is turned into its steps with exact operations (a scaling by a power of
+// two, floor, a subtraction). A term's steps are capped at STEP_CAP (above any
+// segment's room, at most 2^53), and so is a run's total; a sum that reaches
+// 2^53 is no longer exact, but it stays at or above the room, so it still
+// reads as leaving the segment, and only sums below the room are used as
+// exact values.
+constexpr double STEP_CAP = 0x1p54;
+
+RL_HD inline float f32_from_bits(uint32_t b) {
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+// The parity (0 or 1) of an integer-valued v below 2^53.
+RL_HD inline uint32_t parity_of(double v) { return v - 2.0 * __builtin_floor(v * 0.5) != 0.0 ? 1u : 0u; }
+
+// The steps of the f32 term x (finite, >= 0) on the grid whose step is
+// 1 / scale (scale a power of two): x * scale rounded to nearest, an exact tie
+// (*tie set) rounded down.
+RL_HD inline double step_of(float x, double scale, bool *tie) {
+    const double y = (double)x * scale;
+    const double fl = __builtin_floor(y);
+    const double fr = y - fl;
+    *tie = fr == 0.5;
+    const double q = fr > 0.5 ? fl + 1.0 : fl;
+    return q < STEP_CAP ? q : STEP_CAP;
+}
 
 // A run of consecutive terms on the grid of one segment, as a function of the
-// parity p entering it: it adds base + (tie ? (p ^ c) & 1 : 0) steps, and
-// leaves parity p ^ par without a tie, par with one.
+// parity p entering it: it adds base + (tie ? (p ^ c) & 1 : 0) steps. A tie
+// leaves the significand even, so after the run's first tie the parity is
+// known: it is that of base - mark, mark being base just after the last tie.
 struct StepRun {
-    uint64_t base;
-    uint32_t tie, c, par;
+    double base, mark;
+    uint32_t tie, c;
 };
 
-RL_HD inline StepRun run_identity() { return StepRun{0, 0, 0, 0}; }
+RL_HD inline StepRun run_identity() { return StepRun{0.0, 0.0, 0, 0}; }
 
-// Appends the f32 term with bits xb (finite, >= 0) on the grid 2^uexp.
-RL_HD inline void run_add(StepRun &r, uint32_t xb, int uexp) {
+// Appends the f32 term with bits xb on the grid with step 1 / scale.
+RL_HD inline void run_add(StepRun &r, uint32_t xb, double scale) {
     bool t;
-    uint64_t q = inc_of(xb, uexp, &t);  // a tie's increment rounded down
-    q = q < STEP_CAP ? q : STEP_CAP;
+    const double q = step_of(f32_from_bits(xb), scale, &t);
     if (!t) {
         r.base += q;
-        r.par ^= (uint32_t)(q & 1);
     } else if (!r.tie) {
-        // The parity before this tie is p ^ par; it rounds up iff that plus q is odd.
+        // The parity before this tie is p ^ parity(base); the tie rounds up
+        // iff that plus q is odd.
         r.tie = 1;
-        r.c = r.par ^ (uint32_t)(q & 1);
+        r.c = parity_of(r.base) ^ parity_of(q);
         r.base += q;
-        r.par = 0;
+        r.mark = r.base;
     } else {
-        r.base += q + ((r.par ^ q) & 1);
-        r.par = 0;
+        r.base += q + (double)(parity_of(r.base - r.mark) ^ parity_of(q));
+        r.mark = r.base;
     }
 }
 
+// The run's par: the parity it leaves, relative to the entering one without a
+// tie (p ^ par) and absolute with one.
+RL_HD inline uint32_t run_par(const StepRun &r) { return r.tie ? parity_of(r.base - r.mark) : parity_of(r.base); }
+
 // Runs 0, 1, ... in order: T has bit i set when run i holds a tie, O when run
-// i's par is 1. The parity entering run i (0 <= i <= 64; 64 means after the
+// i's run_par is 1. The parity entering run i (0 <= i <= 64; 64 means after the
 // last run) is p0 ^ k when *dep is set (p0 enters run 0), and k otherwise.
 RL_HD inline uint32_t parity_in(uint64_t T, uint64_t O, uint32_t i, uint32_t *dep) {
     const uint64_t below = i ? (~0ull >> (64 - i)) : 0ull;
@@ -263,7 +292,7 @@ RL_HD inline bool seg_multiple(const SumSeg &g, int gx) {
 // barrier behind which the set was last read.
 template <uint32_t NT>
 struct SeqLds {
-    uint64_t wave_base[2][NT / 64];  // steps, every tie resolved but the wave's first (capped)
+    double wave_base[2][NT / 64];    // steps, every tie resolved but the wave's first (capped)
     double wave_fsum[2][NT / 64];    // f64 sum of the wave's terms
     uint32_t wave_bits[2][NT / 64];  // bit 0: a tie; bit 1: the first tie's constant; bit 2: par
     int32_t wave_low[2][NT / 64];    // lowest bit exponent of the wave's nonzero terms
@@ -279,15 +308,6 @@ __device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v, int d) {
 // Butterfly totals across the wave with DPP and permlane exchanges (VALU
 // operations, no LDS round trip); every lane gets the same total (the f64
 // additions are commutative, so both lanes of a pair compute the same sum).
-__device__ __forceinline__ uint64_t wave_total_u64(uint64_t v) {
-    v += lane_xor64<1>(v);
-    v += lane_xor64<2>(v);
-    v += lane_xor64<4>(v);
-    v += lane_xor64<8>(v);
-    v += lane_xor64<16>(v);
-    v += lane_xor64<32>(v);
-    return v;
-}
 template <uint32_t S>
 __device__ __forceinline__ double lane_xor_f64(double v) {
     return f64_from_bits(lane_xor64<S>(f64_bits(v)));
@@ -311,23 +331,18 @@ __device__ __forceinline__ int wave_min_i32(int v) {
     return v;
 }
 
-// Inclusive scans across the wave (lane i gets lanes 0..i), for the passes
-// that locate an event.
-__device__ __forceinline__ uint64_t wave_incl_u64(uint64_t v) {
-    const uint32_t lane = __lane_id();
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint64_t o = shfl_up_u64(v, d);
-        if (lane >= (uint32_t)d) v += o;
-    }
-    return v;
-}
-__device__ __forceinline__ double wave_incl_f64(double v) {
+// Exclusive scans across the wave (lane i gets lanes 0..i-1, lane 0 gets 0),
+// for the passes that locate an event. The sum for lane i never includes lane
+// i's own value, which may be far larger (a capped step count): the sums of
+// the lanes before an event stay exact.
+__device__ __forceinline__ double wave_excl_f64(double v) {
     const uint32_t lane = __lane_id();
     for (int d = 1; d < 64; d <<= 1) {
         const double o = f64_from_bits(shfl_up_u64(f64_bits(v), d));
         if (lane >= (uint32_t)d) v += o;
     }
-    return v;
+    const double e = f64_from_bits(shfl_up_u64(f64_bits(v), 1));
+    return lane == 0 ? 0.0 : e;
 }
 
 // Replays s = fl_P(s + x_j) for j = 0, 1, ... over the n terms
@@ -362,6 +377,10 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
     SumSeg g{0, 0, 0};
     uint32_t pos = 0;  // the next term to add
     uint32_t set = 0;  // the LDS record set this pass writes
+    // Whether passes still test for a tile without rounding: once a tile
+    // fails the test, later ones (a larger sum, a coarser grid) almost never
+    // pass it, and its data (an f64 sum and a lowest bit per term) is skipped.
+    bool try_exact = true;
     uint32_t cur = 0xFFFFFFFFu, nxt = 0xFFFFFFFFu;  // bases of the tiles in xb and nb
     uint32_t xb[ITEMS], nb[ITEMS];  // terms of the current tile, raw bits of the next
     if (n > 0 && pred(0.0)) {
@@ -427,24 +446,32 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
         }
         // This thread's terms: a run on the segment's grid, their f64 sum and
         // their lowest bit.
+        const double scale = mul_pow2(1.0, -g.uexp);  // steps per unit
         StepRun r = run_identity();
         double fs = 0.0;
         int low = 0x7FFFFFFF;
 #pragma unroll
-        for (uint32_t i = 0; i < ITEMS; ++i) {
-            run_add(r, xv[i], g.uexp);
-            fs += (double)__uint_as_float(xv[i]);
-            if (xv[i] & 0x7FFFFFFFu) low = min(low, low_bit_exp(xv[i]));
+        for (uint32_t i = 0; i < ITEMS; ++i) run_add(r, xv[i], scale);
+        if (try_exact) {
+#pragma unroll
+            for (uint32_t i = 0; i < ITEMS; ++i) {
+                fs += (double)__uint_as_float(xv[i]);
+                if (xv[i] & 0x7FFFFFFFu) low = min(low, low_bit_exp(xv[i]));
+            }
         }
         r.base = r.base < STEP_CAP ? r.base : STEP_CAP;
-        const uint64_t T = __ballot(r.tie != 0), O = __ballot((r.par & 1u) != 0);
+        const uint64_t T = __ballot(r.tie != 0), O = __ballot(run_par(r) != 0);
         uint32_t dep;
         const uint32_t k = parity_in(T, O, lane, &dep);
         // The wave's steps with every tie resolved but its first, whose step
         // depends on the parity entering the wave.
-        const uint64_t wb = wave_total_u64(r.base + ((r.tie && !dep) ? ((k ^ r.c) & 1u) : 0u));
-        const double wf = wave_total_f64(fs);
-        const int wl = wave_min_i32(low);
+        const double wb = wave_total_f64(r.base + ((r.tie && !dep) ? (double)((k ^ r.c) & 1u) : 0.0));
+        double wf = 0.0;
+        int wl = (int)0x80000000u;  // fails the test below
+        if (try_exact) {
+            wf = wave_total_f64(fs);
+            wl = wave_min_i32(low);
+        }
         uint32_t bits;
         if (T != 0) {
             const uint32_t ft = (uint32_t)__builtin_ctzll(T);
@@ -468,9 +495,20 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
         }
         __syncthreads();
         // The waves in order, from the segment's parity: the tile's steps, the
-        // parity entering this wave and the steps and f64 sum before it.
+        // parity entering this wave and the steps and f64 sum before it. Lane
+        // w reads wave w's record; the combination reads those lanes into
+        // scalar registers.
+        const uint32_t rl = lane < NW ? lane : 0u;
+        const uint64_t rbase = f64_bits(L->wave_base[set][rl]);
+        const uint32_t rbits = L->wave_bits[set][rl];
+        uint64_t rfsum = 0;
+        int rlow = 0x7FFFFFFF;
+        if (try_exact) {
+            rfsum = f64_bits(L->wave_fsum[set][rl]);
+            rlow = L->wave_low[set][rl];
+        }
         uint32_t p = (uint32_t)(g.n & 1u), pw = 0;
-        uint64_t tot = 0, tot_before = 0;
+        double tot = 0.0, tot_before = 0.0;
         double fsum = 0.0, f_before = 0.0;
         int lowest = 0x7FFFFFFF;
 #pragma unroll
@@ -480,11 +518,16 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
                 pw = p;
                 f_before = fsum;
             }
-            const uint32_t b = L->wave_bits[set][w];
-            tot += L->wave_base[set][w] + ((b & 1u) ? ((p ^ (b >> 1)) & 1u) : 0u);
+            const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)rbits, (int)w);
+            const double bw = f64_from_bits(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(rbase >> 32), (int)w) << 32) |
+                                            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)rbase, (int)w));
+            tot += bw + ((b & 1u) ? (double)((p ^ (b >> 1)) & 1u) : 0.0);
             p = (b & 1u) ? ((b >> 2) & 1u) : (p ^ ((b >> 2) & 1u));
-            fsum += L->wave_fsum[set][w];
-            lowest = min(lowest, L->wave_low[set][w]);
+            if (try_exact) {
+                fsum += f64_from_bits(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(rfsum >> 32), (int)w) << 32) |
+                                      (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)rfsum, (int)w));
+                lowest = min(lowest, __builtin_amdgcn_readlane(rlow, (int)w));
+            }
         }
         set ^= 1u;
         // No addition in the rest of the tile rounds when s and every term are
@@ -493,7 +536,7 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
         // this holds: every subset sum is then representable).
         const double est = s + fsum;
         const int gx = grid_exp_of<P>(est * (1.0 + 0x1p-30));
-        if (lowest >= gx && seg_multiple(g, gx)) {
+        if (try_exact && lowest >= gx && seg_multiple(g, gx)) {
             if (!pred(est)) {
                 s = est;
                 g = seg_of<P>(s);
@@ -501,8 +544,7 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
                 continue;
             }
             // Every partial sum is exact: the first that meets pred.
-            const double incl = wave_incl_f64(fs);
-            double run = (s + f_before) + (incl - fs);
+            double run = (s + f_before) + wave_excl_f64(fs);
             uint32_t my_hit = 0xFFFFFFFFu;
             double v_hit = 0.0;
 #pragma unroll
@@ -525,39 +567,41 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
             __syncthreads();
             return hit;
         }
-        const uint64_t room = g.lim - g.n;
-        if (tot < room && !pred(scaled(g.n + tot, g.uexp))) {
+        try_exact = false;
+        const double room = (double)(g.lim - g.n);
+        if (tot < room && !pred(scaled(g.n + (uint64_t)tot, g.uexp))) {
             // Nothing happens in the rest of this tile.
-            g.n += tot;
+            g.n += (uint64_t)tot;
             s = scaled(g.n, g.uexp);
             pos = base + TILE;
             continue;
         }
         // Something happens here: the parity entering this thread's terms and
         // the steps before them, then its terms one by one.
+        // The steps before this thread's terms are exact: they stay below the
+        // room for every thread up to the event's.
         const uint32_t pl = dep ? (pw ^ k) : k;
-        const uint64_t mine = r.base + (r.tie ? ((pl ^ r.c) & 1u) : 0u);
-        const uint64_t incl = wave_incl_u64(mine);
-        uint64_t I = tot_before + (incl - mine);
+        const double mine = r.base + (r.tie ? (double)((pl ^ r.c) & 1u) : 0.0);
+        double I = tot_before + wave_excl_f64(mine);
         uint32_t par = pl;
         uint32_t my_cross = 0xFFFFFFFFu, my_hit = 0xFFFFFFFFu, x_cross = 0;
-        uint64_t I_cross = 0, I_hit = 0;
+        double I_cross = 0.0, I_hit = 0.0;
 #pragma unroll
         for (uint32_t i = 0; i < ITEMS; ++i) {
             const uint32_t j = j0 + i;
             if (j >= n || my_cross != 0xFFFFFFFFu || my_hit != 0xFFFFFFFFu) break;
             if (j < pos) continue;
             bool t;
-            uint64_t q = inc_of(xv[i], g.uexp, &t);
-            q = q < STEP_CAP ? q : STEP_CAP;
-            const uint64_t step = t ? q + ((par ^ q) & 1u) : q;
-            par = t ? 0u : (par ^ (uint32_t)(q & 1u));
-            const uint64_t In = I + step;
+            const double q = step_of(__uint_as_float(xv[i]), scale, &t);
+            const uint32_t pq = parity_of(q);
+            const double step = t ? q + (double)(par ^ pq) : q;
+            par = t ? 0u : (par ^ pq);
+            const double In = I + step;
             if (In >= room) {  // this term's sum leaves the segment
                 my_cross = j;
                 I_cross = I;
                 x_cross = xv[i];
-            } else if (pred(scaled(g.n + In, g.uexp))) {
+            } else if (pred(scaled(g.n + (uint64_t)In, g.uexp))) {
                 my_hit = j;
                 I_hit = In;
             } else {
@@ -569,7 +613,7 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
         __syncthreads();
         const uint32_t cross = L->cross, hit = L->hit;
         if (hit < cross) {
-            if (my_hit == hit) L->s_new = scaled(g.n + I_hit, g.uexp);
+            if (my_hit == hit) L->s_new = scaled(g.n + (uint64_t)I_hit, g.uexp);
             __syncthreads();
             *sum = L->s_new;
             __syncthreads();
@@ -579,12 +623,12 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
             // Not reached: a step total at or past the room, or pred met at
             // the end, has its event in this tile. Kept so that every path
             // moves pos forward.
-            g.n += tot;
+            g.n += (uint64_t)(tot < room ? tot : 0.0);
             s = scaled(g.n, g.uexp);
             pos = base + TILE;
             continue;
         }
-        if (my_cross == cross) L->s_new = add_p<P>(scaled(g.n + I_cross, g.uexp), __uint_as_float(x_cross));
+        if (my_cross == cross) L->s_new = add_p<P>(scaled(g.n + (uint64_t)I_cross, g.uexp), __uint_as_float(x_cross));
         __syncthreads();
         s = L->s_new;
         __syncthreads();

@@ -292,22 +292,22 @@ static void check_runs() {
             // Per thread and per wave, as the device computes them.
             std::vector<StepRun> run(64 * nw);
             std::vector<uint32_t> k(64 * nw), dep(64 * nw);
-            std::vector<uint64_t> wbase(nw);
+            std::vector<double> wbase(nw);
             std::vector<uint32_t> wbits(nw);
             for (uint32_t w = 0; w < nw; ++w) {
                 uint64_t T = 0, O = 0;
                 for (uint32_t l = 0; l < 64; ++l) {
                     StepRun r = run_identity();
-                    for (uint32_t i = 0; i < items; ++i) run_add(r, x[((w * 64 + l) * items) + i], uexp);
+                    for (uint32_t i = 0; i < items; ++i) run_add(r, x[((w * 64 + l) * items) + i], ldexp(1.0, -uexp));
                     run[w * 64 + l] = r;
                     if (r.tie) T |= 1ull << l;
-                    if (r.par & 1) O |= 1ull << l;
+                    if (run_par(r)) O |= 1ull << l;
                 }
-                uint64_t wb = 0;
+                double wb = 0.0;
                 for (uint32_t l = 0; l < 64; ++l) {
                     const StepRun &r = run[w * 64 + l];
                     k[w * 64 + l] = parity_in(T, O, l, &dep[w * 64 + l]);
-                    wb += r.base + ((r.tie && !dep[w * 64 + l]) ? ((k[w * 64 + l] ^ r.c) & 1u) : 0u);
+                    wb += r.base + ((r.tie && !dep[w * 64 + l]) ? (double)((k[w * 64 + l] ^ r.c) & 1u) : 0.0);
                 }
                 uint32_t bits;
                 if (T) {
@@ -323,35 +323,35 @@ static void check_runs() {
                 wbits[w] = bits;
             }
             uint32_t p = p0;
-            uint64_t tot = 0;
-            std::vector<uint64_t> before(nw);
+            double tot = 0.0;
+            std::vector<double> before(nw);
             std::vector<uint32_t> pin(nw);
             for (uint32_t w = 0; w < nw; ++w) {
                 before[w] = tot;
                 pin[w] = p;
                 const uint32_t b = wbits[w];
-                tot += wbase[w] + ((b & 1u) ? ((p ^ (b >> 1)) & 1u) : 0u);
+                tot += wbase[w] + ((b & 1u) ? (double)((p ^ (b >> 1)) & 1u) : 0.0);
                 p = (b & 1u) ? ((b >> 2) & 1u) : (p ^ ((b >> 2) & 1u));
             }
             // The maps, term by term.
             TermMap acc = map_identity();
             for (uint32_t w = 0; w < nw; ++w) {
-                uint64_t I = before[w];
+                double I = before[w];
                 for (uint32_t l = 0; l < 64; ++l) {
                     const uint32_t t = w * 64 + l;
                     const uint32_t pl = dep[t] ? (pin[w] ^ k[t]) : k[t];
-                    if (map_inc(acc, p0) != I || map_parity(acc, p0) != pl) {
+                    if ((double)map_inc(acc, p0) != I || map_parity(acc, p0) != pl) {
                         if (failures++ < 5)
                             printf("FAIL runs: thread %u of %u, items %u, p0 %u: steps %llu/%llu parity %u/%u\n", t,
                                    64 * nw, items, p0, (unsigned long long)I,
                                    (unsigned long long)map_inc(acc, p0), pl, map_parity(acc, p0));
                         return;
                     }
-                    I += run[t].base + (run[t].tie ? ((pl ^ run[t].c) & 1u) : 0u);
+                    I += run[t].base + (run[t].tie ? (double)((pl ^ run[t].c) & 1u) : 0.0);
                     for (uint32_t i = 0; i < items; ++i) acc = map_then(acc, map_of(x[t * items + i], uexp));
                 }
             }
-            if (map_inc(acc, p0) != tot || map_parity(acc, p0) != p) {
+            if ((double)map_inc(acc, p0) != tot || map_parity(acc, p0) != p) {
                 if (failures++ < 5) printf("FAIL runs: tile total, items %u, p0 %u\n", items, p0);
                 return;
             }

@@ -86,6 +86,17 @@ def term_arrays(seed):
     lg = (g.standard_normal(248320) * 2.0).astype(np.float32)
     lg[g.choice(248320, 16, replace=False)] = g.uniform(8.0, 14.0, 16).astype(np.float32)
     out.append(np.exp(lg - lg.max()).astype(np.float32))
+    # Short significands whose f64 sum crosses from 2^-8 to 2^0 in one step
+    # (the 21st term, 1.75) and lands on a tie there, so that a step count one
+    # off before the crossing changes the result; the crossing lane's own step
+    # count is far above 2^53.
+    out.append(np.array([
+        0x24600000, 0x2FD00000, 0x2E800000, 0x2C700000, 0x2B400000, 0x29800000, 0x30100000, 0x3AA00000,
+        0x37400000, 0x35100000, 0x2B300000, 0x25300000, 0x3B900000, 0x23700000, 0x24A00000, 0x36A00000,
+        0x36E00000, 0x37E00000, 0x35700000, 0x24600000, 0x3FE00000, 0x39C00000, 0x3DC00000, 0x2C100000,
+        0x32800000, 0x25D00000, 0x3D600000, 0x3B000000, 0x37D00000, 0x37F00000, 0x37000000, 0x2E200000,
+        0x2D800000, 0x2E500000, 0x34200000, 0x3C500000, 0x2A400000, 0x2FA00000, 0x3BD00000, 0x36300000],
+        np.uint32).view(np.float32))
     # Ties-heavy rows long enough for many tiles, and a long constant run.
     out.append(np.ldexp(2.0 * g.integers(0, 64, 60000) + 1.0, -24).astype(np.float32))
     out.append(np.full(100000, np.float32(3.0 / 1024.0)))
