@@ -34,7 +34,7 @@ struct FullRow {
     uint32_t done;     // the row is finished (no finite maximum, or the min-p path)
     uint32_t m;        // candidates kept (after top-p and min-p)
     float inv;         // (1 / total) as f32
-    uint32_t qbad;     // a normalised probability is not finite
+    uint32_t qbad;     // a normalised probability may not be finite: the draw walks in order
     uint32_t small;    // the row tries the min-p path first
     uint32_t nsurv;    // min-p survivors collected
     uint32_t overflow; // more survivors than SURV_CAP
@@ -1208,17 +1208,21 @@ __global__ __launch_bounds__(REPLAY_THREADS) void k_full_tail(RowIO a, FullScrat
         total = sh_d_;
     }
     if (tid == 0) {
+        const float inv = (float)(1.0 / total);
         f.row[slot].m = m;
-        f.row[slot].inv = (float)(1.0 / total);
-        f.row[slot].qbad = 0;
+        f.row[slot].inv = inv;
+        // q = p * inv is finite for every kept p when every p is and inv is
+        // (p <= 1 and inv <= 1: the best p is exp(0) = 1, so total >= 1).
+        f.row[slot].qbad = (bad || !(inv <= 3.40282347e38f)) ? 1u : 0u;
     }
 }
 
-// ------------------------------------------------------------- norm ---
-// grid (chunks, slots), FULL_THREADS: q = p * (1 / total) for the kept
-// candidates (sample.rs:344-347), written to the outputs.
-__global__ __launch_bounds__(FULL_THREADS) void k_full_norm(RowIO a, FullScratch f) {
-    const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
+// ------------------------------------------------------- draw and norm ---
+// The kept candidates q = p * (1 / total) (sample.rs:344-347), written to the
+// outputs, for chunk `chunk` of slot's m candidates, by the workgroup's
+// REPLAY_THREADS threads.
+__device__ __forceinline__ void norm_chunk(const RowIO &a, const FullScratch &f, uint32_t slot, uint32_t chunk) {
+    constexpr uint32_t NT = REPLAY_THREADS;
     const FullRow st = f.row[slot];
     if (st.done) return;
     const uint32_t row = a.rows[slot];
@@ -1226,86 +1230,91 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_norm(RowIO a, FullScratch
     const uint32_t m = st.m;
     const uint32_t j0 = chunk_lo(m, chunk, a.chunks), j1 = chunk_lo(m, chunk + 1, a.chunks);
     const uint32_t *ids = f.idA + (uint64_t)slot * V;
-    float *probs = f.probs + (uint64_t)slot * V;
-    uint32_t qbad = 0;
-    for (uint32_t b = j0; b < j1; b += FULL_THREADS * UN) {
-        float pp[UN];
-        uint32_t iv[UN];
+    const float *probs = f.probs + (uint64_t)slot * V;
+    constexpr uint32_t NU = UN / 2;  // as many loads in flight per workgroup as UN at FULL_THREADS
+    for (uint32_t b = j0; b < j1; b += NT * NU) {
+        float pp[NU];
+        uint32_t iv[NU];
 #pragma unroll
-        for (uint32_t u = 0; u < UN; ++u) {
-            const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
+        for (uint32_t u = 0; u < NU; ++u) {
+            const uint32_t j = b + u * NT + threadIdx.x;
             const uint32_t jc = j < j1 ? j : j1 - 1;  // clamped: no branch around the loads
             pp[u] = ((const RL_GLB float *)probs)[jc];
             iv[u] = ((const RL_GLB uint32_t *)ids)[jc];
         }
 #pragma unroll
-        for (uint32_t u = 0; u < UN; ++u) {
-            const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
+        for (uint32_t u = 0; u < NU; ++u) {
+            const uint32_t j = b + u * NT + threadIdx.x;
             if (j < j1) {
-                const float q = pp[u] * st.inv;
-                if (!(q <= 3.40282347e38f)) qbad = 1;
-                // The draw reads the normalised list from the caller's
-                // candidate output when there is one, else from probs.
-                if (a.out_ids) {
-                    a.out_ids[(uint64_t)row * a.cand_stride + j] = iv[u];
-                    a.out_probs[(uint64_t)row * a.cand_stride + j] = q;
-                } else {
-                    probs[j] = q;
-                }
+                a.out_ids[(uint64_t)row * a.cand_stride + j] = iv[u];
+                a.out_probs[(uint64_t)row * a.cand_stride + j] = pp[u] * st.inv;
             }
         }
     }
-    if (__ballot(qbad != 0) != 0 && lane_id() == 0) atomicOr(&f.row[slot].qbad, 1u);
 }
 
-// ------------------------------------------------------------- draw ---
-// grid (slots), REPLAY_THREADS: the f32 running sum against the host's uniform
-// (sample.rs:349-356); a shortfall takes the last candidate (:357-358).
-__global__ __launch_bounds__(REPLAY_THREADS) void k_full_draw(RowIO a, FullScratch f) {
-    __shared__ float stage_[STAGE];
-    __shared__ SeqLds<REPLAY_THREADS> seq;
-    __shared__ uint32_t sh_stop_, sh_tok_;
-    RL_LDS float *stage = (RL_LDS float *)stage_;
-    RL_LDS uint32_t *stop = (RL_LDS uint32_t *)&sh_stop_;
-    const uint32_t slot = blockIdx.x;
+// The f32 running sum of q = p * (1 / total) against the host's uniform
+// (sample.rs:349-356); a shortfall takes the last candidate (:357-358). The
+// whole workgroup, for one slot.
+__device__ __forceinline__ void draw_row(const RowIO &a, const FullScratch &f, uint32_t slot, RL_LDS float *stage,
+                                         RL_LDS uint32_t *stop, RL_LDS uint32_t *tok_out, SeqLds<REPLAY_THREADS> *seq) {
     const FullRow st = f.row[slot];
     if (st.done) return;
     const uint32_t row = a.rows[slot];
     const uint32_t V = a.vocab;
     const uint32_t m = st.m;
     const uint32_t *ids = f.idA + (uint64_t)slot * V;
-    // The normalised list k_full_norm wrote (the caller's candidates when
-    // requested).
-    const float *probs = a.out_probs ? a.out_probs + (uint64_t)row * a.cand_stride : f.probs + (uint64_t)slot * V;
+    const float *probs = f.probs + (uint64_t)slot * V;
+    const float inv = st.inv;
     const float u = a.uniforms[row];
     uint32_t pick;
     if (!st.qbad) {
         double unused;
         const uint32_t j = seq_replay<24, REPLAY_THREADS, SEQ_ITEMS>(
-            [probs](uint32_t j) { return ((const RL_GLB float *)probs)[j]; }, m,
-            [u](double c) { return c > (double)u; }, &seq, &unused);
+            [probs](uint32_t j) { return ((const RL_GLB uint32_t *)probs)[j]; },
+            [inv](uint32_t bits) { return __uint_as_float(bits) * inv; }, m, [u](double c) { return c > (double)u; },
+            seq, &unused);
         pick = j < m ? j : m - 1;
     } else {
-        if (threadIdx.x == 0) sh_tok_ = m - 1;
+        if (threadIdx.x == 0) *tok_out = m - 1;
         __syncthreads();
         float cum = 0.0f;
         staged_walk(probs, m, stage, stop, [&](RL_LDS float *sv, uint32_t b, uint32_t cnt) {
             for (uint32_t i = 0; i < cnt; ++i) {
-                cum += sv[i];
+                cum += sv[i] * inv;
                 if (cum > u) {
-                    sh_tok_ = b + i;
+                    *tok_out = b + i;
                     return true;
                 }
             }
             return false;
         });
         __syncthreads();
-        pick = sh_tok_;
+        pick = *tok_out;
     }
     if (threadIdx.x == 0) {
         a.out_token[row] = ids[pick];
         a.out_kept[row] = m;
         a.out_used[row] = 1;
+    }
+}
+
+// grid (slots + slots * chunks when the candidates are written, else slots),
+// REPLAY_THREADS: workgroup x < slots draws slot x's token; the others write
+// chunk (x - slots) % chunks of slot (x - slots) / chunks's kept candidates.
+// Neither reads what the other writes, so the draws (bound by the replay's
+// arithmetic, one workgroup a row) and the writes (bound by HBM) share the
+// GPU in one launch.
+__global__ __launch_bounds__(REPLAY_THREADS) void k_full_finish(RowIO a, FullScratch f, uint32_t slots) {
+    __shared__ float stage_[STAGE];
+    __shared__ SeqLds<REPLAY_THREADS> seq;
+    __shared__ uint32_t sh_stop_, sh_tok_;
+    const uint32_t x = blockIdx.x;
+    if (x < slots) {
+        draw_row(a, f, x, (RL_LDS float *)stage_, (RL_LDS uint32_t *)&sh_stop_, (RL_LDS uint32_t *)&sh_tok_, &seq);
+    } else {
+        const uint32_t i = x - slots;
+        norm_chunk(a, f, i / a.chunks, i % a.chunks);
     }
 }
 

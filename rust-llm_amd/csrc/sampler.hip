@@ -292,8 +292,10 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
         hipLaunchKernelGGL(k_full_sort, dim3(ng), dim3(SORT_THREADS), 0, st, f, fs);
         hipLaunchKernelGGL(k_full_probs, cgrid, dim3(FULL_THREADS), 0, st, f, fs);
         hipLaunchKernelGGL(k_full_tail, dim3(ng), dim3(REPLAY_THREADS), 0, st, f, fs);
-        hipLaunchKernelGGL(k_full_norm, cgrid, dim3(FULL_THREADS), 0, st, f, fs);
-        hipLaunchKernelGGL(k_full_draw, dim3(ng), dim3(REPLAY_THREADS), 0, st, f, fs);
+        // The draws, and (when the candidates are written) the writes, in one
+        // launch: the draw workgroups first.
+        const uint32_t finish_wgs = ng + (f.out_ids ? ng * f.chunks : 0u);
+        hipLaunchKernelGGL(k_full_finish, dim3(finish_wgs), dim3(REPLAY_THREADS), 0, st, f, fs, ng);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return hip_fail(e, "full-path kernels");
     }
