@@ -1,20 +1,29 @@
 // The FULL device path: rows with top_k == 0, top_k >= vocab or top_k > 64
-// (sample.rs:279-358 over the whole candidate list). Seven launches per group
-// of rows, alternating kernels that spread a row over many workgroups (the
-// HBM- and ALU-heavy steps) with one workgroup per row (the steps that follow
-// the reference's sequential order):
+// (sample.rs:279-358 over the whole candidate list). Up to eight launches per
+// group of rows, alternating kernels that spread a row over many workgroups
+// (the HBM- and ALU-heavy steps) with one workgroup per row (the steps that
+// follow the reference's sequential order):
 //
-//   k_full_keys   (chunks x rows)  total-order keys in id order; the f32::max
-//                                  fold and argmax over the non-window ids
-//   k_full_sort   (rows)           the window's penalised values merged in
-//                                  (max, argmax, keys); the row sorted by the
-//                                  reference's order unless it keeps id order
-//   k_full_probs  (chunks x rows)  p = exp((l - max) / T) in candidate order,
-//                                  per-chunk sums, smallest exponent, min-p
-//                                  counts
-//   k_full_tail   (rows)           mass, top-p cut, min-p, normalising total
-//   k_full_norm   (chunks x rows)  q = p * (1 / total), the kept candidates
-//   k_full_draw   (rows)           the f32 draw against the host's uniform
+//   k_full_keys    (chunks x rows)  total-order keys in id order; the f32::max
+//                                   fold and argmax over the non-window ids
+//   k_full_prep    (rows)           the window's penalised values merged in
+//                                   (max, argmax, keys); rows without a finite
+//                                   maximum answered
+//   k_full_collect (chunks x rows)  min-p rows: p of every id, chunk sums, the
+//                                   survivors (launched when a row may take
+//                                   the min-p path)
+//   k_full_small   (rows)           min-p rows finished from their survivors,
+//                                   or left to the kernels below
+//   k_full_sort    (rows)           the row sorted by the reference's order
+//                                   unless it keeps id order
+//   k_full_probs   (chunks x rows)  p = exp((l - max) / T) in candidate order,
+//                                   per-chunk sums, smallest exponent, min-p
+//                                   counts
+//   k_full_tail    (rows)           mass, top-p cut, min-p, normalising total
+//   k_full_finish  (rows, + chunks  the f32 draw over q = p * (1 / total)
+//                   x rows)         against the host's uniform, one workgroup
+//                                   a row; the other workgroups write the kept
+//                                   candidates
 //
 // The sums are the reference's sequential sums, bit for bit: when every p is a
 // multiple of 2^(e_min - 23) and the mass is below 2^(30 + e_min), every partial
