@@ -225,3 +225,34 @@ def test_full_path_rows_of_equal_keys(device):
     for r in (0, 1, 2, 4):
         k = int(want["kept"][r])
         assert np.array_equal(want["ids"][r, :k], np.arange(k, dtype=np.uint32)), r
+
+
+def test_full_path_rows_with_nans_and_infinities(device):
+    # The rows of the special-rows test on the full path (top-k 0): NaN and
+    # infinite p leave the draw to walk q = p * (1 / total) in order, and the
+    # kept candidates are written beside the draw in the same launch.
+    rng = np.random.default_rng(4)
+    V = 3000
+    logits = rng.normal(0, 1, (10, V)).astype(np.float32)
+    logits[0, :40] = np.nan
+    logits[1, :] = -np.inf
+    logits[2, :] = np.nan
+    logits[3, 100] = np.inf
+    logits[4, :25] = np.nan
+    logits[4, 30] = np.inf
+    logits[5, 5] = np.nan
+    logits[6, :] = 0.0
+    logits[7, ::3] = -np.inf
+    logits[8, 7] = 3.4e38
+    logits[9, :] = 1.0
+    settings = []
+    for r in range(10):
+        settings += [R.sampling(1.0, 0, 0.9, 0.0, 1.3, 8, r), R.sampling(3.0, 0, 1.0, 0.0, 1.0, 0, r),
+                     R.sampling(1e-30, 0, 0.95, 0.05, 1.0, 0, r), R.sampling(0.5, 0, 0.99, 0.02, 1.2, 8, r)]
+    logits = np.repeat(logits, 4, axis=0)
+    rows = logits.shape[0]
+    windows = rng.integers(0, V, (rows, 8)).astype(np.uint32)
+    wlen = np.full(rows, 8, np.uint32)
+    uniforms = rng.random(rows).astype(np.float32)
+    got, want = run_both(device, logits, settings, windows, wlen, uniforms)
+    assert_match("full-path special rows", got, want, settings)
