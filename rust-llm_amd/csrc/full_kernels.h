@@ -605,6 +605,13 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_collect(RowIO a, FullScra
     double sum = 0.0;
     uint32_t ns_key = 0;  // largest key + 1 of a non-survivor
     bool stop = false;
+    // The row's overflow flag loads with a step's keys: the step sees the flag
+    // as it was when the step began, which only delays an early stop (an
+    // overflowing row's results are not used), and no step waits for it on
+    // its own; a wave that overflows the list, or meets a non-finite p, stops
+    // at once. (Loading the next step's keys during this one measured no
+    // faster: a row that overflows, as a tie-heavy one does, stops after one
+    // step and the loads are wasted.)
     for (uint32_t b = j0; b < j1 && !stop; b += FULL_THREADS * UN) {
         uint32_t kk[UN];
 #pragma unroll
@@ -612,6 +619,7 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_collect(RowIO a, FullScra
             const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
             kk[u] = ((const RL_GLB uint32_t *)keys)[j < j1 ? j : j1 - 1];  // clamped: no branch around the load
         }
+        const uint32_t overflow_seen = __hip_atomic_load(&rs->overflow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // The survivors of all UN steps take their list slots with one
         // atomic per wave (the wave waits for its result).
         uint64_t sm[UN];
@@ -642,10 +650,16 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_collect(RowIO a, FullScra
                 }
                 base += (uint32_t)__popcll(sm[u]);
             }
-            if (base > SURV_CAP && lane == 0) atomicOr(&rs->overflow, 1u);
+            if (base > SURV_CAP) {
+                if (lane == 0) atomicOr(&rs->overflow, 1u);
+                stop = true;  // this wave overflowed the list itself
+            }
         }
-        if (ballot(nonfinite) != 0 && lane == 0) atomicOr(&rs->overflow, 1u);
-        stop = __hip_atomic_load(&rs->overflow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+        if (ballot(nonfinite) != 0) {
+            if (lane == 0) atomicOr(&rs->overflow, 1u);
+            stop = true;
+        }
+        stop = stop || uniform_u32(overflow_seen) != 0;
     }
     for (int m = 32; m >= 1; m >>= 1) {
         sum += __shfl_xor(sum, m);
