@@ -1,14 +1,14 @@
 // The FULL device path: rows with top_k == 0, top_k >= vocab or top_k > 64
-// (sample.rs:279-358 over the whole candidate list). Up to eight launches per
+// (sample.rs:279-358 over the whole candidate list). Up to seven launches per
 // group of rows, alternating kernels that spread a row over many workgroups
 // (the HBM- and ALU-heavy steps) with one workgroup per row (the steps that
 // follow the reference's sequential order):
 //
-//   k_full_keys    (chunks x rows)  total-order keys in id order; the f32::max
-//                                   fold and argmax over the non-window ids
-//   k_full_prep    (rows)           the window's penalised values merged in
-//                                   (max, argmax, keys); rows without a finite
-//                                   maximum answered
+//   k_full_keys    (chunks x rows)  total-order keys of the penalised row in id
+//                                   order; per chunk the f32::max fold and
+//                                   argmax, merged by the row's last chunk to
+//                                   finish; rows without a finite maximum
+//                                   answered
 //   k_full_collect (chunks x rows)  min-p rows: p of every id, chunk sums, the
 //                                   survivors (launched when a row may take
 //                                   the min-p path)
@@ -66,6 +66,7 @@ struct FullScratch {
     uint32_t *pfirst_out;               // [slot][chunk] first index with p < min_p
     uint64_t *surv;                     // [slot][SURV_CAP] min-p survivors (composites)
     FullRow *row;                       // [slot]
+    uint32_t *arrive;                   // [slot] keys pass: chunks done; zero between calls
 };
 
 constexpr uint32_t UN = 16;                // elements per thread per step of the bulk loops (loads in flight)
@@ -97,12 +98,21 @@ __device__ __forceinline__ int f32_exponent(float p) {
     return e == 0 ? -126 : e - 127;
 }
 
+// Whether a row tries the min-p path: min-p on, the whole vocabulary as
+// candidates (top_k 0 or >= vocab), sampling (not greedy).
+__device__ __forceinline__ bool small_eligible(const rl_sampling &s, uint32_t V) {
+    return s.min_p > 0.0f && full_k(s, V) == V && s.temperature > 0.0f;
+}
+
 // ------------------------------------------------------------- keys ---
-// grid (chunks, slots), FULL_THREADS: the row's raw logits as total-order keys
-// in id order (the window ids' keys are rewritten by k_full_sort), and per
-// chunk the f32::max fold (NaN ignored) and the argmax composite over the ids
-// outside the window. Dynamic LDS: a bitmap of the chunk's window ids
-// (k_full_keys_lds_bytes).
+// grid (chunks, slots), FULL_THREADS: the penalised row (sample.rs:239-257) as
+// total-order keys in id order, and per chunk the f32::max fold (NaN ignored)
+// and the argmax composite. A window id's key is its penalised logit's,
+// computed from the raw logit, so an id repeated in the window is penalised
+// once. Dynamic LDS: a bitmap of the chunk's window ids
+// (k_full_keys_lds_bytes). The row's last chunk to finish merges the chunks'
+// results (sample.rs:267-277): the row state for the kernels that follow, and
+// the answer of a row without a finite maximum (argmax, no draw).
 // LDS bytes of k_full_keys's bitmap: one bit per element of the largest chunk.
 __host__ __device__ inline size_t k_full_keys_lds_bytes(uint32_t vocab, uint32_t chunks) {
     const uint32_t n4 = vocab / 4;
@@ -127,9 +137,7 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch
     const uint32_t q0 = chunk_lo(n4, chunk, a.chunks), q1 = chunk_lo(n4, chunk + 1, a.chunks);
     // The chunk's elements [e0, e1) (the last chunk also takes the vocab % 4
     // tail). A bitmap of the window ids among them makes the membership test
-    // one LDS read with no probing loop: the test runs whenever a lane's
-    // running maximum rises, which on a random row is nearly every step for
-    // some lane of the wave.
+    // of four consecutive elements one LDS read, with no probing loop.
     const uint32_t e0 = 4 * q0, e1 = chunk == a.chunks - 1 ? V : 4 * q1;
     const uint32_t nwords = (e1 - e0 + 31) / 32;
     if (pen) {
@@ -152,11 +160,8 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch
     uint64_t am = 0;
     auto take = [&](float x, uint32_t id) {
         const uint64_t c = composite(argmax_key(x), id);
-        const bool up_max = x > mx, up_am = c > am;
-        if ((up_max || up_am) && !(pen && ((bm[(id - e0) >> 5] >> ((id - e0) & 31)) & 1u))) {
-            if (up_max) mx = x;
-            if (up_am) am = c;
-        }
+        if (x > mx) mx = x;
+        if (c > am) am = c;
     };
     // Four 16-byte loads in flight per thread; indices past the chunk are
     // clamped to its last element (a cache hit) and their results dropped.
@@ -172,7 +177,16 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch
         for (uint32_t u = 0; u < KU; ++u) {
             const uint32_t qq = q + u * FULL_THREADS;
             if (qq >= q1) break;
-            const float x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+            float x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+            if (pen) {  // the four ids' bits share a word: e0 and 4 * qq are multiples of 4
+                const uint32_t off = 4 * qq - e0;
+                const uint32_t in = (bm[off >> 5] >> (off & 31)) & 15u;
+                if (in != 0) {
+#pragma unroll
+                    for (uint32_t c = 0; c < 4; ++c)
+                        if ((in >> c) & 1u) x[c] = penalize(x[c], s.repeat_penalty);
+                }
+            }
             uint32_t kk[4];
 #pragma unroll
             for (uint32_t c = 0; c < 4; ++c) {
@@ -195,7 +209,8 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch
     if (chunk == a.chunks - 1) {  // the last vocab % 4 elements
         const uint32_t e = 4 * n4 + threadIdx.x;
         if (e < V) {
-            const float x = ((const RL_GLB float *)rowp)[e];
+            float x = ((const RL_GLB float *)rowp)[e];
+            if (pen && ((bm[(e - e0) >> 5] >> ((e - e0) & 31)) & 1u)) x = penalize(x, s.repeat_penalty);
             keys[e] = total_key(x);
             if (write_ids) ids[e] = e;
             take(x, e);
@@ -209,13 +224,45 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch
         red_am[wave] = am;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (uint32_t i = 1; i < FULL_THREADS / WAVE; ++i) {
-            mx = fmaxf(mx, red_max[i]);
-            am = red_am[i] > am ? red_am[i] : am;
-        }
-        f.part_max[slot * a.chunks + chunk] = mx;
-        f.part_am[slot * a.chunks + chunk] = am;
+    if (wave != 0) return;
+    for (uint32_t i = 1; i < FULL_THREADS / WAVE; ++i) {
+        mx = fmaxf(mx, red_max[i]);
+        am = red_am[i] > am ? red_am[i] : am;
+    }
+    // Publish the chunk's result; the row's last chunk to arrive merges them.
+    // The results are written with device-scope stores, which write through
+    // this XCD's L2, and the arrival waits until they have completed; the
+    // merging chunk reads them with device-scope loads after its arrival.
+    const uint32_t lane = lane_id();
+    if (lane == 0) {
+        __hip_atomic_store((uint32_t *)f.part_max + slot * a.chunks + chunk, __float_as_uint(mx), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(f.part_am + slot * a.chunks + chunk, am, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);  // the stores have completed
+    uint32_t old = 0;
+    if (lane == 0) old = atomicAdd(&f.arrive[slot], 1u);
+    if (read_lane_u32(old, 0) != a.chunks - 1) return;
+    // The last chunk (chunks <= MAX_CHUNKS <= WAVE): lane c reads chunk c.
+    const bool ok = lane < a.chunks;
+    const uint32_t mbits = ok ? __hip_atomic_load((const uint32_t *)f.part_max + slot * a.chunks + lane,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                              : __float_as_uint(-__builtin_inff());
+    const uint64_t cam =
+        ok ? __hip_atomic_load(f.part_am + slot * a.chunks + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+    mx = uniform_f32(wave_maxnum_f32(__uint_as_float(mbits)));
+    am = uniform_u64(wave_max_u64(cam));
+    if (lane == 0) {
+        f.arrive[slot] = 0;  // ready for the next call
+        const uint32_t am_tok = comp_key(am) == 0 ? 0u : comp_id(am);
+        const bool finite = mx > -__builtin_inff() && mx < __builtin_inff();
+        FullRow st{};
+        st.M = mx;
+        st.am_tok = am_tok;
+        st.done = finite ? 0u : 1u;
+        st.small = finite && small_eligible(s, V) ? 1u : 0u;
+        f.row[slot] = st;
+        if (!finite) write_single(a, row, am_tok);  // sample.rs:270-277
     }
 }
 
@@ -236,73 +283,6 @@ constexpr uint32_t SORT_ITEMS = 8;                          // elements per lane
 constexpr uint32_t SORT_UN = 8;                             // loads in flight per thread in the key scans
 constexpr uint32_t SORT_TILE = SORT_THREADS * SORT_ITEMS;    // elements per tile
 constexpr uint32_t WAVE_SEG = WAVE * SORT_ITEMS;             // a wave's contiguous share of a tile
-
-// Whether a row tries the min-p path: min-p on, the whole vocabulary as
-// candidates (top_k 0 or >= vocab), sampling (not greedy).
-__device__ __forceinline__ bool small_eligible(const rl_sampling &s, uint32_t V) {
-    return s.min_p > 0.0f && full_k(s, V) == V && s.temperature > 0.0f;
-}
-
-// grid (slots), FULL_THREADS: the penalty's effect on the maximum, the argmax
-// and the keys (sample.rs:241-257, 267-277). The chunks' results cover the ids
-// outside the window; each distinct window id's penalised logit is merged in
-// and its key rewritten (from the raw logit, so a repeated id is rewritten to
-// the same value). A row without a finite maximum is answered here (argmax,
-// no draw). Leaves the row state for the kernels that follow.
-__global__ __launch_bounds__(FULL_THREADS) void k_full_prep(RowIO a, FullScratch f) {
-    __shared__ float red_max[FULL_THREADS / WAVE];
-    __shared__ uint64_t red_am[FULL_THREADS / WAVE];
-    const uint32_t slot = blockIdx.x;
-    const uint32_t row = a.rows[slot];
-    const rl_sampling s = a.settings[row];
-    const uint32_t V = a.vocab;
-    const uint32_t tid = threadIdx.x, wave = tid / WAVE;
-    const uint32_t wl = window_len(a, row);
-    const bool pen = penalises(s) && wl > 0;
-    const float *rowp = a.logits + (uint64_t)row * a.stride;
-    uint32_t *keys = f.keyA + (uint64_t)slot * V;
-    float mx = -__builtin_inff();
-    uint64_t am = 0;
-    for (uint32_t c = tid; c < a.chunks; c += FULL_THREADS) {
-        mx = fmaxf(mx, f.part_max[slot * a.chunks + c]);
-        const uint64_t x = f.part_am[slot * a.chunks + c];
-        am = x > am ? x : am;
-    }
-    if (pen) {
-        const uint32_t *win = a.windows + (uint64_t)row * a.wstride;
-        for (uint32_t i = tid; i < wl; i += FULL_THREADS) {
-            const uint32_t id = win[i];
-            if (id >= V) continue;  // sample.rs:248
-            const float x = penalize(((const RL_GLB float *)rowp)[id], s.repeat_penalty);
-            keys[id] = total_key(x);
-            mx = fmaxf(mx, x);
-            const uint64_t c = composite(argmax_key(x), id);
-            am = c > am ? c : am;
-        }
-    }
-    mx = wave_maxnum_f32(mx);
-    am = wave_max_u64(am);
-    if (lane_id() == 0) {
-        red_max[wave] = mx;
-        red_am[wave] = am;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        for (uint32_t w = 0; w < FULL_THREADS / WAVE; ++w) {
-            mx = fmaxf(mx, red_max[w]);
-            am = red_am[w] > am ? red_am[w] : am;
-        }
-        const uint32_t am_tok = comp_key(am) == 0 ? 0u : comp_id(am);
-        const bool finite = mx > -__builtin_inff() && mx < __builtin_inff();
-        FullRow st{};
-        st.M = mx;
-        st.am_tok = am_tok;
-        st.done = finite ? 0u : 1u;
-        st.small = finite && small_eligible(s, V) ? 1u : 0u;
-        f.row[slot] = st;
-        if (!finite) write_single(a, row, am_tok);  // sample.rs:270-277
-    }
-}
 
 // grid (slots), SORT_THREADS: a stable LSD radix sort of the row's (key, id)
 // pairs by descending key, 8 bits a pass; ids start in ascending order, so

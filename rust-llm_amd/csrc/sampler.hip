@@ -61,6 +61,7 @@ struct rl_sampler_ctx {
     uint32_t *d_pcount = nullptr, *d_pbad = nullptr, *d_plast_in = nullptr, *d_pfirst_out = nullptr;
     uint64_t *d_surv = nullptr;
     FullRow *d_full_row = nullptr;
+    uint32_t *d_full_arrive = nullptr;
     uint64_t *d_argmax_part = nullptr;
     uint32_t *d_tp_nan = nullptr;
     double *d_tp_sum = nullptr;
@@ -138,6 +139,8 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     if (e == hipSuccess) e = c->alloc(&c->d_pfirst_out, fg * MAX_CHUNKS);
     if (e == hipSuccess) e = c->alloc(&c->d_surv, fg * SURV_CAP);
     if (e == hipSuccess) e = c->alloc(&c->d_full_row, fg);
+    if (e == hipSuccess) e = c->alloc(&c->d_full_arrive, fg);
+    if (e == hipSuccess) e = hipMemset(c->d_full_arrive, 0, fg * sizeof(uint32_t));
     if (e == hipSuccess) e = c->alloc(&c->d_argmax_part, std::max<size_t>(CHUNK_SLOTS, max_rows));
     if (e == hipSuccess) e = c->alloc(&c->d_tp_nan, std::max<size_t>(CHUNK_SLOTS, max_rows));
     if (e == hipSuccess) e = c->alloc(&c->d_tp_sum, std::max<size_t>(CHUNK_SLOTS, max_rows));
@@ -277,14 +280,14 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
         f.chunks = std::min(f.chunks, std::max(1u, vocab / 4096));
         FullScratch fs{ctx->d_keyA,     ctx->d_idA,      ctx->d_keyB,       ctx->d_idB,   ctx->d_probs,
                        ctx->d_part_max, ctx->d_part_am,  ctx->d_psum,       ctx->d_pemin, ctx->d_pcount,
-                       ctx->d_pbad,     ctx->d_plast_in, ctx->d_pfirst_out, ctx->d_surv,  ctx->d_full_row};
+                       ctx->d_pbad,     ctx->d_plast_in, ctx->d_pfirst_out, ctx->d_surv,  ctx->d_full_row,
+                       ctx->d_full_arrive};
         const dim3 cgrid(f.chunks, ng);
         const size_t keys_lds = k_full_keys_lds_bytes(vocab, f.chunks);
         if (vec)
             hipLaunchKernelGGL(k_full_keys<true>, cgrid, dim3(FULL_THREADS), keys_lds, st, f, fs);
         else
             hipLaunchKernelGGL(k_full_keys<false>, cgrid, dim3(FULL_THREADS), keys_lds, st, f, fs);
-        hipLaunchKernelGGL(k_full_prep, dim3(ng), dim3(FULL_THREADS), 0, st, f, fs);
         if (ctx->any_small) {
             hipLaunchKernelGGL(k_full_collect, cgrid, dim3(FULL_THREADS), 0, st, f, fs);
             hipLaunchKernelGGL(k_full_small, dim3(ng), dim3(REPLAY_THREADS), 0, st, f, fs);
