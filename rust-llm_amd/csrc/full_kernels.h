@@ -268,15 +268,20 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch
 
 // ------------------------------------------------------------- sort ---
 // One wave's lanes with the same 8-bit digit (among the lanes where valid).
+// Per bit: the lane's bit as a 0 / all-ones word, its ballot, and one
+// three-input logic operation per mask half (m & ~(ballot ^ own)), so the
+// select between a ballot and its complement costs no 64-bit arithmetic.
 __device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
-    uint64_t m = ballot(valid);
+    const uint64_t v = ballot(valid);
+    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
 #pragma unroll
     for (uint32_t b = 0; b < 8; ++b) {
-        const bool bit = (d >> b) & 1u;
-        const uint64_t bb = ballot(bit);
-        m &= bit ? bb : ~bb;
+        const uint32_t own = (uint32_t)((int32_t)(d << (31 - b)) >> 31);  // bit b of d, replicated
+        const uint64_t bb = ballot(own != 0u);
+        lo &= ~((uint32_t)bb ^ own);
+        hi &= ~((uint32_t)(bb >> 32) ^ own);
     }
-    return m;
+    return ((uint64_t)hi << 32) | lo;
 }
 
 constexpr uint32_t SORT_ITEMS = 8;                          // elements per lane per tile
