@@ -284,7 +284,7 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
     return ((uint64_t)hi << 32) | lo;
 }
 
-constexpr uint32_t SORT_ITEMS = 8;                          // elements per lane per tile
+constexpr uint32_t SORT_ITEMS = 10;                         // elements per lane per tile
 constexpr uint32_t SORT_UN = 8;                             // loads in flight per thread in the key scans
 constexpr uint32_t SORT_TILE = SORT_THREADS * SORT_ITEMS;    // elements per tile
 constexpr uint32_t WAVE_SEG = WAVE * SORT_ITEMS;             // a wave's contiguous share of a tile
