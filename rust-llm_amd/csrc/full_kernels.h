@@ -678,6 +678,98 @@ __device__ __forceinline__ void lds_bitonic_desc(RL_LDS uint64_t *v, uint32_t n2
     }
 }
 
+// k_full_small for a row of at most 64 survivors, on one wave: survivor i in
+// lane i after a register bitonic sort, the sequential sums replayed with
+// readlane in candidate order (the same f64 and f32 additions, in the same
+// order, as the block replay), and no workgroup barrier. Leaves the row to
+// the sorting kernels in the same cases as the block path.
+__device__ __forceinline__ void small_one_wave(const RowIO &a, const FullScratch &f, uint32_t slot, uint32_t row,
+                                               const rl_sampling &s, const FullRow &st, uint32_t c) {
+    const uint32_t lane = lane_id();
+    const uint32_t V = a.vocab;
+    const bool by_id = !(s.top_p < 1.0f);  // top-p off: id order, as in the block path
+    const uint64_t *list = f.surv + (uint64_t)slot * SURV_CAP;
+    const bool in = lane < c;
+    uint64_t x = 0;
+    if (in) {
+        x = list[lane];
+        if (by_id) x = ((uint64_t)(uint32_t)x << 32) | comp_key(x);  // ~id in the high half
+    }
+    x = wave_sort64<true>(x);
+    const uint32_t key = by_id ? (uint32_t)x : comp_key(x);
+    const uint32_t id = by_id ? ~(uint32_t)(x >> 32) : comp_id(x);
+    const float p = in ? expf_libm((key_value(key) - st.M) / s.temperature) : 0.0f;
+
+    uint32_t kept = c;
+    double total = 0.0;
+    bool have_total = false;
+    if (!by_id) {
+        if (st.ns_key != 0 && !(read_lane_u32(key, c - 1) >= st.ns_key)) return;
+        if (!(s.top_p > 0.0f)) {
+            kept = 1;  // sample.rs:315-323
+            total = (double)read_lane_f32(p, 0);
+            have_total = true;
+        } else {
+            // The mass interval of the block path (the same S, d and bounds).
+            double S = 0.0;
+            for (uint32_t ch = 0; ch < a.chunks; ++ch) S += f.psum[slot * a.chunks + ch];
+            const double d = 2.25 * ((double)V + 64.0) * 0x1p-53;
+            const double tp = (double)s.top_p;
+            const double t_lo = tp * (S * (1.0 - d)) * (1.0 - 0x1p-50);
+            const double t_hi = tp * (S * (1.0 + d)) * (1.0 + 0x1p-50);
+            // The first partial sums to reach t_lo and t_hi; the cut is
+            // certain when they are the same index.
+            double cum = 0.0, at = 0.0;
+            uint32_t j_lo = c, j_hi = c;
+            for (uint32_t j = 0; j < c; ++j) {
+                cum += (double)read_lane_f32(p, j);
+                if (j_lo == c && cum >= t_lo) {
+                    j_lo = j;
+                    at = cum;
+                }
+                if (cum >= t_hi) {
+                    j_hi = j;
+                    break;
+                }
+            }
+            if (j_lo == c) {
+                at = cum;  // no cut among the survivors: their whole sum
+            } else {
+                if (j_hi != j_lo) return;  // the cut could fall on either side: sort the row
+                kept = j_lo + 1;
+            }
+            total = at;  // the normalising sum, sample.rs:342
+            have_total = true;
+        }
+    }
+    if (!have_total)
+        for (uint32_t j = 0; j < kept; ++j) total += (double)read_lane_f32(p, j);
+    const float inv = (float)(1.0 / total);
+    const float q = p * inv;
+    if (ballot(lane < kept && !(q <= 3.40282347e38f)) != 0) return;  // the sorting kernels walk it in order
+    if (lane < kept && a.out_ids) {
+        a.out_ids[(uint64_t)row * a.cand_stride + lane] = id;
+        a.out_probs[(uint64_t)row * a.cand_stride + lane] = q;
+    }
+    const float u = a.uniforms[row];
+    float cum = 0.0f;  // the draw, sample.rs:349-358
+    uint32_t j = kept - 1;
+    for (uint32_t i = 0; i < kept; ++i) {
+        cum += read_lane_f32(q, i);
+        if (cum > u) {
+            j = i;
+            break;
+        }
+    }
+    const uint32_t tok = read_lane_u32(id, j);
+    if (lane == 0) {
+        a.out_token[row] = tok;
+        a.out_kept[row] = kept;
+        a.out_used[row] = 1;
+        f.row[slot].done = 1;
+    }
+}
+
 // grid (slots), REPLAY_THREADS: finishes a min-p row from its survivors, or
 // leaves it (done stays 0) to the sorting kernels.
 __global__ __launch_bounds__(REPLAY_THREADS) void k_full_small(RowIO a, FullScratch f) {
@@ -697,6 +789,10 @@ __global__ __launch_bounds__(REPLAY_THREADS) void k_full_small(RowIO a, FullScra
     const rl_sampling s = a.settings[row];
     const uint32_t V = a.vocab;
     const uint32_t tid = threadIdx.x;
+    if (c <= WAVE) {  // one wave, no barrier; the other waves leave
+        if (tid < WAVE) small_one_wave(a, f, slot, row, s, st, c);
+        return;
+    }
     // With top-p off the reference keeps id order (no sort, sample.rs:290-305):
     // the survivors are then sorted by ascending id, stored as
     // (~id << 32 | key) so that the same descending sort serves.

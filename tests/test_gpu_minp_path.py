@@ -72,6 +72,27 @@ def test_survivors_at_the_cap(device, n_top):
     case(device, x, settings, label="%d survivors" % n_top)
 
 
+@pytest.mark.parametrize("n_top", [1, 2, 63, 64, 65, 200])
+def test_survivor_counts_around_one_wave(device, n_top):
+    # Up to 64 survivors finish on one wave (register sort, readlane
+    # replays); more take the block path. Spikes in [9, 10] over N(0, 1)
+    # noise: every spike survives min_p >= 0.05 at these temperatures and no
+    # noise element does, so the survivor count is n_top exactly. Row 3 holds
+    # half its spikes at one value (ties, ascending ids).
+    V = 151936
+    rng = np.random.default_rng(1000 + n_top)
+    x = rng.normal(0.0, 1.0, (4, V)).astype(np.float32)
+    for r in range(4):
+        ids = rng.choice(V, n_top, replace=False)
+        x[r, ids] = rng.uniform(9.0, 10.0, n_top)
+        if r == 3:
+            x[r, ids[: max(1, n_top // 2)]] = 9.5
+    settings = [R.sampling(1.0, 0, 0.9, 0.05, 1.0, 0, 1), R.sampling(1.0, 0, 1.0, 0.05, 1.0, 0, 2),
+                R.sampling(0.7, 0, 0.5, 0.1, 1.0, 0, 3), R.sampling(1.0, 0, 0.999, 0.05, 1.0, 0, 4)]
+    got = case(device, x, settings, seed=n_top, label="%d survivors" % n_top)
+    assert got["kept"][1] == n_top  # top-p off: every survivor is kept
+
+
 def test_top_p_off_keeps_id_order(device):
     rng = np.random.default_rng(5)
     V = 30001
