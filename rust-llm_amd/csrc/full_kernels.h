@@ -98,6 +98,23 @@ __device__ __forceinline__ int f32_exponent(float p) {
     return e == 0 ? -126 : e - 127;
 }
 
+// The argument (l - max) / t of the reference's p = exp((l - max) / t)
+// (sample.rs:309). When t is a power of two with a normal reciprocal, the
+// product with that exact reciprocal is the same exact quotient rounded once,
+// so it equals the IEEE division bit for bit; the bulk loops then skip the
+// division's ten-odd instructions (t = 1 on the zipf and ties rows).
+struct TempScale {
+    float t, inv;
+    bool pow2;
+    __device__ explicit TempScale(float t_) : t(t_) {
+        const uint32_t b = __float_as_uint(t_);
+        const uint32_t e = (b >> 23) & 0xFFu;
+        pow2 = (b & 0x807FFFFFu) == 0 && e >= 2 && e <= 252;  // +2^-125 .. +2^125
+        inv = pow2 ? __uint_as_float((254u - e) << 23) : 0.0f;
+    }
+    __device__ float operator()(float d) const { return pow2 ? d * inv : d / t; }
+};
+
 // Whether a row tries the min-p path: min-p on, the whole vocabulary as
 // candidates (top_k 0 or >= vocab), sampling (not greedy).
 __device__ __forceinline__ bool small_eligible(const rl_sampling &s, uint32_t V) {
@@ -585,6 +602,7 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_collect(RowIO a, FullScra
     uint64_t *list = f.surv + (uint64_t)slot * SURV_CAP;
     FullRow *rs = f.row + slot;
     copy_exp_table((RL_LDS uint64_t *)exp_tab);
+    const TempScale tscale(s.temperature);
     const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab};
     const uint32_t lane = lane_id();
     double sum = 0.0;
@@ -614,7 +632,7 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_collect(RowIO a, FullScra
         for (uint32_t u = 0; u < UN; ++u) {
             const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
             const bool ok = j < j1;
-            const float p = ok ? expf_libm_t((key_value(kk[u]) - st.M) / s.temperature, etab) : 0.0f;
+            const float p = ok ? expf_libm_t(tscale(key_value(kk[u]) - st.M), etab) : 0.0f;
             const bool finite = p <= 3.40282347e38f;  // false for NaN
             const bool surv = ok && finite && p >= s.min_p;
             if (ok) sum += (double)p;
@@ -918,6 +936,7 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_probs(RowIO a, FullScratc
     const uint32_t *keys = f.keyA + (uint64_t)slot * V;
     float *probs = f.probs + (uint64_t)slot * V;
     copy_exp_table((RL_LDS uint64_t *)exp_tab);
+    const TempScale tscale(s.temperature);
     const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab};
     double sum = 0.0;
     int emin = 1 << 20;
@@ -944,7 +963,7 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_probs(RowIO a, FullScratc
         for (uint32_t u = 0; u < UN; ++u) {
             const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
             if (j < j1) {
-                const float p = expf_libm_t((key_value(kk[u]) - st.M) / s.temperature, etab);
+                const float p = expf_libm_t(tscale(key_value(kk[u]) - st.M), etab);
                 probs[j] = p;
                 if (!(p <= 3.40282347e38f)) {
                     bad = 1;  // NaN or +inf
