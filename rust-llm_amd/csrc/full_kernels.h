@@ -52,6 +52,8 @@ struct FullRow {
 
 // Survivors the min-p path collects per row (their composites sort in LDS).
 constexpr uint32_t SURV_CAP = 4096;
+// A row's per-chunk results are read one chunk per lane.
+static_assert(MAX_CHUNKS <= WAVE, "a wave holds one lane per chunk");
 
 struct FullScratch {
     uint32_t *keyA, *idA, *keyB, *idB;  // [slot][vocab]
@@ -708,11 +710,13 @@ __device__ __forceinline__ void small_one_wave(const RowIO &a, const FullScratch
     const bool by_id = !(s.top_p < 1.0f);  // top-p off: id order, as in the block path
     const uint64_t *list = f.surv + (uint64_t)slot * SURV_CAP;
     const bool in = lane < c;
-    uint64_t x = 0;
-    if (in) {
-        x = list[lane];
-        if (by_id) x = ((uint64_t)(uint32_t)x << 32) | comp_key(x);  // ~id in the high half
-    }
+    // Every load up front, so that their round trips overlap: the
+    // survivors, the chunks' sums (lane ch holds chunk ch's; chunks <= 64)
+    // and the uniform.
+    uint64_t x = in ? list[lane] : 0ull;
+    const double psum_lane = lane < a.chunks ? f.psum[slot * a.chunks + lane] : 0.0;
+    const float u = a.uniforms[row];
+    if (in && by_id) x = ((uint64_t)(uint32_t)x << 32) | comp_key(x);  // ~id in the high half
     x = wave_sort64<true>(x);
     const uint32_t key = by_id ? (uint32_t)x : comp_key(x);
     const uint32_t id = by_id ? ~(uint32_t)(x >> 32) : comp_id(x);
@@ -728,9 +732,11 @@ __device__ __forceinline__ void small_one_wave(const RowIO &a, const FullScratch
             total = (double)read_lane_f32(p, 0);
             have_total = true;
         } else {
-            // The mass interval of the block path (the same S, d and bounds).
+            // The mass interval of the block path (the same S, summed in the
+            // same order, and the same d and bounds).
             double S = 0.0;
-            for (uint32_t ch = 0; ch < a.chunks; ++ch) S += f.psum[slot * a.chunks + ch];
+            for (uint32_t ch = 0; ch < a.chunks; ++ch)
+                S += __longlong_as_double((long long)read_lane_u64((uint64_t)__double_as_longlong(psum_lane), ch));
             const double d = 2.25 * ((double)V + 64.0) * 0x1p-53;
             const double tp = (double)s.top_p;
             const double t_lo = tp * (S * (1.0 - d)) * (1.0 - 0x1p-50);
@@ -769,7 +775,6 @@ __device__ __forceinline__ void small_one_wave(const RowIO &a, const FullScratch
         a.out_ids[(uint64_t)row * a.cand_stride + lane] = id;
         a.out_probs[(uint64_t)row * a.cand_stride + lane] = q;
     }
-    const float u = a.uniforms[row];
     float cum = 0.0f;  // the draw, sample.rs:349-358
     uint32_t j = kept - 1;
     for (uint32_t i = 0; i < kept; ++i) {
