@@ -858,8 +858,13 @@ __global__ __launch_bounds__(REPLAY_THREADS) void k_full_small(RowIO a, FullScra
             // candidate order) and S (this sum in chunk order) are each
             // within gamma_(V-1) * mass of the exact sum, where
             // gamma_n = n 2^-53 / (1 - n 2^-53); d bounds both, with margin.
+            // Each wave loads the chunks' sums at once (lane ch holds chunk
+            // ch's) and adds them in chunk order.
+            const uint32_t lane = lane_id();
+            const double psum_lane = lane < a.chunks ? f.psum[slot * a.chunks + lane] : 0.0;
             double S = 0.0;
-            for (uint32_t ch = 0; ch < a.chunks; ++ch) S += f.psum[slot * a.chunks + ch];
+            for (uint32_t ch = 0; ch < a.chunks; ++ch)
+                S += __longlong_as_double((long long)read_lane_u64((uint64_t)__double_as_longlong(psum_lane), ch));
             const double d = 2.25 * ((double)V + 64.0) * 0x1p-53;
             const double tp = (double)s.top_p;
             const double t_lo = tp * (S * (1.0 - d)) * (1.0 - 0x1p-50);
