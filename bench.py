@@ -66,10 +66,20 @@ def parse():
 def traffic_bytes(workload):
     """HBM bytes per launch of the dominant kernel, from the PMC runs recorded
     in profiles/traffic.json (FETCH_SIZE + WRITE_SIZE scaled by a copy of known
-    size); None where no such run has been recorded for the workload."""
+    size): a figure of the profile named in `source`, not of this run. None
+    where no such run has been recorded for the workload."""
     try:
         with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
             return json.load(f)[workload]["traffic_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def traffic_source(workload):
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            e = json.load(f)[workload]
+        return "profile: %s (%s)" % (e["source"], e["kernel"])
     except (OSError, KeyError, ValueError):
         return None
 
@@ -99,18 +109,52 @@ def cpu_baseline(wl, logits, windows, wlen, uniforms, settings, budget_s):
     return done / el, done, el
 
 
-def host_threads():
-    """Host threads a CPU baseline may use: the affinity mask, the cgroup CPU
-    quota where one is set, at most 16 (one GPU's share of a box's cores)."""
-    n = len(os.sched_getaffinity(0))
+def host_info():
+    """What a CPU baseline ran on, as the reference's bench reports it
+    (crates/rust-llm/src/bench.rs:457-487): the CPU model, the CPUs the kernel
+    reports (nproc), the affinity mask, the cgroup quota, the one-minute load
+    average and the C library (whose expf the oracle calls). `available` is
+    Rust's available_parallelism: the affinity mask, limited by the quota."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    affinity = len(os.sched_getaffinity(0))
+    available = affinity
+    quota = None
     try:
         with open("/sys/fs/cgroup/cpu.max") as f:
-            quota, period = f.read().split()[:2]
-        if quota != "max":
-            n = min(n, max(1, int(int(quota) // int(period))))
+            quota = f.read().strip()
+        q, period = quota.split()[:2]
+        if q != "max":
+            available = min(available, max(1, int(q) // int(period)))
     except (OSError, ValueError):
         pass
-    return max(1, min(n, 16))
+    load = None
+    try:
+        with open("/proc/loadavg") as f:
+            load = float(f.read().split()[0])
+    except (OSError, ValueError, IndexError):
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity": affinity, "cpu_max": quota,
+            "available_parallelism": available, "load_average_1m": load,
+            "libc": " ".join(os.confstr("CS_GNU_LIBC_VERSION").split()) if hasattr(os, "confstr") else None}
+
+
+# A one-GPU box's share of the host's cores: the threaded baseline uses no
+# more threads than this even where the affinity mask shows more CPUs.
+GPU_CPU_SHARE = 16
+
+
+def host_threads(info):
+    """Threads for the threaded CPU baseline: available_parallelism, capped at
+    one GPU's share of the host (GPU_CPU_SHARE)."""
+    return max(1, min(info["available_parallelism"], GPU_CPU_SHARE))
 
 
 def cpu_baseline_threads(wl, logits, windows, wlen, uniforms, settings, budget_s, threads):
@@ -275,6 +319,7 @@ def bench_embed(args):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_bytes("embed_n%d" % n),
+            "traffic_source": traffic_source("embed_n%d" % n),
             "algorithmic_bytes_per_call": alg_bytes,
             "call_ms_mean": round(mean_ms, 5),
             "call_ms_median_alone": round(median_ms, 5),
@@ -378,6 +423,7 @@ def bench_head(args):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None if sample else traffic_bytes("head_t%d" % t),
+            "traffic_source": None if sample else traffic_source("head_t%d" % t),
             "algorithmic_bytes_per_call": alg_bytes,
             "call_ms_mean": round(mean_ms, 5),
             "call_ms_median_alone": round(median_ms, 5),
@@ -445,8 +491,12 @@ def main():
     ms_per_step, mean_ms, per_call_ms = time_calls(step, args, stream)
     median_ms = per_call_ms[len(per_call_ms) // 2]
     rows_per_s = wl.rows / (ms_per_step / 1e3)
+    kept_total = None
     if args.op == "sample":
-        alg_bytes = wl.algorithmic_bytes() if cs else wl.algorithmic_bytes(kept_out=0)
+        # Every call returns the same kept counts (the calls are idempotent):
+        # the candidates written are the kept set the last call returned.
+        kept_total = int(out_kept.to(torch.int64).sum().item()) if cs else 0
+        alg_bytes = wl.algorithmic_bytes(kept_total)
     else:  # the logits once, and a token (and a probability) per row
         alg_bytes = wl.rows * (wl.vocab * 4 + 4 + (4 if args.op == "top_probability" else 0))
     achieved = alg_bytes / (mean_ms / 1e3) / 1e9
@@ -465,18 +515,23 @@ def main():
     cpu = None
     cpu_n = None
     if args.cpu_seconds > 0 and args.op == "sample":
+        info = host_info()
         rate, n, el = cpu_baseline(wl, logits, windows, wlen, uniforms, settings, args.cpu_seconds)
         cpu = {"value": round(rate, 2), "unit": "rows/s", "cores": 1, "kind": "port",
-               "sample": "%d rows of the same workload (%s) through the oracle on one host core in %.1f s"
-                         % (n, name, el)}
+               "sample": "%d rows of the same workload (%s) through the oracle (the C restatement of the "
+                         "reference sampler) on one host core in %.1f s" % (n, name, el),
+               "host": info}
         print("[bench] cpu baseline %.1f rows/s over %d rows" % (rate, n), file=sys.stderr, flush=True)
-        nt = host_threads()
+        nt = host_threads(info)
         if nt > 1:
             rate_n, n_n, el_n = cpu_baseline_threads(wl, logits, windows, wlen, uniforms, settings,
                                                      args.cpu_seconds / 2, nt)
             cpu_n = {"value": round(rate_n, 2), "unit": "rows/s", "cores": nt, "kind": "port",
                      "sample": "%d rows of the same workload (%s) through the oracle on %d host threads, rows "
-                               "split over them, in %.1f s" % (n_n, name, nt, el_n)}
+                               "split over them, in %.1f s (available_parallelism %d, at most %d: one GPU's "
+                               "share of the host)" % (n_n, name, nt, el_n, info["available_parallelism"],
+                                                      GPU_CPU_SHARE),
+                     "host": info}
             print("[bench] cpu baseline, %d threads: %.1f rows/s over %d rows" % (nt, rate_n, n_n),
                   file=sys.stderr, flush=True)
 
@@ -511,7 +566,9 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_bytes(name) if args.op == "sample" else None,
+            "traffic_source": traffic_source(name) if args.op == "sample" else None,
             "algorithmic_bytes_per_call": alg_bytes,
+            "kept_per_call": kept_total,
             "call_ms_mean": round(mean_ms, 5),
             "call_ms_median_alone": round(median_ms, 5),
         },

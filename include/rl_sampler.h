@@ -15,9 +15,19 @@
  *     Calls are stream-ordered and return before the kernels finish.
  *   - Every entry point returns an rl_status; nothing panics or throws across
  *     the ABI. rl_sampler_last_error() gives a message for the calling thread.
- *   - A context is used by one thread at a time (the reference's Sampler is
- *     `&mut self`, sample.rs:215). All device memory a call needs is allocated
- *     by rl_sampler_create and rl_sampler_configure; sampling allocates nothing
+ *   - A context is used by one thread and one stream at a time (the
+ *     reference's Sampler is `&mut self`, sample.rs:215). A call's scratch
+ *     (per-row arrival counters, chunk candidate lists, row state) lives in the
+ *     context and calls return before their kernels finish, so two calls on
+ *     one context that can overlap on the device (issued to different streams
+ *     without an ordering between them) race and can return wrong tokens. Use
+ *     one context per stream.
+ *   - rl_sampler_configure uploads with a synchronous copy on the null stream,
+ *     which does not wait for work on non-blocking streams: call it only once
+ *     the context's earlier calls have completed (synchronize their stream
+ *     first).
+ *   - All device memory a call needs is allocated by rl_sampler_create;
+ *     neither configure nor sampling allocates, on the device or the host
  *     (the reference's zero-allocation contract, tests/sample_allocations.rs).
  */
 #ifndef RL_SAMPLER_H
@@ -100,8 +110,20 @@ int rl_sampler_required_cand_stride(const rl_sampler_ctx *ctx, uint64_t *out);
  *               Rng for this row (sample.rs:349): 0 for greedy rows and rows
  *               with no finite maximum
  *   out_cand_ids, out_cand_probs [rows][cand_stride]: the survivors and their
- *               normalised probabilities in the reference's order
- *               (Sampler::candidates, sample.rs:188-190); both NULL to skip
+ *               normalised probabilities (Sampler::candidates,
+ *               sample.rs:188-190); both NULL to skip. The order is the
+ *               reference's wherever the reference fixes it: descending logit,
+ *               ascending id on ties, when top-p is on (sample.rs:303-305);
+ *               id order when top-p is off and top-k keeps the whole
+ *               vocabulary (sample.rs:290-296, :326-340). One corner
+ *               differs: with top_p >= 1 and 0 < top_k < vocab the reference
+ *               leaves its candidates in the order Rust's
+ *               select_nth_unstable_by produces (sample.rs:294), which this
+ *               library cannot reproduce; it returns them in descending order
+ *               instead. The kept set and probabilities are the same, but the
+ *               draw walks another order, so the same uniform can pick a
+ *               different token there. Greedy rows and rows with top-p on are
+ *               unaffected.
  * Returns once the work is queued on `stream`. */
 int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t row_stride,
                            uint32_t rows, uint32_t vocab, const uint32_t *windows,

@@ -86,7 +86,13 @@ int rl_host_sampler_verify(rl_host_sampler *s, const float *device_rows, uint64_
  * the sampler's candidates. The committed token is written to *token: it is
  * the verify pick unless an earlier committed row drew nothing (no finite
  * maximum, sample.rs:270-277), in which case the stream gives this row another
- * uniform and the row is sampled again with it. */
+ * uniform and the row is sampled again with it. Row r > 0 was sampled with the
+ * window that assumes drafts[0..r) were accepted, so it can only be committed
+ * while the token committed for row r-1 equals drafts[r-1] (the generation
+ * loop stops at the first mismatch, generate.rs:412-429): otherwise
+ * RL_ERR_ARGUMENT and nothing changes. A sample, batch or reset call in
+ * between abandons the verify. No call here allocates host or device memory
+ * (everything is sized by rl_host_sampler_new). */
 int rl_host_sampler_commit_verified(rl_host_sampler *s, uint32_t row, uint32_t *token);
 
 /* ---- Batched serving: one device call over many samplers ---- */

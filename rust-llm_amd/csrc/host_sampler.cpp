@@ -95,6 +95,9 @@ uint64_t rl_entropy_seed(void) {
 
 }  // extern "C"
 
+// Every buffer a call touches is sized in rl_host_sampler_new, as the
+// reference's Sampler sizes its own in Sampler::new (sample.rs:156-172): no
+// per-call path below allocates host memory (tests/sample_allocations.rs).
 struct rl_host_sampler {
     int device = 0;
     size_t vocab = 0;
@@ -105,7 +108,10 @@ struct rl_host_sampler {
     size_t at = 0, filled = 0;
     rl_rng rng{};
     rl_sampler_ctx *ctx = nullptr;
-    std::vector<rl_sampling> configured;  // what ctx was last configured with
+    // What ctx was last configured with (capacity max_rows), `same_set` holds
+    // max_rows copies of `set`, `batch_set` the settings of a batch call.
+    std::vector<rl_sampling> configured, same_set, batch_set;
+    std::vector<rl_rng> batch_probe;
     uint64_t cand_cap = 1;
     // device buffers
     float *d_row = nullptr;
@@ -118,24 +124,21 @@ struct rl_host_sampler {
     uint32_t *h_windows = nullptr, *h_wlen = nullptr, *h_token = nullptr, *h_kept = nullptr;
     float *h_uniforms = nullptr;
     uint8_t *h_used = nullptr;
-    // the last call's survivors (Sampler::candidates)
+    // the last call's survivors (Sampler::candidates), capacity cand_cap
     std::vector<uint32_t> cand_ids;
     std::vector<float> cand_probs;
     size_t kept = 0;
-    // the last verify, uncommitted
-    struct Verified {
-        uint32_t token, kept;
-        uint8_t used;
-        float uniform;
-        std::vector<uint32_t> ids;
-        std::vector<float> probs;
-    };
-    std::vector<Verified> verified;
-    uint32_t next_commit = 0;
+    // The last verify, uncommitted: per row the pick, its kept count, whether
+    // it drew and the uniform it was given (capacity max_rows each). Row i's
+    // candidates stay in device row i until it is committed.
+    uint32_t v_rows_n = 0, next_commit = 0;
+    std::vector<uint32_t> v_token, v_kept, v_drafts;
+    std::vector<uint8_t> v_used;
+    std::vector<float> v_uniform;
+    uint32_t last_committed = 0;
     const float *v_rows = nullptr;
     uint64_t v_stride = 0;
     void *v_stream = nullptr;
-    std::vector<uint32_t> v_drafts;
 
     ~rl_host_sampler() {
         for (void *p : {(void *)d_row, (void *)d_windows, (void *)d_wlen, (void *)d_token, (void *)d_kept,
@@ -154,29 +157,32 @@ struct rl_host_sampler {
         filled = std::min(filled + 1, recent.size());
     }
 
-    // Configures the device context for `rows` rows of these settings.
-    int ensure_configured(const std::vector<rl_sampling> &want) {
-        if (configured.size() == want.size() &&
-            std::equal(want.begin(), want.end(), configured.begin(), same))
-            return RL_OK;
-        const int rc = rl_sampler_configure(ctx, want.data(), (uint32_t)want.size());
-        if (rc != RL_OK) return rc;
-        configured = want;
+    // Configures the device context for rows 0..n-1 of `want`, unless the
+    // rows it is configured for already begin with exactly these settings
+    // (sample_rows takes any prefix of the configured rows).
+    int ensure_configured(const rl_sampling *want, uint32_t n) {
+        if (n <= configured.size() && std::equal(want, want + n, configured.begin(), same)) return RL_OK;
+        const int rc = rl_sampler_configure(ctx, want, n);
+        if (rc != RL_OK) {
+            configured.clear();
+            return rc;
+        }
+        configured.assign(want, want + n);  // n <= max_rows = capacity
         return RL_OK;
     }
 
-    // The window row `i` of a verify sees: the ring after remembering
-    // drafts[0..i), as recent[..filled].
+    // The window row `i` of a verify sees, recent[..filled] of the ring after
+    // remembering drafts[0..i) (sample.rs:205-212), written to `out`. Draft m
+    // lands in slot (at + m) % len; a later draft overwrites an earlier one.
     size_t window_after(const uint32_t *drafts, uint32_t i, uint32_t *out) const {
-        if (recent.empty()) return 0;
-        std::vector<uint32_t> r = recent;
-        size_t a = at, f = filled;
-        for (uint32_t d = 0; d < i; ++d) {
-            r[a] = drafts[d];
-            a = (a + 1) % r.size();
-            f = std::min(f + 1, r.size());
+        const size_t len = recent.size();
+        if (len == 0) return 0;
+        const size_t f = std::min(filled + (size_t)i, len);
+        std::copy(recent.begin(), recent.begin() + f, out);
+        for (uint32_t m = i > len ? (uint32_t)(i - len) : 0u; m < i; ++m) {
+            const size_t slot = (at + m) % len;
+            if (slot < f) out[slot] = drafts[m];
         }
-        std::copy(r.begin(), r.begin() + f, out);
         return f;
     }
 
@@ -199,8 +205,12 @@ struct rl_host_sampler {
         return RL_OK;
     }
 
+    // Copies device row `row`'s n survivors into ids/probs, whose capacity
+    // (reserved at creation) holds any kept count the settings allow.
     int fetch_candidates(uint32_t row, uint32_t n, std::vector<uint32_t> &ids, std::vector<float> &probs,
                          void *stream) {
+        if (n > ids.capacity() || n > probs.capacity())
+            return herr(RL_ERR_CAPACITY, "more candidates than the sampler was sized for");
         ids.resize(n);
         probs.resize(n);
         hipStream_t st = static_cast<hipStream_t>(stream);
@@ -212,15 +222,21 @@ struct rl_host_sampler {
         return RL_OK;
     }
 
+    void forget_verify() {
+        v_rows_n = 0;
+        next_commit = 0;
+    }
+
     int sample_device(const float *d_logits, size_t n, uint32_t *token, void *stream) {
         if (n != vocab) return herr(RL_ERR_VOCAB, "this sampler was built for a different vocabulary");
-        int rc = ensure_configured(std::vector<rl_sampling>(1, set));
+        int rc = ensure_configured(&set, 1);
         if (rc != RL_OK) return rc;
         const bool pen = penalises(set) && filled > 0;
         h_wlen[0] = pen ? (uint32_t)filled : 0u;
         if (pen) std::copy(recent.begin(), recent.begin() + filled, h_windows);
         rl_rng probe = rng;
         h_uniforms[0] = rl_rng_next_f32(&probe);
+        forget_verify();  // the device rows a verify left are overwritten
         rc = run(d_logits, vocab, 1, stream);
         if (rc != RL_OK) return rc;
         rc = fetch_candidates(0, h_kept[0], cand_ids, cand_probs, stream);
@@ -229,7 +245,6 @@ struct rl_host_sampler {
         if (h_used[0]) rng = probe;
         *token = h_token[0];
         remember(*token);  // sample.rs:217
-        verified.clear();
         return RL_OK;
     }
 };
@@ -248,7 +263,12 @@ int rl_host_sampler_new(int device, size_t vocab, const rl_sampling *set, uint32
     s->vocab = vocab;
     s->set = *set;
     s->max_rows = max_rows;
-    s->recent.assign((size_t)set->repeat_last_n, 0u);
+    try {
+        s->recent.assign((size_t)set->repeat_last_n, 0u);
+    } catch (const std::bad_alloc &) {
+        delete s;
+        return herr(RL_ERR_CAPACITY, "out of host memory");
+    }
     s->wcap = std::max<uint32_t>(1u, (uint32_t)set->repeat_last_n);
     rl_rng_seeded(&s->rng, set->seed);
     // Candidate slots the settings can keep (sample.rs:159: the whole
@@ -284,8 +304,29 @@ int rl_host_sampler_new(int device, size_t vocab, const rl_sampling *set, uint32
         delete s;
         return herr(RL_ERR_DEVICE, hipGetErrorString(e));
     }
-    s->cand_ids.reserve(s->cand_cap);
-    s->cand_probs.reserve(s->cand_cap);
+    try {
+        s->cand_ids.reserve(s->cand_cap);
+        s->cand_probs.reserve(s->cand_cap);
+        s->configured.reserve(max_rows);
+        s->same_set.assign(max_rows, *set);
+        s->batch_set.reserve(max_rows);
+        s->batch_probe.reserve(max_rows);
+        s->v_token.assign(max_rows, 0u);
+        s->v_kept.assign(max_rows, 0u);
+        s->v_drafts.assign(max_rows, 0u);
+        s->v_used.assign(max_rows, 0);
+        s->v_uniform.assign(max_rows, 0.0f);
+    } catch (const std::bad_alloc &) {
+        delete s;
+        return herr(RL_ERR_CAPACITY, "out of host memory");
+    }
+    // Every row of this sampler has its settings: configured once, here, for
+    // all max_rows rows, so a call over any number of them reconfigures nothing.
+    rc = s->ensure_configured(s->same_set.data(), max_rows);
+    if (rc != RL_OK) {
+        delete s;
+        return rc;
+    }
     *out = s;
     return RL_OK;
 }
@@ -298,7 +339,7 @@ void rl_host_sampler_reset(rl_host_sampler *s) {  // sample.rs:194-198
     s->at = 0;
     s->filled = 0;
     s->kept = 0;
-    s->verified.clear();
+    s->forget_verify();
 }
 
 void rl_host_sampler_remember(rl_host_sampler *s, uint32_t token) { s->remember(token); }
@@ -329,9 +370,9 @@ int rl_host_sampler_verify(rl_host_sampler *s, const float *device_rows, uint64_
                            const uint32_t *drafts, uint32_t n_drafts, uint32_t *picks, void *stream) {
     if (!s || !device_rows || !picks || (n_drafts && !drafts)) return herr(RL_ERR_ARGUMENT, "null argument");
     if (n != s->vocab) return herr(RL_ERR_VOCAB, "this sampler was built for a different vocabulary");
+    if (n_drafts >= s->max_rows) return herr(RL_ERR_CAPACITY, "more verify rows than max_rows");
     const uint32_t rows = n_drafts + 1;
-    if (rows > s->max_rows) return herr(RL_ERR_CAPACITY, "more verify rows than max_rows");
-    int rc = s->ensure_configured(std::vector<rl_sampling>(rows, s->set));
+    int rc = s->ensure_configured(s->same_set.data(), rows);
     if (rc != RL_OK) return rc;
     const bool pen = penalises(s->set);
     rl_rng probe = s->rng;
@@ -341,57 +382,62 @@ int rl_host_sampler_verify(rl_host_sampler *s, const float *device_rows, uint64_
         s->h_wlen[i] = (uint32_t)f;
         s->h_uniforms[i] = greedy ? 0.0f : rl_rng_next_f32(&probe);  // one draw per drawing row
     }
+    s->forget_verify();
     rc = s->run(device_rows, row_stride, rows, stream);
     if (rc != RL_OK) return rc;
-    s->verified.assign(rows, {});
     for (uint32_t i = 0; i < rows; ++i) {
-        auto &v = s->verified[i];
-        v.token = s->h_token[i];
-        v.kept = s->h_kept[i];
-        v.used = s->h_used[i];
-        v.uniform = s->h_uniforms[i];
-        rc = s->fetch_candidates(i, v.kept, v.ids, v.probs, stream);
-        if (rc != RL_OK) return rc;
-        picks[i] = v.token;
+        s->v_token[i] = s->h_token[i];
+        s->v_kept[i] = s->h_kept[i];
+        s->v_used[i] = s->h_used[i];
+        s->v_uniform[i] = s->h_uniforms[i];
+        picks[i] = s->h_token[i];
     }
+    std::copy(drafts, drafts + n_drafts, s->v_drafts.begin());
+    s->v_rows_n = rows;
     s->next_commit = 0;
     s->v_rows = device_rows;
     s->v_stride = row_stride;
     s->v_stream = stream;
-    s->v_drafts.assign(drafts, drafts + n_drafts);
     return RL_OK;
 }
 
 int rl_host_sampler_commit_verified(rl_host_sampler *s, uint32_t row, uint32_t *token) {
     if (!s || !token) return herr(RL_ERR_ARGUMENT, "null argument");
-    if (row != s->next_commit || row >= s->verified.size())
+    if (row != s->next_commit || row >= s->v_rows_n)
         return herr(RL_ERR_ARGUMENT, "verify rows are committed in order, once");
-    auto &v = s->verified[row];
+    // Row `row` was sampled with the window after drafts[0..row): committing
+    // it is only meaningful while every earlier committed token was its draft
+    // (generate.rs:412-429 stops at the first mismatch).
+    if (row > 0 && s->last_committed != s->v_drafts[row - 1])
+        return herr(RL_ERR_ARGUMENT, "the previous committed token differs from its draft: the generation loop "
+                                     "stops there, and this row's window assumed the draft");
     // The row was sampled with the uniform the stream would give if every
     // earlier row drew; an earlier row with no finite maximum drew nothing, so
     // recompute this one with the uniform the stream really gives now.
     rl_rng probe = s->rng;
     const float u = rl_rng_next_f32(&probe);
-    if (!(s->set.temperature <= 0.0f) && u != v.uniform) {
+    uint32_t cand_row = row;
+    if (!(s->set.temperature <= 0.0f) && u != s->v_uniform[row]) {
         const bool pen = penalises(s->set) && s->filled > 0;
         s->h_wlen[0] = pen ? (uint32_t)s->filled : 0u;
         if (pen) std::copy(s->recent.begin(), s->recent.begin() + s->filled, s->h_windows);
         s->h_uniforms[0] = u;
-        int rc = s->ensure_configured(std::vector<rl_sampling>(1, s->set));
-        if (rc == RL_OK) rc = s->run(s->v_rows + (uint64_t)row * s->v_stride, s->vocab, 1, s->v_stream);
-        if (rc == RL_OK) rc = s->fetch_candidates(0, s->h_kept[0], v.ids, v.probs, s->v_stream);
+        // Device row 0 belongs to a row already committed; later rows keep theirs.
+        const int rc = s->run(s->v_rows + (uint64_t)row * s->v_stride, s->vocab, 1, s->v_stream);
         if (rc != RL_OK) return rc;
-        v.token = s->h_token[0];
-        v.kept = s->h_kept[0];
-        v.used = s->h_used[0];
+        s->v_token[row] = s->h_token[0];
+        s->v_kept[row] = s->h_kept[0];
+        s->v_used[row] = s->h_used[0];
+        cand_row = 0;
     }
-    if (v.used) s->rng = probe;
-    s->cand_ids = v.ids;
-    s->cand_probs = v.probs;
-    s->kept = v.kept;
-    s->remember(v.token);
+    const int rc = s->fetch_candidates(cand_row, s->v_kept[row], s->cand_ids, s->cand_probs, s->v_stream);
+    if (rc != RL_OK) return rc;
+    if (s->v_used[row]) s->rng = probe;
+    s->kept = s->v_kept[row];
+    s->remember(s->v_token[row]);
+    s->last_committed = s->v_token[row];
     s->next_commit = row + 1;
-    *token = v.token;
+    *token = s->v_token[row];
     return RL_OK;
 }
 
@@ -400,38 +446,34 @@ int rl_host_sample_batch(rl_host_sampler *const *samplers, uint32_t n, const flo
     if (!samplers || n == 0 || !device_logits || !tokens) return herr(RL_ERR_ARGUMENT, "bad argument");
     rl_host_sampler *h = samplers[0];
     if (n > h->max_rows) return herr(RL_ERR_CAPACITY, "more samplers than the first one's max_rows");
-    std::vector<rl_sampling> want(n);
-    std::vector<rl_rng> probes(n);
+    h->batch_set.clear();
+    h->batch_probe.clear();
     for (uint32_t i = 0; i < n; ++i) {
         rl_host_sampler *s = samplers[i];
         if (s->vocab != vocab || vocab != h->vocab)
             return herr(RL_ERR_VOCAB, "this sampler was built for a different vocabulary");
         if (s->filled > h->wcap) return herr(RL_ERR_CAPACITY, "a window longer than the first sampler's");
         if (s->cand_cap > h->cand_cap) return herr(RL_ERR_CAPACITY, "a sampler keeps more candidates than the first");
-        want[i] = s->set;
+        h->batch_set.push_back(s->set);  // within the capacity reserved at creation
         const bool pen = penalises(s->set) && s->filled > 0;
         h->h_wlen[i] = pen ? (uint32_t)s->filled : 0u;
         if (pen) std::copy(s->recent.begin(), s->recent.begin() + s->filled, h->h_windows + (size_t)i * h->wcap);
-        probes[i] = s->rng;
-        h->h_uniforms[i] = rl_rng_next_f32(&probes[i]);
+        h->batch_probe.push_back(s->rng);
+        h->h_uniforms[i] = rl_rng_next_f32(&h->batch_probe[i]);
     }
-    int rc = h->ensure_configured(want);
+    int rc = h->ensure_configured(h->batch_set.data(), n);
     if (rc != RL_OK) return rc;
+    for (uint32_t i = 0; i < n; ++i) samplers[i]->forget_verify();  // h's device rows are overwritten
     rc = h->run(device_logits, row_stride, n, stream);
     if (rc != RL_OK) return rc;
-    std::vector<uint32_t> ids;
-    std::vector<float> probs;
-    std::vector<uint32_t> tok(h->h_token, h->h_token + n), kept(h->h_kept, h->h_kept + n);
-    std::vector<uint8_t> used(h->h_used, h->h_used + n);
     for (uint32_t i = 0; i < n; ++i) {
         rl_host_sampler *s = samplers[i];
-        rc = h->fetch_candidates(i, kept[i], s->cand_ids, s->cand_probs, stream);
+        rc = h->fetch_candidates(i, h->h_kept[i], s->cand_ids, s->cand_probs, stream);
         if (rc != RL_OK) return rc;
-        s->kept = kept[i];
-        if (used[i]) s->rng = probes[i];
-        tokens[i] = tok[i];
-        s->remember(tok[i]);
-        s->verified.clear();
+        s->kept = h->h_kept[i];
+        if (h->h_used[i]) s->rng = h->batch_probe[i];
+        tokens[i] = h->h_token[i];
+        s->remember(h->h_token[i]);
     }
     return RL_OK;
 }

@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -40,6 +41,30 @@ uint64_t row_cand_need(const rl_sampling &s, uint32_t vocab) {
     return s.top_k;
 }
 
+// rl_argmax_rows's grid: (chunks, rows); one 64-bit partial result per
+// (row, chunk) in `part`, merged per row by k_argmax_final.
+uint32_t argmax_chunks(uint32_t rows, uint32_t vocab) {
+    const uint32_t chunks = std::min(MAX_CHUNKS, (TARGET_WGS + rows - 1) / rows);
+    return std::max(1u, std::min(chunks, vocab / 4096));
+}
+
+int launch_argmax(const float *logits, uint64_t row_stride, uint32_t rows, uint32_t vocab, uint32_t *out_token,
+                  uint64_t *part, void *stream) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const uint64_t stride = rows > 1 ? row_stride : vocab;
+    const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (stride % 4 == 0);
+    const uint32_t chunks = argmax_chunks(rows, vocab);
+    dim3 grid(chunks, rows);
+    if (vec)
+        hipLaunchKernelGGL(k_argmax_part<true>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks, part);
+    else
+        hipLaunchKernelGGL(k_argmax_part<false>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks, part);
+    hipLaunchKernelGGL(k_argmax_final, dim3((rows + 255) / 256), dim3(256), 0, st, part, rows, chunks, out_token);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "argmax kernels");
+    return RL_OK;
+}
+
 }  // namespace
 
 void rl::set_last_error(const std::string &msg) { g_last_error = msg; }
@@ -69,7 +94,7 @@ struct rl_sampler_ctx {
     std::vector<void *> owned;
     // Host copy of the plan made by configure.
     uint32_t configured = 0;
-    std::vector<uint32_t> stream_rows, full_rows;  // ascending
+    std::vector<uint32_t> stream_rows, full_rows;  // ascending; capacity max_rows
     uint64_t cand_need = 0;
     bool any_drawing = false;
     bool any_small = false;  // a full-path row may take the min-p path
@@ -112,6 +137,13 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     while ((1u << bits) < 2 * max_window) ++bits;
     c->hash_bits = bits;
     c->full_group = std::min(max_rows, FULL_GROUP_MAX);
+    try {  // configure fills these in place
+        c->stream_rows.reserve(max_rows);
+        c->full_rows.reserve(max_rows);
+    } catch (const std::bad_alloc &) {
+        delete c;
+        return fail(RL_ERR_CAPACITY, "out of host memory");
+    }
     const size_t fg = c->full_group, V = vocab;
     hipError_t e = hipSuccess;
     if (e == hipSuccess) e = c->alloc(&c->d_settings, max_rows);
@@ -166,17 +198,23 @@ int rl_sampler_configure(rl_sampler_ctx *ctx, const rl_sampling *settings, uint3
         return fail(RL_ERR_CAPACITY, "rows must be in 1..max_rows");
     DeviceGuard g(ctx->device);
     if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select device");
-    std::vector<uint32_t> sr, fr;
+    // The plan is rebuilt in place (the lists' capacity is max_rows, so this
+    // allocates nothing); until the upload succeeds the context is unconfigured.
+    ctx->configured = 0;
+    ctx->stream_rows.clear();
+    ctx->full_rows.clear();
     uint64_t need = 0;
     bool drawing = false, small = false;
     for (uint32_t r = 0; r < rows; ++r) {
-        (plan_row(settings[r], ctx->vocab) == Path::Stream ? sr : fr).push_back(r);
+        const Path p = plan_row(settings[r], ctx->vocab);
+        (p == Path::Stream ? ctx->stream_rows : ctx->full_rows).push_back(r);
         need = std::max(need, row_cand_need(settings[r], ctx->vocab));
         drawing = drawing || !(settings[r].temperature <= 0.0f);
-        small = small || (plan_row(settings[r], ctx->vocab) == Path::Full && settings[r].min_p > 0.0f &&
-                          settings[r].temperature > 0.0f &&
+        small = small || (p == Path::Full && settings[r].min_p > 0.0f && settings[r].temperature > 0.0f &&
                           (settings[r].top_k == 0 || settings[r].top_k >= ctx->vocab));
     }
+    const auto &sr = ctx->stream_rows;
+    const auto &fr = ctx->full_rows;
     hipError_t e = hipMemcpy(ctx->d_settings, settings, rows * sizeof(rl_sampling), hipMemcpyHostToDevice);
     if (e == hipSuccess && !sr.empty())
         e = hipMemcpy(ctx->d_stream_rows, sr.data(), sr.size() * sizeof(uint32_t), hipMemcpyHostToDevice);
@@ -184,8 +222,6 @@ int rl_sampler_configure(rl_sampler_ctx *ctx, const rl_sampling *settings, uint3
         e = hipMemcpy(ctx->d_full_rows, fr.data(), fr.size() * sizeof(uint32_t), hipMemcpyHostToDevice);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpy (configure)");
     ctx->configured = rows;
-    ctx->stream_rows = std::move(sr);
-    ctx->full_rows = std::move(fr);
     ctx->cand_need = need;
     ctx->any_drawing = drawing;
     ctx->any_small = small;
@@ -316,23 +352,7 @@ int rl_argmax_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t row_stride
     if (rows > 1 && row_stride < vocab) return fail(RL_ERR_ARGUMENT, "row_stride below vocab");
     DeviceGuard g(ctx->device);
     if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select device");
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    const uint64_t stride = rows > 1 ? row_stride : vocab;
-    const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (stride % 4 == 0);
-    uint32_t chunks = std::min(MAX_CHUNKS, (TARGET_WGS + rows - 1) / rows);
-    chunks = std::max(1u, std::min(chunks, vocab / 4096));
-    dim3 grid(chunks, rows);
-    if (vec)
-        hipLaunchKernelGGL(k_argmax_part<true>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
-                           ctx->d_argmax_part);
-    else
-        hipLaunchKernelGGL(k_argmax_part<false>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
-                           ctx->d_argmax_part);
-    hipLaunchKernelGGL(k_argmax_final, dim3((rows + 255) / 256), dim3(256), 0, st, ctx->d_argmax_part, rows,
-                       chunks, out_token);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return hip_fail(e, "argmax kernels");
-    return RL_OK;
+    return launch_argmax(logits, row_stride, rows, vocab, out_token, ctx->d_argmax_part, stream);
 }
 
 int rl_top_probability_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t row_stride, uint32_t rows,

@@ -100,14 +100,14 @@ class Workload:
         wl_lib().wl_verify_history(self.seed, self.vocab, h.ctypes.data)
         return h
 
-    def algorithmic_bytes(self, kept_out=None):
-        """HBM bytes one call must move: the logits once, the windows, the
-        uniforms, and token + kept + kept_out (id, prob) pairs per row."""
-        if kept_out is None:
-            s = self.settings(0)
-            kept_out = 1 if s.temperature <= 0 else (self.vocab if s.top_k == 0 else s.top_k)
-        per_row = self.vocab * 4 + WINDOW * 4 + 4 + 4 + 4 + kept_out * 8
-        return self.rows * per_row
+    def algorithmic_bytes(self, kept_total):
+        """HBM bytes one call must move: per row the logits once, the window,
+        the uniform, the token and the kept count; plus one (id, prob) pair per
+        candidate the call keeps. `kept_total` is the sum over rows of the
+        kept counts the call returned (Sampler::kept, sample.rs:342-347), or 0
+        when the candidates are not written."""
+        per_row = self.vocab * 4 + WINDOW * 4 + 4 + 4 + 4
+        return self.rows * per_row + int(kept_total) * 8
 
 
 S = rl_sampler.sampling

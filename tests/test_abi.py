@@ -94,3 +94,16 @@ def test_the_product_path_fails_loudly_without_its_library(monkeypatch, tmp_path
     monkeypatch.setattr(R, "LIB_PATH", str(tmp_path / "missing.so"))
     with pytest.raises(RuntimeError, match="missing"):
         R.lib()
+
+
+def test_entropy_seed_comes_from_the_os_and_needs_no_device():
+    """entropy_seed (sample.rs:107-112) is a host-only seed from OS entropy:
+    it runs here without a GPU, and successive calls differ (64 bits each: a
+    repeat among 64 calls has probability about 1e-16)."""
+    seeds = [R.entropy_seed() for _ in range(64)]
+    assert len(set(seeds)) == len(seeds)
+    assert all(0 <= s < 1 << 64 for s in seeds)
+    assert any(s >= 1 << 32 for s in seeds), "the high half is never filled"
+    # Each bit position takes both values over the calls.
+    ones = [sum((s >> b) & 1 for s in seeds) for b in range(64)]
+    assert all(0 < c < len(seeds) for c in ones), ones

@@ -136,3 +136,31 @@ def test_a_vocabulary_mismatch_is_an_error_not_a_panic(device):
     with pytest.raises(R.SamplerError) as e:
         s.sample(np.zeros(99, np.float32))
     assert e.value.code == R.RL_ERR_VOCAB
+
+
+def test_committing_past_a_rejected_draft_is_refused(device):
+    """Row r of a verify assumed drafts[0..r) were accepted; once the committed
+    token of row r-1 differs from drafts[r-1] the generation loop stops
+    (generate.rs:412-429), and committing row r is an argument error that
+    changes nothing."""
+    import torch
+    V = 4000
+    rows = np.random.default_rng(4).normal(0, 2, (4, V)).astype(np.float32)
+    set_ = R.sampling(0.7, 20, 0.95, 0.0, 1.2, 16, 5)
+    s = R.HostSampler(V, set_, max_rows=4)
+    d_rows = torch.from_numpy(rows).to(device)
+    # Nothing is committed by a verify, so a second one picks row 0 the same
+    # way: a draft one past that pick is rejected.
+    first_pick = int(s.verify(d_rows, [0, 0, 0])[0])
+    wrong = (first_pick + 1) % V
+    picks = s.verify(d_rows, [wrong, wrong, wrong])
+    assert picks[0] == first_pick
+    assert s.commit_verified(0) == first_pick != wrong
+    state = s.rng_state()
+    ids, probs = s.candidates()
+    with pytest.raises(R.SamplerError) as e:
+        s.commit_verified(1)
+    assert e.value.code == R.RL_ERR_ARGUMENT
+    assert s.rng_state() == state
+    gi, gp = s.candidates()
+    assert np.array_equal(gi, ids) and np.array_equal(gp, probs)

@@ -85,9 +85,26 @@ def test_argmax_takes_the_first_of_a_tie(device):  # sample.rs:410-415
     assert R.host_argmax(np.array([-np.inf, -np.inf], np.float32)) == 0
 
 
+ORDER_BASE = dict(temperature=1.0, top_k=20, top_p=1.0, min_p=0.0, repeat_penalty=1.0, repeat_last_n=0, seed=1)
+
+
+@pytest.mark.xfail(strict=True, reason=(
+    "known deviation: with top_p >= 1 and 0 < top_k < vocab the reference leaves its candidates in the "
+    "order Rust's select_nth_unstable_by produces (sample.rs:294); that order cannot be reproduced here "
+    "(Rust's core library is not available), so the device returns them in descending order; same kept "
+    "set and probabilities, but the draw walks another order"))
+def test_with_top_p_off_the_candidates_are_not_sorted(device):  # tests/sample.rs:286-294
+    l = O.test_logits(1024, 44, 3.0)
+    off = R.HostSampler(l.size, S(**ORDER_BASE))
+    off.sample(l)
+    values = l[off.candidates()[0]]
+    assert values.size == 20
+    assert np.any(values[:-1] < values[1:]), "with top-p off the candidates came back in descending order"
+
+
 def test_the_candidates_are_ordered_where_the_order_is_used(device):  # tests/sample.rs:272-312
     l = O.test_logits(1024, 44, 3.0)
-    base = dict(temperature=1.0, top_k=20, top_p=1.0, min_p=0.0, repeat_penalty=1.0, repeat_last_n=0, seed=1)
+    base = ORDER_BASE
     off = R.HostSampler(l.size, S(**base))
     off.sample(l)
     assert off.candidates()[0].size == 20

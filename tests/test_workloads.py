@@ -84,5 +84,9 @@ def test_uniforms_come_from_the_reference_rng():
 
 
 def test_algorithmic_bytes_of_the_bench_workload():
-    # logits once, 64-id windows, uniforms, token + kept + 20 (id, prob) pairs
-    assert W.WORKLOADS["spikes"].algorithmic_bytes() == 1_017_556_992
+    # logits once, 64-id windows, uniforms, token + kept, and the kept
+    # (id, prob) pairs: 20 per row on the bench workload
+    assert W.WORKLOADS["spikes"].algorithmic_bytes(kept_total=1024 * 20) == 1_017_556_992
+    # a top-k 0 row counts what it keeps, not the vocabulary
+    zipf = W.WORKLOADS["zipf"]
+    assert zipf.algorithmic_bytes(kept_total=700) == 64 * (151936 * 4 + 64 * 4 + 12) + 700 * 8
