@@ -139,6 +139,19 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
 int rl_argmax_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t row_stride, uint32_t rows,
                    uint32_t vocab, uint32_t *out_token, void *stream);
 
+/* No counterpart in the reference: rl_argmax_rows without a context, for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Its partial results
+ * live in a fixed 64 KiB device array inside the library (one copy per GPU,
+ * held until the process ends) instead of a context's buffer, so the call
+ * allocates nothing, on the device or the host. `device` is the HIP device
+ * the logits live on. At most 8192 rows per call (RL_ERR_CAPACITY above).
+ * Every call on one GPU shares that array: calls that can overlap on the
+ * device (issued to different streams, or from different threads) race and
+ * must be serialised by the caller. Results equal rl_argmax_rows's. */
+int rl_argmax_rows_noalloc(int device, const float *logits, uint64_t row_stride, uint32_t rows,
+                           uint32_t vocab, uint32_t *out_token, void *stream);
+
 /* Per row: the argmax and its probability under a softmax over the whole row,
  * 1 / sum_i exp(l_i - l_best) as f32, with the sum in f64 in id order exactly
  * as the reference accumulates it (bit-identical). Replaces `top_probability`

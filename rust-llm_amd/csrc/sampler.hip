@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <new>
@@ -62,6 +63,39 @@ int launch_argmax(const float *logits, uint64_t row_stride, uint32_t rows, uint3
     hipLaunchKernelGGL(k_argmax_final, dim3((rows + 255) / 256), dim3(256), 0, st, part, rows, chunks, out_token);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "argmax kernels");
+    return RL_OK;
+}
+
+// The allocation-free argmax (rl_argmax_rows_noalloc) keeps its partial
+// results in this fixed device array instead of a context's buffer: one per
+// (row, chunk). With rows <= NOALLOC_MAX_ROWS a call needs at most
+// max(rows, 2 * TARGET_WGS) entries (rows >= TARGET_WGS take one chunk each,
+// fewer rows take at most ceil(TARGET_WGS / rows) chunks). Every entry a call
+// reads is written by the same call first, so nothing needs clearing. Each
+// GPU holds its own copy from the library's load until the process ends
+// (64 KiB). Calls that overlap on one GPU share it and race.
+constexpr uint32_t NOALLOC_MAX_ROWS = 8192;
+constexpr size_t NOALLOC_SCRATCH = NOALLOC_MAX_ROWS;
+static_assert(NOALLOC_SCRATCH >= 2 * TARGET_WGS, "scratch below the split rows' partials");
+static __device__ __align__(256) uint64_t scratch[NOALLOC_SCRATCH];
+
+// The array's device address on each GPU, looked up once per device (with
+// that device current). The array's name in host code is not a device
+// address: only these pointers go to kernels.
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::atomic<uint64_t *> g_scratch[NOALLOC_MAX_DEVICES];
+
+int noalloc_scratch(int device, uint64_t **out) {
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES) return fail(RL_ERR_ARGUMENT, "device index out of range");
+    uint64_t *p = g_scratch[device].load(std::memory_order_acquire);
+    if (!p) {
+        void *addr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress (argmax scratch)");
+        p = static_cast<uint64_t *>(addr);
+        g_scratch[device].store(p, std::memory_order_release);
+    }
+    *out = p;
     return RL_OK;
 }
 
@@ -353,6 +387,23 @@ int rl_argmax_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t row_stride
     DeviceGuard g(ctx->device);
     if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select device");
     return launch_argmax(logits, row_stride, rows, vocab, out_token, ctx->d_argmax_part, stream);
+}
+
+int rl_argmax_rows_noalloc(int device, const float *logits, uint64_t row_stride, uint32_t rows, uint32_t vocab,
+                           uint32_t *out_token, void *stream) {
+    if (rows == 0) return RL_OK;
+    if (vocab == 0) return fail(RL_ERR_ARGUMENT, "vocab must be positive");
+    if (rows > NOALLOC_MAX_ROWS)
+        return fail(RL_ERR_CAPACITY, "rl_argmax_rows_noalloc takes at most " + std::to_string(NOALLOC_MAX_ROWS) +
+                                         " rows (its scratch is a fixed device array); use rl_argmax_rows");
+    if (!logits || !out_token) return fail(RL_ERR_ARGUMENT, "null logits or output");
+    if (rows > 1 && row_stride < vocab) return fail(RL_ERR_ARGUMENT, "row_stride below vocab");
+    DeviceGuard g(device);
+    if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select device " + std::to_string(device));
+    uint64_t *part = nullptr;
+    const int rc = noalloc_scratch(device, &part);
+    if (rc != RL_OK) return rc;
+    return launch_argmax(logits, row_stride, rows, vocab, out_token, part, stream);
 }
 
 int rl_top_probability_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t row_stride, uint32_t rows,

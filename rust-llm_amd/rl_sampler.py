@@ -87,6 +87,7 @@ def lib():
         L.rl_sampler_sample_rows.argtypes = [
             _vp, _vp, _u64, _u32, _u32, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u64, _vp]
         L.rl_argmax_rows.argtypes = [_vp, _vp, _u64, _u32, _u32, _vp, _vp]
+        L.rl_argmax_rows_noalloc.argtypes = [ctypes.c_int, _vp, _u64, _u32, _u32, _vp, _vp]
         L.rl_top_probability_rows.argtypes = [_vp, _vp, _u64, _u32, _u32, _vp, _vp, _vp]
         L.rl_sampler_last_error.restype = ctypes.c_char_p
         L.rl_sampler_expf_range.argtypes = [_u32, _u64, _vp, _vp]
@@ -343,6 +344,13 @@ def host_sample_batch(samplers, logits):
     _check(lib().rl_host_sample_batch(arr, n, logits.data_ptr(), logits.stride(0), logits.shape[1],
                                       out.ctypes.data, current_stream()))
     return out
+
+
+def argmax_rows_noalloc(logits, rows, row_stride, out_token, vocab, device=0, stream=None):
+    """rl_argmax_rows_noalloc: per-row argmax (sample.rs:118-128) with no
+    context and no allocation (its scratch is a fixed device array)."""
+    _check(lib().rl_argmax_rows_noalloc(device, _ptr(logits), row_stride, rows, vocab, _ptr(out_token),
+                                        current_stream() if stream is None else stream))
 
 
 def host_argmax(logits, device=0):
