@@ -1,19 +1,15 @@
 // The FULL device path: rows with top_k == 0, top_k >= vocab or top_k > 64
-// (sample.rs:279-358 over the whole candidate list). Up to seven launches per
-// group of rows, alternating kernels that spread a row over many workgroups
-// (the HBM- and ALU-heavy steps) with one workgroup per row (the steps that
-// follow the reference's sequential order):
+// (sample.rs:279-358 over the whole candidate list). Launches per group of
+// rows, alternating kernels that spread a row over many workgroups (the HBM-
+// and ALU-heavy steps) with one workgroup per row (the steps that follow the
+// reference's sequential order):
 //
-//   k_full_keys    (chunks x rows)  total-order keys of the penalised row in id
-//                                   order; per chunk the f32::max fold and
-//                                   argmax, merged by the row's last chunk to
-//                                   finish; rows without a finite maximum
-//                                   answered
-//   k_full_collect (chunks x rows)  min-p rows: p of every id, chunk sums, the
-//                                   survivors (launched when a row may take
-//                                   the min-p path)
-//   k_full_small   (rows)           min-p rows finished from their survivors,
-//                                   or left to the kernels below
+//   k_full_pass    (chunks x rows)  the one read of every row: the f32::max
+//                                   fold; rows without a finite maximum
+//                                   answered; min-p rows finished from their
+//                                   survivors when the top-p cut is certain
+//   k_full_keys    (chunks x rows)  the rows left: total-order keys of the
+//                                   penalised row in id order
 //   k_full_sort    (rows)           the row sorted by the reference's order
 //                                   unless it keeps id order
 //   k_full_probs   (chunks x rows)  p = exp((l - max) / T) in candidate order,
@@ -39,18 +35,13 @@ namespace rl {
 
 struct FullRow {
     float M;           // the f32::max fold of the penalised row
-    uint32_t am_tok;   // argmax of the penalised row
     uint32_t done;     // the row is finished (no finite maximum, or the min-p path)
     uint32_t m;        // candidates kept (after top-p and min-p)
     float inv;         // (1 / total) as f32
     uint32_t qbad;     // a normalised probability may not be finite: the draw walks in order
-    uint32_t small;    // the row tries the min-p path first
-    uint32_t nsurv;    // min-p survivors collected
-    uint32_t overflow; // more survivors than SURV_CAP
-    uint32_t ns_key;   // the largest key of an element below min-p (+1; 0 when none)
 };
 
-// Survivors the min-p path collects per row (their composites sort in LDS).
+// Candidates the min-p path collects per row (a superset of the survivors).
 constexpr uint32_t SURV_CAP = 4096;
 // A row's per-chunk results are read one chunk per lane.
 static_assert(MAX_CHUNKS <= WAVE, "a wave holds one lane per chunk");
@@ -58,17 +49,17 @@ static_assert(MAX_CHUNKS <= WAVE, "a wave holds one lane per chunk");
 struct FullScratch {
     uint32_t *keyA, *idA, *keyB, *idB;  // [slot][vocab]
     float *probs;                       // [slot][vocab]
-    float *part_max;                    // [slot][chunk] keys pass
-    uint64_t *part_am;                  // [slot][chunk]
-    double *psum;                       // [slot][chunk] probs pass
+    float *part_max;                    // [slot][chunk] k_full_pass: the chunk's maximum
+    uint64_t *part_am;                  // [slot][chunk] k_full_pass: candidates listed << 32 | lowest +inf id
+    double *psum;                       // [slot][chunk] k_full_pass: its mass; then the probs pass's sum
     int *pemin;                         // [slot][chunk]
     uint32_t *pcount;                   // [slot][chunk]
     uint32_t *pbad;                     // [slot][chunk]
     uint32_t *plast_in;                 // [slot][chunk] probs pass: last index + 1 with p >= min_p
     uint32_t *pfirst_out;               // [slot][chunk] first index with p < min_p
-    uint64_t *surv;                     // [slot][SURV_CAP] min-p survivors (composites)
+    uint64_t *surv;                     // [slot][SURV_CAP] min-p candidates (composites), a region per chunk
     FullRow *row;                       // [slot]
-    uint32_t *arrive;                   // [slot] keys pass: chunks done; zero between calls
+    uint32_t *arrive;                   // [slot] k_full_pass: chunks done; zero between calls
 };
 
 constexpr uint32_t UN = 16;                // elements per thread per step of the bulk loops (loads in flight)
@@ -124,15 +115,13 @@ __device__ __forceinline__ bool small_eligible(const rl_sampling &s, uint32_t V)
 }
 
 // ------------------------------------------------------------- keys ---
-// grid (chunks, slots), FULL_THREADS: the penalised row (sample.rs:239-257) as
-// total-order keys in id order, and per chunk the f32::max fold (NaN ignored)
-// and the argmax composite. A window id's key is its penalised logit's,
-// computed from the raw logit, so an id repeated in the window is penalised
-// once. Dynamic LDS: a bitmap of the chunk's window ids
-// (k_full_keys_lds_bytes). The row's last chunk to finish merges the chunks'
-// results (sample.rs:267-277): the row state for the kernels that follow, and
-// the answer of a row without a finite maximum (argmax, no draw).
-// LDS bytes of k_full_keys's bitmap: one bit per element of the largest chunk.
+// grid (chunks, slots), FULL_THREADS, after k_full_pass: for the rows it left
+// to the sorting kernels, the penalised row (sample.rs:239-257) as
+// total-order keys in id order (and the ids, for a row that keeps id order).
+// A window id's key is its penalised logit's, computed from the raw logit, so
+// an id repeated in the window is penalised once. Dynamic LDS: a bitmap of
+// the chunk's window ids (k_full_keys_lds_bytes).
+// LDS bytes of the window bitmap: one bit per element of the largest chunk.
 __host__ __device__ inline size_t k_full_keys_lds_bytes(uint32_t vocab, uint32_t chunks) {
     const uint32_t n4 = vocab / 4;
     const uint32_t most = 4 * ((n4 + chunks - 1) / chunks) + 3;
@@ -143,9 +132,8 @@ template <bool VEC>
 __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch f) {
     extern __shared__ __align__(16) uint8_t smem[];
     RL_LDS uint32_t *bm = (RL_LDS uint32_t *)smem;  // window ids in this chunk, one bit per element
-    __shared__ float red_max[FULL_THREADS / WAVE];
-    __shared__ uint64_t red_am[FULL_THREADS / WAVE];
     const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
+    if (f.row[slot].done) return;
     const uint32_t row = a.rows[slot];
     const rl_sampling s = a.settings[row];
     const uint32_t V = a.vocab;
@@ -175,13 +163,6 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch
     // The ids in id order are written only for a row that keeps that order
     // (no sort); the sort's first pass makes them from positions.
     const bool write_ids = identity_order(s, V);
-    float mx = -__builtin_inff();
-    uint64_t am = 0;
-    auto take = [&](float x, uint32_t id) {
-        const uint64_t c = composite(argmax_key(x), id);
-        if (x > mx) mx = x;
-        if (c > am) am = c;
-    };
     // Four 16-byte loads in flight per thread; indices past the chunk are
     // clamped to its last element (a cache hit) and their results dropped.
     constexpr uint32_t KU = 4;
@@ -208,10 +189,7 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch
             }
             uint32_t kk[4];
 #pragma unroll
-            for (uint32_t c = 0; c < 4; ++c) {
-                kk[c] = total_key(x[c]);
-                take(x[c], 4 * qq + c);
-            }
+            for (uint32_t c = 0; c < 4; ++c) kk[c] = total_key(x[c]);
             if (vstore) {
                 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
                 *(RL_GLB u32x4 *)(keys + 4 * qq) = u32x4{kk[0], kk[1], kk[2], kk[3]};
@@ -232,56 +210,7 @@ __global__ __launch_bounds__(FULL_THREADS) void k_full_keys(RowIO a, FullScratch
             if (pen && ((bm[(e - e0) >> 5] >> ((e - e0) & 31)) & 1u)) x = penalize(x, s.repeat_penalty);
             keys[e] = total_key(x);
             if (write_ids) ids[e] = e;
-            take(x, e);
         }
-    }
-    mx = wave_maxnum_f32(mx);
-    am = wave_max_u64(am);
-    const uint32_t wave = threadIdx.x / WAVE;
-    if (lane_id() == 0) {
-        red_max[wave] = mx;
-        red_am[wave] = am;
-    }
-    __syncthreads();
-    if (wave != 0) return;
-    for (uint32_t i = 1; i < FULL_THREADS / WAVE; ++i) {
-        mx = fmaxf(mx, red_max[i]);
-        am = red_am[i] > am ? red_am[i] : am;
-    }
-    // Publish the chunk's result; the row's last chunk to arrive merges them.
-    // The results are written with device-scope stores, which write through
-    // this XCD's L2, and the arrival waits until they have completed; the
-    // merging chunk reads them with device-scope loads after its arrival.
-    const uint32_t lane = lane_id();
-    if (lane == 0) {
-        __hip_atomic_store((uint32_t *)f.part_max + slot * a.chunks + chunk, __float_as_uint(mx), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(f.part_am + slot * a.chunks + chunk, am, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);  // the stores have completed
-    uint32_t old = 0;
-    if (lane == 0) old = atomicAdd(&f.arrive[slot], 1u);
-    if (read_lane_u32(old, 0) != a.chunks - 1) return;
-    // The last chunk (chunks <= MAX_CHUNKS <= WAVE): lane c reads chunk c.
-    const bool ok = lane < a.chunks;
-    const uint32_t mbits = ok ? __hip_atomic_load((const uint32_t *)f.part_max + slot * a.chunks + lane,
-                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                              : __float_as_uint(-__builtin_inff());
-    const uint64_t cam =
-        ok ? __hip_atomic_load(f.part_am + slot * a.chunks + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
-    mx = uniform_f32(wave_maxnum_f32(__uint_as_float(mbits)));
-    am = uniform_u64(wave_max_u64(cam));
-    if (lane == 0) {
-        f.arrive[slot] = 0;  // ready for the next call
-        const uint32_t am_tok = comp_key(am) == 0 ? 0u : comp_id(am);
-        const bool finite = mx > -__builtin_inff() && mx < __builtin_inff();
-        FullRow st{};
-        st.M = mx;
-        st.am_tok = am_tok;
-        st.done = finite ? 0u : 1u;
-        st.small = finite && small_eligible(s, V) ? 1u : 0u;
-        f.row[slot] = st;
-        if (!finite) write_single(a, row, am_tok);  // sample.rs:270-277
     }
 }
 
@@ -578,109 +507,89 @@ __global__ __launch_bounds__(SORT_THREADS) void k_full_sort(RowIO a, FullScratch
 // ----------------------------------------------------------- min-p path ---
 // A row with min-p on and the whole vocabulary as candidates keeps only
 // candidates with p >= min_p (sample.rs:326-340), usually a few. Those are the
-// first candidates of the reference's order (p falls along the order; checked
-// below, not assumed), so the row needs only them sorted, plus the mass of the
-// whole row for the top-p cut (sample.rs:307-324). The mass's sequential f64
-// sum is not computed here: the sum in another order is within a proven
-// relative bound of it, and the cut is accepted only when no value in that
-// interval could move it. Anything else (too many survivors, a NaN, a cut
-// inside the interval) leaves the row to the sorting kernels.
+// first candidates of the reference's order (p falls along the order; checked,
+// not assumed), so the row needs only them sorted, plus the mass of the whole
+// row for the top-p cut (sample.rs:307-324). k_full_pass reads the row once:
+// per chunk the f32::max fold, the mass relative to the chunk's own maximum
+// and a superset of the survivors; the row's last chunk to finish knows the
+// true maximum, computes the survivors' p exactly, and accepts the top-p cut
+// only when no mass in a proven interval around the reference's could move it.
+// Anything else (too many survivors, a NaN, a cut inside the interval) leaves
+// the row to the sorting kernels.
+//
+// The mass interval. The reference's mass is S_ref = sum of p_j in sorted
+// order (f64, sequential), p_j = expf(fl(fl(l_j - M) / T)). With y_j =
+// (l_j - M) / T exactly, fl rounding twice puts x_j within |y_j| 2^-23 of y_j
+// and libm expf is within 0.502 ulp, so p_j = e^(y_j) (1 + e_j) with |e_j| <=
+// 2^-23 |y_j| + 2^-24 to first order (plus 2^-149 absolute in the subnormal
+// range). The pass computes, relative to a running maximum m <= M that was
+// already seen, q_j = exp2_hw(fl(fl(l_j - m) * c2)) with c2 = fl(log2(e) / T)
+// rounded once from the f64 quotient: the exponent carries at most 3 roundings
+// of 2^-24 relative, so q_j e^((m - M) / T) = e^(y_j) (1 + g_j) with |g_j| <=
+// 3 2^-24 |y_j| + H (H bounds the hardware exp2's own error, see HW_EXP2_REL),
+// and partial sums are rescaled by f64 factors e^((m_old - m_new) / T) as m
+// rises. Splitting at |y| = K: terms with |y_j| <= K are within
+// EPS_NEAR relative of each other in the two computations; terms beyond
+// differ by at most 2.01 e^(-K) + 2^-124 each (both are below e^(-K) (1 +
+// tiny), or flushed subnormals). Summation adds gamma_32 in f32 (each
+// thread's terms of one step), a few f64 roundings, and gamma_(V-1) for the
+// reference's sequential sum. MASS_REL collects the relative terms.
 
-// grid (chunks, slots), FULL_THREADS: for rows on the min-p path, p of every
-// id in this chunk (keys in id order), the chunk's f64 sum of p, the
-// survivors as composites in the row's list, and the largest key of a
-// non-survivor.
-__global__ __launch_bounds__(FULL_THREADS) void k_full_collect(RowIO a, FullScratch f) {
-    __shared__ uint64_t exp_tab[32];
-    __shared__ double red_d[FULL_THREADS / WAVE];
-    const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
-    const FullRow st = f.row[slot];
-    if (st.done || !st.small) return;
-    const uint32_t row = a.rows[slot];
-    const rl_sampling s = a.settings[row];
-    const uint32_t V = a.vocab;
-    const uint32_t j0 = chunk_lo(V, chunk, a.chunks), j1 = chunk_lo(V, chunk + 1, a.chunks);
-    const uint32_t *keys = f.keyA + (uint64_t)slot * V;
-    uint64_t *list = f.surv + (uint64_t)slot * SURV_CAP;
-    FullRow *rs = f.row + slot;
-    copy_exp_table((RL_LDS uint64_t *)exp_tab);
-    const TempScale tscale(s.temperature);
-    const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab};
-    const uint32_t lane = lane_id();
-    double sum = 0.0;
-    uint32_t ns_key = 0;  // largest key + 1 of a non-survivor
-    bool stop = false;
-    // The row's overflow flag loads with a step's keys: the step sees the flag
-    // as it was when the step began, which only delays an early stop (an
-    // overflowing row's results are not used), and no step waits for it on
-    // its own; a wave that overflows the list, or meets a non-finite p, stops
-    // at once. (Loading the next step's keys during this one measured no
-    // faster: a row that overflows, as a tie-heavy one does, stops after one
-    // step and the loads are wasted.)
-    for (uint32_t b = j0; b < j1 && !stop; b += FULL_THREADS * UN) {
-        uint32_t kk[UN];
-#pragma unroll
-        for (uint32_t u = 0; u < UN; ++u) {
-            const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
-            kk[u] = ((const RL_GLB uint32_t *)keys)[j < j1 ? j : j1 - 1];  // clamped: no branch around the load
-        }
-        const uint32_t overflow_seen = __hip_atomic_load(&rs->overflow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // The survivors of all UN steps take their list slots with one
-        // atomic per wave (the wave waits for its result).
-        uint64_t sm[UN];
-        uint32_t wtotal = 0;
-        bool nonfinite = false;
-#pragma unroll
-        for (uint32_t u = 0; u < UN; ++u) {
-            const uint32_t j = b + u * FULL_THREADS + threadIdx.x;
-            const bool ok = j < j1;
-            const float p = ok ? expf_libm_t(tscale(key_value(kk[u]) - st.M), etab) : 0.0f;
-            const bool finite = p <= 3.40282347e38f;  // false for NaN
-            const bool surv = ok && finite && p >= s.min_p;
-            if (ok) sum += (double)p;
-            if (ok && finite && !surv) ns_key = max(ns_key, kk[u] + 1u);  // a finite p's key is below 0xFFFFFFFF
-            nonfinite |= ok && !finite;
-            sm[u] = ballot(surv);
-            wtotal += (uint32_t)__popcll(sm[u]);
-        }
-        if (wtotal != 0) {
-            uint32_t base = 0;
-            if (lane == 0) base = atomicAdd(&rs->nsurv, wtotal);
-            base = uniform_u32(__shfl((int)base, 0));
-#pragma unroll
-            for (uint32_t u = 0; u < UN; ++u) {
-                if ((sm[u] >> lane) & 1ull) {
-                    const uint32_t at = base + lanes_below(sm[u]);
-                    if (at < SURV_CAP) list[at] = composite(kk[u], b + u * FULL_THREADS + threadIdx.x);
-                }
-                base += (uint32_t)__popcll(sm[u]);
-            }
-            if (base > SURV_CAP) {
-                if (lane == 0) atomicOr(&rs->overflow, 1u);
-                stop = true;  // this wave overflowed the list itself
-            }
-        }
-        if (ballot(nonfinite) != 0) {
-            if (lane == 0) atomicOr(&rs->overflow, 1u);
-            stop = true;
-        }
-        stop = stop || uniform_u32(overflow_seen) != 0;
-    }
-    for (int m = 32; m >= 1; m >>= 1) {
-        sum += __shfl_xor(sum, m);
-        ns_key = max(ns_key, (uint32_t)__shfl_xor((int)ns_key, m));
-    }
-    if (lane == 0 && ns_key != 0) atomicMax(&rs->ns_key, ns_key);
-    const uint32_t wave = threadIdx.x / WAVE;
-    if (lane == 0) red_d[wave] = sum;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (uint32_t w = 1; w < FULL_THREADS / WAVE; ++w) sum += red_d[w];
-        f.psum[slot * a.chunks + chunk] = sum;
+constexpr uint32_t PASS_U = 10;                          // float4 per thread per step
+constexpr uint32_t PASS_STEP = FULL_THREADS * PASS_U;    // float4 per step
+constexpr uint32_t FULL_WAVES = FULL_THREADS / WAVE;
+constexpr uint32_t FIN_CAP = 1024;                       // survivors the pass finishes itself
+constexpr uint32_t PASS_CAND = 1024;                     // candidates a chunk holds in LDS
+constexpr uint32_t LIST_OVER = 0xFFFFFFFFu;              // a chunk's candidates did not fit
+constexpr double HW_EXP2_REL = 0x1p-21;                  // v_exp_f32 bound assumed (4 ulp; tested <= 1 ulp)
+constexpr double MASS_K = 32.0;
+constexpr double EPS_NEAR =
+    ((0x1p-23 + 3.0 * 0x1p-24) * MASS_K + 1.004 * 0x1p-24 + HW_EXP2_REL) * (1.0 + 0x1p-7);
+constexpr double MASS_REL = EPS_NEAR / (1.0 - EPS_NEAR) + 33.0 * 0x1p-24 + 0x1p-40;
+constexpr double RESCALE_REL = (0x1p-24 + HW_EXP2_REL) * 1.001;  // one in-loop rescaling factor
+// 2.01 e^(-K) + 2^-124 per term (e^-32 = 1.2664165549e-14).
+constexpr double MASS_ABS_PER_TERM = 2.01 * 1.2664165549094176e-14 + 0x1p-124;
+
+// Loads of k_full_pass's aligned variant are buffer loads: the resource
+// covers the row's n floats (reads past them return zeros, never fault), each
+// lane's byte offset is one register and the step's offset is scalar, so no
+// per-load 64-bit address stays live across a step. gfx9's descriptor word 3
+// (0x00020000: 32-bit data format, raw addressing); nontemporal (aux 2).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const float *row, uint32_t n) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)row, (short)0, (int)(n * 4u), 0x00020000);
+}
+template <bool VEC>
+__device__ __forceinline__ f32x4 pass_load(__amdgpu_buffer_rsrc_t r, const float *row, uint32_t f, uint32_t f_lane,
+                                           uint32_t end) {
+    if constexpr (VEC) {
+        // f = f_step + f_lane: the step part (uniform) goes in the scalar offset.
+        return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, 16u * f_lane, 16u * (f - f_lane), 2));
+    } else {
+        return load4<false>(row, f < end ? f : end - 1);
     }
 }
 
-// Sorts n2 (a power of two, <= SURV_CAP) composites in LDS, descending.
+// 2^z for z <= 0 as an f64 rescaling factor inside the streaming loop:
+// 2^floor(z) exactly (ldexp) times the hardware exp2 of the fraction rounded
+// to f32, so the factor is within 2^-24 + HW_EXP2_REL relative (or below
+// 2^-1022 where the true value is), with no f64 exp polynomial to keep in
+// registers across the loop.
+__device__ __forceinline__ double rescale(double z) {
+    if (!(z > -1100.0)) return 0.0;
+    const double n = __builtin_floor(z);
+    return __builtin_ldexp((double)__builtin_amdgcn_exp2f((float)(z - n)), (int)n);
+}
+
+// Composite of a survivor in the order its row keeps them: the reference's
+// order (descending key, ascending id) when top-p is on; ascending id (stored
+// as ~id << 32 | key, so that one descending sort serves) when it is off.
+__device__ __forceinline__ uint64_t keep_order(uint64_t c, bool by_id) {
+    return by_id ? (((uint64_t)(uint32_t)c << 32) | comp_key(c)) : c;
+}
+__device__ __forceinline__ uint32_t keep_key(uint64_t x, bool by_id) { return by_id ? (uint32_t)x : comp_key(x); }
+__device__ __forceinline__ uint32_t keep_id(uint64_t x, bool by_id) { return by_id ? ~(uint32_t)(x >> 32) : comp_id(x); }
+
+// Sorts n2 (a power of two) composites in LDS, descending, with nt threads.
 __device__ __forceinline__ void lds_bitonic_desc(RL_LDS uint64_t *v, uint32_t n2, uint32_t nt) {
     for (uint32_t size = 2; size <= n2; size <<= 1) {
         for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
@@ -698,71 +607,76 @@ __device__ __forceinline__ void lds_bitonic_desc(RL_LDS uint64_t *v, uint32_t n2
     }
 }
 
-// k_full_small for a row of at most 64 survivors, on one wave: survivor i in
-// lane i after a register bitonic sort, the sequential sums replayed with
-// readlane in candidate order (the same f64 and f32 additions, in the same
-// order, as the block replay), and no workgroup barrier. Leaves the row to
-// the sorting kernels in the same cases as the block path.
-__device__ __forceinline__ void small_one_wave(const RowIO &a, const FullScratch &f, uint32_t slot, uint32_t row,
-                                               const rl_sampling &s, const FullRow &st, uint32_t c) {
+// The row's finish from c <= 64 survivors, on one wave: survivor i in lane i
+// (x: its keep_order composite, unsorted), p by libm-exact exp, the top-p cut
+// certified against [t_lo, t_hi] (the interval that holds the reference's
+// target top_p * mass), the normalising total, q = p * inv and the f32 draw,
+// all replayed with readlane in candidate order (the reference's f64 and f32
+// additions in its order). Returns false (nothing written) when the cut could
+// fall on either side or a q is not finite: the sorting kernels take the row.
+__device__ __forceinline__ bool finish_wave(const RowIO &a, uint32_t row, const rl_sampling &s, float M, uint32_t c,
+                                            uint64_t x, bool by_id, uint32_t ns_key, double t_lo, double t_hi,
+                                            const LdsExpTable &etab) {
     const uint32_t lane = lane_id();
-    const uint32_t V = a.vocab;
-    const bool by_id = !(s.top_p < 1.0f);  // top-p off: id order, as in the block path
-    const uint64_t *list = f.surv + (uint64_t)slot * SURV_CAP;
     const bool in = lane < c;
-    // Every load up front, so that their round trips overlap: the
-    // survivors, the chunks' sums (lane ch holds chunk ch's; chunks <= 64)
-    // and the uniform.
-    uint64_t x = in ? list[lane] : 0ull;
-    const double psum_lane = lane < a.chunks ? f.psum[slot * a.chunks + lane] : 0.0;
     const float u = a.uniforms[row];
-    if (in && by_id) x = ((uint64_t)(uint32_t)x << 32) | comp_key(x);  // ~id in the high half
-    x = wave_sort64<true>(x);
-    const uint32_t key = by_id ? (uint32_t)x : comp_key(x);
-    const uint32_t id = by_id ? ~(uint32_t)(x >> 32) : comp_id(x);
-    const float p = in ? expf_libm((key_value(key) - st.M) / s.temperature) : 0.0f;
-
+    x = wave_sort64<true>(in ? x : 0ull);
+    const uint32_t key = keep_key(x, by_id);
+    const uint32_t id = keep_id(x, by_id);
+    const float p = in ? expf_libm_t((key_value(key) - M) / s.temperature, etab) : 0.0f;
     uint32_t kept = c;
     double total = 0.0;
     bool have_total = false;
     if (!by_id) {
-        if (st.ns_key != 0 && !(read_lane_u32(key, c - 1) >= st.ns_key)) return;
+        // The survivors must be the first c candidates: every other key that
+        // could precede them is below the smallest survivor's.
+        if (ns_key != 0 && !(read_lane_u32(key, c - 1) >= ns_key)) return false;
         if (!(s.top_p > 0.0f)) {
-            kept = 1;  // sample.rs:315-323
+            kept = 1;  // a target <= 0 is met by the first candidate (sample.rs:315-323)
             total = (double)read_lane_f32(p, 0);
             have_total = true;
         } else {
-            // The mass interval of the block path (the same S, summed in the
-            // same order, and the same d and bounds).
-            double S = 0.0;
-            for (uint32_t ch = 0; ch < a.chunks; ++ch)
-                S += __longlong_as_double((long long)read_lane_u64((uint64_t)__double_as_longlong(psum_lane), ch));
-            const double d = 2.25 * ((double)V + 64.0) * 0x1p-53;
-            const double tp = (double)s.top_p;
-            const double t_lo = tp * (S * (1.0 - d)) * (1.0 - 0x1p-50);
-            const double t_hi = tp * (S * (1.0 + d)) * (1.0 + 0x1p-50);
             // The first partial sums to reach t_lo and t_hi; the cut is
             // certain when they are the same index.
-            double cum = 0.0, at = 0.0;
+            double at = 0.0;
             uint32_t j_lo = c, j_hi = c;
-            for (uint32_t j = 0; j < c; ++j) {
-                cum += (double)read_lane_f32(p, j);
-                if (j_lo == c && cum >= t_lo) {
-                    j_lo = j;
-                    at = cum;
+            // Every p here is a normal f32 >= 2^emin, so a multiple of
+            // 2^(emin - 23); with c <= 64 terms <= 1 every partial sum is
+            // below 2^7 and needs at most 30 - emin significant bits: when
+            // that is <= 53 every f64 partial sum is exact, and an inclusive
+            // scan of the wave gives the sequential sums bit for bit.
+            const int e = in ? f32_exponent(p) : 1 << 20;
+            const int emin = (int)uniform_u32((uint32_t)wave_min_i32(e));
+            if (emin >= -23) {
+                double cum = in ? (double)p : 0.0;
+                for (uint32_t d = 1; d < WAVE; d <<= 1) {
+                    const double o = f64_from_bits(shfl_up_u64(f64_bits(cum), (int)d));
+                    if (lane >= d) cum += o;
                 }
-                if (cum >= t_hi) {
-                    j_hi = j;
-                    break;
-                }
-            }
-            if (j_lo == c) {
-                at = cum;  // no cut among the survivors: their whole sum
+                const uint64_t lo = ballot(in && cum >= t_lo), hi = ballot(in && cum >= t_hi);
+                j_lo = lo ? (uint32_t)__ffsll((unsigned long long)lo) - 1u : c;
+                j_hi = hi ? (uint32_t)__ffsll((unsigned long long)hi) - 1u : c;
+                at = f64_from_bits(read_lane_u64(f64_bits(cum), j_lo == c ? c - 1 : j_lo));
             } else {
-                if (j_hi != j_lo) return;  // the cut could fall on either side: sort the row
+                double cum = 0.0;
+                for (uint32_t j = 0; j < c; ++j) {
+                    cum += (double)read_lane_f32(p, j);
+                    if (j_lo == c && cum >= t_lo) {
+                        j_lo = j;
+                        at = cum;
+                    }
+                    if (cum >= t_hi) {
+                        j_hi = j;
+                        break;
+                    }
+                }
+                if (j_lo == c) at = cum;
+            }
+            if (j_lo != c) {
+                if (j_hi != j_lo) return false;
                 kept = j_lo + 1;
             }
-            total = at;  // the normalising sum, sample.rs:342
+            total = at;  // the normalising sum, sample.rs:342 (all c when no cut: min-p decides)
             have_total = true;
         }
     }
@@ -770,7 +684,7 @@ __device__ __forceinline__ void small_one_wave(const RowIO &a, const FullScratch
         for (uint32_t j = 0; j < kept; ++j) total += (double)read_lane_f32(p, j);
     const float inv = (float)(1.0 / total);
     const float q = p * inv;
-    if (ballot(lane < kept && !(q <= 3.40282347e38f)) != 0) return;  // the sorting kernels walk it in order
+    if (ballot(lane < kept && !(q <= 3.40282347e38f)) != 0) return false;
     if (lane < kept && a.out_ids) {
         a.out_ids[(uint64_t)row * a.cand_stride + lane] = id;
         a.out_probs[(uint64_t)row * a.cand_stride + lane] = q;
@@ -789,137 +703,571 @@ __device__ __forceinline__ void small_one_wave(const RowIO &a, const FullScratch
         a.out_token[row] = tok;
         a.out_kept[row] = kept;
         a.out_used[row] = 1;
-        f.row[slot].done = 1;
     }
+    return true;
 }
 
-// grid (slots), REPLAY_THREADS: finishes a min-p row from its survivors, or
-// leaves it (done stays 0) to the sorting kernels.
-__global__ __launch_bounds__(REPLAY_THREADS) void k_full_small(RowIO a, FullScratch f) {
-    __shared__ uint64_t sv_[SURV_CAP];
-    __shared__ float sp_[SURV_CAP];
-    __shared__ SeqLds<REPLAY_THREADS> seq;
+// The same finish for 64 < c <= FIN_CAP survivors: sv holds their
+// keep_order composites, sorted here by the workgroup (NT threads); sp gets
+// their p; one thread then walks them in order exactly as the reference does
+// (the f64 cut and total, the f32 draw), and the workgroup writes the kept
+// candidates. Every thread returns the same verdict.
+template <uint32_t NT>
+__device__ __forceinline__ bool finish_block(const RowIO &a, uint32_t row, const rl_sampling &s, float M, uint32_t c,
+                                             RL_LDS uint64_t *sv, RL_LDS float *sp, RL_LDS uint32_t *sh,
+                                             RL_LDS float *sh_inv, const LdsExpTable &etab, bool by_id,
+                                             uint32_t ns_key, double t_lo, double t_hi) {
+    const uint32_t tid = threadIdx.x;
+    uint32_t n2 = 1;
+    while (n2 < c) n2 <<= 1;
+    for (uint32_t i = c + tid; i < n2; i += NT) sv[i] = 0;
+    __syncthreads();
+    lds_bitonic_desc(sv, n2, NT);
+    for (uint32_t i = tid; i < c; i += NT) sp[i] = expf_libm_t((key_value(keep_key(sv[i], by_id)) - M) / s.temperature, etab);
+    __syncthreads();
+    if (tid == 0) {
+        // sh[0]: kept (0 when the row is left to the sorting kernels), sh[1]: the drawn index.
+        uint32_t kept = c;
+        double total = 0.0;
+        bool ok = true;
+        if (!by_id && ns_key != 0 && !(keep_key(sv[c - 1], false) >= ns_key)) ok = false;
+        if (ok && !by_id && !(s.top_p > 0.0f)) {
+            kept = 1;  // sample.rs:315-323
+            total = (double)sp[0];
+        } else if (ok && !by_id) {
+            double cum = 0.0;
+            uint32_t j_lo = c, j_hi = c;
+            for (uint32_t j = 0; j < c; ++j) {
+                cum += (double)sp[j];
+                if (j_lo == c && cum >= t_lo) {
+                    j_lo = j;
+                    total = cum;
+                }
+                if (cum >= t_hi) {
+                    j_hi = j;
+                    break;
+                }
+            }
+            if (j_lo == c) total = cum;                  // no cut among the survivors
+            else if (j_hi != j_lo) ok = false;           // the cut could fall on either side
+            else kept = j_lo + 1;
+        } else if (ok) {
+            for (uint32_t j = 0; j < kept; ++j) total += (double)sp[j];
+        }
+        float inv = 0.0f;
+        uint32_t pick = 0;
+        if (ok) {
+            inv = (float)(1.0 / total);
+            float cum = 0.0f;  // the draw, sample.rs:349-358
+            const float u = a.uniforms[row];
+            pick = kept - 1;
+            for (uint32_t j = 0; j < kept; ++j) {
+                const float q = sp[j] * inv;
+                if (!(q <= 3.40282347e38f)) ok = false;
+                cum += q;
+                if (cum > u) {
+                    pick = j;
+                    break;
+                }
+            }
+            for (uint32_t j = pick + 1; ok && j < kept; ++j)
+                if (!(sp[j] * inv <= 3.40282347e38f)) ok = false;
+        }
+        sh[0] = ok ? kept : 0u;
+        sh[1] = pick;
+        *sh_inv = inv;
+    }
+    __syncthreads();
+    const uint32_t kept = sh[0];
+    if (kept == 0) return false;
+    const float inv = *sh_inv;
+    if (a.out_ids)
+        for (uint32_t i = tid; i < kept; i += NT) {
+            a.out_ids[(uint64_t)row * a.cand_stride + i] = keep_id(sv[i], by_id);
+            a.out_probs[(uint64_t)row * a.cand_stride + i] = sp[i] * inv;
+        }
+    if (tid == 0) {
+        a.out_token[row] = keep_id(sv[sh[1]], by_id);
+        a.out_kept[row] = kept;
+        a.out_used[row] = 1;
+    }
+    return true;
+}
+
+// Dynamic LDS of k_full_pass: the chunk's window bitmap while streaming, the
+// finisher's survivors (FIN_CAP composites and their p) after.
+__host__ __device__ inline size_t k_full_pass_lds_bytes(uint32_t vocab, uint32_t chunks) {
+    const size_t fin = (size_t)FIN_CAP * (sizeof(uint64_t) + sizeof(float));
+    const size_t bm = k_full_keys_lds_bytes(vocab, chunks);
+    return bm > fin ? bm : fin;
+}
+
+// grid (chunks, slots), FULL_THREADS: the single read of the full path.
+// Every row: the penalised row's f32::max fold per chunk (sample.rs:267-269)
+// and the lowest id holding +inf; the row's last chunk to finish answers rows
+// without a finite maximum (argmax, no draw, sample.rs:270-277) and leaves the
+// maximum in the row state for the sorting kernels. Rows eligible for the
+// min-p path also get, per chunk, the mass relative to the chunk's maximum
+// and the candidates that could survive min-p (appended to the row's list),
+// and the last chunk finishes them when it can (done = 1).
+template <bool VEC>
+__global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScratch f) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    RL_LDS uint32_t *bm = (RL_LDS uint32_t *)smem;  // window ids in this chunk, one bit per element
+    __shared__ float red_m[FULL_WAVES];
+    __shared__ double red_s[FULL_WAVES];
+    __shared__ uint32_t red_i[FULL_WAVES], red_f[FULL_WAVES];
+    __shared__ uint32_t sh_last, sh_count, sh_ns, sh_flag;
+    __shared__ uint32_t sh_fin[2];
+    __shared__ float sh_inv;
     __shared__ uint64_t exp_tab[32];
-    __shared__ uint32_t sh_bad;
-    RL_LDS uint64_t *sv = (RL_LDS uint64_t *)sv_;
-    RL_LDS float *sp = (RL_LDS float *)sp_;
-    const uint32_t slot = blockIdx.x;
-    const FullRow st = f.row[slot];
-    if (st.done || !st.small || st.overflow) return;
-    const uint32_t c = st.nsurv;
-    if (c == 0 || c > SURV_CAP) return;  // no survivor: the reference keeps its first candidate
+    __shared__ uint64_t cbuf[PASS_CAND];  // this chunk's candidates, filtered by its maximum at the end
+    __shared__ uint32_t sh_cn, sh_cover;
+    __shared__ uint32_t red_cnt[MAX_CHUNKS];   // the finisher: each chunk's listed candidates
+    const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
+    const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / WAVE;
     const uint32_t row = a.rows[slot];
     const rl_sampling s = a.settings[row];
     const uint32_t V = a.vocab;
-    const uint32_t tid = threadIdx.x;
-    if (c <= WAVE) {  // one wave, no barrier; the other waves leave
-        if (tid < WAVE) small_one_wave(a, f, slot, row, s, st, c);
+    const uint32_t C = a.chunks;
+    const uint32_t wl = window_len(a, row);
+    const bool pen = penalises(s) && wl > 0;
+    const float *rowp = a.logits + (uint64_t)row * a.stride;
+    const uint32_t n4 = V / 4;
+    const uint32_t q0 = chunk_lo(n4, chunk, C), q1 = chunk_lo(n4, chunk + 1, C);
+    const uint32_t e0 = 4 * q0, e1 = chunk == C - 1 ? V : 4 * q1;
+    const uint32_t nwords = (e1 - e0 + 31) / 32;
+    // The window's ids and the exp table load first; then the first step's
+    // loads (clamped: no branch around them). Vector loads complete in order,
+    // so anything loaded after the step would wait for all of it. The window
+    // bitmap and the tables are built while the step is in flight.
+    constexpr uint32_t WIN_PER = 8;  // window ids per thread (max_window <= 2048)
+    static_assert(WIN_PER * FULL_THREADS >= 2048, "a window's ids fit the threads");
+    // Unconditional (clamped) loads: a load under a divergent branch makes
+    // the compiler wait for every load in flight, the step's included.
+    uint32_t wid[WIN_PER];
+    const uint32_t *win = a.windows + (uint64_t)row * a.wstride;
+    if (pen) {
+#pragma unroll
+        for (uint32_t k = 0; k < WIN_PER; ++k) {
+            const uint32_t i = k * FULL_THREADS + tid;
+            wid[k] = win[i < wl ? i : wl - 1];
+        }
+    }
+    const uint64_t tab = EXP2_32_TAB[tid & 31u];
+    const __amdgpu_buffer_rsrc_t rsrc = row_rsrc(rowp, V);
+    f32x4 A[PASS_U];
+    // Buffer loads need no guard (past the row they return zeros); a uniform
+    // branch here would also make the compiler wait for all loads at its end.
+    if (VEC || q0 < q1) {
+#pragma unroll
+        for (uint32_t u = 0; u < PASS_U; ++u) A[u] = pass_load<VEC>(rsrc, rowp, q0 + u * FULL_THREADS + tid, tid, q1);
+    }
+    if (pen) {
+        for (uint32_t i = tid; i < nwords; i += FULL_THREADS) bm[i] = 0;
+        __syncthreads();
+#pragma unroll
+        for (uint32_t k = 0; k < WIN_PER; ++k) {
+            const uint32_t id = wid[k];
+            if (k * FULL_THREADS + tid < wl && id >= e0 && id < e1)
+                atomicOr((uint32_t *)&bm[(id - e0) >> 5], 1u << ((id - e0) & 31));
+        }
+    }
+    if (tid == 0) {
+        sh_cn = 0;
+        sh_cover = 0;
+    }
+    if (tid < 32) exp_tab[tid] = tab;  // for the finisher
+    __syncthreads();
+    const bool eligible = small_eligible(s, V);
+    // Workgroup constants, kept in scalar registers.
+    const double invT_d = uniform_f64(1.0 / (double)s.temperature);
+    const double log2e_T = uniform_f64(1.4426950408889634 * invT_d);
+    // Base-2 exponent per unit of (l - m), and the survival test in it: any
+    // element below ln(min_p) - 1e-3 (with margin for the roundings of z and
+    // of the logarithm) relative to a maximum already seen has p < min_p.
+    const float c2 = uniform_f32((float)log2e_T);
+    const float zthr = uniform_f32((float)(((double)logf(s.min_p) * (1.0 + 0x1p-18) - 1e-3) * 1.4426950408889634));
+    // The mass needs a finite c2 and threshold (T not tiny or huge, min_p > 0).
+    bool mass = eligible && c2 < 3.0e38f && c2 > 0.0f && zthr > -3.0e38f;
+    uint64_t *list = f.surv + (uint64_t)slot * SURV_CAP;
+
+    float m_run = -__builtin_inff();  // wave-uniform: the wave's maximum so far
+    double S = 0.0;                   // per lane: mass relative to m_run
+    uint32_t first_inf = 0xFFFFFFFFu;
+    bool nan_seen = false;
+    // The penalised logit of element e of this chunk, re-read from memory
+    // (the candidates' rare path; their row was just read).
+    auto value_at = [&](uint32_t e) {
+        float v = ((const RL_GLB float *)rowp)[e];
+        if (pen && ((bm[(e - e0) >> 5] >> ((e - e0) & 31)) & 1u)) v = penalize(v, s.repeat_penalty);
+        return v;
+    };
+    // Appends this lane's candidates (the set bits i of mb; id_of(i) is the
+    // vocabulary id of candidate i) to the chunk's LDS buffer: one LDS atomic
+    // per wave, slots by an exclusive scan of the lanes' counts. A full
+    // buffer sends the row to the sorting kernels.
+    auto append = [&](uint64_t mb, auto id_of) {
+        const uint32_t mine = (uint32_t)__popcll(mb);
+        uint32_t incl = mine;
+        for (uint32_t d = 1; d < WAVE; d <<= 1) {
+            const uint32_t o = (uint32_t)__shfl_up((int)incl, d);
+            if (lane >= d) incl += o;
+        }
+        const uint32_t wtotal = (uint32_t)__shfl((int)incl, WAVE - 1);
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd((uint32_t *)&sh_cn, wtotal);
+        base = uniform_u32((uint32_t)__shfl((int)base, 0));
+        uint32_t at = base + incl - mine;
+        while (mb != 0) {
+            const uint32_t i = (uint32_t)__ffsll((unsigned long long)mb) - 1u;
+            mb &= mb - 1ull;
+            const uint32_t e = id_of(i);
+            if (at < PASS_CAND) cbuf[at] = composite(total_key(value_at(e)), e);
+            ++at;
+        }
+        if (base + wtotal > PASS_CAND) {
+            if (lane == 0) sh_cover = 1;
+            mass = false;  // the row leaves the min-p path
+        }
+    };
+    // A step's PASS_U float4 per thread are all in flight at once (a chunk
+    // of the 64-row workload is one step); the penalty is applied in place.
+    for (uint32_t b = q0; b < q1; b += PASS_STEP) {
+        if (b != q0) {
+#pragma unroll
+            for (uint32_t u = 0; u < PASS_U; ++u) A[u] = pass_load<VEC>(rsrc, rowp, b + u * FULL_THREADS + tid, tid, q1);
+        }
+        float tmax = -__builtin_inff();
+#pragma unroll
+        for (uint32_t u = 0; u < PASS_U; ++u) {
+            const uint32_t qq = b + u * FULL_THREADS + tid;
+            if (pen && qq < q1) {  // the four ids' bits share a word: e0 and 4 * qq are multiples of 4
+                const uint32_t off = 4 * qq - e0;
+                const uint32_t in = (bm[off >> 5] >> (off & 31)) & 15u;
+                if (in != 0) {
+#pragma unroll
+                    for (uint32_t c = 0; c < 4; ++c)
+                        if ((in >> c) & 1u) A[u][c] = penalize(A[u][c], s.repeat_penalty);
+                }
+            }
+            if (qq < q1) tmax = fmaxf(tmax, fmaxf(fmaxf(A[u].x, A[u].y), fmaxf(A[u].z, A[u].w)));
+        }
+        tmax = uniform_f32(wave_maxnum_f32(tmax));
+        if (tmax > m_run) {
+            if (tmax == __builtin_inff()) {  // the first +inf of this wave's elements
+                uint32_t fi = 0xFFFFFFFFu;
+#pragma unroll
+                for (uint32_t u = 0; u < PASS_U; ++u) {
+                    const uint32_t qq = b + u * FULL_THREADS + tid;
+#pragma unroll
+                    for (uint32_t c = 0; c < 4; ++c)
+                        if (qq < q1 && A[u][c] == __builtin_inff()) fi = min(fi, 4 * qq + c);
+                }
+                first_inf = min(first_inf, fi);
+                mass = false;  // the row has no finite maximum
+            } else if (m_run > -__builtin_inff()) {
+                S *= rescale(((double)m_run - (double)tmax) * log2e_T);
+            }
+            m_run = tmax;
+        }
+        if (mass && m_run > -__builtin_inff()) {
+            // The step's terms and the largest z of this lane's elements; a
+            // full step needs no per-element bounds test.
+            float acc = 0.0f, zmax = -__builtin_inff();
+            if (b + PASS_STEP <= q1) {
+#pragma unroll
+                for (uint32_t u = 0; u < PASS_U; ++u)
+#pragma unroll
+                    for (uint32_t c = 0; c < 4; ++c) {
+                        const float z = (A[u][c] - m_run) * c2;
+                        acc += __builtin_amdgcn_exp2f(z);
+                        zmax = fmaxf(zmax, z);
+                    }
+            } else {
+#pragma unroll
+                for (uint32_t u = 0; u < PASS_U; ++u) {
+                    const bool ok = b + u * FULL_THREADS + tid < q1;
+#pragma unroll
+                    for (uint32_t c = 0; c < 4; ++c) {
+                        const float z = (A[u][c] - m_run) * c2;
+                        const float q = __builtin_amdgcn_exp2f(z);
+                        if (ok) {
+                            acc += q;
+                            zmax = fmaxf(zmax, z);
+                        }
+                    }
+                }
+            }
+            S += (double)acc;
+            if (ballot(zmax >= zthr) != 0) {  // rare: this wave holds candidates
+                uint64_t mb = 0;  // this lane's: bit 4u + c
+#pragma unroll
+                for (uint32_t u = 0; u < PASS_U; ++u) {
+                    const bool ok = b + u * FULL_THREADS + tid < q1;
+#pragma unroll
+                    for (uint32_t c = 0; c < 4; ++c)
+                        if (ok && (A[u][c] - m_run) * c2 >= zthr) mb |= 1ull << (4 * u + c);
+                }
+                append(mb, [&](uint32_t i) { return 4 * (b + (i >> 2) * FULL_THREADS + tid) + (i & 3u); });
+            }
+        } else if (eligible && m_run == -__builtin_inff()) {
+            // Nothing finite so far: no mass, but a NaN must still send the
+            // row to the sorting kernels.
+#pragma unroll
+            for (uint32_t u = 0; u < PASS_U; ++u)
+#pragma unroll
+                for (uint32_t c = 0; c < 4; ++c)
+                    if (b + u * FULL_THREADS + tid < q1 && A[u][c] != A[u][c]) nan_seen = true;
+        }
+    }
+    if (chunk == C - 1) {  // the last vocab % 4 elements, one per thread (at most 3)
+        const uint32_t e = 4 * n4 + tid;
+        float xe = -__builtin_inff();
+        const bool ok = e < V;
+        if (ok) {
+            xe = ((const RL_GLB float *)rowp)[e];
+            if (pen && ((bm[(e - e0) >> 5] >> ((e - e0) & 31)) & 1u)) xe = penalize(xe, s.repeat_penalty);
+        }
+        const float tmax = uniform_f32(wave_maxnum_f32(xe));
+        if (tmax > m_run) {
+            if (tmax == __builtin_inff()) {
+                first_inf = min(first_inf, (ok && xe == __builtin_inff()) ? e : 0xFFFFFFFFu);
+                mass = false;
+            } else if (m_run > -__builtin_inff()) {
+                S *= exp(((double)m_run - (double)tmax) * invT_d);
+            }
+            m_run = tmax;
+        }
+        if (mass && m_run > -__builtin_inff()) {
+            const float z = (xe - m_run) * c2;
+            if (ok) S += (double)__builtin_amdgcn_exp2f(z);
+            const uint64_t mb = (ok && z >= zthr) ? 1ull : 0ull;
+            if (ballot(mb != 0) != 0) append(mb, [&](uint32_t) { return e; });
+        } else if (eligible && ok && xe != xe) {
+            nan_seen = true;
+        }
+    }
+    // The wave's record: its maximum, its mass relative to it (NaN when a NaN
+    // was met), the lowest +inf id.
+    S = wave_total_f64(S);
+    if (ballot(nan_seen) != 0) S = __builtin_nan("");
+    {
+        uint32_t fi = first_inf;
+        for (int m = 32; m >= 1; m >>= 1) fi = min(fi, (uint32_t)__shfl_xor((int)fi, m));
+        first_inf = fi;
+    }
+    if (lane == 0) {
+        red_m[wave] = m_run;
+        red_s[wave] = S;
+        red_i[wave] = first_inf;
+    }
+    __syncthreads();
+    float Mc = -__builtin_inff();
+    for (uint32_t w = 0; w < FULL_WAVES; ++w) Mc = fmaxf(Mc, red_m[w]);
+    // The chunk's candidates against its own maximum (still a superset of
+    // the row's survivors: M >= Mc), compacted into the chunk's own region of
+    // the row's list (SURV_CAP / C entries) with device-scope stores. The
+    // count goes with the chunk's record; LIST_OVER marks a region too small.
+    const uint32_t region = SURV_CAP / C;
+    uint32_t nkeep = 0;
+    if (eligible && Mc > -__builtin_inff() && Mc < __builtin_inff() && sh_cover == 0) {
+        const uint32_t n = min(sh_cn, PASS_CAND);
+        uint32_t mine = 0;  // this wave's kept candidates, its slice of the buffer
+        const uint32_t per = (n + FULL_WAVES - 1) / FULL_WAVES;
+        const uint32_t lo = min(n, wave * per), hi = min(n, lo + per);
+        for (uint32_t b = lo; b < hi; b += WAVE) {
+            const uint32_t i = b + lane;
+            const uint64_t cc = i < hi ? cbuf[i] : 0ull;
+            mine += (uint32_t)__popcll(ballot(i < hi && (key_value(comp_key(cc)) - Mc) * c2 >= zthr));
+        }
+        if (lane == 0) red_f[wave] = mine;
+        __syncthreads();
+        uint32_t at = 0;
+        for (uint32_t w = 0; w < FULL_WAVES; ++w) {
+            if (w < wave) at += red_f[w];
+            nkeep += red_f[w];
+        }
+        if (nkeep <= region) {
+            uint64_t *dst = list + chunk * region;
+            for (uint32_t b = lo; b < hi; b += WAVE) {
+                const uint32_t i = b + lane;
+                const uint64_t cc = i < hi ? cbuf[i] : 0ull;
+                const bool keep = i < hi && (key_value(comp_key(cc)) - Mc) * c2 >= zthr;
+                const uint64_t mk = ballot(keep);
+                if (keep) __hip_atomic_store(dst + at + lanes_below(mk), cc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                at += (uint32_t)__popcll(mk);
+            }
+        } else {
+            nkeep = LIST_OVER;
+        }
+    } else if (sh_cover != 0) {
+        nkeep = LIST_OVER;
+    }
+    if (wave == 0) {
+        uint32_t fi = 0xFFFFFFFFu;
+        for (uint32_t w = 0; w < FULL_WAVES; ++w) fi = min(fi, red_i[w]);
+        double Sc = 0.0;
+        if (Mc > -__builtin_inff() && Mc < __builtin_inff())
+            for (uint32_t w = 0; w < FULL_WAVES; ++w)
+                if (red_m[w] > -__builtin_inff()) Sc += red_s[w] * exp(((double)red_m[w] - (double)Mc) * invT_d);
+        for (uint32_t w = 0; w < FULL_WAVES; ++w)
+            if (red_s[w] != red_s[w]) Sc = __builtin_nan("");
+        // Publish the chunk's record with device-scope stores (they write
+        // through this XCD's L2); the arrival waits until every store of this
+        // workgroup's waves has completed, the list entries included.
+        if (lane == 0) {
+            const uint32_t i = slot * C + chunk;
+            __hip_atomic_store((uint32_t *)f.part_max + i, __float_as_uint(Mc), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store((uint64_t *)f.psum + i, (uint64_t)__double_as_longlong(Sc), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(f.part_am + i, ((uint64_t)nkeep << 32) | fi, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);  // this wave's stores have completed
+    __syncthreads();                          // and every other wave's
+    if (tid == 0) sh_last = atomicAdd(&f.arrive[slot], 1u) == C - 1 ? 1u : 0u;
+    __syncthreads();
+    if (!sh_last) return;
+
+    // ---- the row's last chunk: every chunk's record, then the row ----
+    // The first K = SPEC * FULL_THREADS / C entries of every chunk's region
+    // load now, before the counts are known (thread t takes entries
+    // t % (K / SPEC) + j K / SPEC of chunk t / (K / SPEC)): most chunks list
+    // fewer than K, so their entries need no second round trip.
+    constexpr uint32_t SPEC = 4;
+    const uint32_t region_c = SURV_CAP / C, KT = FULL_THREADS / C, K = SPEC * KT;
+    const uint32_t sch = tid / KT, sidx = tid % KT;
+    uint64_t spec[SPEC];
+#pragma unroll
+    for (uint32_t j = 0; j < SPEC; ++j)
+        spec[j] = (eligible && sch < C) ? __hip_atomic_load(list + sch * region_c + sidx + j * KT, __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_AGENT)
+                                        : 0ull;
+    const bool okc = lane < C;  // C <= MAX_CHUNKS <= WAVE: lane c holds chunk c
+    const float Mr = okc ? __uint_as_float(__hip_atomic_load((const uint32_t *)f.part_max + slot * C + lane,
+                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+                         : -__builtin_inff();
+    const double Sc = okc ? __longlong_as_double((long long)__hip_atomic_load(
+                                (const uint64_t *)f.psum + slot * C + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+                          : 0.0;
+    const uint64_t rec = okc ? __hip_atomic_load(f.part_am + slot * C + lane, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT)
+                             : ((uint64_t)0 << 32) | 0xFFFFFFFFu;
+    uint32_t fi = (uint32_t)rec;
+    const uint32_t nc = (uint32_t)(rec >> 32);  // chunk lane's listed candidates, or LIST_OVER
+    const bool lover = ballot(nc == LIST_OVER) != 0;
+    // How many candidates all chunks listed.
+    uint32_t incl = nc == LIST_OVER ? 0u : nc;
+    for (uint32_t d = 1; d < WAVE; d <<= 1) {
+        const uint32_t o = (uint32_t)__shfl_up((int)incl, d);
+        if (lane >= d) incl += o;
+    }
+    const uint32_t nlist = uniform_u32((uint32_t)__shfl((int)incl, WAVE - 1));
+    if (wave == 0 && okc) red_cnt[lane] = nc == LIST_OVER ? 0u : nc;
+    const float M = uniform_f32(wave_maxnum_f32(Mr));
+    for (int m = 32; m >= 1; m >>= 1) fi = min(fi, (uint32_t)__shfl_xor((int)fi, m));
+    if (tid == 0) f.arrive[slot] = 0;  // ready for the next call
+    const bool finite = M > -__builtin_inff() && M < __builtin_inff();
+    if (!finite || !eligible) {
+        if (tid == 0) {
+            FullRow st{};
+            st.M = M;
+            st.done = finite ? 0u : 1u;
+            f.row[slot] = st;
+            // sample.rs:270-277: argmax, no draw; the first +inf, or 0 when
+            // nothing is above -inf.
+            if (!finite) write_single(a, row, M == __builtin_inff() ? uniform_u32(fi) : 0u);
+        }
         return;
     }
-    // With top-p off the reference keeps id order (no sort, sample.rs:290-305):
-    // the survivors are then sorted by ascending id, stored as
-    // (~id << 32 | key) so that the same descending sort serves.
+    // The mass interval (identical on every wave).
+    const double term = (okc && Mr > -__builtin_inff()) ? Sc * exp(((double)Mr - (double)M) * invT_d) : 0.0;
+    const double Smid = wave_total_f64(term);
+    bool ok_row = Smid == Smid && !lover && nlist > 0 && c2 < 3.0e38f && c2 > 0.0f && zthr > -3.0e38f;
+    // The survivors: every listed candidate's exact p (sample.rs:309), kept
+    // when p >= min_p (sample.rs:333); the largest key of one that is not.
+    RL_LDS uint64_t *sv = (RL_LDS uint64_t *)smem;
+    RL_LDS float *sp = (RL_LDS float *)(smem + FIN_CAP * sizeof(uint64_t));
     const bool by_id = !(s.top_p < 1.0f);
-    uint32_t n2 = 1;
-    while (n2 < c) n2 <<= 1;
-    const uint64_t *list = f.surv + (uint64_t)slot * SURV_CAP;
-    for (uint32_t i = tid; i < n2; i += REPLAY_THREADS) {
-        uint64_t x = 0;
-        if (i < c) {
-            x = list[i];
-            if (by_id) x = ((uint64_t)(uint32_t)x << 32) | comp_key(x);  // ~id in the high half
-        }
-        sv[i] = x;
-    }
-    if (tid == 0) sh_bad = 0;
-    copy_exp_table((RL_LDS uint64_t *)exp_tab);
-    const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab};
-    lds_bitonic_desc(sv, n2, REPLAY_THREADS);
-    auto key_at = [&](uint32_t i) { return by_id ? (uint32_t)sv[i] : comp_key(sv[i]); };
-    auto id_at = [&](uint32_t i) { return by_id ? ~(uint32_t)(sv[i] >> 32) : comp_id(sv[i]); };
-    for (uint32_t i = tid; i < c; i += REPLAY_THREADS)
-        sp[i] = expf_libm_t((key_value(key_at(i)) - st.M) / s.temperature, etab);
-    __syncthreads();
-    const auto term = [sp](uint32_t j) { return sp[j]; };
-
-    uint32_t kept = c;
-    double total = 0.0;
-    bool have_total = false;  // the normalising sum already known from the cut's replay
-    if (!by_id) {
-        // The survivors must be the first c candidates: every other key is
-        // below the smallest survivor key (equal keys have equal p).
-        if (st.ns_key != 0 && !(key_at(c - 1) >= st.ns_key)) return;
-        if (!(s.top_p > 0.0f)) {
-            kept = 1;  // a target <= 0 is met by the first candidate (sample.rs:315-323)
-            total = (double)sp[0];
-            have_total = true;
-        } else {
-            // The reference's mass (a sequential f64 sum of all V p's in
-            // candidate order) and S (this sum in chunk order) are each
-            // within gamma_(V-1) * mass of the exact sum, where
-            // gamma_n = n 2^-53 / (1 - n 2^-53); d bounds both, with margin.
-            // Each wave loads the chunks' sums at once (lane ch holds chunk
-            // ch's) and adds them in chunk order.
-            const uint32_t lane = lane_id();
-            const double psum_lane = lane < a.chunks ? f.psum[slot * a.chunks + lane] : 0.0;
-            double S = 0.0;
-            for (uint32_t ch = 0; ch < a.chunks; ++ch)
-                S += __longlong_as_double((long long)read_lane_u64((uint64_t)__double_as_longlong(psum_lane), ch));
-            const double d = 2.25 * ((double)V + 64.0) * 0x1p-53;
-            const double tp = (double)s.top_p;
-            const double t_lo = tp * (S * (1.0 - d)) * (1.0 - 0x1p-50);
-            const double t_hi = tp * (S * (1.0 + d)) * (1.0 + 0x1p-50);
-            double at;
-            const uint32_t j_lo =
-                seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, c, [t_lo](double v) { return v >= t_lo; }, &seq, &at);
-            if (j_lo < c) {
-                // Partial sums never decrease and the one before j_lo is below
-                // t_lo <= t_hi, so when the sum at j_lo reaches t_hi too, j_lo
-                // is also the first index to reach t_hi.
-                if (!(at >= t_hi)) {
-                    double unused;
-                    const uint32_t j_hi = seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(
-                        term, c, [t_hi](double v) { return v >= t_hi; }, &seq, &unused);
-                    if (j_hi != j_lo) return;  // the cut could fall on either side: sort the row
-                }
-                kept = j_lo + 1;
-            }
-            // The normalising total (sample.rs:342) is the same f64 sum of
-            // the same terms in the same order, up to the last kept one: the
-            // partial sum the cut's replay stopped at (all c of them when no
-            // cut). Min-p removes none of them: every survivor is >= min_p.
-            total = at;
-            have_total = true;
-        }
-    }
-    // Normalise over the kept candidates (sample.rs:342-347) and draw
-    // (:349-358), both in their order.
-    if (!have_total) seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(term, kept, NeverStop{}, &seq, &total);
-    const float inv = (float)(1.0 / total);
-    for (uint32_t i = tid; i < kept; i += REPLAY_THREADS) {
-        const float q = sp[i] * inv;
-        if (!(q <= 3.40282347e38f)) sh_bad = 1;
-    }
-    __syncthreads();
-    if (sh_bad) return;  // a non-finite probability: the sorting kernels walk it in order
-    for (uint32_t i = tid; i < kept; i += REPLAY_THREADS) {
-        const float q = sp[i] * inv;
-        sp[i] = q;
-        if (a.out_ids) {
-            a.out_ids[(uint64_t)row * a.cand_stride + i] = id_at(i);
-            a.out_probs[(uint64_t)row * a.cand_stride + i] = q;
-        }
-    }
-    __syncthreads();
-    const float u = a.uniforms[row];
-    double unused;
-    const uint32_t j =
-        seq_replay<24, REPLAY_THREADS, SEQ_ITEMS>(term, kept, [u](double v) { return v > (double)u; }, &seq, &unused);
     if (tid == 0) {
-        a.out_token[row] = id_at(j < kept ? j : kept - 1);
-        a.out_kept[row] = kept;
-        a.out_used[row] = 1;
-        f.row[slot].done = 1;
+        sh_count = 0;
+        sh_ns = 0;
+    }
+    __syncthreads();  // red_cnt, sh_count and sh_ns are set
+    const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab};
+    const TempScale tscale(s.temperature);
+    if (ok_row) {
+        uint32_t ns = 0;
+        auto take = [&](uint64_t c) {
+            const uint32_t key = comp_key(c);
+            const float p = expf_libm_t(tscale(key_value(key) - M), etab);
+            if (p >= s.min_p) {
+                const uint32_t at = atomicAdd((uint32_t *)&sh_count, 1u);
+                if (at < FIN_CAP) sv[at] = keep_order(c, by_id);
+            } else {
+                ns = max(ns, key + 1u);  // a finite p's key is below 0xFFFFFFFF
+            }
+        };
+#pragma unroll
+        for (uint32_t j = 0; j < SPEC; ++j)
+            if (sch < C && sidx + j * KT < red_cnt[sch]) take(spec[j]);
+        // The entries at K and beyond of chunks that listed more, all loads
+        // of one pass in flight together (entry i of them belongs to the last
+        // chunk whose count of extras before it is <= i).
+        uint32_t extra = 0;
+        for (uint32_t ch = 0; ch < C; ++ch) extra += red_cnt[ch] > K ? red_cnt[ch] - K : 0u;
+        for (uint32_t i = tid; i < extra; i += FULL_THREADS) {
+            uint32_t ch = 0, before = 0, acc = 0;
+            for (uint32_t k = 0; k < C; ++k) {
+                const uint32_t e = red_cnt[k] > K ? red_cnt[k] - K : 0u;
+                if (acc <= i && e != 0) {
+                    ch = k;
+                    before = acc;
+                }
+                acc += e;
+            }
+            take(__hip_atomic_load(list + ch * region_c + K + (i - before), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        }
+        for (int m = 32; m >= 1; m >>= 1) ns = max(ns, (uint32_t)__shfl_xor((int)ns, m));
+        if (lane == 0 && ns != 0) atomicMax((uint32_t *)&sh_ns, ns);
+    }
+    __syncthreads();
+    const uint32_t c = sh_count, ns_key = sh_ns;
+    ok_row = ok_row && c > 0 && c <= FIN_CAP;
+    // t_lo <= top_p * S_ref <= t_hi, with the reference's target rounding.
+    // Each step after a chunk's first can rescale the terms before it once
+    // more (RESCALE_REL each); the absolute terms cover the far terms and
+    // factors below 2^-1022.
+    const uint32_t steps = (chunk_lo(V / 4, 1, C) + PASS_STEP) / PASS_STEP;  // the largest chunk's steps, or more
+    const double rel = MASS_REL + (double)steps * RESCALE_REL;
+    const double abs_err = MASS_ABS_PER_TERM * (double)V + (double)V * 0x1p-1000;
+    const double gam = ((double)V + 64.0) * 0x1p-53;
+    const double S_lo = (Smid * (1.0 - rel) - abs_err) * (1.0 - gam);
+    const double S_hi = (Smid * (1.0 + rel) + abs_err) * (1.0 + gam);
+    const double tp = (double)s.top_p;
+    const double t_lo = tp * S_lo * (1.0 - 0x1p-48);
+    const double t_hi = tp * S_hi * (1.0 + 0x1p-48);
+    bool fin = false;
+    if (ok_row && c <= WAVE) {
+        if (wave == 0) {
+            const uint64_t xw = lane < c ? sv[lane] : 0ull;
+            fin = finish_wave(a, row, s, M, c, xw, by_id, ns_key, t_lo, t_hi, etab);
+            if (lane == 0) sh_flag = fin ? 1u : 0u;
+        }
+        __syncthreads();
+        fin = sh_flag != 0;
+    } else if (ok_row) {
+        fin = finish_block<FULL_THREADS>(a, row, s, M, c, sv, sp, (RL_LDS uint32_t *)sh_fin, (RL_LDS float *)&sh_inv,
+                                         etab, by_id, ns_key, t_lo, t_hi);
+    }
+    if (tid == 0) {
+        FullRow st{};
+        st.M = M;
+        st.done = fin ? 1u : 0u;
+        f.row[slot] = st;
     }
 }
 

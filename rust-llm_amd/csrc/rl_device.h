@@ -76,6 +76,9 @@ __device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
     return ((uint64_t)hi << 32) | lo;
 }
 __device__ __forceinline__ float uniform_f32(float v) { return __uint_as_float(uniform_u32(__float_as_uint(v))); }
+__device__ __forceinline__ double uniform_f64(double v) {
+    return __longlong_as_double((long long)uniform_u64((uint64_t)__double_as_longlong(v)));
+}
 
 __device__ __forceinline__ uint32_t read_lane_u32(uint32_t v, uint32_t lane) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)lane);

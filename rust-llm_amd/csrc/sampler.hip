@@ -131,7 +131,6 @@ struct rl_sampler_ctx {
     std::vector<uint32_t> stream_rows, full_rows;  // ascending; capacity max_rows
     uint64_t cand_need = 0;
     bool any_drawing = false;
-    bool any_small = false;  // a full-path row may take the min-p path
 
     template <class T>
     hipError_t alloc(T **p, size_t count) {
@@ -238,14 +237,12 @@ int rl_sampler_configure(rl_sampler_ctx *ctx, const rl_sampling *settings, uint3
     ctx->stream_rows.clear();
     ctx->full_rows.clear();
     uint64_t need = 0;
-    bool drawing = false, small = false;
+    bool drawing = false;
     for (uint32_t r = 0; r < rows; ++r) {
         const Path p = plan_row(settings[r], ctx->vocab);
         (p == Path::Stream ? ctx->stream_rows : ctx->full_rows).push_back(r);
         need = std::max(need, row_cand_need(settings[r], ctx->vocab));
         drawing = drawing || !(settings[r].temperature <= 0.0f);
-        small = small || (p == Path::Full && settings[r].min_p > 0.0f && settings[r].temperature > 0.0f &&
-                          (settings[r].top_k == 0 || settings[r].top_k >= ctx->vocab));
     }
     const auto &sr = ctx->stream_rows;
     const auto &fr = ctx->full_rows;
@@ -258,7 +255,6 @@ int rl_sampler_configure(rl_sampler_ctx *ctx, const rl_sampling *settings, uint3
     ctx->configured = rows;
     ctx->cand_need = need;
     ctx->any_drawing = drawing;
-    ctx->any_small = small;
     return RL_OK;
 }
 
@@ -353,14 +349,14 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
                        ctx->d_pbad,     ctx->d_plast_in, ctx->d_pfirst_out, ctx->d_surv,  ctx->d_full_row,
                        ctx->d_full_arrive};
         const dim3 cgrid(f.chunks, ng);
+        const size_t pass_lds = k_full_pass_lds_bytes(vocab, f.chunks);
         const size_t keys_lds = k_full_keys_lds_bytes(vocab, f.chunks);
-        if (vec)
+        if (vec) {
+            hipLaunchKernelGGL(k_full_pass<true>, cgrid, dim3(FULL_THREADS), pass_lds, st, f, fs);
             hipLaunchKernelGGL(k_full_keys<true>, cgrid, dim3(FULL_THREADS), keys_lds, st, f, fs);
-        else
+        } else {
+            hipLaunchKernelGGL(k_full_pass<false>, cgrid, dim3(FULL_THREADS), pass_lds, st, f, fs);
             hipLaunchKernelGGL(k_full_keys<false>, cgrid, dim3(FULL_THREADS), keys_lds, st, f, fs);
-        if (ctx->any_small) {
-            hipLaunchKernelGGL(k_full_collect, cgrid, dim3(FULL_THREADS), 0, st, f, fs);
-            hipLaunchKernelGGL(k_full_small, dim3(ng), dim3(REPLAY_THREADS), 0, st, f, fs);
         }
         hipLaunchKernelGGL(k_full_sort, dim3(ng), dim3(SORT_THREADS), 0, st, f, fs);
         hipLaunchKernelGGL(k_full_probs, cgrid, dim3(FULL_THREADS), 0, st, f, fs);

@@ -160,3 +160,54 @@ def test_small_and_ragged_vocabularies(device):
         settings = [R.sampling(1.0, 0, 0.9, 0.05, 1.0, 0, 0), R.sampling(1.0, 0, 1.0, 0.5, 1.0, 0, 1),
                     R.sampling(0.5, 0, 0.5, 0.001, 1.0, 0, 2), R.sampling(1.0, 0, 0.0, 0.9, 1.0, 0, 3)]
         case(device, x, settings, seed=V, label="V=%d" % V)
+
+
+def test_infinities_and_empty_chunks_across_the_single_read(device):
+    # The single read keeps, per chunk and per wave, the lowest id holding
+    # +inf, and a row's maximum from every chunk: +inf at several ids in
+    # several chunks (the lowest wins), a chunk of -inf only next to finite
+    # chunks, NaN inside a chunk of -inf only (the row must leave the min-p
+    # path), and a maximum that rises steadily along the row (many stale
+    # candidates).
+    V = 151936
+    rng = np.random.default_rng(21)
+    x = rng.normal(0.0, 2.0, (8, V)).astype(np.float32)
+    x[0, [140000, 70001, 70000, 99999]] = np.inf
+    x[1, :20000] = -np.inf
+    x[2, :20000] = -np.inf
+    x[2, 777] = np.nan
+    x[3] = np.linspace(-20.0, 10.0, V, dtype=np.float32)
+    x[4, :] = -np.inf
+    x[4, 151935] = -3.0
+    x[5, :] = -np.inf
+    x[5, 3] = np.nan
+    x[6, 151935] = np.inf
+    x[7] = np.linspace(10.0, -20.0, V, dtype=np.float32)
+    settings = [R.sampling(1.0, 0, 0.9, 0.05, 1.0, 0, r) for r in range(8)]
+    case(device, x, settings, label="infinities and empty chunks")
+
+
+@pytest.mark.parametrize("n_top", [1000, 1024, 1025])
+def test_survivors_at_the_in_kernel_cap(device, n_top):
+    # Up to 1024 survivors finish inside the single read; more go to the sort.
+    V = 151936
+    rng = np.random.default_rng(2000 + n_top)
+    x = rng.normal(0.0, 1.0, (3, V)).astype(np.float32)
+    for r in range(3):
+        x[r, rng.choice(V, n_top, replace=False)] = rng.uniform(9.0, 10.0, n_top)
+    settings = [R.sampling(1.0, 0, 0.999, 0.05, 1.0, 0, 1), R.sampling(1.0, 0, 1.0, 0.05, 1.0, 0, 2),
+                R.sampling(1.0, 0, 0.5, 0.05, 1.0, 0, 3)]
+    got = case(device, x, settings, seed=n_top, label="%d survivors" % n_top)
+    assert got["kept"][1] == n_top
+
+
+def test_extreme_temperatures(device):
+    # A temperature too small for the mass's exponent scale (the row leaves
+    # the min-p path), huge ones (every element a candidate: the list
+    # overflows), and ordinary ones beside them.
+    V = 30000
+    rng = np.random.default_rng(22)
+    x = rng.normal(0.0, 2.0, (6, V)).astype(np.float32)
+    settings = [R.sampling(t, 0, 0.9, 0.05, 1.0, 0, r)
+                for r, t in enumerate([1e-30, 1e-6, 1e30, 3.0e38, 0.05, 20.0])]
+    case(device, x, settings, label="extreme temperatures")
