@@ -1,0 +1,847 @@
+// The FULL path's second launch, k_full_rest: one workgroup per row that
+// k_full_pass left unfinished. It puts the row's candidates in the reference's
+// order (descending penalised logit, ascending id; sample.rs:279-305) with a
+// stable LSD radix sort whose passes are chosen by one histogram read, computes
+// p = exp((l - max) / T) as the last pass writes each candidate in place
+// (:309), takes the mass, the top-p cut, min-p and the normalising total
+// (:307-343), draws against the host's uniform (:349-358) and writes the kept
+// candidates q = p * (1 / total) (:344-347).
+//
+// HBM per row: the logits once or twice for the digit histograms, one read of
+// the logits for the first pass, 8 bytes read and 8 written per element for
+// each further pass (the last writes ids and p, to the candidate outputs when
+// the caller asked for them), a read of p for the per-chunk sums, and a read
+// and write of the kept prefix for the normalisation (the draw reads up to its
+// pick). A row the pass finished exits at once, so a call whose rows all
+// finished in the pass costs one empty launch here.
+#pragma once
+#include "full_kernels.h"
+
+namespace rl {
+
+constexpr uint32_t REST_THREADS = 1024;
+constexpr uint32_t REST_WAVES = REST_THREADS / WAVE;
+constexpr uint32_t REST_ITEMS = 8;                         // elements per lane per tile of a pass
+constexpr uint32_t REST_TILE = REST_THREADS * REST_ITEMS;  // elements per tile
+constexpr uint32_t REST_SEG = WAVE * REST_ITEMS;           // a wave's contiguous share of a tile
+constexpr uint32_t HIST_ITEMS = 12;                        // loads per thread per histogram step
+constexpr uint32_t HIST_STEP = REST_THREADS * HIST_ITEMS;  // elements per histogram step
+constexpr uint32_t STAT_CHUNKS = 64;                       // most chunks of the candidate list's sums
+constexpr uint32_t STAT_MIN = 2048;                        // fewest candidates per chunk (but one chunk)
+static_assert(HIST_STEP >= REST_TILE, "the window bitmap covers a tile");
+
+struct RestLds {
+    union {
+        struct {
+            uint32_t k[REST_TILE];  // the tile's keys, reordered by digit
+            uint32_t i[REST_TILE];  // and their ids
+        } tile;
+        uint32_t wh[REST_WAVES][2][256];  // per-wave histograms of two digits
+        struct {
+            float stage[STAGE];
+            SeqLds<REST_THREADS> seq;
+        } rep;
+    } u;
+    uint32_t hist[4][256];           // the row's digit histograms (digits flipped: 255 - d)
+    uint32_t offs[256];              // a pass's next output position per digit
+    uint32_t cnt[REST_WAVES][256];   // per wave: the tile's count per digit
+    uint32_t pos[REST_WAVES][256];   // per wave: its start within the digit's run of the tile
+    uint32_t tcount[256], tstart[256];
+    uint32_t bm[HIST_STEP / 32];     // window ids in the current step, one bit per element
+    uint32_t cls[4];                 // OR and AND of the keys with the top bit clear, then set
+    uint64_t exp_tab[32];
+    // Per chunk of the candidate list: the f64 sum of p, the smallest binary
+    // exponent of a nonzero p, the count with p >= min_p, a NaN or infinite
+    // p, the last index + 1 with p >= min_p and the first with p < min_p.
+    double csum[STAT_CHUNKS];
+    int cemin[STAT_CHUNKS];
+    uint32_t ccount[STAT_CHUNKS], cbad[STAT_CHUNKS], clast_in[STAT_CHUNKS], cfirst_out[STAT_CHUNKS];
+    double red_d[REST_WAVES];
+    int64_t red_l[REST_WAVES];
+    uint32_t red_u[REST_WAVES];
+    uint32_t sh_m, sh_stop, sh_hit, sh_tok;
+    double sh_d, sh_hit_sum;
+};
+
+// A buffer resource over n 32-bit words at p (raw addressing; gfx9's
+// descriptor word 3, 0x00020000: 32-bit data format). Loads at byte offsets
+// past 4n return zero and stores there are dropped, so tiles need no clamps;
+// each access takes one 32-bit offset register (plus an immediate) instead of
+// a 64-bit address.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t words_rsrc(const void *p, uint32_t n) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)(n * 4u), 0x00020000);
+}
+// The words [from, from + n) of p, or none when from is past n words.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tail_rsrc(const uint32_t *p, uint32_t from, uint32_t n) {
+    return from < n ? words_rsrc(p + from, n - from) : words_rsrc(p, 0);
+}
+template <bool NT = false>
+__device__ __forceinline__ uint32_t bload(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, NT ? 2 : 0);
+}
+__device__ __forceinline__ void bstore(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, uint32_t v) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, byte_off, 0, 0);
+}
+
+// ------------------------------------------------------ block helpers ---
+template <uint32_t NT>
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, RL_LDS uint32_t *red) {
+    for (int m = 32; m >= 1; m >>= 1) v += (uint32_t)__shfl_xor((int)v, m);
+    __syncthreads();
+    if (lane_id() == 0) red[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    uint32_t t = 0;
+    for (uint32_t w = 0; w < NT / WAVE; ++w) t += red[w];
+    return t;
+}
+
+template <uint32_t NT>
+__device__ __forceinline__ int64_t block_max_i64(int64_t v, RL_LDS int64_t *red) {
+    for (int m = 32; m >= 1; m >>= 1) {
+        const int64_t o = (int64_t)shfl_xor_u64((uint64_t)v, m);
+        v = o > v ? o : v;
+    }
+    __syncthreads();
+    if (lane_id() == 0) red[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    int64_t t = red[0];
+    for (uint32_t w = 1; w < NT / WAVE; ++w) t = red[w] > t ? red[w] : t;
+    return t;
+}
+
+// Exclusive prefix of v over the workgroup's threads in thread order; *total
+// gets the sum. For doubles it is only used where every partial sum is exact.
+template <uint32_t NT, class T>
+__device__ __forceinline__ T block_exclusive(T v, RL_LDS T *red, T *total) {
+    const uint32_t lane = lane_id(), wave = threadIdx.x / WAVE;
+    T incl = v;
+    for (uint32_t d = 1; d < WAVE; d <<= 1) {
+        const T o = __shfl_up(incl, d);
+        if (lane >= d) incl += o;
+    }
+    __syncthreads();
+    if (lane == WAVE - 1) red[wave] = incl;
+    __syncthreads();
+    T before = 0, all = 0;
+    for (uint32_t w = 0; w < NT / WAVE; ++w) {
+        if (w < wave) before += red[w];
+        all += red[w];
+    }
+    *total = all;
+    return before + incl - v;
+}
+
+// Walks src[0..n) in order on thread 0, one LDS-staged block at a time; the
+// whole workgroup stages. body(stage, base, count) returns true to stop.
+template <uint32_t NT, class Body>
+__device__ __forceinline__ void staged_walk(const float *src, uint32_t n, RL_LDS float *stage, RL_LDS uint32_t *stop,
+                                            Body body) {
+    for (uint32_t b = 0; b < n; b += STAGE) {
+        const uint32_t cnt = min(STAGE, n - b);
+        for (uint32_t i = threadIdx.x; i < cnt; i += NT) stage[i] = ((const RL_GLB float *)src)[b + i];
+        __syncthreads();
+        if (threadIdx.x == 0) *stop = body(stage, b, cnt) ? 1u : 0u;
+        __syncthreads();
+        if (*stop) break;
+    }
+}
+
+// Where every partial sum of the probabilities is exact: the first j in
+// [lo, hi) with base + p[lo] + ... + p[j] >= target, and that sum in *at; or
+// hi, with the sum of them all in *at. Any order of addition gives these exact
+// sums, so a block scan serves. Whole workgroup.
+template <uint32_t NT>
+__device__ __forceinline__ uint32_t exact_first_reaching(const float *probs, uint32_t lo, uint32_t hi, double base, double target,
+                                         RL_LDS double *red, RL_LDS uint32_t *hit, RL_LDS double *hit_sum,
+                                         double *at) {
+    for (uint32_t b = lo; b < hi; b += NT * CI) {
+        const uint32_t j0 = b + threadIdx.x * CI;
+        float pv[CI];
+        double mine = 0.0;
+#pragma unroll
+        for (uint32_t i = 0; i < CI; ++i) {
+            pv[i] = j0 + i < hi ? ((const RL_GLB float *)probs)[j0 + i] : 0.0f;
+            mine += (double)pv[i];
+        }
+        if (threadIdx.x == 0) *hit = 0xFFFFFFFFu;
+        double step_total;
+        double c = base + block_exclusive<NT, double>(mine, red, &step_total);
+        uint32_t my_hit = 0xFFFFFFFFu;
+        double my_sum = 0.0;
+#pragma unroll
+        for (uint32_t i = 0; i < CI; ++i) {
+            if (my_hit == 0xFFFFFFFFu && j0 + i < hi) {
+                c += (double)pv[i];
+                if (c >= target) {
+                    my_hit = j0 + i;
+                    my_sum = c;
+                }
+            }
+        }
+        if (my_hit != 0xFFFFFFFFu) atomicMin((uint32_t *)hit, my_hit);
+        __syncthreads();
+        const uint32_t h = *hit;
+        if (h != 0xFFFFFFFFu) {
+            if (my_hit == h) *hit_sum = my_sum;
+            __syncthreads();
+            *at = *hit_sum;
+            __syncthreads();
+            return h;
+        }
+        base += step_total;
+        __syncthreads();
+    }
+    *at = base;
+    return hi;
+}
+
+// Adds one wave-item's digits d (lanes where valid) to the wave's private
+// histogram h. The first valid lane's digit is counted with one add for all
+// lanes that share it (a row's commonest digit, such as a tied logit's, would
+// otherwise make every lane holding it wait on the same counter); the other
+// lanes add one each.
+__device__ __forceinline__ void hist_add(RL_LDS uint32_t *h, uint32_t d, bool valid, uint32_t lane) {
+    const uint64_t vm = ballot(valid);
+    if (vm == 0) return;
+    const uint32_t f = (uint32_t)__builtin_ctzll(vm);
+    const uint32_t d0 = uniform_u32(read_lane_u32(d, f));
+    const uint64_t m0 = ballot(valid && d == d0);
+    if (lane == f) {
+        atomicAdd((uint32_t *)&h[d0], (uint32_t)__popcll(m0));
+    } else if (valid && d != d0) {
+        atomicAdd((uint32_t *)&h[d], 1u);
+    }
+}
+
+// What a pass needs of its row.
+struct RestRow {
+    const float *rowp;   // the raw logits
+    const uint32_t *win; // the recent-token window
+    uint32_t V, k, wl;
+    bool pen;
+    float penalty, M;
+    TempScale tscale;
+};
+
+// Window ids in [e0, e0 + n) as bits of L->bm (n <= HIST_STEP). Whole
+// workgroup; two barriers.
+__device__ __forceinline__ void window_bits(RL_LDS RestLds *L, const RestRow &r, uint32_t e0, uint32_t n) {
+    for (uint32_t i = threadIdx.x; i < (n + 31) / 32; i += REST_THREADS) L->bm[i] = 0;
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < r.wl; i += REST_THREADS) {
+        const uint32_t id = r.win[i];
+        if (id >= e0 && id - e0 < n) atomicOr((uint32_t *)&L->bm[(id - e0) >> 5], 1u << ((id - e0) & 31));
+    }
+    __syncthreads();
+}
+
+// The penalised logit (sample.rs:239-257) of element e0 + off, x its raw
+// value, from the bits of the step that starts at e0. An id repeated in the
+// window has one bit, so it is penalised once.
+__device__ __forceinline__ float penalised(RL_LDS const RestLds *L, const RestRow &r, float x, uint32_t off) {
+    return ((L->bm[off >> 5] >> (off & 31)) & 1u) ? penalize(x, r.penalty) : x;
+}
+
+// The histograms of digits hi and lo (8 bits at 8 * hi and 8 * lo) of the
+// penalised row's total-order keys into L->hist[hi] and L->hist[lo], and with
+// `cls` the OR and AND of the keys of each sign into L->cls. One read of the
+// logits, HIST_ITEMS loads per thread in flight.
+__device__ __forceinline__ void rest_histograms(RL_LDS RestLds *L, const RestRow &r, uint32_t hi, uint32_t lo,
+                                                bool cls) {
+    const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / WAVE;
+    const uint32_t V = r.V;
+    for (uint32_t i = tid; i < REST_WAVES * 2 * 256; i += REST_THREADS) (&L->u.wh[0][0][0])[i] = 0;
+    if (cls && tid < 4) L->cls[tid] = (tid & 1) ? 0xFFFFFFFFu : 0u;
+    __syncthreads();
+    RL_LDS uint32_t *h_hi = &L->u.wh[wave][0][0];
+    RL_LDS uint32_t *h_lo = &L->u.wh[wave][1][0];
+    uint32_t or0 = 0u, and0 = 0xFFFFFFFFu, or1 = 0u, and1 = 0xFFFFFFFFu;
+    const uint32_t s_hi = 8 * hi, s_lo = 8 * lo;
+    // A step gives each wave a contiguous segment, HIST_ITEMS elements a lane
+    // 64 apart; the next step's loads are issued before this step's
+    // elements are counted.
+    const uint32_t wbase = wave * WAVE * HIST_ITEMS + lane;
+    const uint32_t *raw = (const uint32_t *)r.rowp;
+    uint32_t nx[HIST_ITEMS];
+    {
+        const auto rs = tail_rsrc(raw, 0, V);
+#pragma unroll
+        for (uint32_t i = 0; i < HIST_ITEMS; ++i) nx[i] = bload<true>(rs, 4 * (wbase + i * WAVE));
+    }
+    for (uint32_t b = 0; b < V; b += HIST_STEP) {
+        uint32_t x[HIST_ITEMS];
+        const auto rs = tail_rsrc(raw, b + HIST_STEP, V);
+#pragma unroll
+        for (uint32_t i = 0; i < HIST_ITEMS; ++i) {
+            x[i] = nx[i];
+            nx[i] = bload<true>(rs, 4 * (wbase + i * WAVE));
+        }
+        if (r.pen) window_bits(L, r, b, min(HIST_STEP, V - b));
+#pragma unroll
+        for (uint32_t i = 0; i < HIST_ITEMS; ++i) {
+            const uint32_t off = wbase + i * WAVE;
+            const bool valid = b + off < V;
+            const float v = r.pen ? penalised(L, r, __uint_as_float(x[i]), off) : __uint_as_float(x[i]);
+            const uint32_t key = total_key(v);
+            if (cls && valid) {
+                if (key >> 31) {
+                    or1 |= key;
+                    and1 &= key;
+                } else {
+                    or0 |= key;
+                    and0 &= key;
+                }
+            }
+            hist_add(h_hi, 255u - ((key >> s_hi) & 255u), valid, lane);
+            hist_add(h_lo, 255u - ((key >> s_lo) & 255u), valid, lane);
+        }
+        if (r.pen) __syncthreads();  // the bits are rebuilt for the next step
+    }
+    if (cls) {
+        for (int m = 32; m >= 1; m >>= 1) {
+            or0 |= (uint32_t)__shfl_xor((int)or0, m);
+            and0 &= (uint32_t)__shfl_xor((int)and0, m);
+            or1 |= (uint32_t)__shfl_xor((int)or1, m);
+            and1 &= (uint32_t)__shfl_xor((int)and1, m);
+        }
+        if (lane == 0) {
+            atomicOr((uint32_t *)&L->cls[0], or0);
+            atomicAnd((uint32_t *)&L->cls[1], and0);
+            atomicOr((uint32_t *)&L->cls[2], or1);
+            atomicAnd((uint32_t *)&L->cls[3], and1);
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < 2 * 256; i += REST_THREADS) {
+        uint32_t c = 0;
+        for (uint32_t w = 0; w < REST_WAVES; ++w) c += L->u.wh[w][i >> 8][i & 255u];
+        L->hist[(i >> 8) ? lo : hi][i & 255u] = c;
+    }
+    __syncthreads();
+}
+
+// Exclusive prefix over the 256 digits of src into dst; the first wave, four
+// digits a lane.
+__device__ __forceinline__ void digit_prefix(RL_LDS const uint32_t *src, RL_LDS uint32_t *dst) {
+    const uint32_t lane = lane_id();
+    uint32_t v[4], sum = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+        v[q] = src[4 * lane + q];
+        sum += v[q];
+    }
+    uint32_t incl = sum;
+    for (uint32_t d = 1; d < WAVE; d <<= 1) {
+        const uint32_t o = (uint32_t)__shfl_up((int)incl, d);
+        if (lane >= d) incl += o;
+    }
+    uint32_t run = incl - sum;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+        dst[4 * lane + q] = run;
+        run += v[q];
+    }
+}
+
+// One stable pass of the sort on digit t (bits 8t..8t+7, descending): from the
+// raw logits (FROM_LOGITS: keys computed here, ids = positions) or from
+// kin/iin, to kout/iout, or (FINAL) the ids to iout and p to fp for the first
+// k positions. Each tile gives every wave a contiguous segment; a wave ranks
+// its items in order (lanes with the same digit found by ballots, the wave's
+// running count per digit in LDS, advanced by the first such lane with one
+// atomic whose old value the others read from it), the workgroup reorders
+// the tile by digit in LDS and writes it out in runs, so consecutive threads
+// write consecutive addresses.
+template <bool FROM_LOGITS, bool FINAL>
+__device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, const LdsExpTable &etab, uint32_t t,
+                          const uint32_t *kin, const uint32_t *iin, uint32_t *kout, uint32_t *iout, float *fp) {
+    const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / WAVE;
+    const uint32_t V = r.V, shift = 8 * t;
+    if (tid < WAVE) digit_prefix(L->hist[t], L->offs);
+    __syncthreads();
+    uint32_t nk[REST_ITEMS], ni[REST_ITEMS];
+    const uint32_t voff = 4 * (wave * REST_SEG + lane);  // item i adds 256 i bytes
+    auto fetch = [&](uint32_t tb) {  // tile tb's keys and ids (zeros past the row)
+        if constexpr (FROM_LOGITS) {
+            const auto rl = tail_rsrc((const uint32_t *)r.rowp, tb, V);
+#pragma unroll
+            for (uint32_t i = 0; i < REST_ITEMS; ++i) nk[i] = bload<true>(rl, voff + 256 * i);
+        } else {
+            const auto rk = tail_rsrc(kin, tb, V), ri = tail_rsrc(iin, tb, V);
+#pragma unroll
+            for (uint32_t i = 0; i < REST_ITEMS; ++i) {
+                nk[i] = bload(rk, voff + 256 * i);
+                ni[i] = bload(ri, voff + 256 * i);
+            }
+        }
+    };
+    // The outputs: past the first k, final writes are dropped (only those are
+    // candidates, and the caller's buffers may hold no more).
+    const auto rko = words_rsrc(kout, FINAL ? 0u : V);
+    const auto rio = words_rsrc(iout, FINAL ? r.k : V);
+    const auto rpo = words_rsrc(fp, FINAL ? r.k : 0u);
+    fetch(0);
+    for (uint32_t tb = 0; tb < V; tb += REST_TILE) {
+        const uint32_t e0 = tb + wave * REST_SEG + lane;
+        const uint32_t tn = min(REST_TILE, V - tb);
+        uint32_t kk[REST_ITEMS], ii[REST_ITEMS];
+#pragma unroll
+        for (uint32_t i = 0; i < REST_ITEMS; ++i) {
+            kk[i] = nk[i];
+            ii[i] = FROM_LOGITS ? e0 + i * WAVE : ni[i];
+        }
+        fetch(tb + REST_TILE);
+        if constexpr (FROM_LOGITS) {
+            if (r.pen) window_bits(L, r, tb, tn);
+#pragma unroll
+            for (uint32_t i = 0; i < REST_ITEMS; ++i) {
+                float v = __uint_as_float(kk[i]);
+                if (r.pen) v = penalised(L, r, v, e0 + i * WAVE - tb);
+                kk[i] = total_key(v);
+            }
+        }
+        for (uint32_t d = lane; d < 256; d += WAVE) L->cnt[wave][d] = 0;
+        // Rank: item i's lanes with digit d follow the wave's earlier items'.
+        uint32_t rk[REST_ITEMS];
+#pragma unroll
+        for (uint32_t i = 0; i < REST_ITEMS; ++i) {
+            const bool valid = e0 + i * WAVE < V;
+            const uint32_t d = 255u - ((kk[i] >> shift) & 255u);
+            const uint64_t peers = match_digit(d, valid);
+            const uint32_t below = lanes_below(peers);
+            const uint32_t lead = valid ? (uint32_t)__builtin_ctzll(peers) : lane;
+            uint32_t old = 0;
+            if (valid && below == 0) old = atomicAdd((uint32_t *)&L->cnt[wave][d], (uint32_t)__popcll(peers));
+            rk[i] = below + (uint32_t)__shfl((int)old, (int)lead);
+        }
+        __syncthreads();
+        // Per digit: each wave's start within the digit's run of the tile, and
+        // the run's length; then the runs' starts.
+        if (tid < 256) {
+            uint32_t run = 0;
+            for (uint32_t w = 0; w < REST_WAVES; ++w) {
+                L->pos[w][tid] = run;
+                run += L->cnt[w][tid];
+            }
+            L->tcount[tid] = run;
+        }
+        __syncthreads();
+        if (tid < WAVE) digit_prefix(L->tcount, L->tstart);
+        __syncthreads();
+#pragma unroll
+        for (uint32_t i = 0; i < REST_ITEMS; ++i) {
+            if (e0 + i * WAVE < V) {
+                const uint32_t d = 255u - ((kk[i] >> shift) & 255u);
+                const uint32_t at = L->tstart[d] + L->pos[wave][d] + rk[i];
+                L->u.tile.k[at] = kk[i];
+                L->u.tile.i[at] = ii[i];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t q = 0; q < REST_ITEMS; ++q) {
+            const uint32_t j = q * REST_THREADS + tid;
+            if (j < tn) {
+                const uint32_t key = L->u.tile.k[j];
+                const uint32_t d = 255u - ((key >> shift) & 255u);
+                const uint32_t dst = L->offs[d] + (j - L->tstart[d]);
+                bstore(rio, 4 * dst, L->u.tile.i[j]);
+                if constexpr (FINAL) {
+                    if (dst < r.k) bstore(rpo, 4 * dst, __float_as_uint(expf_libm_t(r.tscale(key_value(key) - r.M), etab)));
+                } else {
+                    bstore(rko, 4 * dst, key);
+                }
+            }
+        }
+        __syncthreads();
+        if (tid < 256) L->offs[tid] += L->tcount[tid];
+        __syncthreads();
+    }
+}
+
+// The candidates in id order (no sort: top-p off with every id a candidate,
+// or every key alike): ids = positions and p, for the first k.
+__device__ __forceinline__ void rest_direct(RL_LDS RestLds *L, const RestRow &r, const LdsExpTable &etab, uint32_t *iout, float *fp) {
+    const uint32_t lane = lane_id(), wave = threadIdx.x / WAVE;
+    const uint32_t V = r.V;
+    const uint32_t wbase = wave * WAVE * HIST_ITEMS + lane;
+    const uint32_t *raw = (const uint32_t *)r.rowp;
+    for (uint32_t b = 0; b < r.k; b += HIST_STEP) {
+        uint32_t x[HIST_ITEMS];
+        const auto rs = tail_rsrc(raw, b, V);
+#pragma unroll
+        for (uint32_t i = 0; i < HIST_ITEMS; ++i) x[i] = bload<true>(rs, 4 * (wbase + i * WAVE));
+        if (r.pen) window_bits(L, r, b, min(HIST_STEP, V - b));
+        const auto ri = tail_rsrc(iout, b, r.k), rp = tail_rsrc((const uint32_t *)fp, b, r.k);
+#pragma unroll
+        for (uint32_t i = 0; i < HIST_ITEMS; ++i) {
+            const uint32_t off = wbase + i * WAVE;
+            if (b + off < r.k) {
+                const float v = r.pen ? penalised(L, r, __uint_as_float(x[i]), off) : __uint_as_float(x[i]);
+                bstore(ri, 4 * off, b + off);
+                bstore(rp, 4 * off, __float_as_uint(expf_libm_t(r.tscale(v - r.M), etab)));
+            }
+        }
+        if (r.pen) __syncthreads();
+    }
+}
+
+// grid (slots), REST_THREADS: the rows k_full_pass left (done == 0).
+__global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch f) {
+    __shared__ RestLds L_;
+    RL_LDS RestLds *L = (RL_LDS RestLds *)&L_;
+    const uint32_t slot = blockIdx.x;
+    const FullRow st = f.row[slot];
+    if (st.done) return;
+    const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / WAVE;
+    const uint32_t row = a.rows[slot];
+    const rl_sampling s = a.settings[row];
+    const uint32_t V = a.vocab;
+    const uint32_t k = full_k(s, V);
+    const uint32_t wl = window_len(a, row);
+    const RestRow r{a.logits + (uint64_t)row * a.stride,
+                    wl > 0 ? a.windows + (uint64_t)row * a.wstride : nullptr,
+                    V,
+                    k,
+                    wl,
+                    penalises(s) && wl > 0,
+                    s.repeat_penalty,
+                    st.M,
+                    TempScale(s.temperature)};
+    copy_exp_table(L->exp_tab);
+    const LdsExpTable etab{L->exp_tab};
+    const bool out = a.out_ids != nullptr;
+    uint32_t *keyA = f.keyA + (uint64_t)slot * V, *idA = f.idA + (uint64_t)slot * V;
+    uint32_t *keyB = f.keyB + (uint64_t)slot * V, *idB = f.idB + (uint64_t)slot * V;
+    float *fp = out ? a.out_probs + (uint64_t)row * a.cand_stride : f.probs + (uint64_t)slot * V;
+    uint32_t *fid = out ? a.out_ids + (uint64_t)row * a.cand_stride : idA;
+
+    // ---- the candidates in order: fid[0..V), fp[0..k) ----
+    if (identity_order(s, V)) {
+        rest_direct(L, r, etab, fid, fp);
+    } else {
+        // Which passes run: per sign, the OR and the AND of its keys give the
+        // bits in which keys of that sign differ. A lower digit's pass is
+        // skipped when the digit is the same for all keys of each sign (as
+        // for logits on a bf16 grid, whose low 16 key bits follow the sign):
+        // keys that agree above it agree on it, so it cannot change the
+        // order. The top digit's pass is skipped when it is the same for all.
+        rest_histograms(L, r, 3, 2, true);
+        const uint32_t c0 = L->cls[0], c1 = L->cls[1], c2 = L->cls[2], c3 = L->cls[3];
+        const bool has0 = c1 != 0xFFFFFFFFu, has1 = c2 != 0u;
+        const uint32_t vary_sign = (has0 ? (c0 ^ c1) : 0u) | (has1 ? (c2 ^ c3) : 0u);
+        const uint32_t all_or = (has0 ? c0 : 0u) | (has1 ? c2 : 0u);
+        const uint32_t all_and = (has0 ? c1 : 0xFFFFFFFFu) & (has1 ? c3 : 0xFFFFFFFFu);
+        uint32_t passes[4], np = 0;
+        for (uint32_t t = 0; t < 3; ++t)
+            if (((vary_sign >> (8 * t)) & 255u) != 0) passes[np++] = t;
+        if (((all_or ^ all_and) >> 24) != 0) passes[np++] = 3;
+        if (np > 0 && passes[0] < 2) rest_histograms(L, r, 1, 0, false);
+        if (np == 0) {
+            rest_direct(L, r, etab, fid, fp);
+        } else {
+            // Pass i writes A when i is even, B when odd; the last writes the
+            // ids where the candidates go (not into the buffer it reads).
+            const uint32_t *kin = nullptr, *iin = nullptr;
+            for (uint32_t i = 0; i < np; ++i) {
+                const bool last = i + 1 == np;
+                uint32_t *ko = (i & 1) ? keyB : keyA, *io = (i & 1) ? idB : idA;
+                if (last && !out) fid = (i & 1) ? idB : idA;
+                if (i == 0 && last) rest_pass<true, true>(L, r, etab, passes[i], nullptr, nullptr, nullptr, fid, fp);
+                else if (i == 0) rest_pass<true, false>(L, r, etab, passes[i], nullptr, nullptr, ko, io, nullptr);
+                else if (last) rest_pass<false, true>(L, r, etab, passes[i], kin, iin, nullptr, fid, fp);
+                else rest_pass<false, false>(L, r, etab, passes[i], kin, iin, ko, io, nullptr);
+                kin = ko;
+                iin = io;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- per-chunk sums of the candidate list, one wave a chunk ----
+    const uint32_t CS = max(1u, min(STAT_CHUNKS, k / STAT_MIN));
+    for (uint32_t c = wave; c < CS; c += REST_WAVES) {
+        const uint32_t j0 = chunk_lo(k, c, CS), j1 = chunk_lo(k, c + 1, CS);
+        double sum = 0.0;
+        int emin = 1 << 20;
+        uint32_t count = 0, bad = 0, last_in = 0, first_out = 0xFFFFFFFFu;
+        constexpr uint32_t SU = 8;
+        for (uint32_t b = j0; b < j1; b += WAVE * SU) {
+            float pv[SU];
+#pragma unroll
+            for (uint32_t u = 0; u < SU; ++u) {
+                const uint32_t j = b + u * WAVE + lane;
+                pv[u] = ((const RL_GLB float *)fp)[j < j1 ? j : j1 - 1];
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < SU; ++u) {
+                const uint32_t j = b + u * WAVE + lane;
+                if (j < j1) {
+                    const float p = pv[u];
+                    if (!(p <= 3.40282347e38f)) {
+                        bad = 1;  // NaN or +inf
+                    } else if (p > 0.0f) {
+                        emin = min(emin, f32_exponent(p));
+                    }
+                    sum += (double)p;
+                    if (p >= s.min_p) {
+                        ++count;
+                        last_in = max(last_in, j + 1);
+                    } else {
+                        first_out = min(first_out, j);
+                    }
+                }
+            }
+        }
+        for (int m = 32; m >= 1; m >>= 1) {
+            sum += __shfl_xor(sum, m);
+            emin = min(emin, __shfl_xor(emin, m));
+            count += (uint32_t)__shfl_xor((int)count, m);
+            bad |= (uint32_t)__shfl_xor((int)bad, m);
+            last_in = max(last_in, (uint32_t)__shfl_xor((int)last_in, m));
+            first_out = min(first_out, (uint32_t)__shfl_xor((int)first_out, m));
+        }
+        if (lane == 0) {
+            L->csum[c] = sum;
+            L->cemin[c] = emin;
+            L->ccount[c] = count;
+            L->cbad[c] = bad;
+            L->clast_in[c] = last_in;
+            L->cfirst_out[c] = first_out;
+        }
+    }
+    __syncthreads();
+
+    // ---- the mass, the top-p cut (sample.rs:307-324), min-p (:326-340) and
+    // the normalising total (:342-343) ----
+    RL_LDS float *stage = L->u.rep.stage;
+    RL_LDS uint32_t *stop = &L->sh_stop;
+    const auto term = [fp](uint32_t j) { return ((const RL_GLB float *)fp)[j]; };
+    bool bad = false;
+    int emin = 1 << 20;
+    uint32_t count = 0, last_in = 0, first_out = 0xFFFFFFFFu;
+    double tree_mass = 0.0;
+    for (uint32_t c = 0; c < CS; ++c) {
+        bad |= L->cbad[c] != 0;
+        emin = min(emin, L->cemin[c]);
+        count += L->ccount[c];
+        last_in = max(last_in, L->clast_in[c]);
+        first_out = min(first_out, L->cfirst_out[c]);
+        tree_mass += L->csum[c];
+    }
+    // The candidates with p >= min_p form a prefix of the list.
+    const bool surv_prefix = last_in <= first_out;
+    // Every partial sum exact: all p are multiples of 2^(emin-23), the mass is
+    // below 2^53 of those steps. Then the chunk sums are the exact sums too.
+    const bool exact = !bad && (emin > 1000 || tree_mass < mul_pow2(1.0, 30 + emin));
+    // The exact sum of p[0..n), from the chunk sums and one partial chunk.
+    auto exact_prefix = [&](uint32_t n) {
+        double b = 0.0;
+        uint32_t c = 0;
+        while (c < CS && chunk_lo(k, c + 1, CS) <= n) b += L->csum[c++];
+        if (c == CS || chunk_lo(k, c, CS) == n) return b;
+        double at;
+        exact_first_reaching<REST_THREADS>(fp, chunk_lo(k, c, CS), n, b, __builtin_inf(), L->red_d, &L->sh_hit,
+                                           &L->sh_hit_sum, &at);
+        return at;
+    };
+
+    uint32_t m = k;
+    bool have_sum_m = false;  // sum_m: the sequential sum of p[0..m)
+    double sum_m = 0.0;
+    if (s.top_p < 1.0f) {
+        double mass = 0.0;
+        if (exact) {
+            mass = tree_mass;
+        } else if (!bad) {
+            seq_replay<53, REST_THREADS, SEQ_ITEMS>(term, k, NeverStop{}, (SeqLds<REST_THREADS> *)&L->u.rep.seq, &mass);
+        } else {
+            staged_walk<REST_THREADS>(fp, k, stage, stop, [&](RL_LDS float *sv, uint32_t, uint32_t cnt) {
+                for (uint32_t i = 0; i < cnt; ++i) mass += (double)sv[i];
+                return false;
+            });
+            if (tid == 0) L->sh_d = mass;
+            __syncthreads();
+            mass = L->sh_d;
+        }
+        const double target = (double)s.top_p * mass;
+        if (exact) {
+            // The chunk where the running sum first reaches the target.
+            double b = 0.0;
+            uint32_t c = 0;
+            while (c < CS && !(b + L->csum[c] >= target)) b += L->csum[c++];
+            if (c < CS) {
+                double at;
+                const uint32_t j = exact_first_reaching<REST_THREADS>(fp, chunk_lo(k, c, CS), chunk_lo(k, c + 1, CS), b,
+                                                                      target, L->red_d, &L->sh_hit, &L->sh_hit_sum, &at);
+                m = j + 1;
+                have_sum_m = true;
+                sum_m = at;
+            } else {
+                have_sum_m = true;
+                sum_m = mass;
+            }
+        } else if (!bad) {
+            double at;
+            const uint32_t j = seq_replay<53, REST_THREADS, SEQ_ITEMS>(
+                term, k, [target](double c) { return c >= target; }, (SeqLds<REST_THREADS> *)&L->u.rep.seq, &at);
+            have_sum_m = true;
+            if (j < k) {
+                m = j + 1;
+                sum_m = at;
+            } else {
+                sum_m = mass;
+            }
+        } else {
+            if (tid == 0) L->sh_m = k;
+            __syncthreads();
+            double cum = 0.0;
+            staged_walk<REST_THREADS>(fp, k, stage, stop, [&](RL_LDS float *sv, uint32_t b, uint32_t cnt) {
+                for (uint32_t i = 0; i < cnt; ++i) {
+                    cum += (double)sv[i];
+                    if (cum >= target) {
+                        L->sh_m = b + i + 1;
+                        return true;
+                    }
+                }
+                return false;
+            });
+            __syncthreads();
+            m = L->sh_m;
+        }
+    }
+    if (s.min_p > 0.0f) {  // a stable in-place compaction
+        uint32_t w;
+        if (!bad && surv_prefix) {
+            // The survivors are the first `count` of all k candidates (so it
+            // is with sorted candidates, where p falls along the order), and
+            // min(m, count) of the first m: nothing moves.
+            w = min(m, count);
+        } else {
+            // Survivors anywhere: count them, and compact unless they are
+            // already a prefix.
+            uint32_t fo = 0xFFFFFFFFu, li = 0, cnt = 0;
+            for (uint32_t b = 0; b < m; b += REST_THREADS) {
+                const uint32_t j = b + tid;
+                if (j < m) {
+                    if (((const RL_GLB float *)fp)[j] >= s.min_p) {
+                        ++cnt;
+                        li = j + 1;
+                    } else if (fo == 0xFFFFFFFFu) {
+                        fo = j;
+                    }
+                }
+            }
+            w = block_sum_u32<REST_THREADS>(cnt, L->red_u);
+            const uint32_t lo_out = (uint32_t)-block_max_i64<REST_THREADS>(-(int64_t)fo, L->red_l);
+            const uint32_t hi_in = (uint32_t)block_max_i64<REST_THREADS>((int64_t)li, L->red_l);
+            if (hi_in > lo_out) {
+                uint32_t done = 0;
+                for (uint32_t b = 0; b < m; b += REST_THREADS * CI) {
+                    const uint32_t j0 = b + tid * CI;
+                    float pv[CI];
+                    uint32_t iv[CI];
+                    uint32_t mine = 0;
+#pragma unroll
+                    for (uint32_t i = 0; i < CI; ++i) {
+                        const bool ok = j0 + i < m;
+                        pv[i] = ok ? fp[j0 + i] : 0.0f;
+                        iv[i] = ok ? fid[j0 + i] : 0u;
+                        mine += (ok && pv[i] >= s.min_p) ? 1u : 0u;
+                    }
+                    uint32_t step_total;
+                    uint32_t dst = done + block_exclusive<REST_THREADS, uint32_t>(mine, L->red_u, &step_total);
+#pragma unroll
+                    for (uint32_t i = 0; i < CI; ++i) {
+                        if (j0 + i < m && pv[i] >= s.min_p) {
+                            fid[dst] = iv[i];
+                            fp[dst] = pv[i];
+                            ++dst;
+                        }
+                    }
+                    done += step_total;
+                    __syncthreads();
+                }
+            }
+        }
+        if (w != m) have_sum_m = false;
+        m = w > 1 ? w : 1u;
+    }
+    double total = 0.0;
+    if (have_sum_m) {
+        total = sum_m;  // the same terms in the same order as the top-p pass
+    } else if (exact && (surv_prefix || !(s.min_p > 0.0f))) {
+        total = exact_prefix(m);  // min-p moved nothing: the chunk sums still apply
+    } else if (exact) {
+        exact_first_reaching<REST_THREADS>(fp, 0, m, 0.0, __builtin_inf(), L->red_d, &L->sh_hit, &L->sh_hit_sum,
+                                           &total);
+    } else if (!bad) {
+        seq_replay<53, REST_THREADS, SEQ_ITEMS>(term, m, NeverStop{}, (SeqLds<REST_THREADS> *)&L->u.rep.seq, &total);
+    } else {
+        staged_walk<REST_THREADS>(fp, m, stage, stop, [&](RL_LDS float *sv, uint32_t, uint32_t cnt) {
+            for (uint32_t i = 0; i < cnt; ++i) total += (double)sv[i];
+            return false;
+        });
+        if (tid == 0) L->sh_d = total;
+        __syncthreads();
+        total = L->sh_d;
+    }
+    const float inv = (float)(1.0 / total);
+    // q = p * inv is finite for every kept p when every p is and inv is (p <= 1
+    // and inv <= 1: the best p is exp(0) = 1, so total >= 1).
+    const bool qbad = bad || !(inv <= 3.40282347e38f);
+
+    // ---- the draw: the f32 running sum of q against the uniform
+    // (sample.rs:349-356); a shortfall takes the last candidate (:357-358) ----
+    const float u = a.uniforms[row];
+    uint32_t pick;
+    if (!qbad) {
+        double unused;
+        const uint32_t j = seq_replay<24, REST_THREADS, SEQ_ITEMS>(
+            [fp](uint32_t j) { return ((const RL_GLB uint32_t *)fp)[j]; },
+            [inv](uint32_t bits) { return __uint_as_float(bits) * inv; }, m, [u](double c) { return c > (double)u; },
+            (SeqLds<REST_THREADS> *)&L->u.rep.seq, &unused);
+        pick = j < m ? j : m - 1;
+    } else {
+        if (tid == 0) L->sh_tok = m - 1;
+        __syncthreads();
+        float cum = 0.0f;
+        staged_walk<REST_THREADS>(fp, m, stage, stop, [&](RL_LDS float *sv, uint32_t b, uint32_t cnt) {
+            for (uint32_t i = 0; i < cnt; ++i) {
+                cum += sv[i] * inv;
+                if (cum > u) {
+                    L->sh_tok = b + i;
+                    return true;
+                }
+            }
+            return false;
+        });
+        __syncthreads();
+        pick = L->sh_tok;
+    }
+    __syncthreads();  // every read of p by the draw precedes the writes of q
+    if (tid == 0) {
+        a.out_token[row] = fid[pick];
+        a.out_kept[row] = m;
+        a.out_used[row] = 1;
+    }
+    // ---- the kept candidates: q = p * (1 / total) in place (sample.rs:344-347) ----
+    if (out) {
+        constexpr uint32_t NU = 8;
+        for (uint32_t b = 0; b < m; b += REST_THREADS * NU) {
+            float pv[NU];
+#pragma unroll
+            for (uint32_t q = 0; q < NU; ++q) {
+                const uint32_t j = b + q * REST_THREADS + tid;
+                pv[q] = ((const RL_GLB float *)fp)[j < m ? j : m - 1];
+            }
+#pragma unroll
+            for (uint32_t q = 0; q < NU; ++q) {
+                const uint32_t j = b + q * REST_THREADS + tid;
+                if (j < m) fp[j] = pv[q] * inv;
+            }
+        }
+    }
+}
+
+}  // namespace rl

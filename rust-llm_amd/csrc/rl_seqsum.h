@@ -511,7 +511,7 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
         double tot = 0.0, tot_before = 0.0;
         double fsum = 0.0, f_before = 0.0;
         int lowest = 0x7FFFFFFF;
-#pragma unroll
+#pragma unroll 2
         for (uint32_t w = 0; w < NW; ++w) {
             if (w == wave) {
                 tot_before = tot;

@@ -13,7 +13,7 @@
 #include "rl_error.h"
 #include "rl_runtime.h"
 #include "rl_sampler.h"
-#include "full_kernels.h"
+#include "full_rest.h"
 #include "top_probability.h"
 
 using namespace rl;
@@ -116,8 +116,6 @@ struct rl_sampler_ctx {
     float *d_part_max = nullptr;
     uint64_t *d_part_am = nullptr;
     double *d_psum = nullptr;
-    int *d_pemin = nullptr;
-    uint32_t *d_pcount = nullptr, *d_pbad = nullptr, *d_plast_in = nullptr, *d_pfirst_out = nullptr;
     uint64_t *d_surv = nullptr;
     FullRow *d_full_row = nullptr;
     uint32_t *d_full_arrive = nullptr;
@@ -197,11 +195,6 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     if (e == hipSuccess) e = c->alloc(&c->d_part_max, fg * MAX_CHUNKS);
     if (e == hipSuccess) e = c->alloc(&c->d_part_am, fg * MAX_CHUNKS);
     if (e == hipSuccess) e = c->alloc(&c->d_psum, fg * MAX_CHUNKS);
-    if (e == hipSuccess) e = c->alloc(&c->d_pemin, fg * MAX_CHUNKS);
-    if (e == hipSuccess) e = c->alloc(&c->d_pcount, fg * MAX_CHUNKS);
-    if (e == hipSuccess) e = c->alloc(&c->d_pbad, fg * MAX_CHUNKS);
-    if (e == hipSuccess) e = c->alloc(&c->d_plast_in, fg * MAX_CHUNKS);
-    if (e == hipSuccess) e = c->alloc(&c->d_pfirst_out, fg * MAX_CHUNKS);
     if (e == hipSuccess) e = c->alloc(&c->d_surv, fg * SURV_CAP);
     if (e == hipSuccess) e = c->alloc(&c->d_full_row, fg);
     if (e == hipSuccess) e = c->alloc(&c->d_full_arrive, fg);
@@ -344,27 +337,15 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
         f.rows = ctx->d_full_rows + g0;
         f.chunks = std::max(1u, std::min(MAX_CHUNKS, (TARGET_WGS + ng - 1) / ng));
         f.chunks = std::min(f.chunks, std::max(1u, vocab / 4096));
-        FullScratch fs{ctx->d_keyA,     ctx->d_idA,      ctx->d_keyB,       ctx->d_idB,   ctx->d_probs,
-                       ctx->d_part_max, ctx->d_part_am,  ctx->d_psum,       ctx->d_pemin, ctx->d_pcount,
-                       ctx->d_pbad,     ctx->d_plast_in, ctx->d_pfirst_out, ctx->d_surv,  ctx->d_full_row,
-                       ctx->d_full_arrive};
+        FullScratch fs{ctx->d_keyA,    ctx->d_idA,     ctx->d_keyB, ctx->d_idB,     ctx->d_probs, ctx->d_part_max,
+                       ctx->d_part_am, ctx->d_psum,    ctx->d_surv, ctx->d_full_row, ctx->d_full_arrive};
         const dim3 cgrid(f.chunks, ng);
         const size_t pass_lds = k_full_pass_lds_bytes(vocab, f.chunks);
-        const size_t keys_lds = k_full_keys_lds_bytes(vocab, f.chunks);
-        if (vec) {
+        if (vec)
             hipLaunchKernelGGL(k_full_pass<true>, cgrid, dim3(FULL_THREADS), pass_lds, st, f, fs);
-            hipLaunchKernelGGL(k_full_keys<true>, cgrid, dim3(FULL_THREADS), keys_lds, st, f, fs);
-        } else {
+        else
             hipLaunchKernelGGL(k_full_pass<false>, cgrid, dim3(FULL_THREADS), pass_lds, st, f, fs);
-            hipLaunchKernelGGL(k_full_keys<false>, cgrid, dim3(FULL_THREADS), keys_lds, st, f, fs);
-        }
-        hipLaunchKernelGGL(k_full_sort, dim3(ng), dim3(SORT_THREADS), 0, st, f, fs);
-        hipLaunchKernelGGL(k_full_probs, cgrid, dim3(FULL_THREADS), 0, st, f, fs);
-        hipLaunchKernelGGL(k_full_tail, dim3(ng), dim3(REPLAY_THREADS), 0, st, f, fs);
-        // The draws, and (when the candidates are written) the writes, in one
-        // launch: the draw workgroups first.
-        const uint32_t finish_wgs = ng + (f.out_ids ? ng * f.chunks : 0u);
-        hipLaunchKernelGGL(k_full_finish, dim3(finish_wgs), dim3(REPLAY_THREADS), 0, st, f, fs, ng);
+        hipLaunchKernelGGL(k_full_rest, dim3(ng), dim3(REST_THREADS), 0, st, f, fs);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return hip_fail(e, "full-path kernels");
     }
@@ -430,7 +411,7 @@ int rl_top_probability_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t r
         hipLaunchKernelGGL(k_tp_sum<false>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
                            ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum, ctx->d_tp_small);
     }
-    hipLaunchKernelGGL(k_tp_final, dim3(rows), dim3(REPLAY_THREADS), 0, st, logits, stride, vocab, chunks,
+    hipLaunchKernelGGL(k_tp_final, dim3(rows), dim3(TP_FINAL_THREADS), 0, st, logits, stride, vocab, chunks,
                        ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum, ctx->d_tp_small, out_token, out_prob);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "top_probability kernels");

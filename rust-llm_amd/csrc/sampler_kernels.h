@@ -27,8 +27,6 @@ constexpr uint32_t KMAX = 64;     // largest top_k the stream path takes (one pe
 constexpr uint32_t UNROLL = 8;    // float4 loads per thread per tile
 constexpr uint32_t MAX_CHUNKS = 32;
 constexpr uint32_t FULL_THREADS = 256;
-constexpr uint32_t SORT_THREADS = 1024;
-constexpr uint32_t SORT_WAVES = SORT_THREADS / WAVE;
 constexpr uint32_t STAGE = 4096;  // elements staged in LDS per sequential block
 
 struct RowIO {

@@ -200,14 +200,16 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
     }
 }
 
-// grid (rows), REPLAY_THREADS: the token, and 1 / sum certified from the
+constexpr uint32_t TP_FINAL_THREADS = 512;  // 8 waves a row for the exact sum replay
+
+// grid (rows), TP_FINAL_THREADS: the token, and 1 / sum certified from the
 // chunk sums or from the replayed sequential sum.
-__global__ __launch_bounds__(REPLAY_THREADS) void k_tp_final(const float *logits, uint64_t stride, uint32_t vocab,
+__global__ __launch_bounds__(TP_FINAL_THREADS) void k_tp_final(const float *logits, uint64_t stride, uint32_t vocab,
                                                              uint32_t chunks, const uint64_t *part_am,
                                                              const uint32_t *part_nan, const double *part_sum,
                                                              const uint32_t *part_small, uint32_t *out_token,
                                                              float *out_prob) {
-    __shared__ SeqLds<REPLAY_THREADS> seq;
+    __shared__ SeqLds<TP_FINAL_THREADS> seq;
     __shared__ uint64_t exp_tab[32];
     const uint32_t row = blockIdx.x;
     uint64_t am;
@@ -248,7 +250,7 @@ __global__ __launch_bounds__(REPLAY_THREADS) void k_tp_final(const float *logits
         copy_exp_table((RL_LDS uint64_t *)exp_tab);
         const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab};
         double sum;
-        seq_replay<53, REPLAY_THREADS, SEQ_ITEMS>(
+        seq_replay<53, TP_FINAL_THREADS, SEQ_ITEMS>(
             [rowp](uint32_t j) { return ((const RL_GLB uint32_t *)rowp)[j]; },
             [best, etab](uint32_t bits) { return expf_libm_t(__uint_as_float(bits) - best, etab); }, vocab,
             NeverStop{}, &seq, &sum);

@@ -6,7 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "full_kernels.h"
+#include "full_rest.h"
+#include "top_probability.h"
 
 namespace {
 
@@ -44,8 +45,9 @@ int launch(const float *terms, const uint64_t *off, const uint32_t *n, const dou
 
 }  // namespace
 
-// shape 0: the library's (REPLAY_THREADS threads, SEQ_ITEMS terms each);
-// shape 1: 128 threads, 3 terms each. Every pointer is device memory; a
+// shape 0: the sampler's (REST_THREADS threads, SEQ_ITEMS terms each);
+// shape 1: 128 threads, 3 terms each; shape 2: top_probability's
+// (TP_FINAL_THREADS threads, SEQ_ITEMS terms each). Every pointer is device memory; a
 // case's terms are terms[off[c] .. off[c] + n[c]).
 extern "C" int seqsum_gpu_run(int precision, int shape, const float *terms, const uint64_t *off, const uint32_t *n,
                               const double *thr, const uint32_t *mode, uint32_t cases, uint32_t *out_idx,
@@ -54,12 +56,17 @@ extern "C" int seqsum_gpu_run(int precision, int shape, const float *terms, cons
     hipStream_t st = (hipStream_t)stream;
     if (shape == 0) {
         if (precision == 24)
-            return launch<24, rl::REPLAY_THREADS, rl::SEQ_ITEMS>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
+            return launch<24, rl::REST_THREADS, rl::SEQ_ITEMS>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
         if (precision == 53)
-            return launch<53, rl::REPLAY_THREADS, rl::SEQ_ITEMS>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
+            return launch<53, rl::REST_THREADS, rl::SEQ_ITEMS>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
     } else if (shape == 1) {
         if (precision == 24) return launch<24, 128, 3>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
         if (precision == 53) return launch<53, 128, 3>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
+    } else if (shape == 2) {
+        if (precision == 24)
+            return launch<24, rl::TP_FINAL_THREADS, rl::SEQ_ITEMS>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
+        if (precision == 53)
+            return launch<53, rl::TP_FINAL_THREADS, rl::SEQ_ITEMS>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
     }
     return -1;
 }

@@ -5,8 +5,8 @@ The reference's sums are sequential: f64 for the probability mass, the top-p
 cumulative sum and the normalising total (sample.rs:307-324, :342) and for
 top_probability (forward.rs:1678), f32 for the draw (sample.rs:349-356). The
 harness tests/native/seqsum_gpu.hip runs the device replay on arbitrary term
-arrays, one workgroup per case, with the library's workgroup shape and a
-second one (128 threads of 3 terms). Each case asks for the whole sum or for
+arrays, one workgroup per case, with the sampler's workgroup shape (1024
+threads), top_probability's (512) and a third one (128 threads of 3 terms). Each case asks for the whole sum or for
 the first partial sum >= or > a threshold (every partial sum, its neighbours,
 0 and -1); numpy's cumulative sums (sequential, in the terms' precision) give
 the expected index and value.
@@ -163,6 +163,6 @@ def run_cases(device, precision, shape, seed):
 
 
 @pytest.mark.parametrize("precision", [24, 53])
-@pytest.mark.parametrize("shape", [0, 1])
+@pytest.mark.parametrize("shape", [0, 1, 2])
 def test_replay_matches_sequential_loops(device, precision, shape):
     run_cases(device, precision, shape, seed=1000 + precision + shape)
