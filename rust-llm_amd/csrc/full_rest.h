@@ -39,7 +39,7 @@ struct RestLds {
         uint32_t wh[REST_WAVES][2][256];  // per-wave histograms of two digits
         struct {
             float stage[STAGE];
-            SeqLds<REST_THREADS> seq;
+            ChunkLds cr;
         } rep;
     } u;
     uint32_t hist[4][256];           // the row's digit histograms (digits flipped: 255 - d)
@@ -616,7 +616,9 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
     // the normalising total (:342-343) ----
     RL_LDS float *stage = L->u.rep.stage;
     RL_LDS uint32_t *stop = &L->sh_stop;
-    const auto term = [fp](uint32_t j) { return ((const RL_GLB float *)fp)[j]; };
+    const uint32_t *fpw = (const uint32_t *)fp;
+    const auto as_f32 = [](uint32_t b) { return __uint_as_float(b); };
+    RL_LDS ChunkLds *cr = &L->u.rep.cr;
     bool bad = false;
     int emin = 1 << 20;
     uint32_t count = 0, last_in = 0, first_out = 0xFFFFFFFFu;
@@ -653,19 +655,7 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
         double mass = 0.0;
         if (exact) {
             mass = tree_mass;
-        } else if (!bad) {
-            seq_replay<53, REST_THREADS, SEQ_ITEMS>(term, k, NeverStop{}, (SeqLds<REST_THREADS> *)&L->u.rep.seq, &mass);
-        } else {
-            staged_walk<REST_THREADS>(fp, k, stage, stop, [&](RL_LDS float *sv, uint32_t, uint32_t cnt) {
-                for (uint32_t i = 0; i < cnt; ++i) mass += (double)sv[i];
-                return false;
-            });
-            if (tid == 0) L->sh_d = mass;
-            __syncthreads();
-            mass = L->sh_d;
-        }
-        const double target = (double)s.top_p * mass;
-        if (exact) {
+            const double target = (double)s.top_p * mass;
             // The chunk where the running sum first reaches the target.
             double b = 0.0;
             uint32_t c = 0;
@@ -682,17 +672,35 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
                 sum_m = mass;
             }
         } else if (!bad) {
-            double at;
-            const uint32_t j = seq_replay<53, REST_THREADS, SEQ_ITEMS>(
-                term, k, [target](double c) { return c >= target; }, (SeqLds<REST_THREADS> *)&L->u.rep.seq, &at);
-            have_sum_m = true;
-            if (j < k) {
-                m = j + 1;
-                sum_m = at;
-            } else {
-                sum_m = mass;
+            // The mass, then the cut, through one call site of the replay
+            // (a target of +inf is never met by a finite sum).
+            double tgt = __builtin_inf();
+            for (uint32_t job = 0; job < 2; ++job) {
+                double at;
+                const uint32_t j =
+                    chunk_replay<53, REST_THREADS>(fpw, as_f32, k, [tgt](double c) { return c >= tgt; }, cr, &at);
+                if (job == 0) {
+                    mass = at;
+                    tgt = (double)s.top_p * mass;
+                } else {
+                    have_sum_m = true;
+                    if (j < k) {
+                        m = j + 1;
+                        sum_m = at;
+                    } else {
+                        sum_m = mass;
+                    }
+                }
             }
         } else {
+            staged_walk<REST_THREADS>(fp, k, stage, stop, [&](RL_LDS float *sv, uint32_t, uint32_t cnt) {
+                for (uint32_t i = 0; i < cnt; ++i) mass += (double)sv[i];
+                return false;
+            });
+            if (tid == 0) L->sh_d = mass;
+            __syncthreads();
+            mass = L->sh_d;
+            const double target = (double)s.top_p * mass;
             if (tid == 0) L->sh_m = k;
             __syncthreads();
             double cum = 0.0;
@@ -776,7 +784,7 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
         exact_first_reaching<REST_THREADS>(fp, 0, m, 0.0, __builtin_inf(), L->red_d, &L->sh_hit, &L->sh_hit_sum,
                                            &total);
     } else if (!bad) {
-        seq_replay<53, REST_THREADS, SEQ_ITEMS>(term, m, NeverStop{}, (SeqLds<REST_THREADS> *)&L->u.rep.seq, &total);
+        chunk_replay<53, REST_THREADS>(fpw, as_f32, m, [](double) { return false; }, cr, &total);
     } else {
         staged_walk<REST_THREADS>(fp, m, stage, stop, [&](RL_LDS float *sv, uint32_t, uint32_t cnt) {
             for (uint32_t i = 0; i < cnt; ++i) total += (double)sv[i];
@@ -797,10 +805,9 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
     uint32_t pick;
     if (!qbad) {
         double unused;
-        const uint32_t j = seq_replay<24, REST_THREADS, SEQ_ITEMS>(
-            [fp](uint32_t j) { return ((const RL_GLB uint32_t *)fp)[j]; },
-            [inv](uint32_t bits) { return __uint_as_float(bits) * inv; }, m, [u](double c) { return c > (double)u; },
-            (SeqLds<REST_THREADS> *)&L->u.rep.seq, &unused);
+        const uint32_t j = chunk_replay<24, REST_THREADS>(
+            fpw, [inv](uint32_t bits) { return __uint_as_float(bits) * inv; }, m,
+            [u](double c) { return c > (double)u; }, cr, &unused);
         pick = j < m ? j : m - 1;
     } else {
         if (tid == 0) L->sh_tok = m - 1;

@@ -345,7 +345,18 @@ __device__ __forceinline__ double wave_excl_f64(double v) {
     return lane == 0 ? 0.0 : e;
 }
 
-// Replays s = fl_P(s + x_j) for j = 0, 1, ... over the n terms
+// The workgroup's barrier, or (WAVE_ONLY) the wave's own LDS sync.
+template <bool WAVE_ONLY>
+__device__ __forceinline__ void replay_sync() {
+    if constexpr (WAVE_ONLY) {
+        wave_lds_sync();
+    } else {
+        __syncthreads();
+    }
+}
+
+// Replays s = fl_P(s + x_j) for j = 0, 1, ... from s = s0 (a P-bit value >= 0;
+// seq_replay starts from +0) over the n terms
 // x_j = term(fetch(j)) (finite, >= 0), in order, with the whole workgroup (NT
 // threads, ITEMS consecutive terms per thread per tile). fetch(j) returns the
 // raw 32 bits a term is made from and term turns them into the f32 term, so
@@ -355,7 +366,8 @@ __device__ __forceinline__ double wave_excl_f64(double v) {
 // true as the sum grows), or n; when it returns n, *sum is the sequential sum
 // of all n terms, and otherwise the partial sum at the returned index. Every
 // thread of the workgroup must call it with the same arguments; it contains
-// barriers.
+// barriers. With WAVE_ONLY (NT = 64) one wave runs it by itself: its syncs are
+// the wave's own, and the other waves of the workgroup take no part.
 //
 // Tiles are aligned to NT * ITEMS terms and the next tile is loaded while the
 // current one is reduced. A pass over (the rest of) a tile reduces, per wave,
@@ -367,14 +379,16 @@ __device__ __forceinline__ double wave_excl_f64(double v) {
 // Otherwise a scan locates the event: the first term whose sum meets pred, or
 // leaves the segment (added with the IEEE addition; the rest of the tile is
 // then processed again from registers under the new segment).
-template <int P, uint32_t NT, uint32_t ITEMS, class Fetch, class Term, class Pred>
-__device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t n, Pred pred, SeqLds<NT> *L, double *sum) {
+template <int P, uint32_t NT, uint32_t ITEMS, bool WAVE_ONLY, class Fetch, class Term, class Pred>
+__device__ __forceinline__ uint32_t seq_replay_from(Fetch fetch, Term term, uint32_t n, Pred pred, double s0,
+                                                    SeqLds<NT> *L, double *sum) {
+    static_assert(!WAVE_ONLY || NT == 64, "a wave-only replay is one wave");
     constexpr uint32_t TILE = NT * ITEMS;
     constexpr uint32_t NW = NT / 64;
-    const uint32_t tid = threadIdx.x, lane = __lane_id(), wave = tid / 64;
-    double s = 0.0;
-    bool zero = true;
-    SumSeg g{0, 0, 0};
+    const uint32_t tid = WAVE_ONLY ? __lane_id() : threadIdx.x, lane = __lane_id(), wave = tid / 64;
+    double s = s0;
+    bool zero = !(s0 > 0.0);
+    SumSeg g = zero ? SumSeg{0, 0, 0} : seg_of<P>(s0);
     uint32_t pos = 0;  // the next term to add
     uint32_t set = 0;  // the LDS record set this pass writes
     // Whether passes still test for a tile without rounding: once a tile
@@ -383,9 +397,10 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
     bool try_exact = true;
     uint32_t cur = 0xFFFFFFFFu, nxt = 0xFFFFFFFFu;  // bases of the tiles in xb and nb
     uint32_t xb[ITEMS], nb[ITEMS];  // terms of the current tile, raw bits of the next
-    if (n > 0 && pred(0.0)) {
-        // A predicate that +0 already meets is met by the first term's sum.
-        *sum = add_p<P>(0.0, term(fetch(0)));
+    if (n > 0 && pred(s0)) {
+        // A predicate that the start already meets is met by the first term's
+        // sum (the sum only grows).
+        *sum = add_p<P>(s0, term(fetch(0)));
         return 0;
     }
     while (pos < n) {
@@ -414,7 +429,7 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
         if (zero) {
             // The sum stays +0 up to the first nonzero term.
             if (tid == 0) L->nonzero = 0xFFFFFFFFu;
-            __syncthreads();
+            replay_sync<WAVE_ONLY>();
             uint32_t my_nz = 0xFFFFFFFFu, x_nz = 0;
 #pragma unroll
             for (uint32_t i = 0; i < ITEMS; ++i) {
@@ -424,17 +439,17 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
                 }
             }
             if (my_nz != 0xFFFFFFFFu) atomicMin(&L->nonzero, my_nz);
-            __syncthreads();
+            replay_sync<WAVE_ONLY>();
             const uint32_t jz = L->nonzero;
-            __syncthreads();
+            replay_sync<WAVE_ONLY>();
             if (jz == 0xFFFFFFFFu) {
                 pos = base + TILE;
                 continue;
             }
             if (my_nz == jz) L->s_new = (double)__uint_as_float(x_nz);
-            __syncthreads();
+            replay_sync<WAVE_ONLY>();
             s = L->s_new;
-            __syncthreads();
+            replay_sync<WAVE_ONLY>();
             zero = false;
             if (pred(s)) {
                 *sum = s;
@@ -493,7 +508,7 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
             L->cross = 0xFFFFFFFFu;
             L->hit = 0xFFFFFFFFu;
         }
-        __syncthreads();
+        replay_sync<WAVE_ONLY>();
         // The waves in order, from the segment's parity: the tile's steps, the
         // parity entering this wave and the steps and f64 sum before it. Lane
         // w reads wave w's record; the combination reads those lanes into
@@ -559,12 +574,12 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
                 }
             }
             if (my_hit != 0xFFFFFFFFu) atomicMin(&L->hit, my_hit);
-            __syncthreads();
+            replay_sync<WAVE_ONLY>();
             const uint32_t hit = L->hit;
             if (my_hit == hit) L->s_new = v_hit;
-            __syncthreads();
+            replay_sync<WAVE_ONLY>();
             *sum = L->s_new;
-            __syncthreads();
+            replay_sync<WAVE_ONLY>();
             return hit;
         }
         try_exact = false;
@@ -610,13 +625,13 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
         }
         if (my_cross != 0xFFFFFFFFu) atomicMin(&L->cross, my_cross);
         if (my_hit != 0xFFFFFFFFu) atomicMin(&L->hit, my_hit);
-        __syncthreads();
+        replay_sync<WAVE_ONLY>();
         const uint32_t cross = L->cross, hit = L->hit;
         if (hit < cross) {
             if (my_hit == hit) L->s_new = scaled(g.n + (uint64_t)I_hit, g.uexp);
-            __syncthreads();
+            replay_sync<WAVE_ONLY>();
             *sum = L->s_new;
-            __syncthreads();
+            replay_sync<WAVE_ONLY>();
             return hit;
         }
         if (cross == 0xFFFFFFFFu) {
@@ -629,9 +644,9 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
             continue;
         }
         if (my_cross == cross) L->s_new = add_p<P>(scaled(g.n + (uint64_t)I_cross, g.uexp), __uint_as_float(x_cross));
-        __syncthreads();
+        replay_sync<WAVE_ONLY>();
         s = L->s_new;
-        __syncthreads();
+        replay_sync<WAVE_ONLY>();
         if (pred(s)) {
             *sum = s;
             return cross;
@@ -642,11 +657,314 @@ __device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t 
     *sum = s;
     return n;
 }
+template <int P, uint32_t NT, uint32_t ITEMS, class Fetch, class Term, class Pred>
+__device__ __forceinline__ uint32_t seq_replay(Fetch fetch, Term term, uint32_t n, Pred pred, SeqLds<NT> *L, double *sum) {
+    return seq_replay_from<P, NT, ITEMS, false>(fetch, term, n, pred, 0.0, L, sum);
+}
 // The same over terms that need no transformation: load(j) is the f32 term.
 template <int P, uint32_t NT, uint32_t ITEMS, class Load, class Pred>
 __device__ __forceinline__ uint32_t seq_replay(Load load, uint32_t n, Pred pred, SeqLds<NT> *L, double *sum) {
     return seq_replay<P, NT, ITEMS>([load](uint32_t j) { return __float_as_uint(load(j)); },
                                     [](uint32_t bits) { return __uint_as_float(bits); }, n, pred, L, sum);
+}
+
+// ------------------------------------------------------ chunked replay ---
+// The same replay for long sums with a workgroup of 1024 threads, in rounds
+// of CR_ROUND chunks of CR_CH terms. A round's terms are staged in LDS by
+// one load per thread (the next round's loads are issued before this round's
+// chain, so they are in flight while it runs); each half wave takes a chunk
+// (CR_ITEMS consecutive terms a lane) and computes its f64 sum, from which
+// every chunk's start is predicted; each half wave then counts its chunk's
+// steps on the grid of the binade its start is predicted in, ties resolved
+// but the first (the record seq_replay keeps per wave). One wave chains the
+// records in order from the exact running sum: a record applies when the sum
+// is on its grid, and the chunk then has no event if its end stays in the
+// binade and fails pred (the partial sums only grow); any other chunk (the
+// first nonzero term, a binade left, pred met, a start off the predicted
+// grid) is added by that wave alone from LDS (wave_walk). A long sum thus
+// costs a wave pass per binade crossing plus a few barriers per round, not a
+// workgroup pass per tile.
+constexpr uint32_t CR_ITEMS = 8;              // consecutive terms per lane
+constexpr uint32_t CR_CH = 32 * CR_ITEMS;     // terms per chunk (half a wave's)
+constexpr uint32_t CR_ROUND = 32;             // chunks per round: two a wave
+constexpr uint32_t CR_TERMS = CR_ROUND * CR_CH;
+
+struct ChunkLds {
+    __attribute__((aligned(16))) uint32_t terms[CR_TERMS];  // the round's terms
+    double fsum[CR_ROUND];   // f64 sum of each chunk's terms (the prediction)
+    double base[CR_ROUND];   // its steps, every tie resolved but the first (capped)
+    uint32_t bits[CR_ROUND]; // bit 0: a tie; bit 1: the first tie's constant; bit 2: par
+    int32_t uexp[CR_ROUND];  // the grid its steps count; INT32_MIN: no record
+    double s;                // the running sum at the end of the round
+    uint32_t hit;            // the first index meeting pred, or n
+};
+
+// Sum of v over the 32 lanes of this half wave (every lane gets it).
+__device__ __forceinline__ double half_total_f64(double v) {
+    v += lane_xor_f64<1>(v);
+    v += lane_xor_f64<2>(v);
+    v += lane_xor_f64<4>(v);
+    v += lane_xor_f64<8>(v);
+    v += lane_xor_f64<16>(v);
+    return v;
+}
+
+// Inclusive scan of v over the wave's lanes.
+__device__ __forceinline__ double wave_incl_f64(double v) {
+    const uint32_t lane = __lane_id();
+    for (int d = 1; d < 64; d <<= 1) {
+        const double o = f64_from_bits(shfl_up_u64(f64_bits(v), d));
+        if (lane >= (uint32_t)d) v += o;
+    }
+    return v;
+}
+
+__device__ __forceinline__ double read_lane_f64(double v, uint32_t l) {
+    const uint64_t b = f64_bits(v);
+    return f64_from_bits(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), (int)l) << 32) |
+                         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, (int)l));
+}
+
+// One wave adds the len (<= 64 * WK) terms t[0..len) to the running sum s
+// (a P-bit value >= 0) in order, every lane the same: lane l holds terms
+// l * WK .. l * WK + WK - 1. Per event (the sum leaving its binade, or pred
+// becoming true) one pass: every lane counts its terms' steps on the
+// segment's grid with the ties resolved (StepRun, parity_in), an exclusive
+// scan gives each lane's start, a ballot finds the first lane whose terms
+// hold the event, and that lane's terms are stepped through one by one (the
+// term that leaves the binade is added with the IEEE addition, and the
+// terms after it are counted again on the new grid). Returns the index of
+// the first term whose partial sum meets pred, with that sum in s, or len
+// with the total in s.
+template <int P, uint32_t WK, class Pred>
+__device__ __forceinline__ uint32_t wave_walk(RL_LDS const uint32_t *t, uint32_t len, Pred pred, double &s) {
+    const uint32_t lane = __lane_id();
+    uint32_t x[WK];
+#pragma unroll
+    for (uint32_t i = 0; i < WK; ++i) x[i] = lane * WK + i < len ? t[lane * WK + i] : 0u;
+    uint32_t pos = 0;  // the next term to add
+    for (;;) {
+        if (!(s > 0.0)) {
+            // The sum stays +0 up to the first nonzero term, which it then equals.
+            uint32_t jz = 0xFFFFFFFFu;
+#pragma unroll
+            for (uint32_t i = 0; i < WK; ++i)
+                if (jz == 0xFFFFFFFFu && lane * WK + i >= pos && (x[i] & 0x7FFFFFFFu) != 0) jz = lane * WK + i;
+            const uint64_t nz = __ballot(jz != 0xFFFFFFFFu);
+            if (nz == 0) return len;
+            const uint32_t l = (uint32_t)__builtin_ctzll(nz);
+            const uint32_t j = (uint32_t)__builtin_amdgcn_readlane((int)jz, (int)l);
+            uint32_t xb = 0;
+#pragma unroll
+            for (uint32_t i = 0; i < WK; ++i)
+                if (j - l * WK == i) xb = (uint32_t)__builtin_amdgcn_readlane((int)x[i], (int)l);
+            s = (double)__uint_as_float(xb);
+            if (pred(s)) return j;
+            pos = j + 1;
+            continue;
+        }
+        const SumSeg g = seg_of<P>(s);
+        const double scale = mul_pow2(1.0, -g.uexp);
+        StepRun r = run_identity();
+#pragma unroll
+        for (uint32_t i = 0; i < WK; ++i) run_add(r, lane * WK + i >= pos ? x[i] : 0u, scale);
+        r.base = r.base < STEP_CAP ? r.base : STEP_CAP;
+        const uint64_t T = __ballot(r.tie != 0), O = __ballot(run_par(r) != 0);
+        uint32_t dep;
+        const uint32_t k = parity_in(T, O, lane, &dep);
+        const uint32_t pl = dep ? ((uint32_t)(g.n & 1u) ^ k) : k;  // the parity entering this lane's terms
+        const double mine = r.base + (r.tie ? (double)((pl ^ r.c) & 1u) : 0.0);
+        const double before = wave_excl_f64(mine);  // exact below the room, where it is used
+        const double room = (double)(g.lim - g.n);
+        const double upto = before + mine;
+        const bool ev = !(upto < room) || pred(scaled(g.n + (uint64_t)upto, g.uexp));
+        const uint64_t evm = __ballot(ev);
+        if (evm == 0) {
+            s = scaled(g.n + (uint64_t)read_lane_f64(upto, 63), g.uexp);
+            return len;
+        }
+        // The first lane holding an event steps through its terms.
+        const uint32_t l = (uint32_t)__builtin_ctzll(evm);
+        uint64_t nn = g.n + (uint64_t)read_lane_f64(before, l);
+        uint32_t par = (uint32_t)(nn & 1u);
+        bool crossed = false;
+#pragma unroll
+        for (uint32_t i = 0; i < WK; ++i) {
+            const uint32_t j = l * WK + i;
+            if (crossed || j < pos || j >= len) continue;
+            const uint32_t xb = (uint32_t)__builtin_amdgcn_readlane((int)x[i], (int)l);
+            bool tie;
+            const double q = step_of(__uint_as_float(xb), scale, &tie);
+            const uint32_t pq = parity_of(q);
+            const double step = tie ? q + (double)(par ^ pq) : q;
+            if ((double)nn + step >= (double)g.lim) {
+                // This term leaves the binade: the IEEE addition, then a new
+                // segment from the next term.
+                s = add_p<P>(scaled(nn, g.uexp), __uint_as_float(xb));
+                if (pred(s)) return j;
+                pos = j + 1;
+                crossed = true;
+                continue;
+            }
+            nn += (uint64_t)step;
+            par = tie ? 0u : (par ^ pq);
+            if (pred(scaled(nn, g.uexp))) {
+                s = scaled(nn, g.uexp);
+                return j;
+            }
+        }
+        if (!crossed) {  // not reached: the lane's event is in its terms
+            s = scaled(nn, g.uexp);
+            pos = (l + 1) * WK;
+        }
+    }
+}
+
+// Returns as seq_replay does, for the terms x_j = term(src[j]) (raw 32-bit
+// words), j < n; every thread of the workgroup (1024) calls it.
+template <int P, uint32_t NT, class Term, class Pred>
+__device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term, uint32_t n, Pred pred,
+                                                 RL_LDS ChunkLds *L, double *sum) {
+    static_assert(NT / 64 * 2 == CR_ROUND, "two chunks a wave");
+    const uint32_t tid = threadIdx.x, lane = __lane_id(), wave = tid / 64;
+    const uint32_t half = lane >> 5, hl = lane & 31u, my = 2 * wave + half;  // this half wave's chunk
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, (int)(n * 4u), 0x00020000);
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    // This thread's CR_ITEMS raw words of round r (zeros past n: they add
+    // nothing).
+    u32x4 xr[CR_ITEMS / 4];
+    auto fetch_round = [&](uint32_t r) {
+#pragma unroll
+        for (uint32_t q = 0; q < CR_ITEMS / 4; ++q)
+            xr[q] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 4u * (r * CR_TERMS + tid * CR_ITEMS) + 16u * q, 0, 0));
+    };
+    const uint32_t rounds = (uint32_t)(((uint64_t)n + CR_TERMS - 1) / CR_TERMS);
+    const uint32_t chunks = (uint32_t)(((uint64_t)n + CR_CH - 1) / CR_CH);
+    double s = 0.0;
+    uint32_t hit = n;
+    if (n > 0 && pred(0.0)) {
+        // A predicate that +0 already meets is met by the first term's sum.
+        *sum = add_p<P>(0.0, term(__builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 0)));
+        return 0;
+    }
+    fetch_round(0);
+    for (uint32_t r = 0; r < rounds && hit == n; ++r) {
+        // Stage the terms; each chunk's f64 sum.
+        uint32_t x[CR_ITEMS];
+        double fs = 0.0;
+#pragma unroll
+        for (uint32_t q = 0; q < CR_ITEMS / 4; ++q)
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) {
+                x[4 * q + i] = __float_as_uint(term(xr[q][i]));
+                fs += (double)__uint_as_float(x[4 * q + i]);
+            }
+#pragma unroll
+        for (uint32_t q = 0; q < CR_ITEMS / 4; ++q)
+            *(RL_LDS u32x4 *)&L->terms[tid * CR_ITEMS + 4 * q] = u32x4{x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
+        fs = half_total_f64(fs);
+        if (hl == 0) L->fsum[my] = fs;
+        fetch_round(r + 1);  // in flight through the rest of the round
+        __syncthreads();
+        // This chunk's predicted start: s plus the sums of the chunks before.
+        const double pre = wave_excl_f64(lane < CR_ROUND ? L->fsum[lane] : 0.0);
+        const double start =
+            s + f64_from_bits(((uint64_t)(uint32_t)__shfl((int)(uint32_t)(f64_bits(pre) >> 32), (int)my) << 32) |
+                              (uint32_t)__shfl((int)(uint32_t)f64_bits(pre), (int)my));
+        // The chunk's record on that start's grid.
+        const bool rec = start > 0.0;
+        const int32_t ux = rec ? seg_of<P>(start).uexp : INT32_MIN;
+        const double scale = rec ? mul_pow2(1.0, -ux) : 1.0;
+        StepRun rr = run_identity();
+#pragma unroll
+        for (uint32_t i = 0; i < CR_ITEMS; ++i) run_add(rr, x[i], scale);
+        rr.base = rr.base < STEP_CAP ? rr.base : STEP_CAP;
+        const uint64_t Tw = __ballot(rr.tie != 0), Ow = __ballot(run_par(rr) != 0);
+        const uint64_t T = half ? (Tw >> 32) : (Tw & 0xFFFFFFFFull);
+        const uint64_t O = half ? (Ow >> 32) : (Ow & 0xFFFFFFFFull);
+        uint32_t dep;
+        const uint32_t k = parity_in(T, O, hl, &dep);
+        const double wb = half_total_f64(rr.base + ((rr.tie && !dep) ? (double)((k ^ rr.c) & 1u) : 0.0));
+        uint32_t bits;
+        const uint32_t ft = T != 0 ? (uint32_t)__builtin_ctzll(T) : 0u;
+        const uint32_t cf = (uint32_t)__shfl((int)rr.c, (int)(half * 32 + ft));
+        if (T != 0) {
+            uint32_t d0, d1;
+            const uint32_t kf = parity_in(T, O, ft, &d0);
+            const uint32_t po = parity_in(T, O, 32, &d1);
+            bits = 1u | (((kf ^ cf) & 1u) << 1) | (po << 2);
+        } else {
+            bits = (popc64(O) & 1u) << 2;
+        }
+        if (hl == 0) {
+            L->uexp[my] = ux;
+            L->base[my] = wb < STEP_CAP ? wb : STEP_CAP;
+            L->bits[my] = bits;
+        }
+        __syncthreads();
+        // The chain, on wave 0; lane c holds chunk c's record. From the
+        // current chunk on, the chunks on the sum's grid without a tie add
+        // their steps (a scan); the first one whose end leaves the binade or
+        // meets pred, or whose record does not apply, stops the run, and is
+        // added by wave_walk (or by its record, when only a tie stopped it).
+        if (wave == 0) {
+            const uint32_t nr = min(CR_ROUND, chunks - r * CR_ROUND);
+            const bool lr = lane < nr;
+            const int32_t rux = lr ? L->uexp[lane] : INT32_MIN;
+            const uint32_t rbits = lr ? L->bits[lane] : 0u;
+            const double rbase = lr ? L->base[lane] : 0.0;
+            uint32_t c = 0;
+            while (c < nr) {
+                if (s > 0.0) {
+                    const SumSeg g = seg_of<P>(s);
+                    const double room = (double)(g.lim - g.n);
+                    const bool ok = lane >= c && lr && rux == g.uexp && !(rbits & 1u);
+                    const double incl = wave_incl_f64(ok ? rbase : 0.0);
+                    const bool good = ok && incl < room && !pred(scaled(g.n + (uint64_t)incl, g.uexp));
+                    const uint64_t stopm = __ballot(lane >= c && lr && !good);
+                    const uint32_t f = stopm ? (uint32_t)__builtin_ctzll(stopm) : nr;
+                    if (f > c) {
+                        s = scaled(g.n + (uint64_t)read_lane_f64(incl, f - 1), g.uexp);
+                        c = f;
+                        continue;
+                    }
+                    if (__builtin_amdgcn_readlane(rux, (int)c) == g.uexp) {
+                        // Only a tie stopped it: the record with the parity.
+                        const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)rbits, (int)c);
+                        const double inc = read_lane_f64(rbase, c) +
+                                           ((b & 1u) ? (double)(((uint32_t)(g.n & 1u) ^ (b >> 1)) & 1u) : 0.0);
+                        if (inc < room) {
+                            const double e = scaled(g.n + (uint64_t)inc, g.uexp);
+                            if (!pred(e)) {
+                                s = e;
+                                ++c;
+                                continue;
+                            }
+                        }
+                    }
+                }
+                const uint32_t start_j = (r * CR_ROUND + c) * CR_CH;
+                const uint32_t len = min(CR_CH, n - start_j);
+                const uint32_t j = wave_walk<P, CR_CH / 64>(&L->terms[c * CR_CH], len, pred, s);
+                if (j < len) {
+                    hit = start_j + j;
+                    break;
+                }
+                ++c;
+            }
+            if (lane == 0) {
+                L->s = s;
+                L->hit = hit;
+            }
+        }
+        __syncthreads();
+        s = L->s;
+        hit = L->hit;
+    }
+    *sum = s;
+    return hit;
 }
 #endif  // __HIPCC__
 

@@ -35,6 +35,26 @@ __global__ __launch_bounds__(NT) void k_seqsum_cases(const float *terms, const u
     }
 }
 
+// The chunked replay (rl::chunk_replay), one workgroup of REST_THREADS per case.
+template <int P>
+__global__ __launch_bounds__(rl::REST_THREADS) void k_chunk_cases(const float *terms, const uint64_t *off,
+                                                                  const uint32_t *n, const double *thr,
+                                                                  const uint32_t *mode, uint32_t *out_idx,
+                                                                  double *out_sum) {
+    __shared__ rl::ChunkLds cr_;
+    RL_LDS rl::ChunkLds *cr = (RL_LDS rl::ChunkLds *)&cr_;
+    const uint32_t c = blockIdx.x;
+    const uint32_t *x = (const uint32_t *)(terms + off[c]);
+    const CasePred pred{thr[c], mode[c]};
+    double sum = -1.0;
+    const uint32_t idx = rl::chunk_replay<P, rl::REST_THREADS>(
+        x, [](uint32_t b) { return __uint_as_float(b); }, n[c], pred, cr, &sum);
+    if (threadIdx.x == 0) {
+        out_idx[c] = idx;
+        out_sum[c] = sum;
+    }
+}
+
 template <int P, uint32_t NT, uint32_t ITEMS>
 int launch(const float *terms, const uint64_t *off, const uint32_t *n, const double *thr, const uint32_t *mode,
            uint32_t cases, uint32_t *out_idx, double *out_sum, hipStream_t st) {
@@ -45,9 +65,10 @@ int launch(const float *terms, const uint64_t *off, const uint32_t *n, const dou
 
 }  // namespace
 
-// shape 0: the sampler's (REST_THREADS threads, SEQ_ITEMS terms each);
-// shape 1: 128 threads, 3 terms each; shape 2: top_probability's
-// (TP_FINAL_THREADS threads, SEQ_ITEMS terms each). Every pointer is device memory; a
+// shape 0: REST_THREADS threads, SEQ_ITEMS terms each; shape 1: 128
+// threads, 3 terms each; shape 2: top_probability's (TP_FINAL_THREADS
+// threads, SEQ_ITEMS terms each); shape 3: the chunked replay the sampler
+// uses (REST_THREADS threads). Every pointer is device memory; a
 // case's terms are terms[off[c] .. off[c] + n[c]).
 extern "C" int seqsum_gpu_run(int precision, int shape, const float *terms, const uint64_t *off, const uint32_t *n,
                               const double *thr, const uint32_t *mode, uint32_t cases, uint32_t *out_idx,
@@ -62,6 +83,17 @@ extern "C" int seqsum_gpu_run(int precision, int shape, const float *terms, cons
     } else if (shape == 1) {
         if (precision == 24) return launch<24, 128, 3>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
         if (precision == 53) return launch<53, 128, 3>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
+    } else if (shape == 3) {
+        if (precision == 24) {
+            hipLaunchKernelGGL(k_chunk_cases<24>, dim3(cases), dim3(rl::REST_THREADS), 0, st, terms, off, n, thr, mode,
+                               out_idx, out_sum);
+            return (int)hipGetLastError();
+        }
+        if (precision == 53) {
+            hipLaunchKernelGGL(k_chunk_cases<53>, dim3(cases), dim3(rl::REST_THREADS), 0, st, terms, off, n, thr, mode,
+                               out_idx, out_sum);
+            return (int)hipGetLastError();
+        }
     } else if (shape == 2) {
         if (precision == 24)
             return launch<24, rl::TP_FINAL_THREADS, rl::SEQ_ITEMS>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);

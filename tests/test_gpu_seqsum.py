@@ -5,8 +5,10 @@ The reference's sums are sequential: f64 for the probability mass, the top-p
 cumulative sum and the normalising total (sample.rs:307-324, :342) and for
 top_probability (forward.rs:1678), f32 for the draw (sample.rs:349-356). The
 harness tests/native/seqsum_gpu.hip runs the device replay on arbitrary term
-arrays, one workgroup per case, with the sampler's workgroup shape (1024
-threads), top_probability's (512) and a third one (128 threads of 3 terms). Each case asks for the whole sum or for
+arrays, one workgroup per case, with 1024 threads, top_probability's shape
+(512), a third one (128 threads of 3 terms), and the chunked replay the
+sampler uses (chunk summaries chained by one wave, which replays the chunks
+holding a binade crossing or the event term by term). Each case asks for the whole sum or for
 the first partial sum >= or > a threshold (every partial sum, its neighbours,
 0 and -1); numpy's cumulative sums (sequential, in the terms' precision) give
 the expected index and value.
@@ -97,6 +99,10 @@ def term_arrays(seed):
         0x32800000, 0x25D00000, 0x3D600000, 0x3B000000, 0x37D00000, 0x37F00000, 0x37000000, 0x2E200000,
         0x2D800000, 0x2E500000, 0x34200000, 0x3C500000, 0x2A400000, 0x2FA00000, 0x3BD00000, 0x36300000],
         np.uint32).view(np.float32))
+    # A sampler draw's terms: 150 000 near-equal probabilities normalised
+    # to sum to about 1, descending (the running f32 sum crosses 17 binades).
+    q = np.sort((0.9 + 0.1 * g.random(150000)) / 142500.0)[::-1].astype(np.float32)
+    out.append(q)
     # Ties-heavy rows long enough for many tiles, and a long constant run.
     out.append(np.ldexp(2.0 * g.integers(0, 64, 60000) + 1.0, -24).astype(np.float32))
     out.append(np.full(100000, np.float32(3.0 / 1024.0)))
@@ -163,6 +169,6 @@ def run_cases(device, precision, shape, seed):
 
 
 @pytest.mark.parametrize("precision", [24, 53])
-@pytest.mark.parametrize("shape", [0, 1, 2])
+@pytest.mark.parametrize("shape", [0, 1, 2, 3])
 def test_replay_matches_sequential_loops(device, precision, shape):
     run_cases(device, precision, shape, seed=1000 + precision + shape)
