@@ -76,7 +76,7 @@ typedef struct rl_sampler_ctx rl_sampler_ctx;
 /* Allocates every device buffer for up to `max_rows` logit rows of `vocab`
  * entries and windows of up to `max_window` token ids. Replaces the allocation
  * half of Sampler::new (sample.rs:156-172). `device` is a HIP device index.
- * max_window must be <= 2048. */
+ * max_window must be <= 2048 and vocab <= 2^21 (2 097 152). */
 int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t max_window,
                       rl_sampler_ctx **out);
 

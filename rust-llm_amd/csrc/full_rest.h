@@ -27,7 +27,7 @@ constexpr uint32_t REST_SEG = WAVE * REST_ITEMS;           // a wave's contiguou
 constexpr uint32_t HIST_ITEMS = 12;                        // loads per thread per histogram step
 constexpr uint32_t HIST_STEP = REST_THREADS * HIST_ITEMS;  // elements per histogram step
 constexpr uint32_t STAT_CHUNKS = 64;                       // most chunks of the candidate list's sums
-constexpr uint32_t STAT_MIN = 2048;                        // fewest candidates per chunk (but one chunk)
+constexpr uint32_t STAT_MIN_LOG = 11;                      // chunks of at least 2^11 candidates
 static_assert(HIST_STEP >= REST_TILE, "the window bitmap covers a tile");
 
 struct RestLds {
@@ -486,6 +486,14 @@ __device__ __forceinline__ void rest_direct(RL_LDS RestLds *L, const RestRow &r,
     }
 }
 
+// The chunk size of the candidate list's sums for k candidates: a power of
+// two, at least 2^STAT_MIN_LOG, and at most STAT_CHUNKS chunks.
+__device__ __forceinline__ uint32_t stat_shift(uint32_t k) {
+    uint32_t sh = STAT_MIN_LOG;
+    while (((uint64_t)k + (1ull << sh) - 1) >> sh > STAT_CHUNKS) ++sh;
+    return sh;
+}
+
 // grid (slots), REST_THREADS: the rows k_full_pass left (done == 0).
 __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch f) {
     __shared__ RestLds L_;
@@ -558,56 +566,65 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
     }
     __syncthreads();
 
-    // ---- per-chunk sums of the candidate list, one wave a chunk ----
-    const uint32_t CS = max(1u, min(STAT_CHUNKS, k / STAT_MIN));
-    for (uint32_t c = wave; c < CS; c += REST_WAVES) {
-        const uint32_t j0 = chunk_lo(k, c, CS), j1 = chunk_lo(k, c + 1, CS);
-        double sum = 0.0;
-        int emin = 1 << 20;
-        uint32_t count = 0, bad = 0, last_in = 0, first_out = 0xFFFFFFFFu;
-        constexpr uint32_t SU = 8;
-        for (uint32_t b = j0; b < j1; b += WAVE * SU) {
-            float pv[SU];
+    // ---- per-chunk sums of the candidate list, one wave a chunk at a time:
+    // each lane's share of a chunk (32 consecutive p) in eight 16-byte loads,
+    // all in flight together ----
+    const uint32_t SH = stat_shift(k);
+    const uint32_t CS = (uint32_t)(((uint64_t)k + (1ull << SH) - 1) >> SH);  // chunks of the candidate list
+    auto chunk_start = [&](uint32_t c) { return min(c << SH, k); };
+    {
+        constexpr uint32_t SL = 32;  // consecutive p per lane per step
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        const __amdgpu_buffer_rsrc_t rp = words_rsrc(fp, k);
+        for (uint32_t c = wave; c < CS; c += REST_WAVES) {
+            const uint32_t j0 = chunk_start(c), j1 = chunk_start(c + 1);
+            double sum = 0.0;
+            int emin = 1 << 20;
+            uint32_t count = 0, bad = 0, last_in = 0, first_out = 0xFFFFFFFFu;
+            for (uint32_t b = j0; b < j1; b += WAVE * SL) {
+                const uint32_t jl = b + lane * SL;
+                u32x4 v[SL / 4];
 #pragma unroll
-            for (uint32_t u = 0; u < SU; ++u) {
-                const uint32_t j = b + u * WAVE + lane;
-                pv[u] = ((const RL_GLB float *)fp)[j < j1 ? j : j1 - 1];
-            }
+                for (uint32_t q = 0; q < SL / 4; ++q)
+                    v[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, 4u * jl + 16u * q, 0, 0));
 #pragma unroll
-            for (uint32_t u = 0; u < SU; ++u) {
-                const uint32_t j = b + u * WAVE + lane;
-                if (j < j1) {
-                    const float p = pv[u];
-                    if (!(p <= 3.40282347e38f)) {
-                        bad = 1;  // NaN or +inf
-                    } else if (p > 0.0f) {
-                        emin = min(emin, f32_exponent(p));
+                for (uint32_t q = 0; q < SL / 4; ++q)
+#pragma unroll
+                    for (uint32_t i = 0; i < 4; ++i) {
+                        const uint32_t j = jl + 4 * q + i;
+                        if (j < j1) {
+                            const float p = __uint_as_float(v[q][i]);
+                            if (!(p <= 3.40282347e38f)) {
+                                bad = 1;  // NaN or +inf
+                            } else if (p > 0.0f) {
+                                emin = min(emin, f32_exponent(p));
+                            }
+                            sum += (double)p;
+                            if (p >= s.min_p) {
+                                ++count;
+                                last_in = max(last_in, j + 1);
+                            } else {
+                                first_out = min(first_out, j);
+                            }
+                        }
                     }
-                    sum += (double)p;
-                    if (p >= s.min_p) {
-                        ++count;
-                        last_in = max(last_in, j + 1);
-                    } else {
-                        first_out = min(first_out, j);
-                    }
-                }
             }
-        }
-        for (int m = 32; m >= 1; m >>= 1) {
-            sum += __shfl_xor(sum, m);
-            emin = min(emin, __shfl_xor(emin, m));
-            count += (uint32_t)__shfl_xor((int)count, m);
-            bad |= (uint32_t)__shfl_xor((int)bad, m);
-            last_in = max(last_in, (uint32_t)__shfl_xor((int)last_in, m));
-            first_out = min(first_out, (uint32_t)__shfl_xor((int)first_out, m));
-        }
-        if (lane == 0) {
-            L->csum[c] = sum;
-            L->cemin[c] = emin;
-            L->ccount[c] = count;
-            L->cbad[c] = bad;
-            L->clast_in[c] = last_in;
-            L->cfirst_out[c] = first_out;
+            sum = wave_total_f64(sum);
+            emin = wave_min_i32(emin);
+            for (int m = 32; m >= 1; m >>= 1) {
+                count += (uint32_t)__shfl_xor((int)count, m);
+                bad |= (uint32_t)__shfl_xor((int)bad, m);
+                last_in = max(last_in, (uint32_t)__shfl_xor((int)last_in, m));
+                first_out = min(first_out, (uint32_t)__shfl_xor((int)first_out, m));
+            }
+            if (lane == 0) {
+                L->csum[c] = sum;
+                L->cemin[c] = emin;
+                L->ccount[c] = count;
+                L->cbad[c] = bad;
+                L->clast_in[c] = last_in;
+                L->cfirst_out[c] = first_out;
+            }
         }
     }
     __syncthreads();
@@ -635,15 +652,17 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
     const bool surv_prefix = last_in <= first_out;
     // Every partial sum exact: all p are multiples of 2^(emin-23), the mass is
     // below 2^53 of those steps. Then the chunk sums are the exact sums too.
-    const bool exact = !bad && (emin > 1000 || tree_mass < mul_pow2(1.0, 30 + emin));
+    // (The margin keeps a mass rounded below the bound from passing for one
+    // that is not.)
+    const bool exact = !bad && (emin > 1000 || tree_mass < mul_pow2(1.0 - 0x1p-30, 30 + emin));
     // The exact sum of p[0..n), from the chunk sums and one partial chunk.
     auto exact_prefix = [&](uint32_t n) {
         double b = 0.0;
         uint32_t c = 0;
-        while (c < CS && chunk_lo(k, c + 1, CS) <= n) b += L->csum[c++];
-        if (c == CS || chunk_lo(k, c, CS) == n) return b;
+        while (c < CS && chunk_start(c + 1) <= n) b += L->csum[c++];
+        if (c == CS || chunk_start(c) == n) return b;
         double at;
-        exact_first_reaching<REST_THREADS>(fp, chunk_lo(k, c, CS), n, b, __builtin_inf(), L->red_d, &L->sh_hit,
+        exact_first_reaching<REST_THREADS>(fp, chunk_start(c), n, b, __builtin_inf(), L->red_d, &L->sh_hit,
                                            &L->sh_hit_sum, &at);
         return at;
     };
@@ -662,7 +681,7 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
             while (c < CS && !(b + L->csum[c] >= target)) b += L->csum[c++];
             if (c < CS) {
                 double at;
-                const uint32_t j = exact_first_reaching<REST_THREADS>(fp, chunk_lo(k, c, CS), chunk_lo(k, c + 1, CS), b,
+                const uint32_t j = exact_first_reaching<REST_THREADS>(fp, chunk_start(c), chunk_start(c + 1), b,
                                                                       target, L->red_d, &L->sh_hit, &L->sh_hit_sum, &at);
                 m = j + 1;
                 have_sum_m = true;

@@ -23,6 +23,9 @@ namespace {
 thread_local std::string g_last_error;
 
 constexpr uint32_t MAX_WINDOW = 2048;
+// Vocabularies up to 2^21 ids (every index and count on the device paths
+// fits 32 bits with room to spare).
+constexpr uint32_t MAX_VOCAB = 1u << 21;
 constexpr uint32_t TARGET_WGS = 1024;  // enough workgroups to cover 256 CUs four deep
 constexpr uint32_t FULL_GROUP_MAX = 256;
 constexpr uint32_t CHUNK_SLOTS = 2 * TARGET_WGS;
@@ -156,6 +159,7 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     if (max_rows == 0 || vocab == 0) return fail(RL_ERR_ARGUMENT, "max_rows and vocab must be positive");
     if (max_window > MAX_WINDOW)
         return fail(RL_ERR_CAPACITY, "max_window above " + std::to_string(MAX_WINDOW));
+    if (vocab > MAX_VOCAB) return fail(RL_ERR_CAPACITY, "vocab above " + std::to_string(MAX_VOCAB));
     DeviceGuard g(device);
     if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select device " + std::to_string(device));
     auto *c = new (std::nothrow) rl_sampler_ctx();

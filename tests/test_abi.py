@@ -36,6 +36,8 @@ def test_status_codes_without_a_device():
     assert lib.rl_sampler_create(0, 0, 100, 64, ctypes.byref(h)) == R.RL_ERR_ARGUMENT
     assert lib.rl_sampler_create(0, 4, 100, 5000, ctypes.byref(h)) == R.RL_ERR_CAPACITY
     assert b"max_window" in lib.rl_sampler_last_error()
+    assert lib.rl_sampler_create(0, 4, (1 << 21) + 1, 64, ctypes.byref(h)) == R.RL_ERR_CAPACITY
+    assert b"vocab" in lib.rl_sampler_last_error()
     assert lib.rl_sampler_create(0, 4, 100, 64, None) == R.RL_ERR_ARGUMENT
     assert lib.rl_sampler_configure(None, None, 1) == R.RL_ERR_ARGUMENT
     assert lib.rl_sampler_sample_rows(None, None, 0, 1, 1, None, 0, None, None, None, None, None, None,
