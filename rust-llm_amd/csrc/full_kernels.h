@@ -163,20 +163,23 @@ constexpr double RESCALE_REL = (0x1p-24 + HW_EXP2_REL) * 1.001;  // one in-loop 
 // 2.01 e^(-K) + 2^-124 per term (e^-32 = 1.2664165549e-14).
 constexpr double MASS_ABS_PER_TERM = 2.01 * 1.2664165549094176e-14 + 0x1p-124;
 
-// Loads of k_full_pass's aligned variant are buffer loads: the resource
-// covers the row's n floats (reads past them return zeros, never fault), each
-// lane's byte offset is one register and the step's offset is scalar, so no
-// per-load 64-bit address stays live across a step. gfx9's descriptor word 3
-// (0x00020000: 32-bit data format, raw addressing); nontemporal (aux 2).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const float *row, uint32_t n) {
-    return __builtin_amdgcn_make_buffer_rsrc((void *)row, (short)0, (int)(n * 4u), 0x00020000);
+// Loads of k_full_pass's aligned variant are buffer loads through a resource
+// that starts at the step and ends at the chunk's end: float4 f of the step
+// is at byte offset 16 f (a lane's register plus nothing else, so no 64-bit
+// address stays live across a step), and a load past the chunk returns zeros
+// without a memory access. gfx9's descriptor word 3 (0x00020000: 32-bit data
+// format, raw addressing); nontemporal (aux 2).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t step_rsrc(const float *row, uint32_t b4, uint32_t end4) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(row + 4 * (uint64_t)b4), (short)0,
+                                             (int)(b4 < end4 ? 16u * (end4 - b4) : 0u), 0x00020000);
 }
+// Float4 f of the chunk that ends at float4 end, from the step at float4 b4
+// (VEC: through r = step_rsrc(row, b4, end)).
 template <bool VEC>
-__device__ __forceinline__ f32x4 pass_load(__amdgpu_buffer_rsrc_t r, const float *row, uint32_t f, uint32_t f_lane,
+__device__ __forceinline__ f32x4 pass_load(__amdgpu_buffer_rsrc_t r, const float *row, uint32_t f, uint32_t b4,
                                            uint32_t end) {
     if constexpr (VEC) {
-        // f = f_step + f_lane: the step part (uniform) goes in the scalar offset.
-        return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, 16u * f_lane, 16u * (f - f_lane), 2));
+        return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, 16u * (f - b4), 0, 2));
     } else {
         return load4<false>(row, f < end ? f : end - 1);
     }
@@ -468,13 +471,13 @@ __global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScra
         }
     }
     const uint64_t tab = EXP2_32_TAB[tid & 31u];
-    const __amdgpu_buffer_rsrc_t rsrc = row_rsrc(rowp, V);
     f32x4 A[PASS_U];
     // Buffer loads need no guard (past the row they return zeros); a uniform
     // branch here would also make the compiler wait for all loads at its end.
     if (VEC || q0 < q1) {
+        const __amdgpu_buffer_rsrc_t rs = step_rsrc(rowp, q0, q1);
 #pragma unroll
-        for (uint32_t u = 0; u < PASS_U; ++u) A[u] = pass_load<VEC>(rsrc, rowp, q0 + u * FULL_THREADS + tid, tid, q1);
+        for (uint32_t u = 0; u < PASS_U; ++u) A[u] = pass_load<VEC>(rs, rowp, q0 + u * FULL_THREADS + tid, q0, q1);
     }
     if (pen) {
         for (uint32_t i = tid; i < nwords; i += FULL_THREADS) bm[i] = 0;
@@ -531,25 +534,28 @@ __global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScra
         uint32_t base = 0;
         if (lane == 0) base = atomicAdd((uint32_t *)&sh_cn, wtotal);
         base = uniform_u32((uint32_t)__shfl((int)base, 0));
+        if (base + wtotal > PASS_CAND) {
+            // The buffer is full: the row leaves the min-p path, and nothing
+            // more is listed (or re-read) for it.
+            if (lane == 0) sh_cover = 1;
+            mass = false;
+            return;
+        }
         uint32_t at = base + incl - mine;
         while (mb != 0) {
             const uint32_t i = (uint32_t)__ffsll((unsigned long long)mb) - 1u;
             mb &= mb - 1ull;
             const uint32_t e = id_of(i);
-            if (at < PASS_CAND) cbuf[at] = composite(total_key(value_at(e)), e);
-            ++at;
-        }
-        if (base + wtotal > PASS_CAND) {
-            if (lane == 0) sh_cover = 1;
-            mass = false;  // the row leaves the min-p path
+            cbuf[at++] = composite(total_key(value_at(e)), e);
         }
     };
     // A step's PASS_U float4 per thread are all in flight at once (a chunk
     // of the 64-row workload is one step); the penalty is applied in place.
     for (uint32_t b = q0; b < q1; b += PASS_STEP) {
         if (b != q0) {
+            const __amdgpu_buffer_rsrc_t rs = step_rsrc(rowp, b, q1);
 #pragma unroll
-            for (uint32_t u = 0; u < PASS_U; ++u) A[u] = pass_load<VEC>(rsrc, rowp, b + u * FULL_THREADS + tid, tid, q1);
+            for (uint32_t u = 0; u < PASS_U; ++u) A[u] = pass_load<VEC>(rs, rowp, b + u * FULL_THREADS + tid, b, q1);
         }
         float tmax = -__builtin_inff();
 #pragma unroll
