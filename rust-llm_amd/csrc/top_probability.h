@@ -32,20 +32,35 @@
 
 namespace rl {
 
+// The argmax of (value, index) pairs merged from another lane or wave: the
+// larger value, and on equal values (-0 equals +0) the lower index, as the
+// reference's strict `v > best` over ascending indices keeps the first.
+__device__ __forceinline__ void tp_take(float &bv, uint32_t &bi, float ov, uint32_t oi) {
+    if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+    }
+}
+
 // grid (chunks, rows), FAST_THREADS: per chunk the argmax composite (argmax's
 // order, sample.rs:118-128, which top_probability's loop shares) and whether a
-// NaN occurs.
+// NaN occurs. Each lane follows the reference's loop over its own elements,
+// which it sees in ascending index order: a value replaces the lane's best
+// only when strictly greater (so NaN and -inf never do, and the first of
+// equal values stays); lanes and waves then merge (tp_take). Three vector
+// operations per element, against a 64-bit composite compare.
 template <bool VEC>
 __global__ __launch_bounds__(FAST_THREADS) void k_tp_max(const float *logits, uint64_t stride, uint32_t vocab,
                                                          uint32_t chunks, uint64_t *part_am, uint32_t *part_nan) {
-    __shared__ uint64_t red[FAST_WAVES];
-    __shared__ uint32_t red_n[FAST_WAVES];
+    __shared__ float red_v[FAST_WAVES];
+    __shared__ uint32_t red_i[FAST_WAVES], red_n[FAST_WAVES];
     const uint32_t row = blockIdx.y, chunk = blockIdx.x;
     const float *rowp = logits + (uint64_t)row * stride;
     const uint32_t n4 = vocab / 4;
     const uint32_t q0 = chunk_lo(n4, chunk, chunks), q1 = chunk_lo(n4, chunk + 1, chunks);
-    uint64_t best = 0;
-    uint32_t nan = 0;
+    float bv = -__builtin_inff();
+    uint32_t bi = 0xFFFFFFFFu;
+    bool nan = false;
     // Tiles of UNROLL float4 per thread, the next in flight while one is
     // scanned; loads past the chunk are clamped and their values skipped.
     constexpr uint32_t STEP = FAST_THREADS * UNROLL;
@@ -54,15 +69,33 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_max(const float *logits, ui
         load_tile_clamped<VEC>(A, rowp, q0, q1);
         for (uint32_t b = q0; b < q1; b += STEP) {
             load_tile_clamped<VEC>(B, rowp, b + STEP, q1);
+            if (b + STEP <= q1) {
 #pragma unroll
-            for (uint32_t u = 0; u < UNROLL; ++u) {
-                const uint32_t q = b + u * FAST_THREADS + threadIdx.x;
-                const float x[4] = {A[u].x, A[u].y, A[u].z, A[u].w};
+                for (uint32_t u = 0; u < UNROLL; ++u) {
+                    const uint32_t q = b + u * FAST_THREADS + threadIdx.x;
+                    const float x[4] = {A[u].x, A[u].y, A[u].z, A[u].w};
 #pragma unroll
-                for (uint32_t c = 0; c < 4; ++c) {
-                    const uint64_t cc = q < q1 ? composite(argmax_key(x[c]), 4 * q + c) : 0ull;
-                    best = cc > best ? cc : best;
-                    nan |= (q < q1 && x[c] != x[c]) ? 1u : 0u;
+                    for (uint32_t c = 0; c < 4; ++c) {
+                        if (x[c] > bv) {
+                            bv = x[c];
+                            bi = 4 * q + c;
+                        }
+                        nan |= x[c] != x[c];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (uint32_t u = 0; u < UNROLL; ++u) {
+                    const uint32_t q = b + u * FAST_THREADS + threadIdx.x;
+                    const float x[4] = {A[u].x, A[u].y, A[u].z, A[u].w};
+#pragma unroll
+                    for (uint32_t c = 0; c < 4; ++c) {
+                        if (q < q1 && x[c] > bv) {
+                            bv = x[c];
+                            bi = 4 * q + c;
+                        }
+                        nan |= q < q1 && x[c] != x[c];
+                    }
                 }
             }
 #pragma unroll
@@ -73,26 +106,35 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_max(const float *logits, ui
         const uint32_t e = 4 * n4 + threadIdx.x;
         if (e < vocab) {
             const float x = ((const RL_GLB float *)rowp)[e];
-            const uint64_t cc = composite(argmax_key(x), e);
-            best = cc > best ? cc : best;
-            nan |= x != x ? 1u : 0u;
+            if (x > bv) {  // past every other element of the chunk
+                bv = x;
+                bi = e;
+            }
+            nan |= x != x;
         }
     }
-    best = wave_max_u64(best);
-    nan = ballot(nan != 0) != 0 ? 1u : 0u;
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = __shfl_xor(bv, m);
+        const uint32_t oi = (uint32_t)__shfl_xor((int)bi, m);
+        tp_take(bv, bi, ov, oi);
+    }
+    const uint32_t anynan = ballot(nan) != 0 ? 1u : 0u;
     const uint32_t wave = threadIdx.x / WAVE;
     if (lane_id() == 0) {
-        red[wave] = best;
-        red_n[wave] = nan;
+        red_v[wave] = bv;
+        red_i[wave] = bi;
+        red_n[wave] = anynan;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
+        uint32_t n = anynan;
         for (uint32_t w = 1; w < FAST_WAVES; ++w) {
-            best = red[w] > best ? red[w] : best;
-            nan |= red_n[w];
+            tp_take(bv, bi, red_v[w], red_i[w]);
+            n |= red_n[w];
         }
-        part_am[(uint64_t)row * chunks + chunk] = best;
-        part_nan[(uint64_t)row * chunks + chunk] = nan;
+        // As a composite (argmax_key: nothing above -inf gives key 0).
+        part_am[(uint64_t)row * chunks + chunk] = bv > -__builtin_inff() ? composite(argmax_key(bv), bi) : 0ull;
+        part_nan[(uint64_t)row * chunks + chunk] = n;
     }
 }
 
