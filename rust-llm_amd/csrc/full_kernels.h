@@ -77,13 +77,13 @@ __device__ __forceinline__ int f32_exponent(float p) {
 struct TempScale {
     float t, inv;
     bool pow2;
-    __device__ explicit TempScale(float t_) : t(t_) {
+    __device__ __forceinline__ explicit TempScale(float t_) : t(t_) {
         const uint32_t b = __float_as_uint(t_);
         const uint32_t e = (b >> 23) & 0xFFu;
         pow2 = (b & 0x807FFFFFu) == 0 && e >= 2 && e <= 252;  // +2^-125 .. +2^125
         inv = pow2 ? __uint_as_float((254u - e) << 23) : 0.0f;
     }
-    __device__ float operator()(float d) const { return pow2 ? d * inv : d / t; }
+    __device__ __forceinline__ float operator()(float d) const { return pow2 ? d * inv : d / t; }
 };
 
 // Whether a row tries the min-p path: min-p on, the whole vocabulary as

@@ -28,6 +28,8 @@ constexpr uint32_t HIST_ITEMS = 12;                        // loads per thread p
 constexpr uint32_t HIST_STEP = REST_THREADS * HIST_ITEMS;  // elements per histogram step
 constexpr uint32_t STAT_CHUNKS = 64;                       // most chunks of the candidate list's sums
 constexpr uint32_t STAT_MIN_LOG = 11;                      // chunks of at least 2^11 candidates
+constexpr uint32_t HIST_COPIES = 16;                       // histogram copies (lanes with equal lane & 15 share one)
+constexpr uint32_t HIST_ROW = 257;                         // a copy's stride: copies of a digit fall in different banks
 static_assert(HIST_STEP >= REST_TILE, "the window bitmap covers a tile");
 
 struct RestLds {
@@ -36,7 +38,7 @@ struct RestLds {
             uint32_t k[REST_TILE];  // the tile's keys, reordered by digit
             uint32_t i[REST_TILE];  // and their ids
         } tile;
-        uint32_t wh[REST_WAVES][2][256];  // per-wave histograms of two digits
+        uint32_t gh[2][HIST_COPIES * HIST_ROW];  // two digits' histograms, one copy per lane group
         struct {
             float stage[STAGE];
             ChunkLds cr;
@@ -59,6 +61,8 @@ struct RestLds {
     double red_d[REST_WAVES];
     int64_t red_l[REST_WAVES];
     uint32_t red_u[REST_WAVES];
+    uint32_t hcnt[REST_WAVES];       // per wave: the tile's elements with the hot key
+    uint32_t sh_hot_key, sh_hot_count, sh_hot_above;
     uint32_t sh_m, sh_stop, sh_hit, sh_tok;
     double sh_d, sh_hit_sum;
 };
@@ -195,24 +199,6 @@ __device__ __forceinline__ uint32_t exact_first_reaching(const float *probs, uin
     return hi;
 }
 
-// Adds one wave-item's digits d (lanes where valid) to the wave's private
-// histogram h. The first valid lane's digit is counted with one add for all
-// lanes that share it (a row's commonest digit, such as a tied logit's, would
-// otherwise make every lane holding it wait on the same counter); the other
-// lanes add one each.
-__device__ __forceinline__ void hist_add(RL_LDS uint32_t *h, uint32_t d, bool valid, uint32_t lane) {
-    const uint64_t vm = ballot(valid);
-    if (vm == 0) return;
-    const uint32_t f = (uint32_t)__builtin_ctzll(vm);
-    const uint32_t d0 = uniform_u32(read_lane_u32(d, f));
-    const uint64_t m0 = ballot(valid && d == d0);
-    if (lane == f) {
-        atomicAdd((uint32_t *)&h[d0], (uint32_t)__popcll(m0));
-    } else if (valid && d != d0) {
-        atomicAdd((uint32_t *)&h[d], 1u);
-    }
-}
-
 // What a pass needs of its row.
 struct RestRow {
     const float *rowp;   // the raw logits
@@ -241,63 +227,121 @@ __device__ __forceinline__ void window_bits(RL_LDS RestLds *L, const RestRow &r,
 __device__ __forceinline__ float penalised(RL_LDS const RestLds *L, const RestRow &r, float x, uint32_t off) {
     return ((L->bm[off >> 5] >> (off & 31)) & 1u) ? penalize(x, r.penalty) : x;
 }
+// The same with off's word (off >> 5) and bit (off & 31) given.
+__device__ __forceinline__ float penalised_at(RL_LDS const RestLds *L, const RestRow &r, float x, uint32_t word,
+                                              uint32_t bit) {
+    return ((L->bm[word] >> bit) & 1u) ? penalize(x, r.penalty) : x;
+}
 
 // The histograms of digits hi and lo (8 bits at 8 * hi and 8 * lo) of the
-// penalised row's total-order keys into L->hist[hi] and L->hist[lo], and with
-// `cls` the OR and AND of the keys of each sign into L->cls. One read of the
-// logits, HIST_ITEMS loads per thread in flight.
+// penalised row's total-order keys into L->hist[hi] and L->hist[lo]. Each
+// lane adds its digits to one of HIST_COPIES copies (lane & 15), so one LDS
+// atomic holds at most four lanes on one counter even when most of a row's
+// logits are tied, and a copy's row of HIST_ROW counters puts the copies of
+// a digit in different banks. The first call (`first`) also puts the OR and
+// AND of the keys of each sign into L->cls, and picks a hot key: from the
+// first step, the key that the most lanes of one wave-item share with the
+// item's first lane, the row's commonest key whenever one key holds a large
+// share of the row (any key would do: it only decides which elements skip the
+// sort). It counts the keys equal to it and above it into L->sh_hot_count and
+// L->sh_hot_above. One read of the logits, HIST_ITEMS loads per thread in
+// flight.
 __device__ __forceinline__ void rest_histograms(RL_LDS RestLds *L, const RestRow &r, uint32_t hi, uint32_t lo,
-                                                bool cls) {
+                                                bool first) {
     const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / WAVE;
     const uint32_t V = r.V;
-    for (uint32_t i = tid; i < REST_WAVES * 2 * 256; i += REST_THREADS) (&L->u.wh[0][0][0])[i] = 0;
-    if (cls && tid < 4) L->cls[tid] = (tid & 1) ? 0xFFFFFFFFu : 0u;
+    constexpr uint32_t GH = HIST_COPIES * HIST_ROW;
+    for (uint32_t i = tid; i < 2 * GH; i += REST_THREADS) (&L->u.gh[0][0])[i] = 0;
+    if (first && tid < 4) L->cls[tid] = (tid & 1) ? 0xFFFFFFFFu : 0u;
+    if (first && tid == 0) {
+        L->sh_hot_count = 0;
+        L->sh_hot_above = 0;
+    }
     __syncthreads();
-    RL_LDS uint32_t *h_hi = &L->u.wh[wave][0][0];
-    RL_LDS uint32_t *h_lo = &L->u.wh[wave][1][0];
+    uint32_t K = first ? 0u : L->sh_hot_key;
+    uint32_t nK = 0, nA = 0;  // this wave's keys equal to K and above it
+    RL_LDS uint32_t *h_hi = &L->u.gh[0][(lane & (HIST_COPIES - 1)) * HIST_ROW];
+    RL_LDS uint32_t *h_lo = &L->u.gh[1][(lane & (HIST_COPIES - 1)) * HIST_ROW];
     uint32_t or0 = 0u, and0 = 0xFFFFFFFFu, or1 = 0u, and1 = 0xFFFFFFFFu;
     const uint32_t s_hi = 8 * hi, s_lo = 8 * lo;
     // A step gives each wave a contiguous segment, HIST_ITEMS elements a lane
     // 64 apart; the next step's loads are issued before this step's
     // elements are counted.
     const uint32_t wbase = wave * WAVE * HIST_ITEMS + lane;
+    const uint32_t hoff = 4 * wbase;  // item i adds 256 i bytes
     const uint32_t *raw = (const uint32_t *)r.rowp;
     uint32_t nx[HIST_ITEMS];
     {
         const auto rs = tail_rsrc(raw, 0, V);
 #pragma unroll
-        for (uint32_t i = 0; i < HIST_ITEMS; ++i) nx[i] = bload<true>(rs, 4 * (wbase + i * WAVE));
+        for (uint32_t i = 0; i < HIST_ITEMS; ++i) nx[i] = bload<true>(rs, hoff + 256 * i);
     }
     for (uint32_t b = 0; b < V; b += HIST_STEP) {
         uint32_t x[HIST_ITEMS];
         const auto rs = tail_rsrc(raw, b + HIST_STEP, V);
+        // The items' offsets are formed from an opaque copy each step, so they
+        // are not all held in registers across the loop.
+        uint32_t ho = hoff;
+        asm volatile("" : "+v"(ho));
 #pragma unroll
         for (uint32_t i = 0; i < HIST_ITEMS; ++i) {
             x[i] = nx[i];
-            nx[i] = bload<true>(rs, 4 * (wbase + i * WAVE));
+            nx[i] = bload<true>(rs, ho + 256 * i);
         }
         if (r.pen) window_bits(L, r, b, min(HIST_STEP, V - b));
 #pragma unroll
         for (uint32_t i = 0; i < HIST_ITEMS; ++i) {
-            const uint32_t off = wbase + i * WAVE;
-            const bool valid = b + off < V;
-            const float v = r.pen ? penalised(L, r, __uint_as_float(x[i]), off) : __uint_as_float(x[i]);
-            const uint32_t key = total_key(v);
-            if (cls && valid) {
-                if (key >> 31) {
-                    or1 |= key;
-                    and1 &= key;
-                } else {
-                    or0 |= key;
-                    and0 &= key;
+            const float v = r.pen ? penalised_at(L, r, __uint_as_float(x[i]), (wbase >> 5) + 2 * i, wbase & 31u)
+                                  : __uint_as_float(x[i]);
+            x[i] = total_key(v);
+        }
+        if (first && b == 0) {
+            uint64_t best = 0;  // (lanes << 32) | key
+#pragma unroll
+            for (uint32_t i = 0; i < HIST_ITEMS; ++i) {
+                const uint64_t vm = ballot((int)wbase < (int)V - (int)(i * WAVE));
+                if (vm != 0) {
+                    const uint32_t k0 = uniform_u32(read_lane_u32(x[i], (uint32_t)__builtin_ctzll(vm)));
+                    const uint64_t c = (uint64_t)__popcll(vm & ballot(x[i] == k0));
+                    const uint64_t cand = (c << 32) | k0;
+                    best = cand > best ? cand : best;
                 }
             }
-            hist_add(h_hi, 255u - ((key >> s_hi) & 255u), valid, lane);
-            hist_add(h_lo, 255u - ((key >> s_lo) & 255u), valid, lane);
+            if (lane == 0) L->red_l[wave] = (int64_t)best;
+            __syncthreads();
+            uint64_t kb = 0;
+            for (uint32_t w = 0; w < REST_WAVES; ++w) kb = (uint64_t)L->red_l[w] > kb ? (uint64_t)L->red_l[w] : kb;
+            K = (uint32_t)kb;
+            if (tid == 0) L->sh_hot_key = K;
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < HIST_ITEMS; ++i) {
+            const bool valid = (int)wbase < (int)(V - b) - (int)(i * WAVE);
+            const uint32_t key = x[i];
+            if (first) {
+                // Keys with the top bit set, then clear (invalid lanes in neither).
+                const uint32_t m1 = valid ? 0u - (key >> 31) : 0u;
+                const uint32_t m0 = valid ? ~m1 : 0u;
+                or1 |= key & m1;
+                and1 &= key | ~m1;
+                or0 |= key & m0;
+                and0 &= key | ~m0;
+                const uint64_t vm = ballot(valid);
+                nK += (uint32_t)__popcll(vm & ballot(key == K));
+                nA += (uint32_t)__popcll(vm & ballot(key > K));
+            }
+            if (valid) {
+                atomicAdd((uint32_t *)&h_hi[255u - ((key >> s_hi) & 255u)], 1u);
+                atomicAdd((uint32_t *)&h_lo[255u - ((key >> s_lo) & 255u)], 1u);
+            }
         }
         if (r.pen) __syncthreads();  // the bits are rebuilt for the next step
     }
-    if (cls) {
+    if (first) {
+        if (lane == 0) {
+            atomicAdd((uint32_t *)&L->sh_hot_count, nK);
+            atomicAdd((uint32_t *)&L->sh_hot_above, nA);
+        }
         for (int m = 32; m >= 1; m >>= 1) {
             or0 |= (uint32_t)__shfl_xor((int)or0, m);
             and0 &= (uint32_t)__shfl_xor((int)and0, m);
@@ -313,9 +357,10 @@ __device__ __forceinline__ void rest_histograms(RL_LDS RestLds *L, const RestRow
     }
     __syncthreads();
     for (uint32_t i = tid; i < 2 * 256; i += REST_THREADS) {
+        const uint32_t x = i >> 8, d = i & 255u;
         uint32_t c = 0;
-        for (uint32_t w = 0; w < REST_WAVES; ++w) c += L->u.wh[w][i >> 8][i & 255u];
-        L->hist[(i >> 8) ? lo : hi][i & 255u] = c;
+        for (uint32_t g = 0; g < HIST_COPIES; ++g) c += L->u.gh[x][g * HIST_ROW + d];
+        L->hist[x ? lo : hi][d] = c;
     }
     __syncthreads();
 }
@@ -343,18 +388,32 @@ __device__ __forceinline__ void digit_prefix(RL_LDS const uint32_t *src, RL_LDS 
     }
 }
 
-// One stable pass of the sort on digit t (bits 8t..8t+7, descending): from the
-// raw logits (FROM_LOGITS: keys computed here, ids = positions) or from
-// kin/iin, to kout/iout, or (FINAL) the ids to iout and p to fp for the first
-// k positions. Each tile gives every wave a contiguous segment; a wave ranks
-// its items in order (lanes with the same digit found by ballots, the wave's
-// running count per digit in LDS, advanced by the first such lane with one
-// atomic whose old value the others read from it), the workgroup reorders
-// the tile by digit in LDS and writes it out in runs, so consecutive threads
-// write consecutive addresses.
+// The row's hot key K when its elements skip the sort: they are `count` of
+// the row, `above` keys are greater, and their p is pK. In the reference's
+// order they form one block at [above, above + count), in ascending id.
+struct RestHot {
+    bool on;
+    uint32_t key, count, above;
+    float pK;
+};
+
+// One stable pass of the sort on digit t (bits 8t..8t+7, descending) over n
+// elements: from the raw logits (FROM_LOGITS: keys computed here, ids =
+// positions) or from kin/iin, to kout/iout, or (FINAL) the ids to iout and p
+// to fp for the first k positions. Each tile gives every wave a contiguous
+// segment; a wave ranks its items in order (lanes with the same digit found by
+// ballots, the wave's running count per digit in LDS, advanced by the first
+// such lane with one atomic whose old value the others read from it), the
+// workgroup reorders the tile by digit in LDS and writes it out in runs, so
+// consecutive threads write consecutive addresses. With hot.on, the pass from
+// the logits leaves the hot key's elements out of the ranking and writes them
+// to their block of hid/hp (the final outputs) in id order, and the final pass
+// places the keys below the hot key after that block.
 template <bool FROM_LOGITS, bool FINAL>
 __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, const LdsExpTable &etab, uint32_t t,
-                          const uint32_t *kin, const uint32_t *iin, uint32_t *kout, uint32_t *iout, float *fp) {
+                                          uint32_t n, const RestHot &hot, uint32_t *hid, float *hp,
+                                          const uint32_t *kin, const uint32_t *iin, uint32_t *kout, uint32_t *iout,
+                                          float *fp) {
     const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / WAVE;
     const uint32_t V = r.V, shift = 8 * t;
     if (tid < WAVE) digit_prefix(L->hist[t], L->offs);
@@ -362,16 +421,20 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
     uint32_t nk[REST_ITEMS], ni[REST_ITEMS];
     const uint32_t voff = 4 * (wave * REST_SEG + lane);  // item i adds 256 i bytes
     auto fetch = [&](uint32_t tb) {  // tile tb's keys and ids (zeros past the row)
+        // The items' offsets come from an opaque copy of voff (one register
+        // and immediate offsets, rather than one register per item).
+        uint32_t vo = voff;
+        asm volatile("" : "+v"(vo));
         if constexpr (FROM_LOGITS) {
-            const auto rl = tail_rsrc((const uint32_t *)r.rowp, tb, V);
+            const auto rl = tail_rsrc((const uint32_t *)r.rowp, tb, n);
 #pragma unroll
-            for (uint32_t i = 0; i < REST_ITEMS; ++i) nk[i] = bload<true>(rl, voff + 256 * i);
+            for (uint32_t i = 0; i < REST_ITEMS; ++i) nk[i] = bload<true>(rl, vo + 256 * i);
         } else {
-            const auto rk = tail_rsrc(kin, tb, V), ri = tail_rsrc(iin, tb, V);
+            const auto rk = tail_rsrc(kin, tb, n), ri = tail_rsrc(iin, tb, n);
 #pragma unroll
             for (uint32_t i = 0; i < REST_ITEMS; ++i) {
-                nk[i] = bload(rk, voff + 256 * i);
-                ni[i] = bload(ri, voff + 256 * i);
+                nk[i] = bload(rk, vo + 256 * i);
+                ni[i] = bload(ri, vo + 256 * i);
             }
         }
     };
@@ -380,10 +443,13 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
     const auto rko = words_rsrc(kout, FINAL ? 0u : V);
     const auto rio = words_rsrc(iout, FINAL ? r.k : V);
     const auto rpo = words_rsrc(fp, FINAL ? r.k : 0u);
+    const bool hot_out = FROM_LOGITS && hot.on;  // block-uniform
+    const auto rhi = words_rsrc(hid, hot_out ? r.k : 0u), rhp = words_rsrc(hp, hot_out ? r.k : 0u);
+    uint32_t hot_done = 0;  // the hot key's elements in earlier tiles
     fetch(0);
-    for (uint32_t tb = 0; tb < V; tb += REST_TILE) {
+    for (uint32_t tb = 0; tb < n; tb += REST_TILE) {
         const uint32_t e0 = tb + wave * REST_SEG + lane;
-        const uint32_t tn = min(REST_TILE, V - tb);
+        uint32_t tn = min(REST_TILE, n - tb);
         uint32_t kk[REST_ITEMS], ii[REST_ITEMS];
 #pragma unroll
         for (uint32_t i = 0; i < REST_ITEMS; ++i) {
@@ -400,12 +466,48 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
                 kk[i] = total_key(v);
             }
         }
+        // With the hot key out of the sort, each wave packs its other elements
+        // (key and id, in id order) at the start of its share of the tile
+        // buffer and its hot ids, in id order, backwards from the share's end,
+        // then ranks only the packed items. The buffer is free: the last
+        // tile's reads of it ended two barriers ago and this tile's reorder
+        // comes after the next two.
+        uint32_t packed = 0, wave_hot = 0;  // wave-uniform counts
+        RL_LDS uint32_t *pk = &L->u.tile.k[wave * REST_SEG];
+        RL_LDS uint32_t *pi = &L->u.tile.i[wave * REST_SEG];
+        if (hot_out) {
+#pragma unroll
+            for (uint32_t i = 0; i < REST_ITEMS; ++i) {
+                const bool in = e0 + i * WAVE < n;
+                const bool is_hot = in && kk[i] == hot.key;
+                const uint64_t km = ballot(in && !is_hot), hm = ballot(is_hot);
+                if (in && !is_hot) {
+                    const uint32_t at = packed + lanes_below(km);
+                    pk[at] = kk[i];
+                    pi[at] = ii[i];
+                }
+                if (is_hot) pk[REST_SEG - 1 - (wave_hot + lanes_below(hm))] = ii[i];
+                packed += (uint32_t)__popcll(km);
+                wave_hot += (uint32_t)__popcll(hm);
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < REST_ITEMS; ++i) {
+                if (i * WAVE < packed) {
+                    kk[i] = pk[i * WAVE + lane];
+                    ii[i] = pi[i * WAVE + lane];
+                }
+            }
+        }
+        // Whether item i takes part in the ranking.
+        auto ranked = [&](uint32_t i) { return hot_out ? i * WAVE + lane < packed : e0 + i * WAVE < n; };
         for (uint32_t d = lane; d < 256; d += WAVE) L->cnt[wave][d] = 0;
         // Rank: item i's lanes with digit d follow the wave's earlier items'.
         uint32_t rk[REST_ITEMS];
 #pragma unroll
         for (uint32_t i = 0; i < REST_ITEMS; ++i) {
-            const bool valid = e0 + i * WAVE < V;
+            rk[i] = 0;
+            if (hot_out && i * WAVE >= packed) continue;  // wave-uniform
+            const bool valid = ranked(i);
             const uint32_t d = 255u - ((kk[i] >> shift) & 255u);
             const uint64_t peers = match_digit(d, valid);
             const uint32_t below = lanes_below(peers);
@@ -414,7 +516,25 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
             if (valid && below == 0) old = atomicAdd((uint32_t *)&L->cnt[wave][d], (uint32_t)__popcll(peers));
             rk[i] = below + (uint32_t)__shfl((int)old, (int)lead);
         }
+        if (hot_out && lane == 0) L->hcnt[wave] = wave_hot;
         __syncthreads();
+        if (hot_out) {
+            // The hot key's elements of this tile, in id order: the waves'
+            // counts give each wave its start; its ids are read back from the
+            // end of its share.
+            uint32_t at = hot.above + hot_done, all = 0;
+            for (uint32_t w = 0; w < REST_WAVES; ++w) {
+                const uint32_t c = L->hcnt[w];
+                at += w < wave ? c : 0u;
+                all += c;
+            }
+            for (uint32_t h = lane; h < wave_hot; h += WAVE) {
+                bstore(rhi, 4 * (at + h), pk[REST_SEG - 1 - h]);
+                bstore(rhp, 4 * (at + h), __float_as_uint(hot.pK));
+            }
+            hot_done += all;
+            tn -= all;
+        }
         // Per digit: each wave's start within the digit's run of the tile, and
         // the run's length; then the runs' starts.
         if (tid < 256) {
@@ -430,7 +550,7 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
         __syncthreads();
 #pragma unroll
         for (uint32_t i = 0; i < REST_ITEMS; ++i) {
-            if (e0 + i * WAVE < V) {
+            if (ranked(i)) {
                 const uint32_t d = 255u - ((kk[i] >> shift) & 255u);
                 const uint32_t at = L->tstart[d] + L->pos[wave][d] + rk[i];
                 L->u.tile.k[at] = kk[i];
@@ -444,7 +564,10 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
             if (j < tn) {
                 const uint32_t key = L->u.tile.k[j];
                 const uint32_t d = 255u - ((key >> shift) & 255u);
-                const uint32_t dst = L->offs[d] + (j - L->tstart[d]);
+                uint32_t dst = L->offs[d] + (j - L->tstart[d]);
+                if constexpr (FINAL) {
+                    if (hot.on && key < hot.key) dst += hot.count;
+                }
                 bstore(rio, 4 * dst, L->u.tile.i[j]);
                 if constexpr (FINAL) {
                     if (dst < r.k) bstore(rpo, 4 * dst, __float_as_uint(expf_libm_t(r.tscale(key_value(key) - r.M), etab)));
@@ -540,25 +663,44 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
         const uint32_t vary_sign = (has0 ? (c0 ^ c1) : 0u) | (has1 ? (c2 ^ c3) : 0u);
         const uint32_t all_or = (has0 ? c0 : 0u) | (has1 ? c2 : 0u);
         const uint32_t all_and = (has0 ? c1 : 0xFFFFFFFFu) & (has1 ? c3 : 0xFFFFFFFFu);
-        uint32_t passes[4], np = 0;
+        uint32_t passes[4], np = 0, pass_mask = 0;
         for (uint32_t t = 0; t < 3; ++t)
             if (((vary_sign >> (8 * t)) & 255u) != 0) passes[np++] = t;
         if (((all_or ^ all_and) >> 24) != 0) passes[np++] = 3;
+        for (uint32_t i = 0; i < np; ++i) pass_mask |= 1u << passes[i];
         if (np > 0 && passes[0] < 2) rest_histograms(L, r, 1, 0, false);
         if (np == 0) {
             rest_direct(L, r, etab, fid, fp);
         } else {
             // Pass i writes A when i is even, B when odd; the last writes the
             // ids where the candidates go (not into the buffer it reads).
+            if (!out) fid = ((np - 1) & 1) ? idB : idA;
+            // The hot key's elements skip the sort when they are at least a
+            // sixteenth of the row and their block, written by the first pass,
+            // stays clear of every later pass's output: always in the caller's
+            // buffers, and in idB with two passes (the first writes A, the last
+            // reads it).
+            RestHot hot{false, L->sh_hot_key, L->sh_hot_count, L->sh_hot_above, 0.0f};
+            hot.on = hot.count >= V / 16 && hot.count < V && (out || np <= 2);
+            uint32_t n1 = V;  // the elements of the passes after the first
+            if (hot.on) {
+                hot.pK = expf_libm_t(r.tscale(key_value(hot.key) - r.M), etab);
+                n1 = V - hot.count;
+                if (tid < 4 && ((pass_mask >> tid) & 1u)) L->hist[tid][255u - ((hot.key >> (8 * tid)) & 255u)] -= hot.count;
+                __syncthreads();
+            }
             const uint32_t *kin = nullptr, *iin = nullptr;
             for (uint32_t i = 0; i < np; ++i) {
                 const bool last = i + 1 == np;
                 uint32_t *ko = (i & 1) ? keyB : keyA, *io = (i & 1) ? idB : idA;
-                if (last && !out) fid = (i & 1) ? idB : idA;
-                if (i == 0 && last) rest_pass<true, true>(L, r, etab, passes[i], nullptr, nullptr, nullptr, fid, fp);
-                else if (i == 0) rest_pass<true, false>(L, r, etab, passes[i], nullptr, nullptr, ko, io, nullptr);
-                else if (last) rest_pass<false, true>(L, r, etab, passes[i], kin, iin, nullptr, fid, fp);
-                else rest_pass<false, false>(L, r, etab, passes[i], kin, iin, ko, io, nullptr);
+                if (i == 0 && last)
+                    rest_pass<true, true>(L, r, etab, passes[i], V, hot, fid, fp, nullptr, nullptr, nullptr, fid, fp);
+                else if (i == 0)
+                    rest_pass<true, false>(L, r, etab, passes[i], V, hot, fid, fp, nullptr, nullptr, ko, io, nullptr);
+                else if (last)
+                    rest_pass<false, true>(L, r, etab, passes[i], n1, hot, nullptr, nullptr, kin, iin, nullptr, fid, fp);
+                else
+                    rest_pass<false, false>(L, r, etab, passes[i], n1, hot, nullptr, nullptr, kin, iin, ko, io, nullptr);
                 kin = ko;
                 iin = io;
             }

@@ -256,3 +256,66 @@ def test_full_path_rows_with_nans_and_infinities(device):
     uniforms = rng.random(rows).astype(np.float32)
     got, want = run_both(device, logits, settings, windows, wlen, uniforms)
     assert_match("full-path special rows", got, want, settings)
+
+
+def hot_key_rows(rng, V):
+    # Rows where one value holds a tenth to three quarters of the ids (at the
+    # top, in the middle or at the bottom of the order) beside other values
+    # that leave the sort one, two or four digit passes: values apart only in
+    # their top byte, bf16-grid values, and f32 values with full mantissas.
+    rows, names = [], []
+    for fill in ("top-byte", "bf16", "f32"):
+        for where in ("max", "mid", "min"):
+            for share in (0.1, 0.4, 0.75):
+                if fill == "top-byte":
+                    x = rng.choice(np.array([0.5, 2.0, 8.0, 32.0, -2.0, -8.0], np.float32), V)
+                    hot = {"max": 128.0, "mid": 2.0, "min": -32.0}[where]
+                elif fill == "bf16":
+                    x = (rng.normal(0, 0.01, V).astype(np.float32).view(np.uint32) & 0xFFFF0000).view(np.float32)
+                    hot = {"max": 0.0625, "mid": -0.0234375, "min": -0.125}[where]
+                else:
+                    x = rng.normal(0, 1.0, V).astype(np.float32)
+                    hot = {"max": 6.5, "mid": 0.3, "min": -7.0}[where]
+                x[rng.random(V) < share] = np.float32(hot)
+                rows.append(x)
+                names.append("%s/%s/%.2f" % (fill, where, share))
+    return np.stack(rows), names
+
+
+@pytest.mark.parametrize("candidates", [True, False])
+def test_full_path_rows_with_a_dominant_key(device, candidates):
+    # The sort leaves a row's commonest key out of its passes when it holds a
+    # sixteenth of the row or more, and writes its ids as one block; the rows
+    # here put that block at the start, inside and at the end of the order,
+    # across several tiles of the sort, with and without the candidate outputs
+    # (without them the block shares a buffer with the last pass's ids).
+    rng = np.random.default_rng(2024 + candidates)
+    V = 20011
+    logits, names = hot_key_rows(rng, V)
+    rows = logits.shape[0]
+    choices = [(1.0, 0, 0.9, 0.0, 1.0), (0.7, 0, 0.99, 0.02, 1.0), (2.0, 0, 0.5, 0.0, 1.3),
+               (1.0, 100, 0.95, 0.0, 1.0), (1.0, 7000, 0.999, 0.0, 0.8), (1.0, V - 1, 0.9, 0.05, 1.0)]
+    settings = [R.sampling(*choices[r % len(choices)], 16, r) for r in range(rows)]
+    windows = rng.integers(0, V, (rows, 16)).astype(np.uint32)
+    wlen = np.full(rows, 16, np.uint32)
+    uniforms = rng.random(rows).astype(np.float32)
+    print("dominant-key rows: %d x %d, candidates %s" % (rows, V, candidates), flush=True)
+    if candidates:
+        got, want = run_both(device, logits, settings, windows, wlen, uniforms)
+        assert_match("dominant key", got, want, settings)
+        return
+    import torch
+    ctx = R.DeviceSampler(rows, V, max_window=16)
+    ctx.configure(settings)
+    tok = torch.empty(rows, dtype=torch.int32, device=device)
+    kept = torch.empty_like(tok)
+    used = torch.empty(rows, dtype=torch.uint8, device=device)
+    ctx.sample_rows(torch.from_numpy(logits.reshape(-1)).to(device), rows, V, tok, kept, used,
+                    windows=torch.from_numpy(windows.view(np.int32)).to(device), window_stride=16,
+                    window_len=torch.from_numpy(wlen.view(np.int32)).to(device),
+                    uniforms=torch.from_numpy(uniforms).to(device))
+    torch.cuda.synchronize()
+    want = O.pick_rows(logits, [as_oracle_settings(s) for s in settings], windows, wlen, uniforms)
+    t, k = tok.cpu().numpy().view(np.uint32), kept.cpu().numpy().view(np.uint32)
+    for r in range(rows):
+        assert (t[r], k[r]) == (want["token"][r], want["kept"][r]), "%s %r" % (names[r], settings[r])
