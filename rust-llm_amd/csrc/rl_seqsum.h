@@ -820,6 +820,43 @@ __device__ __forceinline__ uint32_t wave_walk(RL_LDS const uint32_t *t, uint32_t
     }
 }
 
+// The same as wave_walk, one term after another (every lane alike), four
+// additions between tests of pred (the partial sums only grow, so pred met
+// by the fourth is met first by one of them). t must be 16-byte aligned; the
+// words past len up to the next multiple of 4 are read and ignored. For a
+// chunk whose sum leaves several binades this is cheaper than a wave pass
+// per binade.
+template <int P, class Pred>
+__device__ __forceinline__ uint32_t seq_walk(RL_LDS const uint32_t *t, uint32_t len, Pred pred, double &s) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    for (uint32_t j = 0; j < len; j += 4) {
+        const u32x4 q = *(RL_LDS const u32x4 *)&t[j];
+        const float x0 = __uint_as_float(q[0]);
+        const float x1 = j + 1 < len ? __uint_as_float(q[1]) : 0.0f;
+        const float x2 = j + 2 < len ? __uint_as_float(q[2]) : 0.0f;
+        const float x3 = j + 3 < len ? __uint_as_float(q[3]) : 0.0f;
+        const double a0 = add_p<P>(s, x0), a1 = add_p<P>(a0, x1), a2 = add_p<P>(a1, x2), a3 = add_p<P>(a2, x3);
+        if (pred(a3)) {
+            if (pred(a0)) {
+                s = a0;
+                return j;
+            }
+            if (pred(a1)) {
+                s = a1;
+                return j + 1;
+            }
+            if (pred(a2)) {
+                s = a2;
+                return j + 2;
+            }
+            s = a3;
+            return j + 3;
+        }
+        s = a3;
+    }
+    return len;
+}
+
 // Returns as seq_replay does, for the terms x_j = term(src[j]) (raw 32-bit
 // words), j < n; every thread of the workgroup (1024) calls it.
 template <int P, uint32_t NT, class Term, class Pred>
@@ -947,7 +984,12 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
                 }
                 const uint32_t start_j = (r * CR_ROUND + c) * CR_CH;
                 const uint32_t len = min(CR_CH, n - start_j);
-                const uint32_t j = wave_walk<P, CR_CH / 64>(&L->terms[c * CR_CH], len, pred, s);
+                // A chunk that at least quadruples the sum (or starts it) leaves
+                // two binades or more: term by term; else by wave passes.
+                const double cf = L->fsum[c];
+                const uint32_t j = (!(s > 0.0) || cf >= 3.0 * s)
+                                       ? seq_walk<P>(&L->terms[c * CR_CH], len, pred, s)
+                                       : wave_walk<P, CR_CH / 64>(&L->terms[c * CR_CH], len, pred, s);
                 if (j < len) {
                     hit = start_j + j;
                     break;
