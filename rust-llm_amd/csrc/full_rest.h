@@ -963,12 +963,14 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
     // ---- the draw: the f32 running sum of q against the uniform
     // (sample.rs:349-356); a shortfall takes the last candidate (:357-358) ----
     const float u = a.uniforms[row];
-    uint32_t pick;
+    uint32_t pick, qdone = 0;  // q is in place for the first qdone candidates
     if (!qbad) {
+        // The draw stores q over p for the rounds it stages (when the caller
+        // wants the candidates), so the normalisation below reads only the rest.
         double unused;
         const uint32_t j = chunk_replay<24, REST_THREADS>(
             fpw, [inv](uint32_t bits) { return __uint_as_float(bits) * inv; }, m,
-            [u](double c) { return c > (double)u; }, cr, &unused);
+            [u](double c) { return c > (double)u; }, cr, &unused, out ? (uint32_t *)fp : nullptr, &qdone);
         pick = j < m ? j : m - 1;
     } else {
         if (tid == 0) L->sh_tok = m - 1;
@@ -996,7 +998,7 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
     // ---- the kept candidates: q = p * (1 / total) in place (sample.rs:344-347) ----
     if (out) {
         constexpr uint32_t NU = 8;
-        for (uint32_t b = 0; b < m; b += REST_THREADS * NU) {
+        for (uint32_t b = qdone; b < m; b += REST_THREADS * NU) {
             float pv[NU];
 #pragma unroll
             for (uint32_t q = 0; q < NU; ++q) {

@@ -858,10 +858,14 @@ __device__ __forceinline__ uint32_t seq_walk(RL_LDS const uint32_t *t, uint32_t 
 }
 
 // Returns as seq_replay does, for the terms x_j = term(src[j]) (raw 32-bit
-// words), j < n; every thread of the workgroup (1024) calls it.
+// words), j < n; every thread of the workgroup (1024) calls it. With wb, the
+// terms of every round it stages are also stored to wb[j] (wb may be src: a
+// round's words are read a round before they are written), and *staged gets
+// how many: a prefix of [0, n).
 template <int P, uint32_t NT, class Term, class Pred>
 __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term, uint32_t n, Pred pred,
-                                                 RL_LDS ChunkLds *L, double *sum) {
+                                                 RL_LDS ChunkLds *L, double *sum, uint32_t *wb = nullptr,
+                                                 uint32_t *staged = nullptr) {
     static_assert(NT / 64 * 2 == CR_ROUND, "two chunks a wave");
     const uint32_t tid = threadIdx.x, lane = __lane_id(), wave = tid / 64;
     const uint32_t half = lane >> 5, hl = lane & 31u, my = 2 * wave + half;  // this half wave's chunk
@@ -879,15 +883,19 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
     };
     const uint32_t rounds = (uint32_t)(((uint64_t)n + CR_TERMS - 1) / CR_TERMS);
     const uint32_t chunks = (uint32_t)(((uint64_t)n + CR_CH - 1) / CR_CH);
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void *)wb, (short)0, wb ? (int)(n * 4u) : 0, 0x00020000);
     double s = 0.0;
     uint32_t hit = n;
+    if (staged) *staged = 0;
     if (n > 0 && pred(0.0)) {
         // A predicate that +0 already meets is met by the first term's sum.
         *sum = add_p<P>(0.0, term(__builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 0)));
         return 0;
     }
     fetch_round(0);
-    for (uint32_t r = 0; r < rounds && hit == n; ++r) {
+    uint32_t r = 0;
+    for (; r < rounds && hit == n; ++r) {
         // Stage the terms; each chunk's f64 sum.
         uint32_t x[CR_ITEMS];
         double fs = 0.0;
@@ -901,6 +909,12 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
 #pragma unroll
         for (uint32_t q = 0; q < CR_ITEMS / 4; ++q)
             *(RL_LDS u32x4 *)&L->terms[tid * CR_ITEMS + 4 * q] = u32x4{x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
+        if (wb) {
+#pragma unroll
+            for (uint32_t q = 0; q < CR_ITEMS / 4; ++q)
+                __builtin_amdgcn_raw_buffer_store_b128(u32x4{x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]}, rw,
+                                                       4u * (r * CR_TERMS + tid * CR_ITEMS) + 16u * q, 0, 0);
+        }
         fs = half_total_f64(fs);
         if (hl == 0) L->fsum[my] = fs;
         fetch_round(r + 1);  // in flight through the rest of the round
@@ -1005,6 +1019,7 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
         s = L->s;
         hit = L->hit;
     }
+    if (staged) *staged = (uint32_t)min((uint64_t)n, (uint64_t)r * CR_TERMS);
     *sum = s;
     return hit;
 }
