@@ -37,6 +37,7 @@ struct RestLds {
         struct {
             uint32_t k[REST_TILE];  // the tile's keys, reordered by digit
             uint32_t i[REST_TILE];  // and their ids
+            double csum[HIST_COPIES][STAT_CHUNKS + 1];  // the last pass's chunk sums of p, a copy per lane group
         } tile;
         uint32_t gh[2][HIST_COPIES * HIST_ROW];  // two digits' histograms, one copy per lane group
         struct {
@@ -52,12 +53,13 @@ struct RestLds {
     uint32_t bm[HIST_STEP / 32];     // window ids in the current step, one bit per element
     uint32_t cls[4];                 // OR and AND of the keys with the top bit clear, then set
     uint64_t exp_tab[32];
-    // Per chunk of the candidate list: the f64 sum of p, the smallest binary
-    // exponent of a nonzero p, the count with p >= min_p, a NaN or infinite
-    // p, the last index + 1 with p >= min_p and the first with p < min_p.
-    double csum[STAT_CHUNKS];
-    int cemin[STAT_CHUNKS];
-    uint32_t ccount[STAT_CHUNKS], cbad[STAT_CHUNKS], clast_in[STAT_CHUNKS], cfirst_out[STAT_CHUNKS];
+    // The f64 sum of p per chunk of the candidate list (2^SH candidates, the
+    // last one shorter); and over the whole list the smallest binary exponent
+    // of a nonzero p, a NaN or infinite p, the count with p >= min_p, the last
+    // index + 1 with p >= min_p and the first with p < min_p.
+    double seg_sum[STAT_CHUNKS];
+    int st_emin;
+    uint32_t st_bad, st_count, st_last_in, st_first_out;
     double red_d[REST_WAVES];
     int64_t red_l[REST_WAVES];
     uint32_t red_u[REST_WAVES];
@@ -388,6 +390,53 @@ __device__ __forceinline__ void digit_prefix(RL_LDS const uint32_t *src, RL_LDS 
     }
 }
 
+// A thread's share of the candidate list's statistics (those kept in LDS
+// beside the segments): p at index j seen by add.
+struct PStats {
+    int emin = 1 << 20;
+    uint32_t bad = 0, count = 0, last_in = 0, first_out = 0xFFFFFFFFu;
+    __device__ __forceinline__ void add(float p, uint32_t j, float min_p) {
+        if (!(p <= 3.40282347e38f)) {
+            bad = 1;  // NaN or +inf
+        } else if (p > 0.0f) {
+            emin = min(emin, f32_exponent(p));
+        }
+        if (p >= min_p) {
+            ++count;
+            last_in = max(last_in, j + 1);
+        } else {
+            first_out = min(first_out, j);
+        }
+    }
+    // Folds the wave's shares into L's (lane 0 adds them with LDS atomics,
+    // after L's were set by stats_reset and a barrier).
+    __device__ __forceinline__ void merge(RL_LDS RestLds *L) {
+        for (int m = 32; m >= 1; m >>= 1) {
+            emin = min(emin, __shfl_xor(emin, m));
+            bad |= (uint32_t)__shfl_xor((int)bad, m);
+            count += (uint32_t)__shfl_xor((int)count, m);
+            last_in = max(last_in, (uint32_t)__shfl_xor((int)last_in, m));
+            first_out = min(first_out, (uint32_t)__shfl_xor((int)first_out, m));
+        }
+        if (lane_id() == 0) {
+            atomicMin((int *)&L->st_emin, emin);
+            atomicOr((uint32_t *)&L->st_bad, bad);
+            atomicAdd((uint32_t *)&L->st_count, count);
+            atomicMax((uint32_t *)&L->st_last_in, last_in);
+            atomicMin((uint32_t *)&L->st_first_out, first_out);
+        }
+    }
+};
+
+// The list statistics before any merge (one thread).
+__device__ __forceinline__ void stats_reset(RL_LDS RestLds *L) {
+    L->st_emin = 1 << 20;
+    L->st_bad = 0;
+    L->st_count = 0;
+    L->st_last_in = 0;
+    L->st_first_out = 0xFFFFFFFFu;
+}
+
 // The row's hot key K when its elements skip the sort: they are `count` of
 // the row, `above` keys are greater, and their p is pK. In the reference's
 // order they form one block at [above, above + count), in ascending id.
@@ -413,7 +462,7 @@ template <bool FROM_LOGITS, bool FINAL>
 __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, const LdsExpTable &etab, uint32_t t,
                                           uint32_t n, const RestHot &hot, uint32_t *hid, float *hp,
                                           const uint32_t *kin, const uint32_t *iin, uint32_t *kout, uint32_t *iout,
-                                          float *fp) {
+                                          float *fp, PStats &ps, float min_p, uint32_t SH) {
     const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / WAVE;
     const uint32_t V = r.V, shift = 8 * t;
     if (tid < WAVE) digit_prefix(L->hist[t], L->offs);
@@ -570,7 +619,16 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
                 }
                 bstore(rio, 4 * dst, L->u.tile.i[j]);
                 if constexpr (FINAL) {
-                    if (dst < r.k) bstore(rpo, 4 * dst, __float_as_uint(expf_libm_t(r.tscale(key_value(key) - r.M), etab)));
+                    if (dst < r.k) {
+                        // p, and the list's statistics: its chunk's sum (any
+                        // order: the sums are used only where they are exact)
+                        // and the thread's share of the rest.
+                        const float p = expf_libm_t(r.tscale(key_value(key) - r.M), etab);
+                        bstore(rpo, 4 * dst, __float_as_uint(p));
+                        __hip_atomic_fetch_add(&L->u.tile.csum[lane & (HIST_COPIES - 1)][dst >> SH], (double)p,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                        ps.add(p, dst, min_p);
+                    }
                 } else {
                     bstore(rko, 4 * dst, key);
                 }
@@ -648,6 +706,14 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
     uint32_t *fid = out ? a.out_ids + (uint64_t)row * a.cand_stride : idA;
 
     // ---- the candidates in order: fid[0..V), fp[0..k) ----
+    if (tid == 0) stats_reset(L);
+    PStats ps;                 // this thread's share of the list's statistics
+    bool sorted = false;       // the last sort pass gathered the statistics
+    RestHot hot{false, 0u, 0u, 0u, 0.0f};
+    // The list's chunks: 2^SH candidates each, CS of them.
+    const uint32_t SH = stat_shift(k);
+    const uint32_t CS = (uint32_t)(((uint64_t)k + (1ull << SH) - 1) >> SH);
+    auto chunk_start = [&](uint32_t c) { return min(c << SH, k); };
     if (identity_order(s, V)) {
         rest_direct(L, r, etab, fid, fp);
     } else {
@@ -680,27 +746,35 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
             // stays clear of every later pass's output: always in the caller's
             // buffers, and in idB with two passes (the first writes A, the last
             // reads it).
-            RestHot hot{false, L->sh_hot_key, L->sh_hot_count, L->sh_hot_above, 0.0f};
+            hot = RestHot{false, L->sh_hot_key, L->sh_hot_count, L->sh_hot_above, 0.0f};
             hot.on = hot.count >= V / 16 && hot.count < V && (out || np <= 2);
             uint32_t n1 = V;  // the elements of the passes after the first
             if (hot.on) {
                 hot.pK = expf_libm_t(r.tscale(key_value(hot.key) - r.M), etab);
                 n1 = V - hot.count;
                 if (tid < 4 && ((pass_mask >> tid) & 1u)) L->hist[tid][255u - ((hot.key >> (8 * tid)) & 255u)] -= hot.count;
-                __syncthreads();
             }
+            for (uint32_t i = tid; i < HIST_COPIES * (STAT_CHUNKS + 1); i += REST_THREADS)
+                (&L->u.tile.csum[0][0])[i] = 0.0;
+            __syncthreads();
+            sorted = true;
+            const float min_p = s.min_p;
             const uint32_t *kin = nullptr, *iin = nullptr;
             for (uint32_t i = 0; i < np; ++i) {
                 const bool last = i + 1 == np;
                 uint32_t *ko = (i & 1) ? keyB : keyA, *io = (i & 1) ? idB : idA;
                 if (i == 0 && last)
-                    rest_pass<true, true>(L, r, etab, passes[i], V, hot, fid, fp, nullptr, nullptr, nullptr, fid, fp);
+                    rest_pass<true, true>(L, r, etab, passes[i], V, hot, fid, fp, nullptr, nullptr, nullptr, fid, fp,
+                                          ps, min_p, SH);
                 else if (i == 0)
-                    rest_pass<true, false>(L, r, etab, passes[i], V, hot, fid, fp, nullptr, nullptr, ko, io, nullptr);
+                    rest_pass<true, false>(L, r, etab, passes[i], V, hot, fid, fp, nullptr, nullptr, ko, io, nullptr,
+                                           ps, min_p, SH);
                 else if (last)
-                    rest_pass<false, true>(L, r, etab, passes[i], n1, hot, nullptr, nullptr, kin, iin, nullptr, fid, fp);
+                    rest_pass<false, true>(L, r, etab, passes[i], n1, hot, nullptr, nullptr, kin, iin, nullptr, fid,
+                                           fp, ps, min_p, SH);
                 else
-                    rest_pass<false, false>(L, r, etab, passes[i], n1, hot, nullptr, nullptr, kin, iin, ko, io, nullptr);
+                    rest_pass<false, false>(L, r, etab, passes[i], n1, hot, nullptr, nullptr, kin, iin, ko, io,
+                                            nullptr, ps, min_p, SH);
                 kin = ko;
                 iin = io;
             }
@@ -708,21 +782,43 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
     }
     __syncthreads();
 
-    // ---- per-chunk sums of the candidate list, one wave a chunk at a time:
-    // each lane's share of a chunk (32 consecutive p) in eight 16-byte loads,
-    // all in flight together ----
-    const uint32_t SH = stat_shift(k);
-    const uint32_t CS = (uint32_t)(((uint64_t)k + (1ull << SH) - 1) >> SH);  // chunks of the candidate list
-    auto chunk_start = [&](uint32_t c) { return min(c << SH, k); };
-    {
+    // ---- the candidate list's chunk sums and statistics ----
+    if (sorted) {
+        // The last pass added each candidate's p to its chunk; the hot key's
+        // block adds pK times its overlap with each chunk.
+        const uint32_t hot_in = hot.on && hot.above < k ? min(hot.count, k - hot.above) : 0u;
+        if (tid == 0 && hot_in > 0) {
+            // The hot block's share of the statistics: hot_in equal p.
+            const float p = hot.pK;
+            if (!(p <= 3.40282347e38f)) {
+                ps.bad = 1;
+            } else if (p > 0.0f) {
+                ps.emin = min(ps.emin, f32_exponent(p));
+            }
+            if (p >= s.min_p) {
+                ps.count += hot_in;
+                ps.last_in = max(ps.last_in, hot.above + hot_in);
+            } else {
+                ps.first_out = min(ps.first_out, hot.above);
+            }
+        }
+        if (tid < CS) {
+            double sum = 0.0;
+            for (uint32_t g = 0; g < HIST_COPIES; ++g) sum += L->u.tile.csum[g][tid];
+            const uint32_t lo = max(chunk_start(tid), hot.above), hi = min(chunk_start(tid + 1), hot.above + hot_in);
+            if (hot_in > 0 && lo < hi) sum += (double)(hi - lo) * (double)hot.pK;  // exact where the sums are used
+            L->seg_sum[tid] = sum;
+        }
+    } else {
+        // The candidates in id order: one wave a chunk at a time; each lane's
+        // share of a chunk (32 consecutive p) in eight 16-byte loads, all in
+        // flight together.
         constexpr uint32_t SL = 32;  // consecutive p per lane per step
         typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
         const __amdgpu_buffer_rsrc_t rp = words_rsrc(fp, k);
         for (uint32_t c = wave; c < CS; c += REST_WAVES) {
             const uint32_t j0 = chunk_start(c), j1 = chunk_start(c + 1);
             double sum = 0.0;
-            int emin = 1 << 20;
-            uint32_t count = 0, bad = 0, last_in = 0, first_out = 0xFFFFFFFFu;
             for (uint32_t b = j0; b < j1; b += WAVE * SL) {
                 const uint32_t jl = b + lane * SL;
                 u32x4 v[SL / 4];
@@ -736,39 +832,16 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
                         const uint32_t j = jl + 4 * q + i;
                         if (j < j1) {
                             const float p = __uint_as_float(v[q][i]);
-                            if (!(p <= 3.40282347e38f)) {
-                                bad = 1;  // NaN or +inf
-                            } else if (p > 0.0f) {
-                                emin = min(emin, f32_exponent(p));
-                            }
                             sum += (double)p;
-                            if (p >= s.min_p) {
-                                ++count;
-                                last_in = max(last_in, j + 1);
-                            } else {
-                                first_out = min(first_out, j);
-                            }
+                            ps.add(p, j, s.min_p);
                         }
                     }
             }
             sum = wave_total_f64(sum);
-            emin = wave_min_i32(emin);
-            for (int m = 32; m >= 1; m >>= 1) {
-                count += (uint32_t)__shfl_xor((int)count, m);
-                bad |= (uint32_t)__shfl_xor((int)bad, m);
-                last_in = max(last_in, (uint32_t)__shfl_xor((int)last_in, m));
-                first_out = min(first_out, (uint32_t)__shfl_xor((int)first_out, m));
-            }
-            if (lane == 0) {
-                L->csum[c] = sum;
-                L->cemin[c] = emin;
-                L->ccount[c] = count;
-                L->cbad[c] = bad;
-                L->clast_in[c] = last_in;
-                L->cfirst_out[c] = first_out;
-            }
+            if (lane == 0) L->seg_sum[c] = sum;
         }
     }
+    ps.merge(L);
     __syncthreads();
 
     // ---- the mass, the top-p cut (sample.rs:307-324), min-p (:326-340) and
@@ -778,30 +851,24 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
     const uint32_t *fpw = (const uint32_t *)fp;
     const auto as_f32 = [](uint32_t b) { return __uint_as_float(b); };
     RL_LDS ChunkLds *cr = &L->u.rep.cr;
-    bool bad = false;
-    int emin = 1 << 20;
-    uint32_t count = 0, last_in = 0, first_out = 0xFFFFFFFFu;
+    const bool bad = L->st_bad != 0;
+    const int emin = L->st_emin;
+    const uint32_t count = L->st_count, last_in = L->st_last_in, first_out = L->st_first_out;
     double tree_mass = 0.0;
-    for (uint32_t c = 0; c < CS; ++c) {
-        bad |= L->cbad[c] != 0;
-        emin = min(emin, L->cemin[c]);
-        count += L->ccount[c];
-        last_in = max(last_in, L->clast_in[c]);
-        first_out = min(first_out, L->cfirst_out[c]);
-        tree_mass += L->csum[c];
-    }
+    for (uint32_t c = 0; c < CS; ++c) tree_mass += L->seg_sum[c];
     // The candidates with p >= min_p form a prefix of the list.
     const bool surv_prefix = last_in <= first_out;
     // Every partial sum exact: all p are multiples of 2^(emin-23), the mass is
-    // below 2^53 of those steps. Then the chunk sums are the exact sums too.
-    // (The margin keeps a mass rounded below the bound from passing for one
-    // that is not.)
+    // below 2^53 of those steps. Then any sum of any of them is exact, so the
+    // chunk sums (added in whatever order) are the exact sums too. (The
+    // margin keeps a mass rounded below the bound from passing for one that is
+    // not.)
     const bool exact = !bad && (emin > 1000 || tree_mass < mul_pow2(1.0 - 0x1p-30, 30 + emin));
     // The exact sum of p[0..n), from the chunk sums and one partial chunk.
     auto exact_prefix = [&](uint32_t n) {
         double b = 0.0;
         uint32_t c = 0;
-        while (c < CS && chunk_start(c + 1) <= n) b += L->csum[c++];
+        while (c < CS && chunk_start(c + 1) <= n) b += L->seg_sum[c++];
         if (c == CS || chunk_start(c) == n) return b;
         double at;
         exact_first_reaching<REST_THREADS>(fp, chunk_start(c), n, b, __builtin_inf(), L->red_d, &L->sh_hit,
@@ -820,7 +887,7 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
             // The chunk where the running sum first reaches the target.
             double b = 0.0;
             uint32_t c = 0;
-            while (c < CS && !(b + L->csum[c] >= target)) b += L->csum[c++];
+            while (c < CS && !(b + L->seg_sum[c] >= target)) b += L->seg_sum[c++];
             if (c < CS) {
                 double at;
                 const uint32_t j = exact_first_reaching<REST_THREADS>(fp, chunk_start(c), chunk_start(c + 1), b,
