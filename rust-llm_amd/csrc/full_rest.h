@@ -159,14 +159,16 @@ __device__ __forceinline__ void staged_walk(const float *src, uint32_t n, RL_LDS
 template <uint32_t NT>
 __device__ __forceinline__ uint32_t exact_first_reaching(const float *probs, uint32_t lo, uint32_t hi, double base, double target,
                                          RL_LDS double *red, RL_LDS uint32_t *hit, RL_LDS double *hit_sum,
-                                         double *at) {
+                                         double *at, const HotRange &hr) {
     for (uint32_t b = lo; b < hi; b += NT * CI) {
         const uint32_t j0 = b + threadIdx.x * CI;
         float pv[CI];
         double mine = 0.0;
 #pragma unroll
         for (uint32_t i = 0; i < CI; ++i) {
-            pv[i] = j0 + i < hi ? ((const RL_GLB float *)probs)[j0 + i] : 0.0f;
+            uint32_t w = hr.word;
+            if (j0 + i < hi && !hr.has(j0 + i)) w = ((const RL_GLB uint32_t *)probs)[j0 + i];
+            pv[i] = j0 + i < hi ? __uint_as_float(w) : 0.0f;
             mine += (double)pv[i];
         }
         if (threadIdx.x == 0) *hit = 0xFFFFFFFFu;
@@ -455,12 +457,13 @@ struct RestHot {
 // such lane with one atomic whose old value the others read from it), the
 // workgroup reorders the tile by digit in LDS and writes it out in runs, so
 // consecutive threads write consecutive addresses. With hot.on, the pass from
-// the logits leaves the hot key's elements out of the ranking and writes them
-// to their block of hid/hp (the final outputs) in id order, and the final pass
-// places the keys below the hot key after that block.
+// the logits leaves the hot key's elements out of the ranking and writes their
+// ids to their block of hid (the final ids) in id order (their p, all pK, are
+// not stored: readers of the list take them from a HotRange), and the final
+// pass places the keys below the hot key after that block.
 template <bool FROM_LOGITS, bool FINAL>
 __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, const LdsExpTable &etab, uint32_t t,
-                                          uint32_t n, const RestHot &hot, uint32_t *hid, float *hp,
+                                          uint32_t n, const RestHot &hot, uint32_t *hid,
                                           const uint32_t *kin, const uint32_t *iin, uint32_t *kout, uint32_t *iout,
                                           float *fp, PStats &ps, float min_p, uint32_t SH) {
     const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / WAVE;
@@ -493,7 +496,7 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
     const auto rio = words_rsrc(iout, FINAL ? r.k : V);
     const auto rpo = words_rsrc(fp, FINAL ? r.k : 0u);
     const bool hot_out = FROM_LOGITS && hot.on;  // block-uniform
-    const auto rhi = words_rsrc(hid, hot_out ? r.k : 0u), rhp = words_rsrc(hp, hot_out ? r.k : 0u);
+    const auto rhi = words_rsrc(hid, hot_out ? r.k : 0u);
     uint32_t hot_done = 0;  // the hot key's elements in earlier tiles
     fetch(0);
     for (uint32_t tb = 0; tb < n; tb += REST_TILE) {
@@ -577,10 +580,7 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
                 at += w < wave ? c : 0u;
                 all += c;
             }
-            for (uint32_t h = lane; h < wave_hot; h += WAVE) {
-                bstore(rhi, 4 * (at + h), pk[REST_SEG - 1 - h]);
-                bstore(rhp, 4 * (at + h), __float_as_uint(hot.pK));
-            }
+            for (uint32_t h = lane; h < wave_hot; h += WAVE) bstore(rhi, 4 * (at + h), pk[REST_SEG - 1 - h]);
             hot_done += all;
             tn -= all;
         }
@@ -764,16 +764,16 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
                 const bool last = i + 1 == np;
                 uint32_t *ko = (i & 1) ? keyB : keyA, *io = (i & 1) ? idB : idA;
                 if (i == 0 && last)
-                    rest_pass<true, true>(L, r, etab, passes[i], V, hot, fid, fp, nullptr, nullptr, nullptr, fid, fp,
+                    rest_pass<true, true>(L, r, etab, passes[i], V, hot, fid, nullptr, nullptr, nullptr, fid, fp,
                                           ps, min_p, SH);
                 else if (i == 0)
-                    rest_pass<true, false>(L, r, etab, passes[i], V, hot, fid, fp, nullptr, nullptr, ko, io, nullptr,
+                    rest_pass<true, false>(L, r, etab, passes[i], V, hot, fid, nullptr, nullptr, ko, io, nullptr,
                                            ps, min_p, SH);
                 else if (last)
-                    rest_pass<false, true>(L, r, etab, passes[i], n1, hot, nullptr, nullptr, kin, iin, nullptr, fid,
+                    rest_pass<false, true>(L, r, etab, passes[i], n1, hot, nullptr, kin, iin, nullptr, fid,
                                            fp, ps, min_p, SH);
                 else
-                    rest_pass<false, false>(L, r, etab, passes[i], n1, hot, nullptr, nullptr, kin, iin, ko, io,
+                    rest_pass<false, false>(L, r, etab, passes[i], n1, hot, nullptr, kin, iin, ko, io,
                                             nullptr, ps, min_p, SH);
                 kin = ko;
                 iin = io;
@@ -858,6 +858,22 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
     for (uint32_t c = 0; c < CS; ++c) tree_mass += L->seg_sum[c];
     // The candidates with p >= min_p form a prefix of the list.
     const bool surv_prefix = last_in <= first_out;
+    // The hot key's block of p (all pK) was not stored: the readers below take
+    // it from hr, unless one that reads the list itself runs (a NaN or an
+    // infinite p: the staged walks; survivors not a prefix: the min-p
+    // compaction), for which it is written out first.
+    HotRange hr;
+    {
+        const uint32_t hot_in = hot.on && hot.above < k ? min(hot.count, k - hot.above) : 0u;
+        if (hot_in > 0) {
+            if (bad || !surv_prefix) {
+                for (uint32_t j = hot.above + tid; j < hot.above + hot_in; j += REST_THREADS) fp[j] = hot.pK;
+                __syncthreads();
+            } else {
+                hr = HotRange{hot.above, hot.above + hot_in, __float_as_uint(hot.pK)};
+            }
+        }
+    }
     // Every partial sum exact: all p are multiples of 2^(emin-23), the mass is
     // below 2^53 of those steps. Then any sum of any of them is exact, so the
     // chunk sums (added in whatever order) are the exact sums too. (The
@@ -872,7 +888,7 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
         if (c == CS || chunk_start(c) == n) return b;
         double at;
         exact_first_reaching<REST_THREADS>(fp, chunk_start(c), n, b, __builtin_inf(), L->red_d, &L->sh_hit,
-                                           &L->sh_hit_sum, &at);
+                                           &L->sh_hit_sum, &at, hr);
         return at;
     };
 
@@ -891,7 +907,8 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
             if (c < CS) {
                 double at;
                 const uint32_t j = exact_first_reaching<REST_THREADS>(fp, chunk_start(c), chunk_start(c + 1), b,
-                                                                      target, L->red_d, &L->sh_hit, &L->sh_hit_sum, &at);
+                                                                      target, L->red_d, &L->sh_hit, &L->sh_hit_sum, &at,
+                                                                      hr);
                 m = j + 1;
                 have_sum_m = true;
                 sum_m = at;
@@ -906,7 +923,8 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
             for (uint32_t job = 0; job < 2; ++job) {
                 double at;
                 const uint32_t j =
-                    chunk_replay<53, REST_THREADS>(fpw, as_f32, k, [tgt](double c) { return c >= tgt; }, cr, &at);
+                    chunk_replay<53, REST_THREADS>(fpw, as_f32, k, [tgt](double c) { return c >= tgt; }, cr, &at,
+                                                   nullptr, nullptr, hr);
                 if (job == 0) {
                     mass = at;
                     tgt = (double)s.top_p * mass;
@@ -1010,9 +1028,9 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
         total = exact_prefix(m);  // min-p moved nothing: the chunk sums still apply
     } else if (exact) {
         exact_first_reaching<REST_THREADS>(fp, 0, m, 0.0, __builtin_inf(), L->red_d, &L->sh_hit, &L->sh_hit_sum,
-                                           &total);
+                                           &total, hr);
     } else if (!bad) {
-        chunk_replay<53, REST_THREADS>(fpw, as_f32, m, [](double) { return false; }, cr, &total);
+        chunk_replay<53, REST_THREADS>(fpw, as_f32, m, [](double) { return false; }, cr, &total, nullptr, nullptr, hr);
     } else {
         staged_walk<REST_THREADS>(fp, m, stage, stop, [&](RL_LDS float *sv, uint32_t, uint32_t cnt) {
             for (uint32_t i = 0; i < cnt; ++i) total += (double)sv[i];
@@ -1037,7 +1055,7 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
         double unused;
         const uint32_t j = chunk_replay<24, REST_THREADS>(
             fpw, [inv](uint32_t bits) { return __uint_as_float(bits) * inv; }, m,
-            [u](double c) { return c > (double)u; }, cr, &unused, out ? (uint32_t *)fp : nullptr, &qdone);
+            [u](double c) { return c > (double)u; }, cr, &unused, out ? (uint32_t *)fp : nullptr, &qdone, hr);
         pick = j < m ? j : m - 1;
     } else {
         if (tid == 0) L->sh_tok = m - 1;
@@ -1070,7 +1088,10 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
 #pragma unroll
             for (uint32_t q = 0; q < NU; ++q) {
                 const uint32_t j = b + q * REST_THREADS + tid;
-                pv[q] = ((const RL_GLB float *)fp)[j < m ? j : m - 1];
+                const uint32_t jj = j < m ? j : m - 1;
+                uint32_t w = hr.word;
+                if (!hr.has(jj)) w = ((const RL_GLB uint32_t *)fp)[jj];
+                pv[q] = __uint_as_float(w);
             }
 #pragma unroll
             for (uint32_t q = 0; q < NU; ++q) {

@@ -857,16 +857,29 @@ __device__ __forceinline__ uint32_t seq_walk(RL_LDS const uint32_t *t, uint32_t 
     return len;
 }
 
+// A range of a term array whose words are all one value that is not stored
+// there: readers take `word` for j in [lo, hi) (an empty range by default).
+struct HotRange {
+    uint32_t lo = 0, hi = 0, word = 0;
+    __device__ __forceinline__ bool has(uint32_t j) const { return j - lo < hi - lo; }
+    __device__ __forceinline__ uint32_t fix(uint32_t j, uint32_t w) const { return has(j) ? word : w; }
+};
+
 // Returns as seq_replay does, for the terms x_j = term(src[j]) (raw 32-bit
-// words), j < n; every thread of the workgroup (1024) calls it. With wb, the
+// words; src[j] read as hr.word for j in hr), j < n; every thread of the
+// workgroup (1024) calls it. With wb, the
 // terms of every round it stages are also stored to wb[j] (wb may be src: a
 // round's words are read a round before they are written), and *staged gets
 // how many: a prefix of [0, n).
 template <int P, uint32_t NT, class Term, class Pred>
 __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term, uint32_t n, Pred pred,
                                                  RL_LDS ChunkLds *L, double *sum, uint32_t *wb = nullptr,
-                                                 uint32_t *staged = nullptr) {
+                                                 uint32_t *staged = nullptr, const HotRange &hr_in = HotRange()) {
     static_assert(NT / 64 * 2 == CR_ROUND, "two chunks a wave");
+    // The range cut at n: the words past n are zeros.
+    HotRange hr = hr_in;
+    hr.hi = min(hr.hi, n);
+    hr.lo = min(hr.lo, hr.hi);
     const uint32_t tid = threadIdx.x, lane = __lane_id(), wave = tid / 64;
     const uint32_t half = lane >> 5, hl = lane & 31u, my = 2 * wave + half;  // this half wave's chunk
     const __amdgpu_buffer_rsrc_t rs =
@@ -876,10 +889,16 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
     // nothing).
     u32x4 xr[CR_ITEMS / 4];
     auto fetch_round = [&](uint32_t r) {
+        // A thread whose words all lie in hr loads none.
+        const uint32_t j0 = r * CR_TERMS + tid * CR_ITEMS;
+        if (hr.has(j0) && hr.has(j0 + CR_ITEMS - 1)) {
 #pragma unroll
-        for (uint32_t q = 0; q < CR_ITEMS / 4; ++q)
-            xr[q] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 4u * (r * CR_TERMS + tid * CR_ITEMS) + 16u * q, 0, 0));
+            for (uint32_t q = 0; q < CR_ITEMS / 4; ++q) xr[q] = u32x4{0u, 0u, 0u, 0u};
+        } else {
+#pragma unroll
+            for (uint32_t q = 0; q < CR_ITEMS / 4; ++q)
+                xr[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 4u * j0 + 16u * q, 0, 0));
+        }
     };
     const uint32_t rounds = (uint32_t)(((uint64_t)n + CR_TERMS - 1) / CR_TERMS);
     const uint32_t chunks = (uint32_t)(((uint64_t)n + CR_CH - 1) / CR_CH);
@@ -890,7 +909,7 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
     if (staged) *staged = 0;
     if (n > 0 && pred(0.0)) {
         // A predicate that +0 already meets is met by the first term's sum.
-        *sum = add_p<P>(0.0, term(__builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 0)));
+        *sum = add_p<P>(0.0, term(hr.fix(0, __builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 0))));
         return 0;
     }
     fetch_round(0);
@@ -903,7 +922,7 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
         for (uint32_t q = 0; q < CR_ITEMS / 4; ++q)
 #pragma unroll
             for (uint32_t i = 0; i < 4; ++i) {
-                x[4 * q + i] = __float_as_uint(term(xr[q][i]));
+                x[4 * q + i] = __float_as_uint(term(hr.fix(r * CR_TERMS + tid * CR_ITEMS + 4 * q + i, xr[q][i])));
                 fs += (double)__uint_as_float(x[4 * q + i]);
             }
 #pragma unroll

@@ -279,6 +279,13 @@ def hot_key_rows(rng, V):
                 x[rng.random(V) < share] = np.float32(hot)
                 rows.append(x)
                 names.append("%s/%s/%.2f" % (fill, where, share))
+    # Special hot values: NaN and +inf make p NaN or infinite (the list's own
+    # walks run), -inf gives p = 0, and -0.0 ties +0.0's neighbours.
+    for hot, share in ((np.nan, 0.3), (np.inf, 0.2), (-np.inf, 0.5), (-0.0, 0.4)):
+        x = rng.normal(0, 1.0, V).astype(np.float32)
+        x[rng.random(V) < share] = np.float32(hot)
+        rows.append(x)
+        names.append("f32/special %r/%.2f" % (hot, share))
     return np.stack(rows), names
 
 
