@@ -453,9 +453,8 @@ struct RestHot {
 // positions) or from kin/iin, to kout/iout, or (FINAL) the ids to iout and p
 // to fp for the first k positions. Each tile gives every wave a contiguous
 // segment; a wave ranks its items in order (lanes with the same digit found by
-// ballots, the wave's running count per digit in LDS, advanced by the first
-// such lane with one atomic whose old value the others read from it), the
-// workgroup reorders the tile by digit in LDS and writes it out in runs, so
+// ballots, the wave's running count per digit in LDS, which they all read and
+// then advance by their number), the workgroup reorders the tile by digit in LDS and writes it out in runs, so
 // consecutive threads write consecutive addresses. With hot.on, the pass from
 // the logits leaves the hot key's elements out of the ranking and writes their
 // ids to their block of hid (the final ids) in id order (their p, all pK, are
@@ -562,11 +561,12 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
             const bool valid = ranked(i);
             const uint32_t d = 255u - ((kk[i] >> shift) & 255u);
             const uint64_t peers = match_digit(d, valid);
-            const uint32_t below = lanes_below(peers);
-            const uint32_t lead = valid ? (uint32_t)__builtin_ctzll(peers) : lane;
-            uint32_t old = 0;
-            if (valid && below == 0) old = atomicAdd((uint32_t *)&L->cnt[wave][d], (uint32_t)__popcll(peers));
-            rk[i] = below + (uint32_t)__shfl((int)old, (int)lead);
+            // The wave's own counter: its LDS accesses run in order, so every
+            // peer reads the count before this item and writes the same count
+            // after it.
+            const uint32_t base = L->cnt[wave][d];
+            rk[i] = base + lanes_below(peers);
+            if (valid) L->cnt[wave][d] = base + (uint32_t)__popcll(peers);
         }
         if (hot_out && lane == 0) L->hcnt[wave] = wave_hot;
         __syncthreads();
