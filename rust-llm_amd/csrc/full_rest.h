@@ -64,6 +64,8 @@ struct RestLds {
     int64_t red_l[REST_WAVES];
     uint32_t red_u[REST_WAVES];
     uint32_t hcnt[REST_WAVES];       // per wave: the tile's elements with the hot key
+    uint32_t run0[257];              // packed passes: where each digit's run of the first pass's output starts
+    uint8_t dmap[REST_TILE];         // packed passes: the first pass's digit of each element of the tile
     uint32_t sh_hot_key, sh_hot_count, sh_hot_above;
     uint32_t sh_m, sh_stop, sh_hit, sh_tok;
     double sh_d, sh_hit_sum;
@@ -439,6 +441,18 @@ __device__ __forceinline__ void stats_reset(RL_LDS RestLds *L) {
     L->st_first_out = 0xFFFFFFFFu;
 }
 
+// Two passes on digits 2 and 3 (keys whose low 16 bits are one value per sign,
+// as for logits on a bf16 grid) can pass one word per element between them:
+// the first pass writes (key's top byte << 24) | id, and the second takes the
+// element's digit 2 from its position (the first pass's output is in runs of
+// digit 2, starting at L->run0) and the low 16 bits from its sign.
+struct RestPacked {
+    uint32_t lo_clear, lo_set;  // the low 16 key bits of keys with the top bit clear, set
+    __device__ __forceinline__ uint32_t key(uint32_t d3, uint32_t d2) const {
+        return (d3 << 24) | (d2 << 16) | ((d3 & 0x80u) ? lo_set : lo_clear);
+    }
+};
+
 // The row's hot key K when its elements skip the sort: they are `count` of
 // the row, `above` keys are greater, and their p is pK. In the reference's
 // order they form one block at [above, above + count), in ascending id.
@@ -460,15 +474,21 @@ struct RestHot {
 // ids to their block of hid (the final ids) in id order (their p, all pK, are
 // not stored: readers of the list take them from a HotRange), and the final
 // pass places the keys below the hot key after that block.
-template <bool FROM_LOGITS, bool FINAL>
+template <bool FROM_LOGITS, bool FINAL, bool PACKED = false>
 __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, const LdsExpTable &etab, uint32_t t,
                                           uint32_t n, const RestHot &hot, uint32_t *hid,
                                           const uint32_t *kin, const uint32_t *iin, uint32_t *kout, uint32_t *iout,
-                                          float *fp, PStats &ps, float min_p, uint32_t SH) {
+                                          float *fp, PStats &ps, float min_p, uint32_t SH,
+                                          const RestPacked &pk_ = RestPacked{}) {
     const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / WAVE;
     const uint32_t V = r.V, shift = 8 * t;
     if (tid < WAVE) digit_prefix(L->hist[t], L->offs);
     __syncthreads();
+    if constexpr (PACKED && FROM_LOGITS) {
+        // The runs of the output by digit, for the second pass.
+        if (tid < 256) L->run0[tid] = L->offs[tid];
+        if (tid == 255) L->run0[256] = L->offs[255] + L->hist[t][255];
+    }
     uint32_t nk[REST_ITEMS], ni[REST_ITEMS];
     const uint32_t voff = 4 * (wave * REST_SEG + lane);  // item i adds 256 i bytes
     auto fetch = [&](uint32_t tb) {  // tile tb's keys and ids (zeros past the row)
@@ -480,6 +500,10 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
             const auto rl = tail_rsrc((const uint32_t *)r.rowp, tb, n);
 #pragma unroll
             for (uint32_t i = 0; i < REST_ITEMS; ++i) nk[i] = bload<true>(rl, vo + 256 * i);
+        } else if constexpr (PACKED) {
+            const auto ri = tail_rsrc(iin, tb, n);
+#pragma unroll
+            for (uint32_t i = 0; i < REST_ITEMS; ++i) ni[i] = bload(ri, vo + 256 * i);
         } else {
             const auto rk = tail_rsrc(kin, tb, n), ri = tail_rsrc(iin, tb, n);
 #pragma unroll
@@ -502,10 +526,26 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
         const uint32_t e0 = tb + wave * REST_SEG + lane;
         uint32_t tn = min(REST_TILE, n - tb);
         uint32_t kk[REST_ITEMS], ii[REST_ITEMS];
+        if constexpr (PACKED && !FROM_LOGITS) {
+            // Each element's digit 2 from the run it sits in: the waves
+            // write the tile's map run by run, then read it by position.
+            for (uint32_t f = wave; f < 256; f += REST_WAVES) {
+                const uint32_t lo = max(L->run0[f], tb), hi = min(L->run0[f + 1], tb + tn);
+                for (uint32_t j = lo + lane; j < hi; j += WAVE) L->dmap[j - tb] = (uint8_t)(255u - f);
+            }
+            __syncthreads();
 #pragma unroll
-        for (uint32_t i = 0; i < REST_ITEMS; ++i) {
-            kk[i] = nk[i];
-            ii[i] = FROM_LOGITS ? e0 + i * WAVE : ni[i];
+            for (uint32_t i = 0; i < REST_ITEMS; ++i) {
+                const uint32_t w = ni[i];
+                kk[i] = pk_.key(w >> 24, L->dmap[wave * REST_SEG + i * WAVE + lane]);
+                ii[i] = w & 0x00FFFFFFu;
+            }
+        } else {
+#pragma unroll
+            for (uint32_t i = 0; i < REST_ITEMS; ++i) {
+                kk[i] = nk[i];
+                ii[i] = FROM_LOGITS ? e0 + i * WAVE : ni[i];
+            }
         }
         fetch(tb + REST_TILE);
         if constexpr (FROM_LOGITS) {
@@ -617,8 +657,9 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
                 if constexpr (FINAL) {
                     if (hot.on && key < hot.key) dst += hot.count;
                 }
-                bstore(rio, 4 * dst, L->u.tile.i[j]);
+                const uint32_t id = L->u.tile.i[j];
                 if constexpr (FINAL) {
+                    bstore(rio, 4 * dst, id);
                     if (dst < r.k) {
                         // p, and the list's statistics: its chunk's sum (any
                         // order: the sums are used only where they are exact)
@@ -629,7 +670,10 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                         ps.add(p, dst, min_p);
                     }
+                } else if constexpr (PACKED) {
+                    bstore(rio, 4 * dst, (key & 0xFF000000u) | id);
                 } else {
+                    bstore(rio, 4 * dst, id);
                     bstore(rko, 4 * dst, key);
                 }
             }
@@ -760,6 +804,16 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
             sorted = true;
             const float min_p = s.min_p;
             const uint32_t *kin = nullptr, *iin = nullptr;
+            if (pass_mask == 0xCu && V <= 0x01000000u) {
+                // Digits 2 and 3 only: the first pass hands the second one
+                // word per element (RestPacked).
+                const RestPacked pkd{c0 & 0xFFFFu, c2 & 0xFFFFu};
+                rest_pass<true, false, true>(L, r, etab, 2, V, hot, fid, nullptr, nullptr, nullptr, idA, nullptr, ps,
+                                             min_p, SH, pkd);
+                rest_pass<false, true, true>(L, r, etab, 3, n1, hot, nullptr, nullptr, idA, nullptr, fid, fp, ps,
+                                             min_p, SH, pkd);
+                np = 0;  // done
+            }
             for (uint32_t i = 0; i < np; ++i) {
                 const bool last = i + 1 == np;
                 uint32_t *ko = (i & 1) ? keyB : keyA, *io = (i & 1) ? idB : idA;
