@@ -670,35 +670,39 @@ __device__ __forceinline__ uint32_t seq_replay(Load load, uint32_t n, Pred pred,
 
 // ------------------------------------------------------ chunked replay ---
 // The same replay for long sums with a workgroup of 1024 threads, in rounds
-// of CR_ROUND chunks of CR_CH terms. A round's terms are staged in LDS by
-// one load per thread (the next round's loads are issued before this round's
-// chain, so they are in flight while it runs); each half wave takes a chunk
-// (CR_ITEMS consecutive terms a lane) and computes its f64 sum, from which
-// every chunk's start is predicted; each half wave then counts its chunk's
-// steps on the grid of the binade its start is predicted in, ties resolved
-// but the first (the record seq_replay keeps per wave). One wave chains the
-// records in order from the exact running sum: a record applies when the sum
-// is on its grid, and the chunk then has no event if its end stays in the
-// binade and fails pred (the partial sums only grow); any other chunk (the
-// first nonzero term, a binade left, pred met, a start off the predicted
-// grid) is added by that wave alone from LDS (wave_walk). A long sum thus
-// costs a wave pass per binade crossing plus a few barriers per round, not a
-// workgroup pass per tile.
-constexpr uint32_t CR_ITEMS = 8;              // consecutive terms per lane
-constexpr uint32_t CR_CH = 32 * CR_ITEMS;     // terms per chunk (half a wave's)
-constexpr uint32_t CR_ROUND = 32;             // chunks per round: two a wave
+// of CR_ROUND chunks of CR_CH terms, with two roles that run side by side.
+// Waves 1 .. 15 (the workers) stage the rounds: each thread loads its
+// CR_ITEMS consecutive terms of a round three rounds ahead, each half wave
+// takes a chunk and computes its f64 sum, from which every chunk's start is
+// predicted, and then counts its chunk's steps on the grid of the binade its
+// start is predicted in, ties resolved but the first (the record seq_replay
+// keeps per wave). Wave 0 chains the records of round r in order from the
+// exact running sum while the workers prepare round r + 1 (one barrier per
+// round): a record applies when the sum is on its grid, and the chunk then
+// has no event if its end stays in the binade and fails pred (the partial
+// sums only grow); any other chunk (the first nonzero term, a binade left,
+// pred met, a start off the predicted grid) is added by wave 0 alone from
+// LDS (wave_walk, seq_walk). The start of round r + 1 is predicted from the
+// exact start of round r plus round r's f64 chunk sums; the f32 or f64
+// running sum differs from that by its roundings, far less than a binade, so
+// only a start within that distance of a binade's end misses its grid. A
+// long sum thus costs a wave pass per binade crossing, hidden behind the
+// staging of the next round where it is shorter, plus a barrier per round.
+constexpr uint32_t CR_ITEMS = 8;               // consecutive terms per lane
+constexpr uint32_t CR_CH = 32 * CR_ITEMS;      // terms per chunk (half a wave's)
+constexpr uint32_t CR_WORKERS = 15;            // the waves that stage (all but wave 0)
+constexpr uint32_t CR_ROUND = 2 * CR_WORKERS;  // chunks per round: two a worker wave
 constexpr uint32_t CR_TERMS = CR_ROUND * CR_CH;
 
 struct ChunkLds {
-    __attribute__((aligned(16))) uint32_t terms[CR_TERMS];  // the round's terms
-    double fsum[CR_ROUND];   // f64 sum of each chunk's terms (the prediction)
-    double base[CR_ROUND];   // its steps, every tie resolved but the first (capped)
-    uint32_t bits[CR_ROUND]; // bit 0: a tie; bit 1: the first tie's constant; bit 2: par
-    int32_t uexp[CR_ROUND];  // the grid its steps count; INT32_MIN: no record
-    double s;                // the running sum at the end of the round
-    uint32_t hit;            // the first index meeting pred, or n
+    __attribute__((aligned(16))) uint32_t terms[2][CR_TERMS];  // rounds r and r + 1 (by r & 1)
+    double fsum[3][CR_ROUND];   // f64 sum of each chunk's terms, rounds r .. r + 2 (by r % 3)
+    double base[2][CR_ROUND];   // its steps, every tie resolved but the first (capped)
+    uint32_t bits[2][CR_ROUND]; // bit 0: a tie; bit 1: the first tie's constant; bit 2: par
+    int32_t uexp[2][CR_ROUND];  // the grid its steps count; INT32_MIN: no record
+    double s[2];                // the running sum at the start of round r (by r & 1)
+    uint32_t hit[2];            // the first index meeting pred, or n, as of that start
 };
-
 // Sum of v over the 32 lanes of this half wave (every lane gets it).
 __device__ __forceinline__ double half_total_f64(double v) {
     v += lane_xor_f64<1>(v);
@@ -869,28 +873,30 @@ struct HotRange {
 // words; src[j] read as hr.word for j in hr), j < n; every thread of the
 // workgroup (1024) calls it. With wb, the
 // terms of every round it stages are also stored to wb[j] (wb may be src: a
-// round's words are read a round before they are written), and *staged gets
-// how many: a prefix of [0, n).
+// round's words are read two rounds before they are written), and *staged
+// gets how many: a prefix of [0, n).
 template <int P, uint32_t NT, class Term, class Pred>
 __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term, uint32_t n, Pred pred,
                                                  RL_LDS ChunkLds *L, double *sum, uint32_t *wb = nullptr,
                                                  uint32_t *staged = nullptr, const HotRange &hr_in = HotRange()) {
-    static_assert(NT / 64 * 2 == CR_ROUND, "two chunks a wave");
+    static_assert(NT / 64 - 1 == CR_WORKERS, "wave 0 chains, the other waves stage two chunks each");
     // The range cut at n: the words past n are zeros.
     HotRange hr = hr_in;
     hr.hi = min(hr.hi, n);
     hr.lo = min(hr.lo, hr.hi);
     const uint32_t tid = threadIdx.x, lane = __lane_id(), wave = tid / 64;
-    const uint32_t half = lane >> 5, hl = lane & 31u, my = 2 * wave + half;  // this half wave's chunk
+    const bool worker = wave != 0;
+    const uint32_t wt = tid - 64;  // a worker's thread index
+    const uint32_t half = lane >> 5, hl = lane & 31u, my = 2 * (wave - 1) + half;  // a worker half wave's chunk
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, (int)(n * 4u), 0x00020000);
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    // This thread's CR_ITEMS raw words of round r (zeros past n: they add
+    // A worker's CR_ITEMS raw words of round r (zeros past n: they add
     // nothing).
     u32x4 xr[CR_ITEMS / 4];
     auto fetch_round = [&](uint32_t r) {
         // A thread whose words all lie in hr loads none.
-        const uint32_t j0 = r * CR_TERMS + tid * CR_ITEMS;
+        const uint32_t j0 = r * CR_TERMS + wt * CR_ITEMS;
         if (hr.has(j0) && hr.has(j0 + CR_ITEMS - 1)) {
 #pragma unroll
             for (uint32_t q = 0; q < CR_ITEMS / 4; ++q) xr[q] = u32x4{0u, 0u, 0u, 0u};
@@ -904,46 +910,47 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
     const uint32_t chunks = (uint32_t)(((uint64_t)n + CR_CH - 1) / CR_CH);
     const __amdgpu_buffer_rsrc_t rw =
         __builtin_amdgcn_make_buffer_rsrc((void *)wb, (short)0, wb ? (int)(n * 4u) : 0, 0x00020000);
-    double s = 0.0;
-    uint32_t hit = n;
     if (staged) *staged = 0;
     if (n > 0 && pred(0.0)) {
         // A predicate that +0 already meets is met by the first term's sum.
         *sum = add_p<P>(0.0, term(hr.fix(0, __builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 0))));
         return 0;
     }
-    fetch_round(0);
-    uint32_t r = 0;
-    for (; r < rounds && hit == n; ++r) {
-        // Stage the terms; each chunk's f64 sum.
-        uint32_t x[CR_ITEMS];
+    if (rounds == 0) {
+        *sum = 0.0;
+        return n;
+    }
+    // A worker's terms of the round it stages, and their f64 chunk sum.
+    uint32_t x[CR_ITEMS];
+    auto stage = [&](uint32_t r) {
         double fs = 0.0;
 #pragma unroll
         for (uint32_t q = 0; q < CR_ITEMS / 4; ++q)
 #pragma unroll
             for (uint32_t i = 0; i < 4; ++i) {
-                x[4 * q + i] = __float_as_uint(term(hr.fix(r * CR_TERMS + tid * CR_ITEMS + 4 * q + i, xr[q][i])));
+                x[4 * q + i] = __float_as_uint(term(hr.fix(r * CR_TERMS + wt * CR_ITEMS + 4 * q + i, xr[q][i])));
                 fs += (double)__uint_as_float(x[4 * q + i]);
             }
+        fs = half_total_f64(fs);
+        if (hl == 0) L->fsum[r % 3][my] = fs;
+    };
+    // Round r's terms into LDS (and wb), and each chunk's record on the grid
+    // of its start predicted from s_round, the round's predicted start.
+    auto prepare = [&](uint32_t r, double s_round) {
+        const uint32_t b = r & 1u;
 #pragma unroll
         for (uint32_t q = 0; q < CR_ITEMS / 4; ++q)
-            *(RL_LDS u32x4 *)&L->terms[tid * CR_ITEMS + 4 * q] = u32x4{x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
+            *(RL_LDS u32x4 *)&L->terms[b][wt * CR_ITEMS + 4 * q] = u32x4{x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
         if (wb) {
 #pragma unroll
             for (uint32_t q = 0; q < CR_ITEMS / 4; ++q)
                 __builtin_amdgcn_raw_buffer_store_b128(u32x4{x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]}, rw,
-                                                       4u * (r * CR_TERMS + tid * CR_ITEMS) + 16u * q, 0, 0);
+                                                       4u * (r * CR_TERMS + wt * CR_ITEMS) + 16u * q, 0, 0);
         }
-        fs = half_total_f64(fs);
-        if (hl == 0) L->fsum[my] = fs;
-        fetch_round(r + 1);  // in flight through the rest of the round
-        __syncthreads();
-        // This chunk's predicted start: s plus the sums of the chunks before.
-        const double pre = wave_excl_f64(lane < CR_ROUND ? L->fsum[lane] : 0.0);
+        const double pre = wave_excl_f64(lane < CR_ROUND ? L->fsum[r % 3][lane] : 0.0);
         const double start =
-            s + f64_from_bits(((uint64_t)(uint32_t)__shfl((int)(uint32_t)(f64_bits(pre) >> 32), (int)my) << 32) |
-                              (uint32_t)__shfl((int)(uint32_t)f64_bits(pre), (int)my));
-        // The chunk's record on that start's grid.
+            s_round + f64_from_bits(((uint64_t)(uint32_t)__shfl((int)(uint32_t)(f64_bits(pre) >> 32), (int)my) << 32) |
+                                    (uint32_t)__shfl((int)(uint32_t)f64_bits(pre), (int)my));
         const bool rec = start > 0.0;
         const int32_t ux = rec ? seg_of<P>(start).uexp : INT32_MIN;
         const double scale = rec ? mul_pow2(1.0, -ux) : 1.0;
@@ -956,7 +963,7 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
         const uint64_t O = half ? (Ow >> 32) : (Ow & 0xFFFFFFFFull);
         uint32_t dep;
         const uint32_t k = parity_in(T, O, hl, &dep);
-        const double wb = half_total_f64(rr.base + ((rr.tie && !dep) ? (double)((k ^ rr.c) & 1u) : 0.0));
+        const double wsum = half_total_f64(rr.base + ((rr.tie && !dep) ? (double)((k ^ rr.c) & 1u) : 0.0));
         uint32_t bits;
         const uint32_t ft = T != 0 ? (uint32_t)__builtin_ctzll(T) : 0u;
         const uint32_t cf = (uint32_t)__shfl((int)rr.c, (int)(half * 32 + ft));
@@ -969,22 +976,47 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
             bits = (popc64(O) & 1u) << 2;
         }
         if (hl == 0) {
-            L->uexp[my] = ux;
-            L->base[my] = wb < STEP_CAP ? wb : STEP_CAP;
-            L->bits[my] = bits;
+            L->uexp[b][my] = ux;
+            L->base[b][my] = wsum < STEP_CAP ? wsum : STEP_CAP;
+            L->bits[b][my] = bits;
         }
-        __syncthreads();
-        // The chain, on wave 0; lane c holds chunk c's record. From the
-        // current chunk on, the chunks on the sum's grid without a tie add
-        // their steps (a scan); the first one whose end leaves the binade or
-        // meets pred, or whose record does not apply, stops the run, and is
-        // added by wave_walk (or by its record, when only a tie stopped it).
-        if (wave == 0) {
+    };
+    // Round 0 and the sums of round 1 before the first chain.
+    if (worker) {
+        fetch_round(0);
+        stage(0);
+        if (rounds > 1) fetch_round(1);
+    }
+    if (tid == 0) {
+        L->s[0] = 0.0;
+        L->hit[0] = n;
+    }
+    __syncthreads();
+    if (worker) {
+        prepare(0, 0.0);
+        if (rounds > 1) {
+            stage(1);
+            if (rounds > 2) fetch_round(2);
+        }
+    }
+    __syncthreads();
+    uint32_t r = 0, hit = n;
+    while (true) {
+        if (!worker) {
+            // The chain of round r; lane c holds chunk c's record. From the
+            // current chunk on, the chunks on the sum's grid without a tie add
+            // their steps (a scan); the first one whose end leaves the binade
+            // or meets pred, or whose record does not apply, stops the run, and
+            // is added by wave_walk or seq_walk (or by its record, when only a
+            // tie stopped it).
+            __builtin_amdgcn_s_setprio(2);  // the round's critical path
+            const uint32_t b = r & 1u;
+            double s = L->s[b];
             const uint32_t nr = min(CR_ROUND, chunks - r * CR_ROUND);
             const bool lr = lane < nr;
-            const int32_t rux = lr ? L->uexp[lane] : INT32_MIN;
-            const uint32_t rbits = lr ? L->bits[lane] : 0u;
-            const double rbase = lr ? L->base[lane] : 0.0;
+            const int32_t rux = lr ? L->uexp[b][lane] : INT32_MIN;
+            const uint32_t rbits = lr ? L->bits[b][lane] : 0u;
+            const double rbase = lr ? L->base[b][lane] : 0.0;
             uint32_t c = 0;
             while (c < nr) {
                 if (s > 0.0) {
@@ -1002,9 +1034,9 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
                     }
                     if (__builtin_amdgcn_readlane(rux, (int)c) == g.uexp) {
                         // Only a tie stopped it: the record with the parity.
-                        const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)rbits, (int)c);
+                        const uint32_t bb = (uint32_t)__builtin_amdgcn_readlane((int)rbits, (int)c);
                         const double inc = read_lane_f64(rbase, c) +
-                                           ((b & 1u) ? (double)(((uint32_t)(g.n & 1u) ^ (b >> 1)) & 1u) : 0.0);
+                                           ((bb & 1u) ? (double)(((uint32_t)(g.n & 1u) ^ (bb >> 1)) & 1u) : 0.0);
                         if (inc < room) {
                             const double e = scaled(g.n + (uint64_t)inc, g.uexp);
                             if (!pred(e)) {
@@ -1019,27 +1051,39 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
                 const uint32_t len = min(CR_CH, n - start_j);
                 // A chunk that at least quadruples the sum (or starts it) leaves
                 // two binades or more: term by term; else by wave passes.
-                const double cf = L->fsum[c];
+                const double cf = L->fsum[r % 3][c];
                 const uint32_t j = (!(s > 0.0) || cf >= 3.0 * s)
-                                       ? seq_walk<P>(&L->terms[c * CR_CH], len, pred, s)
-                                       : wave_walk<P, CR_CH / 64>(&L->terms[c * CR_CH], len, pred, s);
+                                       ? seq_walk<P>(&L->terms[b][c * CR_CH], len, pred, s)
+                                       : wave_walk<P, CR_CH / 64>(&L->terms[b][c * CR_CH], len, pred, s);
                 if (j < len) {
                     hit = start_j + j;
                     break;
                 }
                 ++c;
             }
+            __builtin_amdgcn_s_setprio(0);
             if (lane == 0) {
-                L->s = s;
-                L->hit = hit;
+                L->s[b ^ 1u] = s;
+                L->hit[b ^ 1u] = hit;
+            }
+        } else if (r + 1 < rounds) {
+            // Round r + 1 from round r's exact start and its chunk sums; then
+            // the sums of round r + 2 and the loads of round r + 3.
+            const double tot = wave_total_f64(lane < CR_ROUND ? L->fsum[r % 3][lane] : 0.0);
+            prepare(r + 1, L->s[r & 1u] + tot);
+            if (r + 2 < rounds) {
+                stage(r + 2);
+                if (r + 3 < rounds) fetch_round(r + 3);
             }
         }
         __syncthreads();
-        s = L->s;
-        hit = L->hit;
+        ++r;
+        hit = L->hit[r & 1u];
+        if (hit != n || r == rounds) break;
     }
-    if (staged) *staged = (uint32_t)min((uint64_t)n, (uint64_t)r * CR_TERMS);
-    *sum = s;
+    // Rounds 0 .. r were stored to wb (those below rounds).
+    if (staged) *staged = (uint32_t)min((uint64_t)n, (uint64_t)(r + 1) * CR_TERMS);
+    *sum = L->s[r & 1u];
     return hit;
 }
 #endif  // __HIPCC__
