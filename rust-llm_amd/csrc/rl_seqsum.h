@@ -40,6 +40,8 @@
 #include <string.h>
 
 #if defined(__HIPCC__)
+#include <type_traits>
+
 #include "rl_device.h"
 #define RL_HD __host__ __device__
 #else
@@ -97,6 +99,30 @@ RL_HD inline SumSeg seg_of(double s) {
         g.lim = 1ull << P;
     }
     g.n = (uint64_t)mul_pow2(s, -g.uexp);
+    return g;
+}
+
+// The same segment with the step count and its limit held as f64 values:
+// integers below 2^54, exact, so that sums of step counts below the room stay
+// exact with no 64-bit integer conversions (which the device does in software).
+struct SumSegF {
+    int uexp;
+    double n;
+    double lim;
+};
+
+template <int P>
+RL_HD inline SumSegF segf_of(double s) {
+    SumSegF g;
+    const int E = (int)((f64_bits(s) >> 52) & 0x7FF) - 1023;  // s is a normal double here
+    if (P == 24 && E < -126) {
+        g.uexp = -149;
+        g.lim = 0x1p23;
+    } else {
+        g.uexp = E - (P - 1);
+        g.lim = P == 24 ? 0x1p24 : 0x1p53;
+    }
+    g.n = mul_pow2(s, -g.uexp);
     return g;
 }
 
@@ -767,7 +793,7 @@ __device__ __forceinline__ uint32_t wave_walk(RL_LDS const uint32_t *t, uint32_t
             pos = j + 1;
             continue;
         }
-        const SumSeg g = seg_of<P>(s);
+        const SumSegF g = segf_of<P>(s);
         const double scale = mul_pow2(1.0, -g.uexp);
         StepRun r = run_identity();
 #pragma unroll
@@ -776,21 +802,21 @@ __device__ __forceinline__ uint32_t wave_walk(RL_LDS const uint32_t *t, uint32_t
         const uint64_t T = __ballot(r.tie != 0), O = __ballot(run_par(r) != 0);
         uint32_t dep;
         const uint32_t k = parity_in(T, O, lane, &dep);
-        const uint32_t pl = dep ? ((uint32_t)(g.n & 1u) ^ k) : k;  // the parity entering this lane's terms
+        const uint32_t pl = dep ? (parity_of(g.n) ^ k) : k;  // the parity entering this lane's terms
         const double mine = r.base + (r.tie ? (double)((pl ^ r.c) & 1u) : 0.0);
         const double before = wave_excl_f64(mine);  // exact below the room, where it is used
-        const double room = (double)(g.lim - g.n);
+        const double room = g.lim - g.n;
         const double upto = before + mine;
-        const bool ev = !(upto < room) || pred(scaled(g.n + (uint64_t)upto, g.uexp));
+        const bool ev = !(upto < room) || pred(mul_pow2(g.n + upto, g.uexp));
         const uint64_t evm = __ballot(ev);
         if (evm == 0) {
-            s = scaled(g.n + (uint64_t)read_lane_f64(upto, 63), g.uexp);
+            s = mul_pow2(g.n + read_lane_f64(upto, 63), g.uexp);
             return len;
         }
         // The first lane holding an event steps through its terms.
         const uint32_t l = (uint32_t)__builtin_ctzll(evm);
-        uint64_t nn = g.n + (uint64_t)read_lane_f64(before, l);
-        uint32_t par = (uint32_t)(nn & 1u);
+        double nn = g.n + read_lane_f64(before, l);  // exact: below the room
+        uint32_t par = parity_of(nn);
         bool crossed = false;
 #pragma unroll
         for (uint32_t i = 0; i < WK; ++i) {
@@ -801,63 +827,73 @@ __device__ __forceinline__ uint32_t wave_walk(RL_LDS const uint32_t *t, uint32_t
             const double q = step_of(__uint_as_float(xb), scale, &tie);
             const uint32_t pq = parity_of(q);
             const double step = tie ? q + (double)(par ^ pq) : q;
-            if ((double)nn + step >= (double)g.lim) {
+            if (nn + step >= g.lim) {
                 // This term leaves the binade: the IEEE addition, then a new
                 // segment from the next term.
-                s = add_p<P>(scaled(nn, g.uexp), __uint_as_float(xb));
+                s = add_p<P>(mul_pow2(nn, g.uexp), __uint_as_float(xb));
                 if (pred(s)) return j;
                 pos = j + 1;
                 crossed = true;
                 continue;
             }
-            nn += (uint64_t)step;
+            nn += step;
             par = tie ? 0u : (par ^ pq);
-            if (pred(scaled(nn, g.uexp))) {
-                s = scaled(nn, g.uexp);
+            if (pred(mul_pow2(nn, g.uexp))) {
+                s = mul_pow2(nn, g.uexp);
                 return j;
             }
         }
         if (!crossed) {  // not reached: the lane's event is in its terms
-            s = scaled(nn, g.uexp);
+            s = mul_pow2(nn, g.uexp);
             pos = (l + 1) * WK;
         }
     }
 }
 
-// The same as wave_walk, one term after another (every lane alike), four
-// additions between tests of pred (the partial sums only grow, so pred met
-// by the fourth is met first by one of them). t must be 16-byte aligned; the
-// words past len up to the next multiple of 4 are read and ignored. For a
-// chunk whose sum leaves several binades this is cheaper than a wave pass
-// per binade.
+// The same as wave_walk, one term after another (every lane alike), in
+// blocks of SW_BLOCK terms: the next block's 16-byte LDS reads are issued
+// before this block's additions, and pred is tested on a block's last sum
+// first (the partial sums only grow, so a block whose last sum fails pred
+// holds no hit). f32 sums run in f32 registers (the same IEEE additions,
+// with no conversions on the dependency chain). t must be 16-byte aligned;
+// the words past len up to the next multiple of SW_BLOCK are read and
+// ignored. For a chunk whose sum leaves several binades this is cheaper than
+// a wave pass per binade.
+constexpr uint32_t SW_BLOCK = 16;
+
 template <int P, class Pred>
 __device__ __forceinline__ uint32_t seq_walk(RL_LDS const uint32_t *t, uint32_t len, Pred pred, double &s) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    for (uint32_t j = 0; j < len; j += 4) {
-        const u32x4 q = *(RL_LDS const u32x4 *)&t[j];
-        const float x0 = __uint_as_float(q[0]);
-        const float x1 = j + 1 < len ? __uint_as_float(q[1]) : 0.0f;
-        const float x2 = j + 2 < len ? __uint_as_float(q[2]) : 0.0f;
-        const float x3 = j + 3 < len ? __uint_as_float(q[3]) : 0.0f;
-        const double a0 = add_p<P>(s, x0), a1 = add_p<P>(a0, x1), a2 = add_p<P>(a1, x2), a3 = add_p<P>(a2, x3);
-        if (pred(a3)) {
-            if (pred(a0)) {
-                s = a0;
-                return j;
-            }
-            if (pred(a1)) {
-                s = a1;
-                return j + 1;
-            }
-            if (pred(a2)) {
-                s = a2;
-                return j + 2;
-            }
-            s = a3;
-            return j + 3;
+    typedef typename std::conditional<P == 24, float, double>::type acc_t;
+    u32x4 nq[SW_BLOCK / 4];
+#pragma unroll
+    for (uint32_t q = 0; q < SW_BLOCK / 4; ++q) nq[q] = *(RL_LDS const u32x4 *)&t[4 * q];
+    acc_t run = (acc_t)s;  // s is a P-bit value: exact
+    for (uint32_t j = 0; j < len; j += SW_BLOCK) {
+        float x[SW_BLOCK];
+#pragma unroll
+        for (uint32_t q = 0; q < SW_BLOCK / 4; ++q)
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) x[4 * q + i] = j + 4 * q + i < len ? __uint_as_float(nq[q][i]) : 0.0f;
+        if (j + SW_BLOCK < len) {
+#pragma unroll
+            for (uint32_t q = 0; q < SW_BLOCK / 4; ++q) nq[q] = *(RL_LDS const u32x4 *)&t[j + SW_BLOCK + 4 * q];
         }
-        s = a3;
+        acc_t a[SW_BLOCK];
+        a[0] = run + (acc_t)x[0];
+#pragma unroll
+        for (uint32_t i = 1; i < SW_BLOCK; ++i) a[i] = a[i - 1] + (acc_t)x[i];
+        if (pred((double)a[SW_BLOCK - 1])) {
+#pragma unroll
+            for (uint32_t i = 0; i < SW_BLOCK; ++i)
+                if (pred((double)a[i])) {
+                    s = (double)a[i];
+                    return j + i;
+                }
+        }
+        run = a[SW_BLOCK - 1];
     }
+    s = (double)run;
     return len;
 }
 
@@ -1020,15 +1056,15 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
             uint32_t c = 0;
             while (c < nr) {
                 if (s > 0.0) {
-                    const SumSeg g = seg_of<P>(s);
-                    const double room = (double)(g.lim - g.n);
+                    const SumSegF g = segf_of<P>(s);
+                    const double room = g.lim - g.n;
                     const bool ok = lane >= c && lr && rux == g.uexp && !(rbits & 1u);
                     const double incl = wave_incl_f64(ok ? rbase : 0.0);
-                    const bool good = ok && incl < room && !pred(scaled(g.n + (uint64_t)incl, g.uexp));
+                    const bool good = ok && incl < room && !pred(mul_pow2(g.n + incl, g.uexp));
                     const uint64_t stopm = __ballot(lane >= c && lr && !good);
                     const uint32_t f = stopm ? (uint32_t)__builtin_ctzll(stopm) : nr;
                     if (f > c) {
-                        s = scaled(g.n + (uint64_t)read_lane_f64(incl, f - 1), g.uexp);
+                        s = mul_pow2(g.n + read_lane_f64(incl, f - 1), g.uexp);
                         c = f;
                         continue;
                     }
@@ -1036,9 +1072,9 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
                         // Only a tie stopped it: the record with the parity.
                         const uint32_t bb = (uint32_t)__builtin_amdgcn_readlane((int)rbits, (int)c);
                         const double inc = read_lane_f64(rbase, c) +
-                                           ((bb & 1u) ? (double)(((uint32_t)(g.n & 1u) ^ (bb >> 1)) & 1u) : 0.0);
+                                           ((bb & 1u) ? (double)((parity_of(g.n) ^ (bb >> 1)) & 1u) : 0.0);
                         if (inc < room) {
-                            const double e = scaled(g.n + (uint64_t)inc, g.uexp);
+                            const double e = mul_pow2(g.n + inc, g.uexp);
                             if (!pred(e)) {
                                 s = e;
                                 ++c;
