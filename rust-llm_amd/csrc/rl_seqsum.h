@@ -357,19 +357,33 @@ __device__ __forceinline__ int wave_min_i32(int v) {
     return v;
 }
 
-// Exclusive scans across the wave (lane i gets lanes 0..i-1, lane 0 gets 0),
-// for the passes that locate an event. The sum for lane i never includes lane
-// i's own value, which may be far larger (a capped step count): the sums of
-// the lanes before an event stay exact.
-__device__ __forceinline__ double wave_excl_f64(double v) {
-    const uint32_t lane = __lane_id();
-    for (int d = 1; d < 64; d <<= 1) {
-        const double o = f64_from_bits(shfl_up_u64(f64_bits(v), d));
-        if (lane >= (uint32_t)d) v += o;
-    }
-    const double e = f64_from_bits(shfl_up_u64(f64_bits(v), 1));
-    return lane == 0 ? 0.0 : e;
+// Scans across the wave with DPP (VALU operations, no LDS round trip). The
+// inclusive scan adds within each row of 16 lanes the values 1, 2, 4 and 8
+// lanes back (row_shr), then rows 1 and 3 add the last lane of rows 0 and 2
+// (row_bcast:15) and rows 2 and 3 add lane 31 (row_bcast:31); a lane a shift
+// reads from outside its row, or a row the mask leaves out, adds +0. The
+// exclusive scan shifts the wave by one lane first (wave_shr:1; lane 0 gets
+// +0), so the sum for lane i never includes lane i's own value, which may be
+// far larger (a capped step count): the sums of the lanes before an event
+// stay exact. Both add integers (or values whose every partial sum is
+// exact), so the order of the additions does not change the result.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t b = f64_bits(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROWS, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROWS, 0xF, false);
+    return f64_from_bits(((uint64_t)hi << 32) | lo);
 }
+__device__ __forceinline__ double wave_incl_f64(double v) {
+    v += dpp_f64<0x111, 0xF>(v);  // row_shr:1
+    v += dpp_f64<0x112, 0xF>(v);  // row_shr:2
+    v += dpp_f64<0x114, 0xF>(v);  // row_shr:4
+    v += dpp_f64<0x118, 0xF>(v);  // row_shr:8
+    v += dpp_f64<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_f64<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+__device__ __forceinline__ double wave_excl_f64(double v) { return wave_incl_f64(dpp_f64<0x138, 0xF>(v)); }
 
 // The workgroup's barrier, or (WAVE_ONLY) the wave's own LDS sync.
 template <bool WAVE_ONLY>
@@ -739,16 +753,6 @@ __device__ __forceinline__ double half_total_f64(double v) {
     return v;
 }
 
-// Inclusive scan of v over the wave's lanes.
-__device__ __forceinline__ double wave_incl_f64(double v) {
-    const uint32_t lane = __lane_id();
-    for (int d = 1; d < 64; d <<= 1) {
-        const double o = f64_from_bits(shfl_up_u64(f64_bits(v), d));
-        if (lane >= (uint32_t)d) v += o;
-    }
-    return v;
-}
-
 __device__ __forceinline__ double read_lane_f64(double v, uint32_t l) {
     const uint64_t b = f64_bits(v);
     return f64_from_bits(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), (int)l) << 32) |
@@ -984,9 +988,8 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
                                                        4u * (r * CR_TERMS + wt * CR_ITEMS) + 16u * q, 0, 0);
         }
         const double pre = wave_excl_f64(lane < CR_ROUND ? L->fsum[r % 3][lane] : 0.0);
-        const double start =
-            s_round + f64_from_bits(((uint64_t)(uint32_t)__shfl((int)(uint32_t)(f64_bits(pre) >> 32), (int)my) << 32) |
-                                    (uint32_t)__shfl((int)(uint32_t)f64_bits(pre), (int)my));
+        const uint32_t c0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(my - half));  // the wave's first chunk
+        const double start = s_round + (half ? read_lane_f64(pre, c0 + 1) : read_lane_f64(pre, c0));
         const bool rec = start > 0.0;
         const int32_t ux = rec ? seg_of<P>(start).uexp : INT32_MIN;
         const double scale = rec ? mul_pow2(1.0, -ux) : 1.0;
