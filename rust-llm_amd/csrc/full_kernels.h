@@ -264,11 +264,7 @@ __device__ __forceinline__ bool finish_wave(const RowIO &a, uint32_t row, const 
             const int e = in ? f32_exponent(p) : 1 << 20;
             const int emin = (int)uniform_u32((uint32_t)wave_min_i32(e));
             if (emin >= -23) {
-                double cum = in ? (double)p : 0.0;
-                for (uint32_t d = 1; d < WAVE; d <<= 1) {
-                    const double o = f64_from_bits(shfl_up_u64(f64_bits(cum), (int)d));
-                    if (lane >= d) cum += o;
-                }
+                const double cum = wave_incl_f64(in ? (double)p : 0.0);
                 const uint64_t lo = ballot(in && cum >= t_lo), hi = ballot(in && cum >= t_hi);
                 j_lo = lo ? (uint32_t)__ffsll((unsigned long long)lo) - 1u : c;
                 j_hi = hi ? (uint32_t)__ffsll((unsigned long long)hi) - 1u : c;
@@ -525,12 +521,8 @@ __global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScra
     // buffer sends the row to k_full_rest.
     auto append = [&](uint64_t mb, auto id_of) {
         const uint32_t mine = (uint32_t)__popcll(mb);
-        uint32_t incl = mine;
-        for (uint32_t d = 1; d < WAVE; d <<= 1) {
-            const uint32_t o = (uint32_t)__shfl_up((int)incl, d);
-            if (lane >= d) incl += o;
-        }
-        const uint32_t wtotal = (uint32_t)__shfl((int)incl, WAVE - 1);
+        const uint32_t incl = wave_incl_u32(mine);
+        const uint32_t wtotal = (uint32_t)__builtin_amdgcn_readlane((int)incl, WAVE - 1);
         uint32_t base = 0;
         if (lane == 0) base = atomicAdd((uint32_t *)&sh_cn, wtotal);
         base = uniform_u32((uint32_t)__shfl((int)base, 0));
@@ -779,12 +771,8 @@ __global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScra
     const uint32_t nc = (uint32_t)(rec >> 32);  // chunk lane's listed candidates, or LIST_OVER
     const bool lover = ballot(nc == LIST_OVER) != 0;
     // How many candidates all chunks listed.
-    uint32_t incl = nc == LIST_OVER ? 0u : nc;
-    for (uint32_t d = 1; d < WAVE; d <<= 1) {
-        const uint32_t o = (uint32_t)__shfl_up((int)incl, d);
-        if (lane >= d) incl += o;
-    }
-    const uint32_t nlist = uniform_u32((uint32_t)__shfl((int)incl, WAVE - 1));
+    const uint32_t incl = wave_incl_u32(nc == LIST_OVER ? 0u : nc);
+    const uint32_t nlist = (uint32_t)__builtin_amdgcn_readlane((int)incl, WAVE - 1);
     if (wave == 0 && okc) red_cnt[lane] = nc == LIST_OVER ? 0u : nc;
     const float M = uniform_f32(wave_maxnum_f32(Mr));
     for (int m = 32; m >= 1; m >>= 1) fi = min(fi, (uint32_t)__shfl_xor((int)fi, m));

@@ -122,10 +122,12 @@ __device__ __forceinline__ int64_t block_max_i64(int64_t v, RL_LDS int64_t *red)
 template <uint32_t NT, class T>
 __device__ __forceinline__ T block_exclusive(T v, RL_LDS T *red, T *total) {
     const uint32_t lane = lane_id(), wave = threadIdx.x / WAVE;
-    T incl = v;
-    for (uint32_t d = 1; d < WAVE; d <<= 1) {
-        const T o = __shfl_up(incl, d);
-        if (lane >= d) incl += o;
+    T incl;
+    if constexpr (std::is_same<T, double>::value) {
+        incl = wave_incl_f64(v);
+    } else {
+        static_assert(std::is_same<T, uint32_t>::value, "u32 or f64");
+        incl = wave_incl_u32(v);
     }
     __syncthreads();
     if (lane == WAVE - 1) red[wave] = incl;
@@ -381,12 +383,7 @@ __device__ __forceinline__ void digit_prefix(RL_LDS const uint32_t *src, RL_LDS 
         v[q] = src[4 * lane + q];
         sum += v[q];
     }
-    uint32_t incl = sum;
-    for (uint32_t d = 1; d < WAVE; d <<= 1) {
-        const uint32_t o = (uint32_t)__shfl_up((int)incl, d);
-        if (lane >= d) incl += o;
-    }
-    uint32_t run = incl - sum;
+    uint32_t run = wave_incl_u32(sum) - sum;
 #pragma unroll
     for (uint32_t q = 0; q < 4; ++q) {
         dst[4 * lane + q] = run;

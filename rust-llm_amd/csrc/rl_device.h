@@ -151,6 +151,21 @@ __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
     return v;
 }
 
+// Inclusive scan of v over the wave with DPP (VALU operations, no LDS round
+// trip): within each row of 16 lanes the values 1, 2, 4 and 8 lanes back
+// (row_shr), then rows 1 and 3 add the last lane of rows 0 and 2
+// (row_bcast:15) and rows 2 and 3 add lane 31 (row_bcast:31); a lane a shift
+// reads from outside its row, or a row the mask leaves out, adds 0.
+__device__ __forceinline__ uint32_t wave_incl_u32(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);  // row_shr:1
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);  // row_shr:2
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);  // row_shr:8
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);  // row_bcast:31
+    return v;
+}
+
 // One compare-exchange stage of a bitonic network across the wave: lanes i
 // and i^STRIDE, blocks of SIZE lanes alternately descending and ascending
 // (the final SIZE = 64 block runs in the direction DESC).
