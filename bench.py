@@ -500,7 +500,7 @@ def main():
     else:  # the logits once, and a token (and a probability) per row
         alg_bytes = wl.rows * (wl.vocab * 4 + 4 + (4 if args.op == "top_probability" else 0))
     achieved = alg_bytes / (mean_ms / 1e3) / 1e9
-    print("[bench] %s: wall %.3f ms/step, events %.3f ms per call over the timed region; alone: median %.3f min %.3f max %.3f ms" % (
+    print("[bench] %s: wall %.4f ms/step, events %.4f ms per call over the timed region; alone: median %.4f min %.4f max %.4f ms" % (
         name, ms_per_step, mean_ms, median_ms, per_call_ms[0], per_call_ms[-1]), file=sys.stderr, flush=True)
 
     if args.calibration_copy > 0:

@@ -525,7 +525,7 @@ __global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScra
         const uint32_t wtotal = (uint32_t)__builtin_amdgcn_readlane((int)incl, WAVE - 1);
         uint32_t base = 0;
         if (lane == 0) base = atomicAdd((uint32_t *)&sh_cn, wtotal);
-        base = uniform_u32((uint32_t)__shfl((int)base, 0));
+        base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
         if (base + wtotal > PASS_CAND) {
             // The buffer is full: the row leaves the min-p path, and nothing
             // more is listed (or re-read) for it.

@@ -326,11 +326,6 @@ struct SeqLds {
     double s_new;
 };
 
-__device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v, int d) {
-    return ((uint64_t)(uint32_t)__shfl_up((int)(uint32_t)(v >> 32), d) << 32) |
-           (uint32_t)__shfl_up((int)(uint32_t)v, d);
-}
-
 // Butterfly totals across the wave with DPP and permlane exchanges (VALU
 // operations, no LDS round trip); every lane gets the same total (the f64
 // additions are commutative, so both lanes of a pair compute the same sum).
@@ -1005,7 +1000,11 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
         const double wsum = half_total_f64(rr.base + ((rr.tie && !dep) ? (double)((k ^ rr.c) & 1u) : 0.0));
         uint32_t bits;
         const uint32_t ft = T != 0 ? (uint32_t)__builtin_ctzll(T) : 0u;
-        const uint32_t cf = (uint32_t)__shfl((int)rr.c, (int)(half * 32 + ft));
+        // The first tie's constant, from the lane holding it in each half.
+        const uint32_t T0 = (uint32_t)Tw, T1 = (uint32_t)(Tw >> 32);
+        const uint32_t c_lo = (uint32_t)__builtin_amdgcn_readlane((int)rr.c, T0 ? (int)__builtin_ctz(T0) : 0);
+        const uint32_t c_hi = (uint32_t)__builtin_amdgcn_readlane((int)rr.c, T1 ? 32 + (int)__builtin_ctz(T1) : 32);
+        const uint32_t cf = half ? c_hi : c_lo;
         if (T != 0) {
             uint32_t d0, d1;
             const uint32_t kf = parity_in(T, O, ft, &d0);
