@@ -770,12 +770,13 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
         const uint32_t vary_sign = (has0 ? (c0 ^ c1) : 0u) | (has1 ? (c2 ^ c3) : 0u);
         const uint32_t all_or = (has0 ? c0 : 0u) | (has1 ? c2 : 0u);
         const uint32_t all_and = (has0 ? c1 : 0xFFFFFFFFu) & (has1 ? c3 : 0xFFFFFFFFu);
-        uint32_t passes[4], np = 0, pass_mask = 0;
+        // The digits to sort on, as a bit mask (digit t: bit t), lowest first.
+        uint32_t pass_mask = 0;
         for (uint32_t t = 0; t < 3; ++t)
-            if (((vary_sign >> (8 * t)) & 255u) != 0) passes[np++] = t;
-        if (((all_or ^ all_and) >> 24) != 0) passes[np++] = 3;
-        for (uint32_t i = 0; i < np; ++i) pass_mask |= 1u << passes[i];
-        if (np > 0 && passes[0] < 2) rest_histograms(L, r, 1, 0, false);
+            if (((vary_sign >> (8 * t)) & 255u) != 0) pass_mask |= 1u << t;
+        if (((all_or ^ all_and) >> 24) != 0) pass_mask |= 8u;
+        uint32_t np = (uint32_t)__builtin_popcount(pass_mask);
+        if ((pass_mask & 3u) != 0) rest_histograms(L, r, 1, 0, false);
         if (np == 0) {
             rest_direct(L, r, etab, fid, fp);
         } else {
@@ -811,21 +812,24 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
                                              min_p, SH, pkd);
                 np = 0;  // done
             }
+            uint32_t left = np ? pass_mask : 0u;  // the digits still to sort on
             for (uint32_t i = 0; i < np; ++i) {
                 const bool last = i + 1 == np;
+                const uint32_t t = (uint32_t)__builtin_ctz(left);
+                left &= left - 1u;
                 uint32_t *ko = (i & 1) ? keyB : keyA, *io = (i & 1) ? idB : idA;
                 if (i == 0 && last)
-                    rest_pass<true, true>(L, r, etab, passes[i], V, hot, fid, nullptr, nullptr, nullptr, fid, fp,
-                                          ps, min_p, SH);
+                    rest_pass<true, true>(L, r, etab, t, V, hot, fid, nullptr, nullptr, nullptr, fid, fp, ps, min_p,
+                                          SH);
                 else if (i == 0)
-                    rest_pass<true, false>(L, r, etab, passes[i], V, hot, fid, nullptr, nullptr, ko, io, nullptr,
-                                           ps, min_p, SH);
+                    rest_pass<true, false>(L, r, etab, t, V, hot, fid, nullptr, nullptr, ko, io, nullptr, ps, min_p,
+                                           SH);
                 else if (last)
-                    rest_pass<false, true>(L, r, etab, passes[i], n1, hot, nullptr, kin, iin, nullptr, fid,
-                                           fp, ps, min_p, SH);
+                    rest_pass<false, true>(L, r, etab, t, n1, hot, nullptr, kin, iin, nullptr, fid, fp, ps, min_p,
+                                           SH);
                 else
-                    rest_pass<false, false>(L, r, etab, passes[i], n1, hot, nullptr, kin, iin, ko, io,
-                                            nullptr, ps, min_p, SH);
+                    rest_pass<false, false>(L, r, etab, t, n1, hot, nullptr, kin, iin, ko, io, nullptr, ps, min_p,
+                                            SH);
                 kin = ko;
                 iin = io;
             }
