@@ -665,7 +665,7 @@ __global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScra
     if (ballot(nan_seen) != 0) S = __builtin_nan("");
     {
         uint32_t fi = first_inf;
-        for (int m = 32; m >= 1; m >>= 1) fi = min(fi, (uint32_t)__shfl_xor((int)fi, m));
+        fi = wave_fold_u32(fi, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
         first_inf = fi;
     }
     if (lane == 0) {
@@ -775,7 +775,7 @@ __global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScra
     const uint32_t nlist = (uint32_t)__builtin_amdgcn_readlane((int)incl, WAVE - 1);
     if (wave == 0 && okc) red_cnt[lane] = nc == LIST_OVER ? 0u : nc;
     const float M = uniform_f32(wave_maxnum_f32(Mr));
-    for (int m = 32; m >= 1; m >>= 1) fi = min(fi, (uint32_t)__shfl_xor((int)fi, m));
+    fi = wave_fold_u32(fi, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
     if (tid == 0) f.arrive[slot] = 0;  // ready for the next call
     const bool finite = M > -__builtin_inff() && M < __builtin_inff();
     if (!finite || !eligible) {
@@ -838,7 +838,7 @@ __global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScra
             }
             take(__hip_atomic_load(list + ch * region_c + K + (i - before), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
         }
-        for (int m = 32; m >= 1; m >>= 1) ns = max(ns, (uint32_t)__shfl_xor((int)ns, m));
+        ns = wave_fold_u32(ns, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
         if (lane == 0 && ns != 0) atomicMax((uint32_t *)&sh_ns, ns);
     }
     __syncthreads();

@@ -94,7 +94,7 @@ __device__ __forceinline__ void bstore(__amdgpu_buffer_rsrc_t r, uint32_t byte_o
 // ------------------------------------------------------ block helpers ---
 template <uint32_t NT>
 __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, RL_LDS uint32_t *red) {
-    for (int m = 32; m >= 1; m >>= 1) v += (uint32_t)__shfl_xor((int)v, m);
+    v = wave_sum_u32(v);
     __syncthreads();
     if (lane_id() == 0) red[threadIdx.x / WAVE] = v;
     __syncthreads();
@@ -105,10 +105,7 @@ __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, RL_LDS uint32_t *r
 
 template <uint32_t NT>
 __device__ __forceinline__ int64_t block_max_i64(int64_t v, RL_LDS int64_t *red) {
-    for (int m = 32; m >= 1; m >>= 1) {
-        const int64_t o = (int64_t)shfl_xor_u64((uint64_t)v, m);
-        v = o > v ? o : v;
-    }
+    v = (int64_t)wave_fold_u64((uint64_t)v, [](uint64_t a, uint64_t b) { return (int64_t)a > (int64_t)b ? a : b; });
     __syncthreads();
     if (lane_id() == 0) red[threadIdx.x / WAVE] = v;
     __syncthreads();
@@ -350,12 +347,10 @@ __device__ __forceinline__ void rest_histograms(RL_LDS RestLds *L, const RestRow
             atomicAdd((uint32_t *)&L->sh_hot_count, nK);
             atomicAdd((uint32_t *)&L->sh_hot_above, nA);
         }
-        for (int m = 32; m >= 1; m >>= 1) {
-            or0 |= (uint32_t)__shfl_xor((int)or0, m);
-            and0 &= (uint32_t)__shfl_xor((int)and0, m);
-            or1 |= (uint32_t)__shfl_xor((int)or1, m);
-            and1 &= (uint32_t)__shfl_xor((int)and1, m);
-        }
+        or0 = wave_fold_u32(or0, [](uint32_t a, uint32_t b) { return a | b; });
+        and0 = wave_fold_u32(and0, [](uint32_t a, uint32_t b) { return a & b; });
+        or1 = wave_fold_u32(or1, [](uint32_t a, uint32_t b) { return a | b; });
+        and1 = wave_fold_u32(and1, [](uint32_t a, uint32_t b) { return a & b; });
         if (lane == 0) {
             atomicOr((uint32_t *)&L->cls[0], or0);
             atomicAnd((uint32_t *)&L->cls[1], and0);
@@ -412,13 +407,11 @@ struct PStats {
     // Folds the wave's shares into L's (lane 0 adds them with LDS atomics,
     // after L's were set by stats_reset and a barrier).
     __device__ __forceinline__ void merge(RL_LDS RestLds *L) {
-        for (int m = 32; m >= 1; m >>= 1) {
-            emin = min(emin, __shfl_xor(emin, m));
-            bad |= (uint32_t)__shfl_xor((int)bad, m);
-            count += (uint32_t)__shfl_xor((int)count, m);
-            last_in = max(last_in, (uint32_t)__shfl_xor((int)last_in, m));
-            first_out = min(first_out, (uint32_t)__shfl_xor((int)first_out, m));
-        }
+        emin = (int)wave_fold_u32((uint32_t)emin, [](uint32_t a, uint32_t b) { return (int)a < (int)b ? a : b; });
+        bad = wave_fold_u32(bad, [](uint32_t a, uint32_t b) { return a | b; });
+        count = wave_sum_u32(count);
+        last_in = wave_fold_u32(last_in, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+        first_out = wave_fold_u32(first_out, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
         if (lane_id() == 0) {
             atomicMin((int *)&L->st_emin, emin);
             atomicOr((uint32_t *)&L->st_bad, bad);

@@ -46,6 +46,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "rl_device.h"
+
 namespace rl {
 
 constexpr int QK = 256;              // values per quantization block (quant.rs:12)
@@ -141,7 +143,7 @@ __device__ inline float quantize_block_wave(const float *__restrict__ src, uint3
     for (int e = 0; e < 4; ++e) v[e] = 4 * lane + e < valid ? src[4 * lane + e] : 0.0f;
     float amax = 0.0f;
     for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(v[e]));
-    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    amax = wave_maxnum_f32(amax);
     const float d = amax / 127.0f;
     const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
     int q[4];
@@ -151,8 +153,8 @@ __device__ inline float quantize_block_wave(const float *__restrict__ src, uint3
         packed |= ((uint32_t)q[e] & 0xFF) << (8 * e);
     }
     bsum = q[0] + q[1] + q[2] + q[3];
-    bsum += __shfl_xor(bsum, 1);
-    bsum += __shfl_xor(bsum, 2);
+    bsum += (int)lane_xor<1>((uint32_t)bsum);
+    bsum += (int)lane_xor<2>((uint32_t)bsum);
     return d;
 }
 
@@ -635,8 +637,8 @@ void k_head_dot(const uint4 *__restrict__ wq, const uint32_t *__restrict__ ws, c
 #pragma unroll
             for (int tt = 0; tt < T; ++tt) {
                 int v = isum[tt];
-                v += __shfl_xor(v, 16);
-                v += __shfl_xor(v, 32);
+                v += (int)lane_xor<16>((uint32_t)v);
+                v += (int)lane_xor<32>((uint32_t)v);
                 const float scale = adv[tt] * dw;
                 sum[tw][tt] = sum[tw][tt] + scale * (float)v;
             }

@@ -87,25 +87,6 @@ __device__ __forceinline__ float read_lane_f32(float v, uint32_t lane) {
     return __uint_as_float(read_lane_u32(__float_as_uint(v), lane));
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m);
-    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m);
-    return ((uint64_t)hi << 32) | lo;
-}
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-    for (int m = 32; m >= 1; m >>= 1) {
-        const uint64_t o = shfl_xor_u64(v, m);
-        v = o > v ? o : v;
-    }
-    return v;
-}
-
-__device__ __forceinline__ float wave_maxnum_f32(float v) {
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
-    return v;
-}
-
 // Lane exchange: lane i receives v from lane i ^ S, using DPP row operations
 // for S <= 8 and the gfx950 permlane swaps for 16 and 32 (VALU ops, no LDS
 // round trip). Lane layouts as measured on gfx950: quad_perm [1,0,3,2] and
@@ -138,6 +119,52 @@ __device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
 template <uint32_t S>
 __device__ __forceinline__ uint64_t lane_xor64(uint64_t v) {
     return ((uint64_t)lane_xor<S>((uint32_t)(v >> 32)) << 32) | lane_xor<S>((uint32_t)v);
+}
+
+// v combined by op with the values of the lanes i ^ 32, i ^ 16, ..., i ^ 1 in
+// turn (every lane gets the result; the same order as a shuffle butterfly
+// from 32 down).
+template <class Op>
+__device__ __forceinline__ uint32_t wave_fold_u32(uint32_t v, Op op) {
+    v = op(v, lane_xor<32>(v));
+    v = op(v, lane_xor<16>(v));
+    v = op(v, lane_xor<8>(v));
+    v = op(v, lane_xor<4>(v));
+    v = op(v, lane_xor<2>(v));
+    v = op(v, lane_xor<1>(v));
+    return v;
+}
+template <class Op>
+__device__ __forceinline__ uint64_t wave_fold_u64(uint64_t v, Op op) {
+    v = op(v, lane_xor64<32>(v));
+    v = op(v, lane_xor64<16>(v));
+    v = op(v, lane_xor64<8>(v));
+    v = op(v, lane_xor64<4>(v));
+    v = op(v, lane_xor64<2>(v));
+    v = op(v, lane_xor64<1>(v));
+    return v;
+}
+
+// The wave's maximum of v in every lane (butterfly over the lane exchanges;
+// fmaxf ignores a NaN operand, as f32::max does).
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    uint64_t o;
+    o = lane_xor64<32>(v), v = o > v ? o : v;
+    o = lane_xor64<16>(v), v = o > v ? o : v;
+    o = lane_xor64<8>(v), v = o > v ? o : v;
+    o = lane_xor64<4>(v), v = o > v ? o : v;
+    o = lane_xor64<2>(v), v = o > v ? o : v;
+    o = lane_xor64<1>(v), v = o > v ? o : v;
+    return v;
+}
+__device__ __forceinline__ float wave_maxnum_f32(float v) {
+    v = fmaxf(v, __uint_as_float(lane_xor<32>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(lane_xor<16>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(lane_xor<8>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(lane_xor<4>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(lane_xor<2>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(lane_xor<1>(__float_as_uint(v))));
+    return v;
 }
 
 // The wave's total of v in every lane (butterfly over the lane exchanges).

@@ -113,11 +113,14 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_max(const float *logits, ui
             nan |= x != x;
         }
     }
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ov = __shfl_xor(bv, m);
-        const uint32_t oi = (uint32_t)__shfl_xor((int)bi, m);
-        tp_take(bv, bi, ov, oi);
-    }
+    // Butterfly over the lane exchanges, strides 32 down to 1.
+    const auto step = [&](float ov, uint32_t oi) { tp_take(bv, bi, ov, oi); };
+    step(__uint_as_float(lane_xor<32>(__float_as_uint(bv))), lane_xor<32>(bi));
+    step(__uint_as_float(lane_xor<16>(__float_as_uint(bv))), lane_xor<16>(bi));
+    step(__uint_as_float(lane_xor<8>(__float_as_uint(bv))), lane_xor<8>(bi));
+    step(__uint_as_float(lane_xor<4>(__float_as_uint(bv))), lane_xor<4>(bi));
+    step(__uint_as_float(lane_xor<2>(__float_as_uint(bv))), lane_xor<2>(bi));
+    step(__uint_as_float(lane_xor<1>(__float_as_uint(bv))), lane_xor<1>(bi));
     const uint32_t anynan = ballot(nan) != 0 ? 1u : 0u;
     const uint32_t wave = threadIdx.x / WAVE;
     if (lane_id() == 0) {
@@ -223,7 +226,14 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
         const uint32_t e = 4 * n4 + threadIdx.x;
         if (e < vocab) add(sum, ((const RL_GLB float *)rowp)[e]);
     }
-    for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m);
+    // Butterfly over the lane exchanges, strides 32 down to 1 (f64 additions
+    // in the same order as a shuffle butterfly).
+    sum += lane_xor_f64<32>(sum);
+    sum += lane_xor_f64<16>(sum);
+    sum += lane_xor_f64<8>(sum);
+    sum += lane_xor_f64<4>(sum);
+    sum += lane_xor_f64<2>(sum);
+    sum += lane_xor_f64<1>(sum);
     small = wave_sum_u32(small);
     const uint32_t wave = threadIdx.x / WAVE;
     if (lane_id() == 0) {
