@@ -20,14 +20,14 @@ struct rl_head {
     uint4 *wq = nullptr;
     uint32_t *ws = nullptr;
     uint16_t *wd = nullptr;
-    int8_t *aq = nullptr;   // activation quants [tcap][nb][256]
     float *ad = nullptr;    // activation scales [tcap][nb]
+    uint4 *af = nullptr;    // activation fragments [tcap / 16][nb][HEAD_FRAG_UINT4]
     ~rl_head() {
         (void)hipFree(wq);
         (void)hipFree(ws);
         (void)hipFree(wd);
-        (void)hipFree(aq);
         (void)hipFree(ad);
+        (void)hipFree(af);
     }
 };
 
@@ -46,24 +46,25 @@ void launch_head(const rl_head *h, const float *x, uint32_t t0, uint32_t n, floa
                  hipStream_t s) {
     const uint32_t blocks = (h->groups + HEAD_WAVES - 1) / HEAD_WAVES;
     const uint64_t ao = (uint64_t)t0 * h->nb;
+    const uint64_t fo = (uint64_t)(t0 / HEAD_NTILE) * h->nb * HEAD_FRAG_UINT4;  // t0 is a multiple of 32
     if (dot_path(h, n)) {
         auto kern = n == 1 ? k_head_dot<1> : k_head_dot<2>;
         hipLaunchKernelGGL(kern, dim3(blocks), dim3(HEAD_THREADS), dot_lds_bytes(n, h->nb), s, h->wq, h->ws,
                            h->wd, x + (uint64_t)t0 * h->k, h->k, h->nb, h->rows, h->groups, out, stride);
     } else if (n <= HEAD_NTILE) {
         hipLaunchKernelGGL(k_head_mfma_regs<1>, dim3(blocks), dim3(HEAD_THREADS), 0, s, h->wq, h->ws, h->wd,
-                           h->aq + ao * QK, h->ad + ao, n, h->nb, h->rows, h->groups, out, stride);
+                           h->af + fo, h->ad + ao, n, h->nb, h->rows, h->groups, out, stride);
     } else {
         hipLaunchKernelGGL(k_head_mfma_lds<2>, dim3(blocks), dim3(HEAD_THREADS), 0, s, h->wq, h->ws, h->wd,
-                           h->aq + ao * QK, h->ad + ao, n, h->nb, h->rows, h->groups, out, stride);
+                           h->af + fo, h->ad + ao, n, h->nb, h->rows, h->groups, out, stride);
     }
 }
 
 void launch_quantize(const float *x, uint32_t t, uint32_t k, uint32_t nb, float *d, int8_t *qs, int16_t *bs,
-                     hipStream_t s) {
+                     uint4 *frag, hipStream_t s) {
     const uint64_t waves = (uint64_t)t * nb;
     const uint32_t blocks = (uint32_t)((waves + 3) / 4);
-    hipLaunchKernelGGL(k_quantize_rows, dim3(blocks), dim3(256), 0, s, x, t, k, nb, d, qs, bs);
+    hipLaunchKernelGGL(k_quantize_rows, dim3(blocks), dim3(256), 0, s, x, t, k, nb, d, qs, bs, frag);
 }
 
 }  // namespace
@@ -94,12 +95,12 @@ int rl_head_create(int device, uint32_t k, uint32_t rows, uint32_t max_batch, co
     hipError_t e = hipMalloc(&h->wq, bgt * HEAD_QCH * 64 * sizeof(uint4));
     if (e == hipSuccess) e = hipMalloc(&h->ws, bgt * 64 * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&h->wd, bgt * HEAD_TILE * sizeof(uint16_t));
-    if (e == hipSuccess) e = hipMalloc(&h->aq, (uint64_t)h->tcap * nb * QK);
     if (e == hipSuccess) e = hipMalloc(&h->ad, (uint64_t)h->tcap * nb * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&h->af, (uint64_t)(h->tcap / HEAD_NTILE) * nb * HEAD_FRAG_UINT4 * sizeof(uint4));
     // Rows of a column tile past a call's t are read and their products
     // discarded; start them at zero.
-    if (e == hipSuccess) e = hipMemset(h->aq, 0, (uint64_t)h->tcap * nb * QK);
     if (e == hipSuccess) e = hipMemset(h->ad, 0, (uint64_t)h->tcap * nb * sizeof(float));
+    if (e == hipSuccess) e = hipMemset(h->af, 0, (uint64_t)(h->tcap / HEAD_NTILE) * nb * HEAD_FRAG_UINT4 * sizeof(uint4));
     uint8_t *staging = nullptr;
     if (e == hipSuccess) e = hipMalloc(&staging, q6k_bytes);
     if (e == hipSuccess) e = hipMemcpy(staging, q6k, q6k_bytes, hipMemcpyHostToDevice);
@@ -136,7 +137,7 @@ int rl_head_logits(rl_head *h, const float *x, uint32_t t, float *logits, uint64
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const uint32_t per_pass = HEAD_MAX_NT * HEAD_NTILE;
     // The matrix-core passes read the quantized rows; the dot path quantizes its own.
-    if (!dot_path(h, t)) launch_quantize(x, t, h->k, h->nb, h->ad, h->aq, nullptr, s);
+    if (!dot_path(h, t)) launch_quantize(x, t, h->k, h->nb, h->ad, nullptr, nullptr, h->af, s);
     for (uint32_t t0 = 0; t0 < t; t0 += per_pass)
         launch_head(h, x, t0, std::min(per_pass, t - t0), logits + (uint64_t)t0 * row_stride, row_stride, s);
     const hipError_t e = hipGetLastError();
@@ -165,7 +166,7 @@ int rl_quantize_rows(const float *x, uint32_t t, uint32_t k, float *out_d, int8_
     if (t == 0) return RL_OK;
     if (!x || k == 0) return fail(RL_ERR_ARGUMENT, "x must be a device pointer and k positive");
     const uint32_t nb = (k + QK - 1) / QK;
-    launch_quantize(x, t, k, nb, out_d, out_qs, out_bsums, static_cast<hipStream_t>(stream));
+    launch_quantize(x, t, k, nb, out_d, out_qs, out_bsums, nullptr, static_cast<hipStream_t>(stream));
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? RL_OK : hip_fail(e, "rl_quantize_rows launch");
 }

@@ -18,7 +18,8 @@
 // Every operand is an integer an f16 holds exactly (|s_lo (q-32)| <= 480,
 // |s_hi (q-32)| <= 256, |a| <= 127), every product is exact in f32, and every
 // partial sum is an integer below 2^24 (at most 256 * 480 * 127 < 15.7e6), so
-// the accumulation is exact in any order. Then isum = 16 * D_hi + D_lo in i32.
+// the accumulation is exact in any order. Then (float)isum = fl(16 * D_hi +
+// D_lo), one fused multiply-add of the two exact integers.
 //
 // Layouts in HBM (built once by k_q6k_repack from the GGUF bytes), for a
 // vocabulary of `groups` groups of 64 rows, each group four tiles of 16 rows:
@@ -162,12 +163,33 @@ __device__ inline float quantize_block_wave(const float *__restrict__ src, uint3
 // the unpacked weights come out in.
 __device__ inline uint32_t dot_order(uint32_t packed) { return __builtin_amdgcn_perm(packed, packed, 0x03010200u); }
 
+__device__ inline h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
+
+// Four signed int8 activations as two f16 pairs: bytes + 128 under the f16
+// exponent of 1024, minus 1152, exact.
+__device__ inline void act_pairs(uint32_t w, uint32_t &lo, uint32_t &hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    const h2_t bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    lo = __builtin_bit_cast(uint32_t, as_h2(a) + bias);
+    hi = __builtin_bit_cast(uint32_t, as_h2(b) + bias);
+}
+
+// The activation fragments of each 16-row tile and block, the matrix core's B
+// operand in f16 (exact: the quants are integers in [-127, 127]): entry
+// ((tile * nb + ib) * 8 + s) * 64 + 16 h + m holds activation row 16 tile + m,
+// values 64 h + 8 s .. + 7 of block ib, in order.
+constexpr int HEAD_FRAG_UINT4 = 8 * 64;  // uint4 per (tile, block)
+
 // Activations::quantize_batch (quant.rs:337-375). One wave per (row, block).
-// Writes the reference's ActBlock fields; each output may be null.
+// Writes the reference's ActBlock fields and the block's f16 fragments; each
+// output may be null.
 __global__ __launch_bounds__(256) void k_quantize_rows(const float *__restrict__ x, uint32_t t, uint32_t k,
                                                        uint32_t nb, float *__restrict__ out_d,
                                                        int8_t *__restrict__ out_qs,
-                                                       int16_t *__restrict__ out_bsums) {
+                                                       int16_t *__restrict__ out_bsums,
+                                                       uint4 *__restrict__ out_frag) {
     const uint32_t wave = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
     const uint32_t lane = threadIdx.x & 63;
     if (wave >= t * nb) return;
@@ -180,6 +202,18 @@ __global__ __launch_bounds__(256) void k_quantize_rows(const float *__restrict__
     if (out_qs) reinterpret_cast<uint32_t *>(out_qs + blk * QK)[lane] = packed;
     if (out_bsums && (lane & 3) == 0) out_bsums[blk * 16 + lane / 4] = (int16_t)bsum;
     if (out_d && lane == 0) out_d[blk] = d;
+    if (out_frag) {
+        // Values 64 h + 8 s .. + 7 are lanes 16 h + 2 s and the next one's.
+        const uint32_t next = lane_xor<1>(packed);
+        if ((lane & 1) == 0) {
+            uint32_t p0, p1, p2, p3;
+            act_pairs(packed, p0, p1);
+            act_pairs(next, p2, p3);
+            const uint32_t h = lane >> 4, s = (lane & 15) >> 1;
+            out_frag[((uint64_t)(tt >> 4) * nb + ib) * HEAD_FRAG_UINT4 + s * 64 + 16 * h + (tt & 15)] =
+                make_uint4(p0, p1, p2, p3);
+        }
+    }
 }
 
 // ------------------------------------------------------------------- head
@@ -189,7 +223,6 @@ __global__ __launch_bounds__(256) void k_quantize_rows(const float *__restrict__
 __device__ inline int fits24(int v) { return (v << 8) >> 8; }
 
 
-__device__ inline h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
 
 // The masks of the unpacking, held in registers: gfx9 VOP3 takes no literal,
 // so with the constants in registers each field is one v_and_or_b32.
@@ -218,16 +251,6 @@ __device__ inline void unpack_steps(uint32_t p0, uint32_t p1, uint32_t p2, uint3
     x[7] = ((p1 >> 12) & k.m4) | (((p2 >> 10) & k.m2) | k.mag);
 }
 
-// Four signed int8 activations as two f16 pairs: bytes + 128 under the f16
-// exponent of 1024, minus 1152, exact.
-__device__ inline void act_pairs(uint32_t w, uint32_t &lo, uint32_t &hi) {
-    const uint32_t u = w ^ 0x80808080u;
-    const h2_t bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
-    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
-    lo = __builtin_bit_cast(uint32_t, as_h2(a) + bias);
-    hi = __builtin_bit_cast(uint32_t, as_h2(b) + bias);
-}
 
 // One tile's weights for one block: the lane's quant words, scale bytes and the
 // f16 scales of rows 4h .. 4h+3.
@@ -247,43 +270,15 @@ __device__ inline HeadTile load_tile(const uint4 *__restrict__ wq, const uint32_
     return r;
 }
 
-// The activation fragments of one block: row nt*16 + m, bytes 64h .. 64h+63.
+// Copies one block's activation fragments (HEAD_FRAG_UINT4 per column tile,
+// written by k_quantize_rows) into LDS, cooperatively, with the block scale
+// of each activation row.
 template <int NT>
-struct HeadAct {
-    uint4 raw[NT][4];
-    float d[NT];
-};
-
-template <int NT>
-__device__ inline HeadAct<NT> load_act(const int8_t *__restrict__ aq, const float *__restrict__ ad, uint32_t nb,
-                                       uint32_t ib, uint32_t m, uint32_t h) {
-    HeadAct<NT> r;
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const uint64_t arow = (uint64_t)(nt * HEAD_NTILE + m) * nb + ib;
-        const uint4 *ap = reinterpret_cast<const uint4 *>(aq + arow * QK + 64 * h);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) r.raw[nt][c] = ap[c];
-        r.d[nt] = ad[arow];
-    }
-    return r;
-}
-
-// Builds one block's activation fragments in LDS, cooperatively: entry
-// (nt, step s, lane 16h + m) is the f16 fragment of activation row nt*16 + m,
-// values k = 64h + 8s .. +7, as the matrix core's B operand wants it; plus the
-// block scale of each activation row.
-template <int NT>
-__device__ inline void fill_act(uint4 *__restrict__ frag, float *__restrict__ fd, const int8_t *__restrict__ aq,
+__device__ inline void fill_act(uint4 *__restrict__ frag, float *__restrict__ fd, const uint4 *__restrict__ af,
                                 const float *__restrict__ ad, uint32_t nb, uint32_t ib) {
-    for (uint32_t e = threadIdx.x; e < NT * 8 * 64; e += HEAD_THREADS) {
-        const uint32_t nt = e / 512, s = (e / 64) % 8, l = e % 64;
-        const uint32_t n = nt * HEAD_NTILE + (l & 15), hq = l >> 4;
-        const uint2 raw = *reinterpret_cast<const uint2 *>(aq + ((uint64_t)n * nb + ib) * QK + 64 * hq + 8 * s);
-        uint32_t p0, p1, p2, p3;
-        act_pairs(raw.x, p0, p1);
-        act_pairs(raw.y, p2, p3);
-        frag[e] = make_uint4(p0, p1, p2, p3);
+    for (uint32_t e = threadIdx.x; e < NT * HEAD_FRAG_UINT4; e += HEAD_THREADS) {
+        const uint32_t nt = e / HEAD_FRAG_UINT4;
+        frag[e] = af[((uint64_t)nt * nb + ib) * HEAD_FRAG_UINT4 + e % HEAD_FRAG_UINT4];
     }
     if (threadIdx.x < NT * HEAD_NTILE) fd[threadIdx.x] = ad[(uint64_t)threadIdx.x * nb + ib];
 }
@@ -302,7 +297,7 @@ __device__ inline void fill_act(uint4 *__restrict__ frag, float *__restrict__ fd
 template <int NT>
 __global__ __launch_bounds__(HEAD_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
 void k_head_mfma_lds(const uint4 *__restrict__ wq, const uint32_t *__restrict__ ws, const uint16_t *__restrict__ wd,
-                const int8_t *__restrict__ aq, const float *__restrict__ ad, uint32_t t, uint32_t nb,
+                const uint4 *__restrict__ af, const float *__restrict__ ad, uint32_t t, uint32_t nb,
                 uint32_t rows, uint32_t groups, float *__restrict__ out, uint64_t out_stride) {
     __shared__ uint4 stab[256];
     __shared__ uint4 frag[2][NT * 8 * 64];
@@ -317,7 +312,7 @@ void k_head_mfma_lds(const uint4 *__restrict__ wq, const uint32_t *__restrict__ 
         stab[threadIdx.x & 255] = make_uint4(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, clo),
                                              __builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, chi));
     }
-    fill_act<NT>(frag[0], fd[0], aq, ad, nb, 0);
+    fill_act<NT>(frag[0], fd[0], af, ad, nb, 0);
     const uint32_t lane = threadIdx.x & 63;
     // Wave-uniform, so weight addresses are a scalar base plus the lane offset.
     const uint32_t g = __builtin_amdgcn_readfirstlane(blockIdx.x * HEAD_WAVES + threadIdx.x / 64);
@@ -336,7 +331,7 @@ void k_head_mfma_lds(const uint4 *__restrict__ wq, const uint32_t *__restrict__ 
     HeadTile cur = load_tile(wq, ws, wd, (uint64_t)gg * HEAD_TILES, lane, h);
     for (uint32_t ib = 0; ib < nb; ++ib) {
         __syncthreads();  // block ib's fragments are built; block ib - 1's buffer is free
-        if (ib + 1 < nb) fill_act<NT>(frag[(ib + 1) & 1], fd[(ib + 1) & 1], aq, ad, nb, ib + 1);
+        if (ib + 1 < nb) fill_act<NT>(frag[(ib + 1) & 1], fd[(ib + 1) & 1], af, ad, nb, ib + 1);
         const uint4 *bfr = frag[ib & 1];
         float adn[NT];
 #pragma unroll
@@ -387,10 +382,12 @@ void k_head_mfma_lds(const uint4 *__restrict__ wq, const uint32_t *__restrict__ 
             for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int isum = (int)acc_hi[nt][i] * 16 + (int)acc_lo[nt][i];
+                    // (float)isum: 16 D_hi + D_lo is formed exactly (both are
+                    // integers below 2^24) and rounded once.
+                    const float fisum = __builtin_fmaf(acc_hi[nt][i], 16.0f, acc_lo[nt][i]);
                     const float dw = __half2float(__ushort_as_half((uint16_t)(dw2[i >> 1] >> (16 * (i & 1)))));
                     const float scale = adn[nt] * dw;
-                    sum[nt][tw][i] = sum[nt][tw][i] + scale * (float)isum;
+                    sum[nt][tw][i] = sum[nt][tw][i] + scale * fisum;
                 }
             }
             cur = nxt;
@@ -424,7 +421,7 @@ __global__ __launch_bounds__(HEAD_THREADS) __attribute__((amdgpu_waves_per_eu(NT
 void k_head_mfma_regs(const uint4 *__restrict__ wq,
                                                                const uint32_t *__restrict__ ws,
                                                                const uint16_t *__restrict__ wd,
-                                                               const int8_t *__restrict__ aq,
+                                                               const uint4 *__restrict__ af,
                                                                const float *__restrict__ ad, uint32_t t,
                                                                uint32_t nb, uint32_t rows, uint32_t groups,
                                                                float *__restrict__ out, uint64_t out_stride) {
@@ -455,24 +452,15 @@ void k_head_mfma_regs(const uint4 *__restrict__ wq,
     HeadTile cur = load_tile(wq, ws, wd, (uint64_t)g * HEAD_TILES, lane, h);
     for (uint32_t ib = 0; ib < nb; ++ib) {
         const uint32_t nxt_ib = ib + 1 < nb ? ib + 1 : ib;  // the last block re-reads itself (a cache hit)
-        const HeadAct<NT> act = load_act<NT>(aq, ad, nb, ib, m, h);
+        // The block's activation fragments, as k_quantize_rows wrote them.
         h8_t bf[NT][8];
         float adn[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            adn[nt] = act.d[nt];
+            adn[nt] = ad[(uint64_t)(nt * HEAD_NTILE + m) * nb + ib];
+            const uint4 *fp = af + ((uint64_t)nt * nb + ib) * HEAD_FRAG_UINT4 + lane;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const uint32_t w4[4] = {act.raw[nt][c].x, act.raw[nt][c].y, act.raw[nt][c].z, act.raw[nt][c].w};
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {  // step 2c + j: bytes 8 (2c + j) .. +7
-                    uint32_t p0, p1, p2, p3;
-                    act_pairs(w4[2 * j], p0, p1);
-                    act_pairs(w4[2 * j + 1], p2, p3);
-                    const h2_t e0 = as_h2(p0), e1 = as_h2(p1), e2 = as_h2(p2), e3 = as_h2(p3);
-                    bf[nt][2 * c + j] = h8_t{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
-                }
-            }
+            for (int st = 0; st < 8; ++st) bf[nt][st] = __builtin_bit_cast(h8_t, fp[st * 64]);
         }
 #pragma unroll
         for (int tw = 0; tw < HEAD_TILES; ++tw) {
@@ -516,10 +504,12 @@ void k_head_mfma_regs(const uint4 *__restrict__ wq,
             for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int isum = (int)acc_hi[nt][i] * 16 + (int)acc_lo[nt][i];
+                    // (float)isum: 16 D_hi + D_lo is formed exactly (both are
+                    // integers below 2^24) and rounded once.
+                    const float fisum = __builtin_fmaf(acc_hi[nt][i], 16.0f, acc_lo[nt][i]);
                     const float dw = __half2float(__ushort_as_half((uint16_t)(dw2[i >> 1] >> (16 * (i & 1)))));
                     const float scale = adn[nt] * dw;
-                    sum[nt][tw][i] = sum[nt][tw][i] + scale * (float)isum;
+                    sum[nt][tw][i] = sum[nt][tw][i] + scale * fisum;
                 }
             }
             cur = nxt;
