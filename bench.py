@@ -146,8 +146,8 @@ def host_info():
             "libc": " ".join(os.confstr("CS_GNU_LIBC_VERSION").split()) if hasattr(os, "confstr") else None}
 
 
-# A one-GPU box's share of the host's cores: the threaded baseline uses no
-# more threads than this even where the affinity mask shows more CPUs.
+# One GPU's share of a host's cores: the threaded baseline uses no more
+# threads than this even where the affinity mask shows more CPUs.
 GPU_CPU_SHARE = 16
 
 

@@ -3,7 +3,8 @@
 ctypes bindings for liboracle.so, the C restatement of rust-llm's sampler
 (crates/rust-llm/src/sample.rs) and of its tests' naive f64 reference
 (crates/rust-llm/tests/sample.rs:16-83). Only tests/, the smoke check and
-bench.py's CPU-baseline leg import this module, and only as the checker.
+bench.py's CPU-baseline leg import this module, and only to check results
+against (or, in bench.py, to time the CPU baseline).
 """
 import ctypes
 import os
