@@ -55,6 +55,37 @@ __global__ __launch_bounds__(rl::REST_THREADS) void k_chunk_cases(const float *t
     }
 }
 
+// The chunked replay as the sampler's draw runs it: in place (each staged
+// round's terms are stored over its words; the term here doubles the word,
+// exactly), with a range of words [hot_lo, hot_hi) that reads as hot_word
+// whatever memory holds there. out_staged gets the written prefix.
+template <int P>
+__global__ __launch_bounds__(rl::REST_THREADS) void k_chunk_cases_wb(uint32_t *words, const uint64_t *off,
+                                                                     const uint32_t *n, const double *thr,
+                                                                     const uint32_t *mode, const uint32_t *hot_lo,
+                                                                     const uint32_t *hot_hi, const uint32_t *hot_word,
+                                                                     uint32_t *out_idx, double *out_sum,
+                                                                     uint32_t *out_staged) {
+    __shared__ rl::ChunkLds cr_;
+    RL_LDS rl::ChunkLds *cr = (RL_LDS rl::ChunkLds *)&cr_;
+    const uint32_t c = blockIdx.x;
+    uint32_t *x = words + off[c];
+    const CasePred pred{thr[c], mode[c]};
+    rl::HotRange hr;
+    hr.lo = hot_lo[c];
+    hr.hi = hot_hi[c];
+    hr.word = hot_word[c];
+    double sum = -1.0;
+    uint32_t staged = 0xFFFFFFFFu;
+    const uint32_t idx = rl::chunk_replay<P, rl::REST_THREADS>(
+        x, [](uint32_t b) { return 2.0f * __uint_as_float(b); }, n[c], pred, cr, &sum, x, &staged, hr);
+    if (threadIdx.x == 0) {
+        out_idx[c] = idx;
+        out_sum[c] = sum;
+        out_staged[c] = staged;
+    }
+}
+
 template <int P, uint32_t NT, uint32_t ITEMS>
 int launch(const float *terms, const uint64_t *off, const uint32_t *n, const double *thr, const uint32_t *mode,
            uint32_t cases, uint32_t *out_idx, double *out_sum, hipStream_t st) {
@@ -101,4 +132,23 @@ extern "C" int seqsum_gpu_run(int precision, int shape, const float *terms, cons
             return launch<53, rl::TP_FINAL_THREADS, rl::SEQ_ITEMS>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
     }
     return -1;
+}
+
+// The in-place chunked replay with a hot range (k_chunk_cases_wb); words is
+// device memory that the call overwrites.
+extern "C" int seqsum_gpu_run_wb(int precision, uint32_t *words, const uint64_t *off, const uint32_t *n,
+                                 const double *thr, const uint32_t *mode, const uint32_t *hot_lo,
+                                 const uint32_t *hot_hi, const uint32_t *hot_word, uint32_t cases, uint32_t *out_idx,
+                                 double *out_sum, uint32_t *out_staged, void *stream) {
+    if (cases == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    if (precision == 24)
+        hipLaunchKernelGGL(k_chunk_cases_wb<24>, dim3(cases), dim3(rl::REST_THREADS), 0, st, words, off, n, thr, mode,
+                           hot_lo, hot_hi, hot_word, out_idx, out_sum, out_staged);
+    else if (precision == 53)
+        hipLaunchKernelGGL(k_chunk_cases_wb<53>, dim3(cases), dim3(rl::REST_THREADS), 0, st, words, off, n, thr, mode,
+                           hot_lo, hot_hi, hot_word, out_idx, out_sum, out_staged);
+    else
+        return -1;
+    return (int)hipGetLastError();
 }

@@ -13,6 +13,11 @@ the first partial sum >= or > a threshold (every partial sum, its neighbours,
 0 and -1); numpy's cumulative sums (sequential, in the terms' precision) give
 the expected index and value.
 
+A second harness entry runs the chunked replay as the sampler's draw does:
+in place (each staged round's terms written over its words) with a range of
+words read as one value (memory there holds NaN); the written prefix, the
+words past it and the results are checked against numpy.
+
 Cases: uniform, wide and very wide ranges, narrow values whose sums stay
 exact across binades, subnormals, mostly zeros, two values, short
 significands, values near 1, runs of exact rounding ties in f32 and in f64,
@@ -172,3 +177,96 @@ def run_cases(device, precision, shape, seed):
 @pytest.mark.parametrize("shape", [0, 1, 2, 3])
 def test_replay_matches_sequential_loops(device, precision, shape):
     run_cases(device, precision, shape, seed=1000 + precision + shape)
+
+
+def run_wb_cases(device, precision, seed):
+    """The chunked replay as the draw runs it (rust-llm_amd/csrc/full_rest.h):
+    in place, each staged round's terms written over its words, with a range
+    of words read as one value whatever memory holds there (the row's
+    commonest key, whose block the sort does not store). The harness's term
+    doubles the word (exact). Memory under the range holds NaN, so a read of
+    it shows in the sum; the expected results are numpy's sequential cumulative
+    sums of the doubled effective terms, and every written word must be its
+    doubled effective term while the words past the written prefix keep
+    theirs."""
+    import torch
+    g = np.random.default_rng(seed)
+    base = term_arrays(seed)
+    picks_from = [x for x in base if x.size > 0]
+    cases = []
+    for c in range(48):
+        x = picks_from[int(g.integers(0, len(picks_from)))] if c % 4 else picks_from[-1 - (c // 4) % 4]
+        x = x.copy()
+        n = x.size
+        kind = c % 6
+        if kind == 0:
+            lo = hi = 0                        # no range
+        elif kind == 1:
+            lo, hi = 0, n                      # every word
+        elif kind == 2:
+            lo = int(g.integers(0, n)); hi = n + int(g.integers(0, 5000))  # to the end and past it
+        else:
+            lo = int(g.integers(0, n)); hi = min(n, lo + int(g.integers(1, max(2, n // 2))))
+        word = x[lo] if lo < n else np.float32(0.5)
+        eff = x.copy()
+        eff[lo:min(hi, n)] = word
+        mem = x.view(np.uint32).copy()
+        mem[lo:min(hi, n)] = 0x7FC00000         # NaN: must never be read
+        t = (eff.astype(np.float32) * np.float32(2.0)).astype(np.float32)
+        p = np.cumsum(t) if precision == 24 else np.cumsum(t.astype(np.float64))
+        p = p.astype(np.float64)
+        r = int(g.integers(0, 4))
+        if r == 0 or n == 0:
+            thr, mode = 0.0, 0
+        elif r == 1:
+            thr, mode = float(p[int(g.integers(0, n))]), 1 + int(g.integers(0, 2))
+        elif r == 2:
+            thr, mode = float(np.nextafter(p[int(g.integers(0, n))], np.inf)), 2
+        else:
+            thr, mode = -1.0, 1                # met at +0: the first term's sum
+        cases.append((mem, n, thr, mode, lo, hi, np.float32(word).view(np.uint32), t))
+    offs, at = [], 0
+    for mem, *_ in cases:
+        offs.append(at)
+        at += mem.size
+    words = torch.from_numpy(np.concatenate([c[0] for c in cases]).view(np.int32)).to(device)
+    d = lambda a, dt: torch.from_numpy(np.asarray(a, dt)).to(device)
+    u32 = lambda a: d(np.asarray(a, np.uint32).view(np.int32), np.int32)
+    k = len(cases)
+    out_idx = torch.empty(k, dtype=torch.int32, device=device)
+    out_sum = torch.empty(k, dtype=torch.float64, device=device)
+    out_staged = torch.empty(k, dtype=torch.int32, device=device)
+    lib = harness()
+    lib.seqsum_gpu_run_wb.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 8 + [ctypes.c_uint32] + [ctypes.c_void_p] * 4
+    lib.seqsum_gpu_run_wb.restype = ctypes.c_int
+    args = [d(offs, np.int64), u32([c[1] for c in cases]), d([c[2] for c in cases], np.float64),
+            u32([c[3] for c in cases]), u32([c[4] for c in cases]), u32([c[5] for c in cases]),
+            u32([c[6] for c in cases])]
+    print("seqsum in place P=%d: %d cases, %d words" % (precision, k, at), flush=True)
+    rc = lib.seqsum_gpu_run_wb(precision, words.data_ptr(), *[a.data_ptr() for a in args], k, out_idx.data_ptr(),
+                               out_sum.data_ptr(), out_staged.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    gi = out_idx.cpu().numpy().view(np.uint32)
+    gs = out_sum.cpu().numpy()
+    gst = out_staged.cpu().numpy().view(np.uint32)
+    back = words.cpu().numpy().view(np.uint32)
+    for c, (mem, n, thr, mode, lo, hi, wbits, t) in enumerate(cases):
+        want_i, want_s = expected(t, precision, thr, mode)
+        assert gi[c] == want_i and gs[c].tobytes() == np.float64(want_s).tobytes(), (
+            "case %d (n=%d, range [%d, %d), thr %r mode %d): got (%d, %r) want (%d, %r)" % (
+                c, n, lo, hi, thr, mode, gi[c], gs[c], want_i, want_s))
+        st = int(gst[c])
+        assert st <= n, (c, st, n)
+        if want_i < n and not (mode == 1 and thr < 0.0):
+            assert st >= want_i + 1, (c, st, want_i)
+        if want_i == n:
+            assert st == n, (c, st, n)
+        seg = back[offs[c]:offs[c] + n]
+        assert np.array_equal(seg[:st], t[:st].view(np.uint32)), "case %d: written prefix" % c
+        assert np.array_equal(seg[st:], mem[st:]), "case %d: words past the prefix" % c
+
+
+@pytest.mark.parametrize("precision", [24, 53])
+def test_chunked_replay_in_place_with_a_hot_range(device, precision):
+    run_wb_cases(device, precision, seed=3000 + precision)
