@@ -39,8 +39,11 @@ __device__ __constant__ uint64_t EXP2_32_TAB[32] = {
 // tab(i) returns EXP2_32_TAB[i]; kernels that evaluate many exps pass a copy
 // of the table in LDS (copy_exp_table), since a per-lane index into constant
 // memory is a dependent global load on every call.
+// The main path: x * 32/ln2 split into k + r, the table and the polynomial.
+// Equals libm expf wherever its special cases do not apply (|x| < 88, and the
+// finite x up to the overflow and down to the underflow bounds).
 template <class Tab>
-__device__ __forceinline__ float expf_libm_t(float x, Tab tab) {
+__device__ __forceinline__ float expf_libm_core(float x, Tab tab) {
     // Polynomial for 2^(r/32), coefficients pre-divided by 32^3, 32^2, 32.
     const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
     const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
@@ -48,27 +51,51 @@ __device__ __forceinline__ float expf_libm_t(float x, Tab tab) {
     const double INV_LN2_32 = 0x1.71547652b82fep+0 * 32.0;
     const double SHIFT = 0x1.8p+52;
 
-    const uint32_t bits = __float_as_uint(x);
-    const uint32_t abstop = (bits >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) {                            // |x| >= 88 or NaN
-        if (bits == 0xff800000u) return 0.0f;          // exp(-inf)
-        if (abstop >= 0x7f8u) return x + x;            // +inf, NaN
-        if (x > 0x1.62e42ep6f) return __builtin_inff(); // overflows
-        if (x < -0x1.9fe368p6f) return 0.0f;           // underflows to +0
-    }
     const double xd = (double)x;
     double kd = __builtin_fma(INV_LN2_32, xd, SHIFT);
-    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    // k in the low word of kd's bits; s = the bits of tab(k & 31) + (k << 47),
+    // which leaves the low word alone and adds k << 15 to the high word
+    // (mod 2^32, as the 64-bit sum does).
+    const uint32_t ki = (uint32_t)__double_as_longlong(kd);
     kd -= SHIFT;
     const double r = __builtin_fma(INV_LN2_32, xd, -kd);
-    const uint64_t t = tab((uint32_t)(ki & 31u)) + (ki << 47);
-    const double s = __longlong_as_double((long long)t);
+    const uint64_t tb = tab(ki & 31u);
+    const double s = __hiloint2double((int)((uint32_t)(tb >> 32) + (ki << 15)), (int)(uint32_t)tb);
     const double z = __builtin_fma(C0, r, C1);
     const double r2 = r * r;
     double y = __builtin_fma(C2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     y = y * s;
     return (float)y;
+}
+
+// Underflow bound: libm expf returns +0 below it.
+constexpr float EXPF_UNDERFLOW = -0x1.9fe368p6f;
+
+template <class Tab>
+__device__ __forceinline__ float expf_libm_t(float x, Tab tab) {
+    const uint32_t bits = __float_as_uint(x);
+    const uint32_t abstop = (bits >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) {                            // |x| >= 88 or NaN
+        if (bits == 0xff800000u) return 0.0f;          // exp(-inf)
+        if (abstop >= 0x7f8u) return x + x;            // +inf, NaN
+        if (x > 0x1.62e42ep6f) return __builtin_inff(); // overflows
+        if (x < EXPF_UNDERFLOW) return 0.0f;           // underflows to +0
+    }
+    return expf_libm_core(x, tab);
+}
+
+// The float just below EXPF_UNDERFLOW: the main path there gives a double
+// under 2^-150, which rounds to +0 in f32.
+constexpr float EXPF_BELOW_UNDERFLOW = -0x1.9fe36ap6f;
+
+// expf_libm_t for x <= 0 (either zero, -inf included), not NaN: of its
+// special cases only the underflow to +0 (which covers -inf) can apply, and
+// raising x to EXPF_BELOW_UNDERFLOW gives that +0 from the main path itself,
+// with no branch.
+template <class Tab>
+__device__ __forceinline__ float expf_libm_nonpos_t(float x, Tab tab) {
+    return expf_libm_core(__builtin_fmaxf(x, EXPF_BELOW_UNDERFLOW), tab);
 }
 
 __device__ __forceinline__ float expf_libm(float x) {

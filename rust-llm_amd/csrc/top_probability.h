@@ -20,7 +20,9 @@
 // E + 150 binade changes above the smallest f32. Each rounding is at most
 // G / 2: the sequential sum is within (small + 200) * G / 2 of the exact sum,
 // where small counts the nonzero terms below 2^(E-29). The sum pass counts
-// those below 2^-26, which serves every E <= 3; a larger E falls back to the
+// every term below 2^-26, zeros too (a zero term adds without rounding, so
+// counting it only widens the bound), which serves every E <= 3; a larger E
+// falls back to the
 // general bound gamma_(V-1) * S. The chunked sum adds every term
 // into a 32-term sum, those in order per thread, then a tree and the chunks in
 // order: its relative error is at most the depth of that summation times
@@ -158,7 +160,7 @@ __device__ __forceinline__ bool tp_row(const uint64_t *part_am, const uint32_t *
     return nan != 0 || key == 0 || key_value(key) == __builtin_inff();
 }
 
-// Terms counted by the sum pass: nonzero and below 2^-26 (bits 0x32800000).
+// Terms counted by the sum pass: below 2^-26 (bits 0x32800000).
 constexpr uint32_t TP_SMALL = 0x32800000u;
 
 // The depth of k_tp_sum's summation (the additions any term's value passes
@@ -192,12 +194,19 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
     const uint32_t n4 = vocab / 4;
     const uint32_t q0 = chunk_lo(n4, chunk, chunks), q1 = chunk_lo(n4, chunk + 1, chunks);
     double sum = 0.0;
-    uint32_t small = 0;
-    auto add = [&](double &acc, float x) {
-        const float t = expf_libm_t(x - best, etab);
+    uint32_t small = 0;   // this lane's count: the last, partial tile and the tail element
+    uint32_t wsmall = 0;  // the wave's count over the full tiles (the same in every lane)
+    // x - best <= 0 and is not NaN: tp_row has returned for rows holding a
+    // NaN and for a best at +-inf.
+    auto term = [&](double &acc, float x) {
+        const float t = expf_libm_nonpos_t(x - best, etab);
         acc += (double)t;
-        small += __float_as_uint(t) - 1u < TP_SMALL - 1u ? 1u : 0u;  // +0 wraps round and is not counted
+        return __float_as_uint(t) < TP_SMALL;
     };
+    auto add = [&](double &acc, float x) { small += term(acc, x) ? 1u : 0u; };
+    // In a full tile every lane of the workgroup is active, so a term's count
+    // can be a ballot, which the wave keeps in scalar registers.
+    auto add_full = [&](double &acc, float x) { wsmall += (uint32_t)__builtin_popcountll(ballot(term(acc, x))); };
     // Tiles as in k_tp_max: the next tile's loads overlap this tile's exps.
     // Each tile's terms are summed on their own, then added to the thread's
     // sum, which bounds the depth of the summation (tp_sum_depth).
@@ -208,13 +217,23 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
         for (uint32_t b = q0; b < q1; b += STEP) {
             load_tile_clamped<VEC>(B, rowp, b + STEP, q1);
             double ts = 0.0;
+            if (b + STEP <= q1) {
 #pragma unroll
-            for (uint32_t u = 0; u < UNROLL; ++u) {
-                if (b + u * FAST_THREADS + threadIdx.x < q1) {
-                    add(ts, A[u].x);
-                    add(ts, A[u].y);
-                    add(ts, A[u].z);
-                    add(ts, A[u].w);
+                for (uint32_t u = 0; u < UNROLL; ++u) {
+                    add_full(ts, A[u].x);
+                    add_full(ts, A[u].y);
+                    add_full(ts, A[u].z);
+                    add_full(ts, A[u].w);
+                }
+            } else {
+#pragma unroll
+                for (uint32_t u = 0; u < UNROLL; ++u) {
+                    if (b + u * FAST_THREADS + threadIdx.x < q1) {
+                        add(ts, A[u].x);
+                        add(ts, A[u].y);
+                        add(ts, A[u].z);
+                        add(ts, A[u].w);
+                    }
                 }
             }
             sum += ts;
@@ -234,7 +253,7 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
     sum += lane_xor_f64<4>(sum);
     sum += lane_xor_f64<2>(sum);
     sum += lane_xor_f64<1>(sum);
-    small = wave_sum_u32(small);
+    small = wave_sum_u32(small) + wsmall;
     const uint32_t wave = threadIdx.x / WAVE;
     if (lane_id() == 0) {
         red[wave] = sum;
@@ -304,7 +323,7 @@ __global__ __launch_bounds__(TP_FINAL_THREADS) void k_tp_final(const float *logi
         double sum;
         seq_replay<53, TP_FINAL_THREADS, SEQ_ITEMS>(
             [rowp](uint32_t j) { return ((const RL_GLB uint32_t *)rowp)[j]; },
-            [best, etab](uint32_t bits) { return expf_libm_t(__uint_as_float(bits) - best, etab); }, vocab,
+            [best, etab](uint32_t bits) { return expf_libm_nonpos_t(__uint_as_float(bits) - best, etab); }, vocab,
             NeverStop{}, &seq, &sum);
         prob = (float)(1.0 / sum);
     }
