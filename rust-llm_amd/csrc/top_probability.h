@@ -174,6 +174,36 @@ __host__ __device__ inline uint32_t tp_sum_depth(uint32_t vocab, uint32_t chunks
     return 32 + tiles + 1 + 6 + (FAST_WAVES - 1) + chunks;
 }
 
+// load_tile_clamped for the sum pass. With aligned rows the loads go through
+// a buffer resource over the row (n4 float4, under 2^21 * 4 bytes, so byte
+// offsets fit 32 bits): the tile's base is a scalar offset, each lane's
+// offset is min(lane * 16, a scalar limit), one vector operation a load
+// instead of the index, clamp and 64-bit address of a global load. Indices
+// at or past `end` are clamped to end - 1 as in load_tile_clamped (a base at
+// or past end loads element end - 1 in every lane), so every access stays
+// inside the row.
+template <bool VEC>
+__device__ __forceinline__ void load_sum_tile(f32x4 *dst, const float *row, uint32_t n4, uint32_t base,
+                                              uint32_t end) {
+    if constexpr (VEC) {
+        const __amdgpu_buffer_rsrc_t rsrc =
+            __builtin_amdgcn_make_buffer_rsrc((void *)row, (short)0, (int)(n4 * 16u), 0x00020000);
+        const uint32_t bb = base < end ? base : end - 1;
+        const uint32_t lim = (end - 1 - bb) * 16u;  // the last element's byte offset from bb
+        const uint32_t lane16 = threadIdx.x * 16u;
+#pragma unroll
+        for (uint32_t u = 0; u < UNROLL; ++u) {
+            const uint32_t su = u * FAST_THREADS * 16u < lim ? u * FAST_THREADS * 16u : lim;
+            const uint32_t vl = lim - su;
+            const uint32_t voff = lane16 < vl ? lane16 : vl;
+            dst[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)voff,
+                                                                                 (int)(bb * 16u + su), 2));
+        }
+    } else {
+        load_tile_clamped<VEC>(dst, row, base, end);
+    }
+}
+
 // grid (chunks, rows), FAST_THREADS: per chunk the f64 sum of exp(l_i - best)
 // (forward.rs:1678), in any order, and how many terms are small (above).
 template <bool VEC>
@@ -213,9 +243,9 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
     constexpr uint32_t STEP = FAST_THREADS * UNROLL;
     if (q1 > q0) {
         f32x4 A[UNROLL], B[UNROLL];
-        load_tile_clamped<VEC>(A, rowp, q0, q1);
+        load_sum_tile<VEC>(A, rowp, n4, q0, q1);
         for (uint32_t b = q0; b < q1; b += STEP) {
-            load_tile_clamped<VEC>(B, rowp, b + STEP, q1);
+            load_sum_tile<VEC>(B, rowp, n4, b + STEP, q1);
             double ts = 0.0;
             if (b + STEP <= q1) {
 #pragma unroll
