@@ -173,7 +173,7 @@ def assert_same(got, want, label):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("rows, V, scale", [(1, 248320, 2.0), (9, 151936, 2.5), (64, 4099, 5.0), (300, 1000, 1.0),
-                                            (1100, 257, 3.0), (4, 3, 1.0)])
+                                            (1100, 257, 3.0), (4, 3, 1.0), (290, 248320, 2.0)])
 def test_rows_match_the_oracle(device, rows, V, scale):
     rng = np.random.default_rng(rows * 7 + V)
     x = rng.normal(0, scale, (rows, V)).astype(np.float32)
