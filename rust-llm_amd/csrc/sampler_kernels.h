@@ -197,18 +197,26 @@ __device__ __forceinline__ uint32_t stream_key(const Stream &w, float x) {
     return w.greedy ? total_key(x + 0.0f) : total_key(x);
 }
 
+// A float4 group of the wave: most groups have no lane past the prefilter;
+// of the others, usually one or two of the four components do, and only
+// those run the exact test (the skip is a scalar test of the prefilter's
+// lane mask).
 template <bool CHECK>
 __device__ __forceinline__ void offer_group(Stream &w, f32x4 v, uint32_t id0, uint32_t nvalid) {
     const float x[4] = {v.x, v.y, v.z, v.w};
+    bool pf[4];
     bool any = false;
 #pragma unroll
-    for (uint32_t c = 0; c < 4; ++c) any |= (!CHECK || c < nvalid) && prefilter(w, x[c]);
+    for (uint32_t c = 0; c < 4; ++c) {
+        pf[c] = (!CHECK || c < nvalid) && prefilter(w, x[c]);
+        any |= pf[c];
+    }
     if (ballot(any) == 0) return;
 #pragma unroll
     for (uint32_t c = 0; c < 4; ++c) {
+        if (ballot(pf[c]) == 0) continue;
         const uint64_t comp = composite(stream_key(w, x[c]), id0 + c);
-        const bool p = (!CHECK || c < nvalid) && prefilter(w, x[c]) && comp > w.T &&
-                       (!w.greedy || x[c] >= -3.40282347e38f);
+        const bool p = pf[c] && comp > w.T && (!w.greedy || x[c] >= -3.40282347e38f);
         offer(w, p, comp);
     }
 }
