@@ -401,8 +401,12 @@ int rl_top_probability_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t r
     hipStream_t st = static_cast<hipStream_t>(stream);
     const uint64_t stride = rows > 1 ? row_stride : vocab;
     const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (stride % 4 == 0);
-    uint32_t chunks = std::min(MAX_CHUNKS, (TARGET_WGS + rows - 1) / rows);
-    chunks = std::max(1u, std::min(chunks, vocab / 4096));
+    // Two workgroups a CU slot (the sum pass is bound by its arithmetic, and
+    // more, shorter workgroups even out the CUs), within the chunk arrays'
+    // max(CHUNK_SLOTS, max_rows) entries.
+    const uint32_t slots = std::max(CHUNK_SLOTS, ctx->max_rows);
+    uint32_t chunks = std::min(MAX_CHUNKS, (2 * TARGET_WGS + rows - 1) / rows);
+    chunks = std::max(1u, std::min({chunks, vocab / 4096, slots / rows}));
     dim3 grid(chunks, rows);
     if (vec) {
         hipLaunchKernelGGL(k_tp_max<true>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
