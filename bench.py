@@ -13,6 +13,12 @@ with --workload.
 --op embed times the embedding lookup from the same resident tensor
 (rl_head_embed_rows: --tokens rows of 2560 f32 each).
 
+--op host_verify times the host Sampler's speculative-verify walk on the host
+wall clock (rl_host_sampler_verify over the 9-row verify workload, then
+rl_host_sampler_commit_verified row by row, every draft accepted), --op
+host_batch one rl_host_sample_batch call over 16 host Samplers; each beside
+the device time of the same rows' rl_sampler_sample_rows call.
+
 --op head times the output head instead (rl_head_logits: t normed hidden rows
 times the tied Q6_K embedding [2560, 248320], logits into HBM); --op head_sample
 times the head followed by sampling its logits, the device path from hidden
@@ -48,11 +54,14 @@ def parse():
     ap.add_argument("--no-candidates", action="store_true",
                     help="skip the candidate outputs (tokens only)")
     ap.add_argument("--op", default="sample",
-                    choices=["sample", "top_probability", "argmax", "head", "head_sample", "embed"],
+                    choices=["sample", "top_probability", "argmax", "head", "head_sample", "embed", "host_verify",
+                             "host_batch"],
                     help="sample: rl_sampler_sample_rows (the benchmark); top_probability and argmax time "
                          "rl_top_probability_rows and rl_argmax_rows on the same logits; head times "
                          "rl_head_logits, head_sample the head followed by sampling its logits; embed times "
-                         "rl_head_embed_rows, the embedding lookup from the same tensor")
+                         "rl_head_embed_rows, the embedding lookup from the same tensor; host_verify and "
+                         "host_batch time the host Sampler's verify+commit walk and a 16-sampler batch on the "
+                         "host wall clock")
     ap.add_argument("--tokens", type=int, default=1,
                     help="tokens per embedding lookup (1 = a decode step, more = a prompt)")
     ap.add_argument("--head-rows", type=int, default=1,
@@ -432,6 +441,142 @@ def bench_head(args):
     }
     print(json.dumps(line), flush=True)
 
+def device_call_ms(ctx, d_logits, rows, settings, windows, wlen, uniforms, calls, stream):
+    """Median HIP-event time of rl_sampler_sample_rows alone over `rows` rows
+    (each call between its own events), candidates out."""
+    import numpy as np
+    import torch
+
+    import rl_sampler as R
+    dev = d_logits.device
+    ctx.configure(settings)
+    cs = ctx.required_cand_stride()
+    tok = torch.empty(rows, dtype=torch.int32, device=dev)
+    kept = torch.empty_like(tok)
+    used = torch.empty(rows, dtype=torch.uint8, device=dev)
+    ids = torch.empty((rows, cs), dtype=torch.int32, device=dev)
+    probs = torch.empty((rows, cs), dtype=torch.float32, device=dev)
+    d_win = torch.from_numpy(np.ascontiguousarray(windows).view(np.int32)).to(dev)
+    d_wlen = torch.from_numpy(wlen.view(np.int32)).to(dev)
+    d_uni = torch.from_numpy(uniforms).to(dev)
+    out = []
+    for i in range(calls + 3):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        ctx.sample_rows(d_logits, rows, d_logits.stride(0), tok, kept, used, windows=d_win,
+                        window_stride=windows.shape[1], window_len=d_wlen, uniforms=d_uni, out_ids=ids,
+                        out_probs=probs, cand_stride=cs, stream=stream.cuda_stream)
+        b.record(stream)
+        torch.cuda.synchronize()
+        if i >= 3:
+            out.append(a.elapsed_time(b))
+    return sorted(out)[len(out) // 2]
+
+
+def bench_host(args):
+    """--op host_verify / host_batch: the host Sampler on the host wall clock."""
+    import numpy as np
+    import torch
+
+    import rl_sampler as R
+    import workloads as W
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    walls = []
+    if args.op == "host_verify":
+        name = args.workload or "verify"
+        wl = W.WORKLOADS[name]
+        rows, windows, wlen = wl.generate()
+        n = wl.rows
+        d_rows = torch.from_numpy(rows).to(dev)
+        set_ = wl.settings(0)
+        history = wl.history()
+        s = R.HostSampler(wl.vocab, set_, max_rows=n)
+        for t in history:
+            s.remember(int(t))
+        committed = 0
+        for i in range(args.warmup + args.steps):
+            # The drafts every row accepts from this state: row i's pick
+            # depends on drafts 0..i-1 and its uniform only, so iterating the
+            # (uncommitted) verify reaches them within n calls; untimed.
+            drafts = np.zeros(n - 1, np.uint32)
+            for _ in range(n):
+                picks = s.verify(d_rows, drafts)
+                if np.array_equal(picks[:-1], drafts):
+                    break
+                drafts = picks[:-1].copy()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            s.verify(d_rows, drafts)
+            k = 0
+            for r in range(n):
+                t = s.commit_verified(r)
+                k += 1
+                if r < n - 1 and t != drafts[r]:
+                    break
+            el = time.perf_counter() - t0
+            if i >= args.warmup:
+                walls.append(el * 1e3)
+                committed += k
+        # the device call the walk makes, alone: the same rows and windows
+        ctx = R.DeviceSampler(n, wl.vocab, max_window=W.WINDOW)
+        dev_ms = device_call_ms(ctx, d_rows, n, wl.settings_list(), windows, wlen, wl.uniforms(), 20, stream)
+        what = "%s: one verify of %d rows then a commit per row (%.1f rows committed a walk)" % (
+            name, n, committed / args.steps)
+        metric = "host walks/s, speculative verify+commit over %d x %d fp32 logits" % (n, wl.vocab)
+        unit = "walks/s"
+    else:
+        name = args.workload or "spikes"
+        wl = W.WORKLOADS[name]
+        n = 16
+        rows, windows, wlen = wl.generate(0, n)
+        settings = wl.settings_list(0, n)
+        d_rows = torch.from_numpy(rows).to(dev)
+        samplers = [R.HostSampler(wl.vocab, settings[r], max_rows=n if r == 0 else 1) for r in range(n)]
+        for r in range(n):
+            for t in windows[r, :wlen[r]]:
+                samplers[r].remember(int(t))
+        for i in range(args.warmup + args.steps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            R.host_sample_batch(samplers, d_rows)
+            el = time.perf_counter() - t0
+            if i >= args.warmup:
+                walls.append(el * 1e3)
+        ctx = R.DeviceSampler(n, wl.vocab, max_window=W.WINDOW)
+        dev_ms = device_call_ms(ctx, d_rows, n, settings, windows, wlen, wl.uniforms(0, n), 20, stream)
+        what = "%s rows 0..15: one rl_host_sample_batch call over 16 host Samplers" % name
+        metric = "host batch calls/s, 16 host Samplers over 16 x %d fp32 logits" % wl.vocab
+        unit = "calls/s"
+    walls.sort()
+    med = walls[len(walls) // 2]
+    mean = sum(walls) / len(walls)
+    print("[bench] %s: host wall median %.4f ms (min %.4f, max %.4f); device call alone median %.4f ms" % (
+        what, med, walls[0], walls[-1], dev_ms), file=sys.stderr, flush=True)
+    line = {
+        "metric": metric,
+        "value": round(1e3 / mean, 1),
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(mean, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded generator, rust-llm_amd/csrc/workloads.c)",
+        "config": {"workload": what, "rows": n, "vocab": wl.vocab},
+        "host_wall_ms_median": round(med, 5),
+        "host_wall_ms_min": round(walls[0], 5),
+        "device_call_ms_median": round(dev_ms, 5),
+        "host_overhead_ms": round(med - dev_ms, 5),
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
 
 def main():
     args = parse()
@@ -445,6 +590,9 @@ def main():
         return
     if args.op in ("head", "head_sample"):
         bench_head(args)
+        return
+    if args.op in ("host_verify", "host_batch"):
+        bench_host(args)
         return
     import numpy as np
     import torch

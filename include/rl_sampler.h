@@ -76,7 +76,21 @@ typedef struct rl_sampler_ctx rl_sampler_ctx;
 /* Allocates every device buffer for up to `max_rows` logit rows of `vocab`
  * entries and windows of up to `max_window` token ids. Replaces the allocation
  * half of Sampler::new (sample.rs:156-172). `device` is a HIP device index.
- * max_window must be <= 2048 and vocab <= 2^21 (2 097 152). */
+ *
+ * Two limits the reference does not have (RL_ERR_CAPACITY above them):
+ *   max_window <= 2048. The reference sizes its ring from any repeat_last_n
+ *     (sample.rs:166; the CLI parses it as any usize, main.rs:604, :641-644).
+ *     Here a row's distinct window ids live in on-chip memory while its logits
+ *     stream past: an open-addressed set of twice the call's window stride in
+ *     LDS (up to 32 KiB) on the stream path, eight ids a thread on the full
+ *     path's pass. Windows of 65..2048 ids are tested against the oracle.
+ *   vocab <= 2^21 (2 097 152). The reference takes any vocabulary
+ *     (sample.rs:156-172). Every index and count on the device paths is 32-bit
+ *     with this much room; Qwen's 248 320 is far below it.
+ *
+ * The stream path's window set is sized per call from window_stride, not from
+ * max_window, so a context made for long windows costs nothing on calls whose
+ * windows are short. */
 int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t max_window,
                       rl_sampler_ctx **out);
 

@@ -18,6 +18,7 @@
 // sequential rounding in parallel. Rows with a NaN or infinite p (NaN logits,
 // a NaN temperature, 1 / total overflowing) are walked in order by one thread.
 #pragma once
+#include "minp_bound.h"
 #include "sampler_kernels.h"
 
 namespace rl {
@@ -130,38 +131,16 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
 // Anything else (too many survivors, a NaN, a cut inside the interval) leaves
 // the row to k_full_rest.
 //
-// The mass interval. The reference's mass is S_ref = sum of p_j in sorted
-// order (f64, sequential), p_j = expf(fl(fl(l_j - M) / T)). With y_j =
-// (l_j - M) / T exactly, fl rounding twice puts x_j within |y_j| 2^-23 of y_j
-// and libm expf is within 0.502 ulp, so p_j = e^(y_j) (1 + e_j) with |e_j| <=
-// 2^-23 |y_j| + 2^-24 to first order (plus 2^-149 absolute in the subnormal
-// range). The pass computes, relative to a running maximum m <= M that was
-// already seen, q_j = exp2_hw(fl(fl(l_j - m) * c2)) with c2 = fl(log2(e) / T)
-// rounded once from the f64 quotient: the exponent carries at most 3 roundings
-// of 2^-24 relative, so q_j e^((m - M) / T) = e^(y_j) (1 + g_j) with |g_j| <=
-// 3 2^-24 |y_j| + H (H bounds the hardware exp2's own error, see HW_EXP2_REL),
-// and partial sums are rescaled by f64 factors e^((m_old - m_new) / T) as m
-// rises. Splitting at |y| = K: terms with |y_j| <= K are within
-// EPS_NEAR relative of each other in the two computations; terms beyond
-// differ by at most 2.01 e^(-K) + 2^-124 each (both are below e^(-K) (1 +
-// tiny), or flushed subnormals). Summation adds gamma_32 in f32 (each
-// thread's terms of one step), a few f64 roundings, and gamma_(V-1) for the
-// reference's sequential sum. MASS_REL collects the relative terms.
+// The mass interval that certifies the top-p cut, and the constants it rests
+// on, are in minp_bound.h (shared with a host-built test of the bound).
 
-constexpr uint32_t PASS_U = 10;                          // float4 per thread per step
-constexpr uint32_t PASS_STEP = FULL_THREADS * PASS_U;    // float4 per step
+using minp::PASS_U;
+using minp::PASS_STEP;
+static_assert(minp::PASS_THREADS == FULL_THREADS, "the certificate's step shape is k_full_pass's");
 constexpr uint32_t FULL_WAVES = FULL_THREADS / WAVE;
 constexpr uint32_t FIN_CAP = 1024;                       // survivors the pass finishes itself
 constexpr uint32_t PASS_CAND = 1024;                     // candidates a chunk holds in LDS
 constexpr uint32_t LIST_OVER = 0xFFFFFFFFu;              // a chunk's candidates did not fit
-constexpr double HW_EXP2_REL = 0x1p-21;                  // v_exp_f32 bound assumed (4 ulp; tested <= 1 ulp)
-constexpr double MASS_K = 32.0;
-constexpr double EPS_NEAR =
-    ((0x1p-23 + 3.0 * 0x1p-24) * MASS_K + 1.004 * 0x1p-24 + HW_EXP2_REL) * (1.0 + 0x1p-7);
-constexpr double MASS_REL = EPS_NEAR / (1.0 - EPS_NEAR) + 33.0 * 0x1p-24 + 0x1p-40;
-constexpr double RESCALE_REL = (0x1p-24 + HW_EXP2_REL) * 1.001;  // one in-loop rescaling factor
-// 2.01 e^(-K) + 2^-124 per term (e^-32 = 1.2664165549e-14).
-constexpr double MASS_ABS_PER_TERM = 2.01 * 1.2664165549094176e-14 + 0x1p-124;
 
 // Loads of k_full_pass's aligned variant are buffer loads through a resource
 // that starts at the step and ends at the chunk's end: float4 f of the step
@@ -844,19 +823,9 @@ __global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScra
     __syncthreads();
     const uint32_t c = sh_count, ns_key = sh_ns;
     ok_row = ok_row && c > 0 && c <= FIN_CAP;
-    // t_lo <= top_p * S_ref <= t_hi, with the reference's target rounding.
-    // Each step after a chunk's first can rescale the terms before it once
-    // more (RESCALE_REL each); the absolute terms cover the far terms and
-    // factors below 2^-1022.
-    const uint32_t steps = (chunk_lo(V / 4, 1, C) + PASS_STEP) / PASS_STEP;  // the largest chunk's steps, or more
-    const double rel = MASS_REL + (double)steps * RESCALE_REL;
-    const double abs_err = MASS_ABS_PER_TERM * (double)V + (double)V * 0x1p-1000;
-    const double gam = ((double)V + 64.0) * 0x1p-53;
-    const double S_lo = (Smid * (1.0 - rel) - abs_err) * (1.0 - gam);
-    const double S_hi = (Smid * (1.0 + rel) + abs_err) * (1.0 + gam);
-    const double tp = (double)s.top_p;
-    const double t_lo = tp * S_lo * (1.0 - 0x1p-48);
-    const double t_hi = tp * S_hi * (1.0 + 0x1p-48);
+    // t_lo <= top_p * S_ref <= t_hi (minp_bound.h).
+    double t_lo, t_hi;
+    minp::target_interval(Smid, V, C, s.top_p, &t_lo, &t_hi);
     bool fin = false;
     if (ok_row && c <= WAVE) {
         if (wave == 0) {

@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "rl_error.h"
+#include "rl_pack.h"
 #include "rl_sampler.h"
 #include "rl_sampler_host.h"
 
@@ -113,17 +114,19 @@ struct rl_host_sampler {
     std::vector<rl_sampling> configured, same_set, batch_set;
     std::vector<rl_rng> batch_probe;
     uint64_t cand_cap = 1;
-    // device buffers
+    // Device buffers. d_in is one call's input, uploaded with one copy:
+    // uniforms[max_rows] (f32), window lengths[max_rows], then the windows,
+    // rows at the call's stride (the longest window of the call).
     float *d_row = nullptr;
-    uint32_t *d_windows = nullptr, *d_wlen = nullptr, *d_token = nullptr, *d_kept = nullptr;
-    float *d_uniforms = nullptr;
+    uint32_t *d_in = nullptr, *d_token = nullptr, *d_kept = nullptr;
     uint8_t *d_used = nullptr;
     uint32_t *d_ids = nullptr;
     float *d_probs = nullptr;
-    // pinned host staging
-    uint32_t *h_windows = nullptr, *h_wlen = nullptr, *h_token = nullptr, *h_kept = nullptr;
-    float *h_uniforms = nullptr;
-    uint8_t *h_used = nullptr;
+    // Pinned host memory: h_in is d_in's host side; h_out (coherent) is where
+    // the device writes every row's results (rl_pack.h), d_out its device
+    // address.
+    uint32_t *h_in = nullptr;
+    rl::PackedRow *h_out = nullptr, *d_out = nullptr;
     // the last call's survivors (Sampler::candidates), capacity cand_cap
     std::vector<uint32_t> cand_ids;
     std::vector<float> cand_probs;
@@ -141,14 +144,17 @@ struct rl_host_sampler {
     void *v_stream = nullptr;
 
     ~rl_host_sampler() {
-        for (void *p : {(void *)d_row, (void *)d_windows, (void *)d_wlen, (void *)d_token, (void *)d_kept,
-                        (void *)d_uniforms, (void *)d_used, (void *)d_ids, (void *)d_probs})
+        for (void *p : {(void *)d_row, (void *)d_in, (void *)d_token, (void *)d_kept, (void *)d_used, (void *)d_ids,
+                        (void *)d_probs})
             if (p) (void)hipFree(p);
-        for (void *p : {(void *)h_windows, (void *)h_wlen, (void *)h_token, (void *)h_kept, (void *)h_uniforms,
-                        (void *)h_used})
+        for (void *p : {(void *)h_in, (void *)h_out})
             if (p) (void)hipHostFree(p);
         rl_sampler_destroy(ctx);
     }
+
+    float *h_uniforms() { return reinterpret_cast<float *>(h_in); }
+    uint32_t *h_wlen() { return h_in + max_rows; }
+    uint32_t *h_windows() { return h_in + 2 * (size_t)max_rows; }
 
     void remember(uint32_t t) {  // sample.rs:205-212
         if (recent.empty()) return;
@@ -186,38 +192,56 @@ struct rl_host_sampler {
         return f;
     }
 
-    // Uploads windows/uniforms for `rows` rows, runs the device, and brings
-    // back tokens, kept counts and the used flags. Candidates stay on device.
-    int run(const float *d_logits, uint64_t stride, uint32_t rows, void *stream) {
+    // Uploads the input block (uniforms, window lengths and `rows` windows at
+    // stride ws), runs the device and packs every row's results into h_out:
+    // one copy, two launches and one synchronisation.
+    int run(const float *d_logits, uint64_t stride, uint32_t rows, uint32_t ws, void *stream) {
         hipStream_t st = static_cast<hipStream_t>(stream);
-        hipError_t e = hipMemcpyAsync(d_windows, h_windows, (size_t)rows * wcap * 4, hipMemcpyHostToDevice, st);
-        if (e == hipSuccess) e = hipMemcpyAsync(d_wlen, h_wlen, rows * 4, hipMemcpyHostToDevice, st);
-        if (e == hipSuccess) e = hipMemcpyAsync(d_uniforms, h_uniforms, rows * 4, hipMemcpyHostToDevice, st);
+        const size_t words = 2 * (size_t)max_rows + (size_t)rows * ws;
+        hipError_t e = hipMemcpyAsync(d_in, h_in, words * 4, hipMemcpyHostToDevice, st);
         if (e != hipSuccess) return herr(RL_ERR_DEVICE, hipGetErrorString(e));
-        const int rc = rl_sampler_sample_rows(ctx, d_logits, stride, rows, (uint32_t)vocab, d_windows, wcap, d_wlen,
-                                              d_uniforms, d_token, d_kept, d_used, d_ids, d_probs, cand_cap, stream);
+        int rc = rl_sampler_sample_rows(ctx, d_logits, stride, rows, (uint32_t)vocab, d_in + 2 * (size_t)max_rows, ws,
+                                        d_in + max_rows, reinterpret_cast<const float *>(d_in), d_token, d_kept,
+                                        d_used, d_ids, d_probs, cand_cap, stream);
         if (rc != RL_OK) return rc;
-        e = hipMemcpyAsync(h_token, d_token, rows * 4, hipMemcpyDeviceToHost, st);
-        if (e == hipSuccess) e = hipMemcpyAsync(h_kept, d_kept, rows * 4, hipMemcpyDeviceToHost, st);
-        if (e == hipSuccess) e = hipMemcpyAsync(h_used, d_used, rows, hipMemcpyDeviceToHost, st);
-        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        rc = rl::launch_pack_rows(d_token, d_kept, d_used, d_ids, d_probs, cand_cap, rows, d_out, stream);
+        if (rc != RL_OK) return rc;
+        e = hipStreamSynchronize(st);
         if (e != hipSuccess) return herr(RL_ERR_DEVICE, hipGetErrorString(e));
         return RL_OK;
     }
 
-    // Copies device row `row`'s n survivors into ids/probs, whose capacity
-    // (reserved at creation) holds any kept count the settings allow.
-    int fetch_candidates(uint32_t row, uint32_t n, std::vector<uint32_t> &ids, std::vector<float> &probs,
-                         void *stream) {
+    // Packed row `slot`'s survivors into ids/probs (capacity reserved at
+    // creation for any kept count the settings allow): the first PACK_CANDS
+    // from the packed results; the rest of a row that keeps more is copied
+    // from device row `slot` on `stream`, and *queued is set (the caller
+    // synchronises once for all its rows).
+    int take_candidates(uint32_t slot, std::vector<uint32_t> &ids, std::vector<float> &probs, void *stream,
+                        bool *queued) {
+        const rl::PackedRow &pr = h_out[slot];
+        const uint32_t n = pr.kept;
         if (n > ids.capacity() || n > probs.capacity())
             return herr(RL_ERR_CAPACITY, "more candidates than the sampler was sized for");
         ids.resize(n);
         probs.resize(n);
-        hipStream_t st = static_cast<hipStream_t>(stream);
-        hipError_t e = hipMemcpyAsync(ids.data(), d_ids + (uint64_t)row * cand_cap, n * 4, hipMemcpyDeviceToHost, st);
-        if (e == hipSuccess)
-            e = hipMemcpyAsync(probs.data(), d_probs + (uint64_t)row * cand_cap, n * 4, hipMemcpyDeviceToHost, st);
-        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        const uint32_t head = std::min(n, rl::PACK_CANDS);
+        std::copy(pr.ids, pr.ids + head, ids.begin());
+        std::copy(pr.probs, pr.probs + head, probs.begin());
+        if (n > head) {
+            hipStream_t st = static_cast<hipStream_t>(stream);
+            const uint64_t at = (uint64_t)slot * cand_cap + head;
+            hipError_t e = hipMemcpyAsync(ids.data() + head, d_ids + at, (n - head) * 4, hipMemcpyDeviceToHost, st);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(probs.data() + head, d_probs + at, (n - head) * 4, hipMemcpyDeviceToHost, st);
+            if (e != hipSuccess) return herr(RL_ERR_DEVICE, hipGetErrorString(e));
+            *queued = true;
+        }
+        return RL_OK;
+    }
+
+    static int finish_copies(bool queued, void *stream) {
+        if (!queued) return RL_OK;
+        const hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
         if (e != hipSuccess) return herr(RL_ERR_DEVICE, hipGetErrorString(e));
         return RL_OK;
     }
@@ -232,18 +256,21 @@ struct rl_host_sampler {
         int rc = ensure_configured(&set, 1);
         if (rc != RL_OK) return rc;
         const bool pen = penalises(set) && filled > 0;
-        h_wlen[0] = pen ? (uint32_t)filled : 0u;
-        if (pen) std::copy(recent.begin(), recent.begin() + filled, h_windows);
+        h_wlen()[0] = pen ? (uint32_t)filled : 0u;
+        if (pen) std::copy(recent.begin(), recent.begin() + filled, h_windows());
         rl_rng probe = rng;
-        h_uniforms[0] = rl_rng_next_f32(&probe);
+        h_uniforms()[0] = rl_rng_next_f32(&probe);
         forget_verify();  // the device rows a verify left are overwritten
-        rc = run(d_logits, vocab, 1, stream);
+        rc = run(d_logits, vocab, 1, std::max<uint32_t>(1u, h_wlen()[0]), stream);
         if (rc != RL_OK) return rc;
-        rc = fetch_candidates(0, h_kept[0], cand_ids, cand_probs, stream);
+        bool queued = false;
+        rc = take_candidates(0, cand_ids, cand_probs, stream, &queued);
+        if (rc == RL_OK) rc = finish_copies(queued, stream);
         if (rc != RL_OK) return rc;
-        kept = h_kept[0];
-        if (h_used[0]) rng = probe;
-        *token = h_token[0];
+        const rl::PackedRow &pr = h_out[0];
+        kept = pr.kept;
+        if (pr.used) rng = probe;
+        *token = pr.token;
         remember(*token);  // sample.rs:217
         return RL_OK;
     }
@@ -284,21 +311,21 @@ int rl_host_sampler_new(int device, size_t vocab, const rl_sampling *set, uint32
     int prev = 0;
     (void)hipGetDevice(&prev);
     (void)hipSetDevice(device);
+    const size_t in_words = 2 * (size_t)max_rows + (size_t)max_rows * s->wcap;
     hipError_t e = hipMalloc(&s->d_row, vocab * 4);
-    if (e == hipSuccess) e = hipMalloc(&s->d_windows, (size_t)max_rows * s->wcap * 4);
-    if (e == hipSuccess) e = hipMalloc(&s->d_wlen, max_rows * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->d_in, in_words * 4);
     if (e == hipSuccess) e = hipMalloc(&s->d_token, max_rows * 4);
     if (e == hipSuccess) e = hipMalloc(&s->d_kept, max_rows * 4);
-    if (e == hipSuccess) e = hipMalloc(&s->d_uniforms, max_rows * 4);
     if (e == hipSuccess) e = hipMalloc(&s->d_used, max_rows);
     if (e == hipSuccess) e = hipMalloc(&s->d_ids, (size_t)max_rows * s->cand_cap * 4);
     if (e == hipSuccess) e = hipMalloc(&s->d_probs, (size_t)max_rows * s->cand_cap * 4);
-    if (e == hipSuccess) e = hipHostMalloc(&s->h_windows, (size_t)max_rows * s->wcap * 4);
-    if (e == hipSuccess) e = hipHostMalloc(&s->h_wlen, max_rows * 4);
-    if (e == hipSuccess) e = hipHostMalloc(&s->h_token, max_rows * 4);
-    if (e == hipSuccess) e = hipHostMalloc(&s->h_kept, max_rows * 4);
-    if (e == hipSuccess) e = hipHostMalloc(&s->h_uniforms, max_rows * 4);
-    if (e == hipSuccess) e = hipHostMalloc(&s->h_used, max_rows);
+    if (e == hipSuccess) e = hipHostMalloc(&s->h_in, in_words * 4);
+    if (e == hipSuccess) {
+        std::fill(s->h_in, s->h_in + in_words, 0u);
+        e = hipHostMalloc(&s->h_out, (size_t)max_rows * sizeof(rl::PackedRow),
+                          hipHostMallocMapped | hipHostMallocCoherent);
+    }
+    if (e == hipSuccess) e = hipHostGetDevicePointer(reinterpret_cast<void **>(&s->d_out), s->h_out, 0);
     (void)hipSetDevice(prev);
     if (e != hipSuccess) {
         delete s;
@@ -377,20 +404,25 @@ int rl_host_sampler_verify(rl_host_sampler *s, const float *device_rows, uint64_
     const bool pen = penalises(s->set);
     rl_rng probe = s->rng;
     const bool greedy = s->set.temperature <= 0.0f;
+    // Row i's window holds min(filled + i, len) ids: the last row's is the
+    // longest, and the call's stride.
+    const uint32_t ws = std::max<uint32_t>(
+        1u, pen && !s->recent.empty() ? (uint32_t)std::min(s->filled + n_drafts, s->recent.size()) : 0u);
     for (uint32_t i = 0; i < rows; ++i) {
-        const size_t f = pen ? s->window_after(drafts, i, s->h_windows + (size_t)i * s->wcap) : 0;
-        s->h_wlen[i] = (uint32_t)f;
-        s->h_uniforms[i] = greedy ? 0.0f : rl_rng_next_f32(&probe);  // one draw per drawing row
+        const size_t f = pen ? s->window_after(drafts, i, s->h_windows() + (size_t)i * ws) : 0;
+        s->h_wlen()[i] = (uint32_t)f;
+        s->h_uniforms()[i] = greedy ? 0.0f : rl_rng_next_f32(&probe);  // one draw per drawing row
     }
     s->forget_verify();
-    rc = s->run(device_rows, row_stride, rows, stream);
+    rc = s->run(device_rows, row_stride, rows, ws, stream);
     if (rc != RL_OK) return rc;
     for (uint32_t i = 0; i < rows; ++i) {
-        s->v_token[i] = s->h_token[i];
-        s->v_kept[i] = s->h_kept[i];
-        s->v_used[i] = s->h_used[i];
-        s->v_uniform[i] = s->h_uniforms[i];
-        picks[i] = s->h_token[i];
+        const rl::PackedRow &pr = s->h_out[i];
+        s->v_token[i] = pr.token;
+        s->v_kept[i] = pr.kept;
+        s->v_used[i] = (uint8_t)pr.used;
+        s->v_uniform[i] = s->h_uniforms()[i];
+        picks[i] = pr.token;
     }
     std::copy(drafts, drafts + n_drafts, s->v_drafts.begin());
     s->v_rows_n = rows;
@@ -416,21 +448,24 @@ int rl_host_sampler_commit_verified(rl_host_sampler *s, uint32_t row, uint32_t *
     // recompute this one with the uniform the stream really gives now.
     rl_rng probe = s->rng;
     const float u = rl_rng_next_f32(&probe);
-    uint32_t cand_row = row;
+    uint32_t slot = row;
     if (!(s->set.temperature <= 0.0f) && u != s->v_uniform[row]) {
         const bool pen = penalises(s->set) && s->filled > 0;
-        s->h_wlen[0] = pen ? (uint32_t)s->filled : 0u;
-        if (pen) std::copy(s->recent.begin(), s->recent.begin() + s->filled, s->h_windows);
-        s->h_uniforms[0] = u;
-        // Device row 0 belongs to a row already committed; later rows keep theirs.
-        const int rc = s->run(s->v_rows + (uint64_t)row * s->v_stride, s->vocab, 1, s->v_stream);
+        s->h_wlen()[0] = pen ? (uint32_t)s->filled : 0u;
+        if (pen) std::copy(s->recent.begin(), s->recent.begin() + s->filled, s->h_windows());
+        s->h_uniforms()[0] = u;
+        // Packed row 0 belongs to a row already committed; later rows keep theirs.
+        const int rc = s->run(s->v_rows + (uint64_t)row * s->v_stride, s->vocab, 1,
+                              std::max<uint32_t>(1u, s->h_wlen()[0]), s->v_stream);
         if (rc != RL_OK) return rc;
-        s->v_token[row] = s->h_token[0];
-        s->v_kept[row] = s->h_kept[0];
-        s->v_used[row] = s->h_used[0];
-        cand_row = 0;
+        s->v_token[row] = s->h_out[0].token;
+        s->v_kept[row] = s->h_out[0].kept;
+        s->v_used[row] = (uint8_t)s->h_out[0].used;
+        slot = 0;
     }
-    const int rc = s->fetch_candidates(cand_row, s->v_kept[row], s->cand_ids, s->cand_probs, s->v_stream);
+    bool queued = false;
+    int rc = s->take_candidates(slot, s->cand_ids, s->cand_probs, s->v_stream, &queued);
+    if (rc == RL_OK) rc = s->finish_copies(queued, s->v_stream);
     if (rc != RL_OK) return rc;
     if (s->v_used[row]) s->rng = probe;
     s->kept = s->v_kept[row];
@@ -448,32 +483,44 @@ int rl_host_sample_batch(rl_host_sampler *const *samplers, uint32_t n, const flo
     if (n > h->max_rows) return herr(RL_ERR_CAPACITY, "more samplers than the first one's max_rows");
     h->batch_set.clear();
     h->batch_probe.clear();
+    uint32_t ws = 1;  // the call's window stride: its longest window
     for (uint32_t i = 0; i < n; ++i) {
         rl_host_sampler *s = samplers[i];
         if (s->vocab != vocab || vocab != h->vocab)
             return herr(RL_ERR_VOCAB, "this sampler was built for a different vocabulary");
         if (s->filled > h->wcap) return herr(RL_ERR_CAPACITY, "a window longer than the first sampler's");
         if (s->cand_cap > h->cand_cap) return herr(RL_ERR_CAPACITY, "a sampler keeps more candidates than the first");
+        if (penalises(s->set)) ws = std::max(ws, (uint32_t)s->filled);
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        rl_host_sampler *s = samplers[i];
         h->batch_set.push_back(s->set);  // within the capacity reserved at creation
         const bool pen = penalises(s->set) && s->filled > 0;
-        h->h_wlen[i] = pen ? (uint32_t)s->filled : 0u;
-        if (pen) std::copy(s->recent.begin(), s->recent.begin() + s->filled, h->h_windows + (size_t)i * h->wcap);
+        h->h_wlen()[i] = pen ? (uint32_t)s->filled : 0u;
+        if (pen) std::copy(s->recent.begin(), s->recent.begin() + s->filled, h->h_windows() + (size_t)i * ws);
         h->batch_probe.push_back(s->rng);
-        h->h_uniforms[i] = rl_rng_next_f32(&h->batch_probe[i]);
+        h->h_uniforms()[i] = rl_rng_next_f32(&h->batch_probe[i]);
     }
     int rc = h->ensure_configured(h->batch_set.data(), n);
     if (rc != RL_OK) return rc;
     for (uint32_t i = 0; i < n; ++i) samplers[i]->forget_verify();  // h's device rows are overwritten
-    rc = h->run(device_logits, row_stride, n, stream);
+    rc = h->run(device_logits, row_stride, n, ws, stream);
     if (rc != RL_OK) return rc;
+    // Every row's candidates: from the packed results, plus one copy for each
+    // row that keeps more, all waited for by one synchronisation.
+    bool queued = false;
+    for (uint32_t i = 0; i < n && rc == RL_OK; ++i) rc = h->take_candidates(i, samplers[i]->cand_ids,
+                                                                          samplers[i]->cand_probs, stream, &queued);
+    const int rc2 = h->finish_copies(queued, stream);
+    if (rc != RL_OK) return rc;
+    if (rc2 != RL_OK) return rc2;
     for (uint32_t i = 0; i < n; ++i) {
         rl_host_sampler *s = samplers[i];
-        rc = h->fetch_candidates(i, h->h_kept[i], s->cand_ids, s->cand_probs, stream);
-        if (rc != RL_OK) return rc;
-        s->kept = h->h_kept[i];
-        if (h->h_used[i]) s->rng = h->batch_probe[i];
-        tokens[i] = h->h_token[i];
-        s->remember(h->h_token[i]);
+        const rl::PackedRow &pr = h->h_out[i];
+        s->kept = pr.kept;
+        if (pr.used) s->rng = h->batch_probe[i];
+        tokens[i] = pr.token;
+        s->remember(pr.token);
     }
     return RL_OK;
 }

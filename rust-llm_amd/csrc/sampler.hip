@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "rl_error.h"
+#include "rl_pack.h"
 #include "rl_runtime.h"
 #include "rl_sampler.h"
 #include "full_rest.h"
@@ -31,6 +32,17 @@ constexpr uint32_t FULL_GROUP_MAX = 256;
 constexpr uint32_t CHUNK_SLOTS = 2 * TARGET_WGS;
 
 enum class Path : uint8_t { Stream, Full };
+
+// log2 of the stream kernel's window-set slots for windows of up to n ids: at
+// least twice n (a half-full open-addressed set), at least 64. The set is
+// sized per call from the call's window stride, which bounds every row's
+// window, so a context made for long windows costs the kernel no LDS on calls
+// with short ones.
+uint32_t window_hash_bits(uint32_t n) {
+    uint32_t bits = 6;
+    while ((1u << bits) < 2 * n) ++bits;
+    return bits;
+}
 
 // Which device path a row's settings take (see sampler_kernels.h).
 Path plan_row(const rl_sampling &s, uint32_t vocab) {
@@ -102,13 +114,44 @@ int noalloc_scratch(int device, uint64_t **out) {
     return RL_OK;
 }
 
+// One wave per row: the row's token, kept count and used flag, and its first
+// PACK_CANDS candidates, into the host's result block.
+__global__ __launch_bounds__(WAVE) void k_pack_rows(const uint32_t *token, const uint32_t *kept, const uint8_t *used,
+                                                    const uint32_t *ids, const float *probs, uint64_t cand_stride,
+                                                    PackedRow *out) {
+    const uint32_t row = blockIdx.x, lane = threadIdx.x;
+    const uint32_t k = kept[row];
+    const uint32_t n = k < PACK_CANDS ? k : PACK_CANDS;
+    PackedRow *o = out + row;
+    if (lane < n) {
+        o->ids[lane] = ids[(uint64_t)row * cand_stride + lane];
+        o->probs[lane] = probs[(uint64_t)row * cand_stride + lane];
+    }
+    if (lane == 0) {
+        o->token = token[row];
+        o->kept = k;
+        o->used = used[row];
+    }
+}
+
 }  // namespace
 
 void rl::set_last_error(const std::string &msg) { g_last_error = msg; }
 
+int rl::launch_pack_rows(const uint32_t *token, const uint32_t *kept, const uint8_t *used, const uint32_t *ids,
+                         const float *probs, uint64_t cand_stride, uint32_t rows, PackedRow *out, void *stream) {
+    if (rows == 0) return RL_OK;
+    static_assert(PACK_CANDS <= WAVE, "one lane per packed candidate");
+    hipLaunchKernelGGL(k_pack_rows, dim3(rows), dim3(WAVE), 0, static_cast<hipStream_t>(stream), token, kept, used,
+                       ids, probs, cand_stride, out);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "pack kernel");
+    return RL_OK;
+}
+
 struct rl_sampler_ctx {
     int device = 0;
-    uint32_t max_rows = 0, vocab = 0, max_window = 0, hash_bits = 0, full_group = 0;
+    uint32_t max_rows = 0, vocab = 0, max_window = 0, full_group = 0;
     rl_sampling *d_settings = nullptr;
     uint32_t *d_stream_rows = nullptr, *d_full_rows = nullptr;
     uint64_t *d_chunk_cands = nullptr;
@@ -168,9 +211,6 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     c->max_rows = max_rows;
     c->vocab = vocab;
     c->max_window = max_window;
-    uint32_t bits = 6;
-    while ((1u << bits) < 2 * max_window) ++bits;
-    c->hash_bits = bits;
     c->full_group = std::min(max_rows, FULL_GROUP_MAX);
     try {  // configure fills these in place
         c->stream_rows.reserve(max_rows);
@@ -303,7 +343,7 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
     io.out_ids = out_cand_ids;
     io.out_probs = out_cand_probs;
     io.cand_stride = cand_stride;
-    io.hash_bits = ctx->hash_bits;
+    io.hash_bits = window_hash_bits(io.wstride);
     const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (io.stride % 4 == 0);
 
     // Rows below `rows` on each path (the lists are ascending).
@@ -326,7 +366,7 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
         chunks = std::min(chunks, std::max(1u, (n4 + STEP4 - 1) / STEP4));
         s.chunks = std::max(chunks, 1u);
         FastScratch sc{ctx->d_chunk_cands, ctx->d_chunk_counts, ctx->d_arrive};
-        const size_t lds = window_lds_bytes(ctx->hash_bits);
+        const size_t lds = window_lds_bytes(io.hash_bits);
         dim3 grid(s.chunks, ns);
         if (vec)
             hipLaunchKernelGGL(k_stream<true>, grid, dim3(FAST_THREADS), lds, st, s, sc);
