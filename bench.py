@@ -16,8 +16,10 @@ with --workload.
 --op host_verify times the host Sampler's speculative-verify walk on the host
 wall clock (rl_host_sampler_verify over the 9-row verify workload, then
 rl_host_sampler_commit_verified row by row, every draft accepted), --op
-host_batch one rl_host_sample_batch call over 16 host Samplers; each beside
-the device time of the same rows' rl_sampler_sample_rows call.
+host_batch one rl_host_sample_batch call over 16 host Samplers, --op
+host_sample one rl_host_sampler_sample_device call on one row; each timed from
+C++ (rust-llm_amd/librl_hostbench.so) and printed beside the device time of
+the same rows' rl_sampler_sample_rows call.
 
 --op head times the output head instead (rl_head_logits: t normed hidden rows
 times the tied Q6_K embedding [2560, 248320], logits into HBM); --op head_sample
@@ -55,7 +57,7 @@ def parse():
                     help="skip the candidate outputs (tokens only)")
     ap.add_argument("--op", default="sample",
                     choices=["sample", "top_probability", "argmax", "head", "head_sample", "embed", "host_verify",
-                             "host_batch"],
+                             "host_batch", "host_sample"],
                     help="sample: rl_sampler_sample_rows (the benchmark); top_probability and argmax time "
                          "rl_top_probability_rows and rl_argmax_rows on the same logits; head times "
                          "rl_head_logits, head_sample the head followed by sampling its logits; embed times "
@@ -66,6 +68,9 @@ def parse():
                     help="tokens per embedding lookup (1 = a decode step, more = a prompt)")
     ap.add_argument("--head-rows", type=int, default=1,
                     help="activation rows per head call (1 = a decode step, 9 or 17 = a verify batch)")
+    ap.add_argument("--max-window", type=int, default=None,
+                    help="the sampling context's max_window (default: the workload's 64-id windows); the "
+                         "call's windows stay 64 ids")
     ap.add_argument("--calibration-copy", type=int, default=0,
                     help="after the timed steps, run this many plain device copies of the logits "
                          "(known bytes) so profiler byte counters can be scaled")
@@ -473,17 +478,38 @@ def device_call_ms(ctx, d_logits, rows, settings, windows, wlen, uniforms, calls
     return sorted(out)[len(out) // 2]
 
 
+def hostbench_lib():
+    """librl_hostbench.so: the host Sampler's calls timed from C++ (no
+    interpreter between the calls)."""
+    import ctypes
+    path = os.path.join(ROOT, "rust-llm_amd", "librl_hostbench.so")
+    if not os.path.exists(path):
+        raise RuntimeError("%s is missing: build it with `make -C rust-llm_amd`" % path)
+    L = ctypes.CDLL(path)
+    vp, u64, sz, u32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_size_t, ctypes.c_uint32
+    L.rlb_verify_walks.argtypes = [ctypes.c_int, vp, u64, sz, vp, vp, sz, u32, u32, vp, vp]
+    L.rlb_batch_calls.argtypes = [ctypes.c_int, vp, u64, sz, vp, u32, vp, u32, vp, u32, vp]
+    L.rlb_sample_calls.argtypes = [ctypes.c_int, vp, sz, vp, vp, sz, u32, vp]
+    return L
+
+
 def bench_host(args):
-    """--op host_verify / host_batch: the host Sampler on the host wall clock."""
+    """--op host_verify / host_batch / host_sample: the host Sampler's calls on
+    the host wall clock, timed natively, beside the device time of the same
+    rows' rl_sampler_sample_rows call."""
+    import ctypes
+
     import numpy as np
     import torch
 
     import rl_sampler as R
     import workloads as W
 
+    L = hostbench_lib()
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
-    walls = []
+    calls = args.warmup + args.steps
+    us = np.zeros(calls, np.float64)
     if args.op == "host_verify":
         name = args.workload or "verify"
         wl = W.WORKLOADS[name]
@@ -491,67 +517,58 @@ def bench_host(args):
         n = wl.rows
         d_rows = torch.from_numpy(rows).to(dev)
         set_ = wl.settings(0)
-        history = wl.history()
-        s = R.HostSampler(wl.vocab, set_, max_rows=n)
-        for t in history:
-            s.remember(int(t))
-        committed = 0
-        for i in range(args.warmup + args.steps):
-            # The drafts every row accepts from this state: row i's pick
-            # depends on drafts 0..i-1 and its uniform only, so iterating the
-            # (uncommitted) verify reaches them within n calls; untimed.
-            drafts = np.zeros(n - 1, np.uint32)
-            for _ in range(n):
-                picks = s.verify(d_rows, drafts)
-                if np.array_equal(picks[:-1], drafts):
-                    break
-                drafts = picks[:-1].copy()
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            s.verify(d_rows, drafts)
-            k = 0
-            for r in range(n):
-                t = s.commit_verified(r)
-                k += 1
-                if r < n - 1 and t != drafts[r]:
-                    break
-            el = time.perf_counter() - t0
-            if i >= args.warmup:
-                walls.append(el * 1e3)
-                committed += k
-        # the device call the walk makes, alone: the same rows and windows
+        history = np.ascontiguousarray(wl.history(), np.uint32)
+        committed = np.zeros(calls, np.uint32)
+        torch.cuda.synchronize()
+        rc = L.rlb_verify_walks(0, d_rows.data_ptr(), d_rows.stride(0), wl.vocab, ctypes.addressof(set_),
+                                history.ctypes.data, history.size, n, calls, us.ctypes.data, committed.ctypes.data)
+        if rc != 0:
+            raise RuntimeError("rlb_verify_walks: %d (%s)" % (rc, R.lib().rl_sampler_last_error().decode()))
         ctx = R.DeviceSampler(n, wl.vocab, max_window=W.WINDOW)
         dev_ms = device_call_ms(ctx, d_rows, n, wl.settings_list(), windows, wlen, wl.uniforms(), 20, stream)
-        what = "%s: one verify of %d rows then a commit per row (%.1f rows committed a walk)" % (
-            name, n, committed / args.steps)
+        what = "%s: one rl_host_sampler_verify of %d rows, then rl_host_sampler_commit_verified row by row " \
+               "(%.1f rows committed a walk)" % (name, n, committed[args.warmup:].mean())
         metric = "host walks/s, speculative verify+commit over %d x %d fp32 logits" % (n, wl.vocab)
         unit = "walks/s"
-    else:
+    elif args.op == "host_batch":
         name = args.workload or "spikes"
         wl = W.WORKLOADS[name]
         n = 16
         rows, windows, wlen = wl.generate(0, n)
         settings = wl.settings_list(0, n)
+        sets = (R.Sampling * n)(*settings)
         d_rows = torch.from_numpy(rows).to(dev)
-        samplers = [R.HostSampler(wl.vocab, settings[r], max_rows=n if r == 0 else 1) for r in range(n)]
-        for r in range(n):
-            for t in windows[r, :wlen[r]]:
-                samplers[r].remember(int(t))
-        for i in range(args.warmup + args.steps):
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            R.host_sample_batch(samplers, d_rows)
-            el = time.perf_counter() - t0
-            if i >= args.warmup:
-                walls.append(el * 1e3)
+        torch.cuda.synchronize()
+        rc = L.rlb_batch_calls(0, d_rows.data_ptr(), d_rows.stride(0), wl.vocab, ctypes.addressof(sets), n,
+                               windows.ctypes.data, windows.shape[1], wlen.ctypes.data, calls, us.ctypes.data)
+        if rc != 0:
+            raise RuntimeError("rlb_batch_calls: %d (%s)" % (rc, R.lib().rl_sampler_last_error().decode()))
         ctx = R.DeviceSampler(n, wl.vocab, max_window=W.WINDOW)
         dev_ms = device_call_ms(ctx, d_rows, n, settings, windows, wlen, wl.uniforms(0, n), 20, stream)
         what = "%s rows 0..15: one rl_host_sample_batch call over 16 host Samplers" % name
         metric = "host batch calls/s, 16 host Samplers over 16 x %d fp32 logits" % wl.vocab
         unit = "calls/s"
-    walls.sort()
-    med = walls[len(walls) // 2]
-    mean = sum(walls) / len(walls)
+    else:
+        name = args.workload or "single"
+        wl = W.WORKLOADS[name]
+        n = 1
+        rows, windows, wlen = wl.generate(0, 1)
+        set_ = wl.settings(0)
+        d_rows = torch.from_numpy(rows).to(dev)
+        hist = np.ascontiguousarray(windows[0, :wlen[0]], np.uint32)
+        torch.cuda.synchronize()
+        rc = L.rlb_sample_calls(0, d_rows.data_ptr(), wl.vocab, ctypes.addressof(set_), hist.ctypes.data, hist.size,
+                                calls, us.ctypes.data)
+        if rc != 0:
+            raise RuntimeError("rlb_sample_calls: %d (%s)" % (rc, R.lib().rl_sampler_last_error().decode()))
+        ctx = R.DeviceSampler(1, wl.vocab, max_window=W.WINDOW)
+        dev_ms = device_call_ms(ctx, d_rows, 1, [set_], windows, wlen, wl.uniforms(0, 1), 20, stream)
+        what = "%s: rl_host_sampler_sample_device on one device row" % name
+        metric = "host samples/s, one host Sampler over 1 x %d fp32 logits" % wl.vocab
+        unit = "samples/s"
+    walls = np.sort(us[args.warmup:] / 1e3)
+    med = float(walls[len(walls) // 2])
+    mean = float(walls.mean())
     print("[bench] %s: host wall median %.4f ms (min %.4f, max %.4f); device call alone median %.4f ms" % (
         what, med, walls[0], walls[-1], dev_ms), file=sys.stderr, flush=True)
     line = {
@@ -569,9 +586,9 @@ def bench_host(args):
         "data": "synthetic (seeded generator, rust-llm_amd/csrc/workloads.c)",
         "config": {"workload": what, "rows": n, "vocab": wl.vocab},
         "host_wall_ms_median": round(med, 5),
-        "host_wall_ms_min": round(walls[0], 5),
+        "host_wall_ms_min": round(float(walls[0]), 5),
         "device_call_ms_median": round(dev_ms, 5),
-        "host_overhead_ms": round(med - dev_ms, 5),
+        "host_over_device_ms": round(med - dev_ms, 5),
         "roofline": None,
         "cpu_baseline": None,
     }
@@ -591,7 +608,7 @@ def main():
     if args.op in ("head", "head_sample"):
         bench_head(args)
         return
-    if args.op in ("host_verify", "host_batch"):
+    if args.op in ("host_verify", "host_batch", "host_sample"):
         bench_host(args)
         return
     import numpy as np
@@ -613,7 +630,7 @@ def main():
     d_win = torch.from_numpy(windows.view(np.int32)).to(dev)
     d_wlen = torch.from_numpy(wlen.view(np.int32)).to(dev)
     d_uni = torch.from_numpy(uniforms).to(dev)
-    ctx = R.DeviceSampler(wl.rows, wl.vocab, max_window=W.WINDOW)
+    ctx = R.DeviceSampler(wl.rows, wl.vocab, max_window=args.max_window or W.WINDOW)
     ctx.configure(settings)
     cs = 0 if args.no_candidates else ctx.required_cand_stride()
     out_tok = torch.empty(wl.rows, dtype=torch.int32, device=dev)
@@ -706,6 +723,7 @@ def main():
             "temperature": s0.temperature, "top_k": s0.top_k, "top_p": s0.top_p, "min_p": s0.min_p,
             "repeat_penalty": s0.repeat_penalty, "repeat_last_n": s0.repeat_last_n,
             "candidates_out": bool(cs),
+            "max_window": args.max_window or W.WINDOW,
         },
         "roofline": {
             "bound": "hbm",

@@ -104,7 +104,10 @@ void rl_sampler_destroy(rl_sampler_ctx *ctx);
 int rl_sampler_configure(rl_sampler_ctx *ctx, const rl_sampling *settings, uint32_t rows);
 
 /* Candidates per row the configured settings can keep: the smallest
- * cand_stride rl_sampler_sample_rows accepts with candidate output on. */
+ * cand_stride rl_sampler_sample_rows accepts with candidate output on for
+ * every configured row. A call over rows 0..n-1 needs only what those rows
+ * can keep (1 for greedy rows, top_k for rows with 0 < top_k < vocab, else
+ * vocab). */
 int rl_sampler_required_cand_stride(const rl_sampler_ctx *ctx, uint64_t *out);
 
 /* Samples rows 0..rows-1 (rows <= configured rows). Replaces Sampler::pick

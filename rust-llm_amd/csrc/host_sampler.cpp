@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstring>
 #include <new>
 #include <random>
@@ -32,6 +33,12 @@ uint64_t rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
 bool penalises(const rl_sampling &s) { return s.repeat_penalty != 1.0f && s.repeat_last_n > 0; }
 
 bool same(const rl_sampling &a, const rl_sampling &b) { return std::memcmp(&a, &b, sizeof a) == 0; }
+
+// A row's kept count while its results are pending (a real count is at most
+// the vocabulary, below 2^21).
+constexpr uint32_t KEPT_PENDING = 0xFFFFFFFFu;
+// How long a call polls its results before it waits on the stream instead.
+constexpr double POLL_US = 2000.0;
 
 }  // namespace
 
@@ -114,19 +121,23 @@ struct rl_host_sampler {
     std::vector<rl_sampling> configured, same_set, batch_set;
     std::vector<rl_rng> batch_probe;
     uint64_t cand_cap = 1;
-    // Device buffers. d_in is one call's input, uploaded with one copy:
-    // uniforms[max_rows] (f32), window lengths[max_rows], then the windows,
-    // rows at the call's stride (the longest window of the call).
+    // Device buffers (d_in: a call's inputs when they are uploaded).
     float *d_row = nullptr;
     uint32_t *d_in = nullptr, *d_token = nullptr, *d_kept = nullptr;
     uint8_t *d_used = nullptr;
     uint32_t *d_ids = nullptr;
     float *d_probs = nullptr;
-    // Pinned host memory: h_in is d_in's host side; h_out (coherent) is where
-    // the device writes every row's results (rl_pack.h), d_out its device
-    // address.
-    uint32_t *h_in = nullptr;
-    rl::PackedRow *h_out = nullptr, *d_out = nullptr;
+    // Coherent pinned host memory, with the device's address of each block
+    // (hd_*). h_in holds a call's inputs: uniforms[max_rows] (f32), window
+    // lengths[max_rows], then the windows at the call's stride (its longest
+    // window). h_res receives a call's results (rl_pack.h): token, kept and
+    // used[max_rows], then the first candidates of every row. A call whose
+    // rows all take the stream path reads h_in and writes h_res from its
+    // kernel; any other call uploads h_in to d_in (the full path re-reads a
+    // row's window in every pass) and packs its results into h_res.
+    uint32_t *h_in = nullptr, *hd_in = nullptr;
+    uint8_t *h_res = nullptr, *hd_res = nullptr;
+    size_t res_cands_at = 0;  // byte offset of the candidates in h_res
     // the last call's survivors (Sampler::candidates), capacity cand_cap
     std::vector<uint32_t> cand_ids;
     std::vector<float> cand_probs;
@@ -147,7 +158,7 @@ struct rl_host_sampler {
         for (void *p : {(void *)d_row, (void *)d_in, (void *)d_token, (void *)d_kept, (void *)d_used, (void *)d_ids,
                         (void *)d_probs})
             if (p) (void)hipFree(p);
-        for (void *p : {(void *)h_in, (void *)h_out})
+        for (void *p : {(void *)h_in, (void *)h_res})
             if (p) (void)hipHostFree(p);
         rl_sampler_destroy(ctx);
     }
@@ -155,6 +166,17 @@ struct rl_host_sampler {
     float *h_uniforms() { return reinterpret_cast<float *>(h_in); }
     uint32_t *h_wlen() { return h_in + max_rows; }
     uint32_t *h_windows() { return h_in + 2 * (size_t)max_rows; }
+    // The result block's arrays, in host (dev = false) or device addresses.
+    uint32_t *res_token(bool dev = false) { return reinterpret_cast<uint32_t *>(dev ? hd_res : h_res); }
+    uint32_t *res_kept(bool dev = false) { return res_token(dev) + max_rows; }
+    uint8_t *res_used(bool dev = false) { return reinterpret_cast<uint8_t *>(res_token(dev) + 2 * (size_t)max_rows); }
+    rl::PackedCands *res_cands(bool dev = false) {
+        return reinterpret_cast<rl::PackedCands *>((dev ? hd_res : h_res) + res_cands_at);
+    }
+    static size_t res_layout(uint32_t rows, size_t *cands_at) {
+        *cands_at = ((size_t)rows * 9 + 15) / 16 * 16;  // token, kept, used; candidates 16-byte aligned
+        return *cands_at + (size_t)rows * sizeof(rl::PackedCands);
+    }
 
     void remember(uint32_t t) {  // sample.rs:205-212
         if (recent.empty()) return;
@@ -192,22 +214,62 @@ struct rl_host_sampler {
         return f;
     }
 
-    // Uploads the input block (uniforms, window lengths and `rows` windows at
-    // stride ws), runs the device and packs every row's results into h_out:
-    // one copy, two launches and one synchronisation.
+    // Runs rows 0..rows-1 (windows in h_in at stride ws) and leaves every
+    // row's results in h_res. A call whose rows all take the stream path is
+    // one launch that reads h_in and writes h_res; any other call uploads
+    // h_in (one copy), launches, and packs the results (one more launch).
+    // Either way the host then polls the results (wait_results).
     int run(const float *d_logits, uint64_t stride, uint32_t rows, uint32_t ws, void *stream) {
         hipStream_t st = static_cast<hipStream_t>(stream);
-        const size_t words = 2 * (size_t)max_rows + (size_t)rows * ws;
-        hipError_t e = hipMemcpyAsync(d_in, h_in, words * 4, hipMemcpyHostToDevice, st);
-        if (e != hipSuccess) return herr(RL_ERR_DEVICE, hipGetErrorString(e));
-        int rc = rl_sampler_sample_rows(ctx, d_logits, stride, rows, (uint32_t)vocab, d_in + 2 * (size_t)max_rows, ws,
-                                        d_in + max_rows, reinterpret_cast<const float *>(d_in), d_token, d_kept,
-                                        d_used, d_ids, d_probs, cand_cap, stream);
+        const bool direct = rl::rows_all_stream(ctx, rows);
+        std::fill(res_kept(), res_kept() + rows, KEPT_PENDING);
+        const uint32_t *in = hd_in;
+        hipError_t e = hipSuccess;
+        if (!direct) {
+            const size_t words = 2 * (size_t)max_rows + (size_t)rows * ws;
+            e = hipMemcpyAsync(d_in, h_in, words * 4, hipMemcpyHostToDevice, st);
+            if (e != hipSuccess) return herr(RL_ERR_DEVICE, hipGetErrorString(e));
+            in = d_in;
+        }
+        const uint32_t *win = in + 2 * (size_t)max_rows, *wlen = in + max_rows;
+        const float *uni = reinterpret_cast<const float *>(in);
+        int rc;
+        if (direct) {
+            rl::PackedCands *c = res_cands(true);
+            rc = rl_sampler_sample_rows(ctx, d_logits, stride, rows, (uint32_t)vocab, win, ws, wlen, uni,
+                                        res_token(true), res_kept(true), res_used(true), c->ids, c->probs,
+                                        rl::PACK_STRIDE, stream);
+        } else {
+            rc = rl_sampler_sample_rows(ctx, d_logits, stride, rows, (uint32_t)vocab, win, ws, wlen, uni, d_token,
+                                        d_kept, d_used, d_ids, d_probs, cand_cap, stream);
+            if (rc == RL_OK)
+                rc = rl::launch_pack_rows(d_token, d_kept, d_used, d_ids, d_probs, cand_cap, rows, res_token(true),
+                                          res_kept(true), res_used(true), res_cands(true), stream);
+        }
         if (rc != RL_OK) return rc;
-        rc = rl::launch_pack_rows(d_token, d_kept, d_used, d_ids, d_probs, cand_cap, rows, d_out, stream);
-        if (rc != RL_OK) return rc;
-        e = hipStreamSynchronize(st);
+        return wait_results(rows, stream);
+    }
+
+    // Every row's kept count is the last word of its results the device
+    // writes (it was set to KEPT_PENDING before the launch), so the call is
+    // complete once every row's has changed: the host polls them, which
+    // returns several microseconds sooner than a stream synchronisation.
+    // After POLL_US it waits on the stream instead, which also reports a
+    // device error; a row still pending after that is a device error too.
+    int wait_results(uint32_t rows, void *stream) {
+        using clk = std::chrono::steady_clock;
+        const clk::time_point t0 = clk::now();
+        uint32_t r = 0;
+        for (;;) {
+            while (r < rows && __atomic_load_n(res_kept() + r, __ATOMIC_ACQUIRE) != KEPT_PENDING) ++r;
+            if (r == rows) return RL_OK;
+            if (std::chrono::duration<double, std::micro>(clk::now() - t0).count() > POLL_US) break;
+        }
+        const hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
         if (e != hipSuccess) return herr(RL_ERR_DEVICE, hipGetErrorString(e));
+        for (; r < rows; ++r)
+            if (__atomic_load_n(res_kept() + r, __ATOMIC_ACQUIRE) == KEPT_PENDING)
+                return herr(RL_ERR_DEVICE, "a row's results never arrived");
         return RL_OK;
     }
 
@@ -218,16 +280,16 @@ struct rl_host_sampler {
     // synchronises once for all its rows).
     int take_candidates(uint32_t slot, std::vector<uint32_t> &ids, std::vector<float> &probs, void *stream,
                         bool *queued) {
-        const rl::PackedRow &pr = h_out[slot];
-        const uint32_t n = pr.kept;
+        const rl::PackedCands &pc = res_cands()[slot];
+        const uint32_t n = res_kept()[slot];
         if (n > ids.capacity() || n > probs.capacity())
             return herr(RL_ERR_CAPACITY, "more candidates than the sampler was sized for");
         ids.resize(n);
         probs.resize(n);
         const uint32_t head = std::min(n, rl::PACK_CANDS);
-        std::copy(pr.ids, pr.ids + head, ids.begin());
-        std::copy(pr.probs, pr.probs + head, probs.begin());
-        if (n > head) {
+        std::copy(pc.ids, pc.ids + head, ids.begin());
+        std::copy(pc.probs, pc.probs + head, probs.begin());
+        if (n > head) {  // only a call with full-path rows keeps more: its candidates are in d_ids/d_probs
             hipStream_t st = static_cast<hipStream_t>(stream);
             const uint64_t at = (uint64_t)slot * cand_cap + head;
             hipError_t e = hipMemcpyAsync(ids.data() + head, d_ids + at, (n - head) * 4, hipMemcpyDeviceToHost, st);
@@ -267,10 +329,9 @@ struct rl_host_sampler {
         rc = take_candidates(0, cand_ids, cand_probs, stream, &queued);
         if (rc == RL_OK) rc = finish_copies(queued, stream);
         if (rc != RL_OK) return rc;
-        const rl::PackedRow &pr = h_out[0];
-        kept = pr.kept;
-        if (pr.used) rng = probe;
-        *token = pr.token;
+        kept = res_kept()[0];
+        if (res_used()[0]) rng = probe;
+        *token = res_token()[0];
         remember(*token);  // sample.rs:217
         return RL_OK;
     }
@@ -312,6 +373,8 @@ int rl_host_sampler_new(int device, size_t vocab, const rl_sampling *set, uint32
     (void)hipGetDevice(&prev);
     (void)hipSetDevice(device);
     const size_t in_words = 2 * (size_t)max_rows + (size_t)max_rows * s->wcap;
+    const size_t res_bytes = rl_host_sampler::res_layout(max_rows, &s->res_cands_at);
+    constexpr unsigned pinned = hipHostMallocMapped | hipHostMallocCoherent;
     hipError_t e = hipMalloc(&s->d_row, vocab * 4);
     if (e == hipSuccess) e = hipMalloc(&s->d_in, in_words * 4);
     if (e == hipSuccess) e = hipMalloc(&s->d_token, max_rows * 4);
@@ -319,13 +382,14 @@ int rl_host_sampler_new(int device, size_t vocab, const rl_sampling *set, uint32
     if (e == hipSuccess) e = hipMalloc(&s->d_used, max_rows);
     if (e == hipSuccess) e = hipMalloc(&s->d_ids, (size_t)max_rows * s->cand_cap * 4);
     if (e == hipSuccess) e = hipMalloc(&s->d_probs, (size_t)max_rows * s->cand_cap * 4);
-    if (e == hipSuccess) e = hipHostMalloc(&s->h_in, in_words * 4);
+    if (e == hipSuccess) e = hipHostMalloc(&s->h_in, in_words * 4, pinned);
+    if (e == hipSuccess) e = hipHostMalloc(&s->h_res, res_bytes, pinned);
+    if (e == hipSuccess) e = hipHostGetDevicePointer(reinterpret_cast<void **>(&s->hd_in), s->h_in, 0);
+    if (e == hipSuccess) e = hipHostGetDevicePointer(reinterpret_cast<void **>(&s->hd_res), s->h_res, 0);
     if (e == hipSuccess) {
         std::fill(s->h_in, s->h_in + in_words, 0u);
-        e = hipHostMalloc(&s->h_out, (size_t)max_rows * sizeof(rl::PackedRow),
-                          hipHostMallocMapped | hipHostMallocCoherent);
+        std::fill(s->h_res, s->h_res + res_bytes, (uint8_t)0);
     }
-    if (e == hipSuccess) e = hipHostGetDevicePointer(reinterpret_cast<void **>(&s->d_out), s->h_out, 0);
     (void)hipSetDevice(prev);
     if (e != hipSuccess) {
         delete s;
@@ -417,12 +481,11 @@ int rl_host_sampler_verify(rl_host_sampler *s, const float *device_rows, uint64_
     rc = s->run(device_rows, row_stride, rows, ws, stream);
     if (rc != RL_OK) return rc;
     for (uint32_t i = 0; i < rows; ++i) {
-        const rl::PackedRow &pr = s->h_out[i];
-        s->v_token[i] = pr.token;
-        s->v_kept[i] = pr.kept;
-        s->v_used[i] = (uint8_t)pr.used;
+        s->v_token[i] = s->res_token()[i];
+        s->v_kept[i] = s->res_kept()[i];
+        s->v_used[i] = s->res_used()[i];
         s->v_uniform[i] = s->h_uniforms()[i];
-        picks[i] = pr.token;
+        picks[i] = s->v_token[i];
     }
     std::copy(drafts, drafts + n_drafts, s->v_drafts.begin());
     s->v_rows_n = rows;
@@ -454,13 +517,13 @@ int rl_host_sampler_commit_verified(rl_host_sampler *s, uint32_t row, uint32_t *
         s->h_wlen()[0] = pen ? (uint32_t)s->filled : 0u;
         if (pen) std::copy(s->recent.begin(), s->recent.begin() + s->filled, s->h_windows());
         s->h_uniforms()[0] = u;
-        // Packed row 0 belongs to a row already committed; later rows keep theirs.
+        // Result row 0 belongs to a row already committed; later rows keep theirs.
         const int rc = s->run(s->v_rows + (uint64_t)row * s->v_stride, s->vocab, 1,
                               std::max<uint32_t>(1u, s->h_wlen()[0]), s->v_stream);
         if (rc != RL_OK) return rc;
-        s->v_token[row] = s->h_out[0].token;
-        s->v_kept[row] = s->h_out[0].kept;
-        s->v_used[row] = (uint8_t)s->h_out[0].used;
+        s->v_token[row] = s->res_token()[0];
+        s->v_kept[row] = s->res_kept()[0];
+        s->v_used[row] = s->res_used()[0];
         slot = 0;
     }
     bool queued = false;
@@ -516,11 +579,10 @@ int rl_host_sample_batch(rl_host_sampler *const *samplers, uint32_t n, const flo
     if (rc2 != RL_OK) return rc2;
     for (uint32_t i = 0; i < n; ++i) {
         rl_host_sampler *s = samplers[i];
-        const rl::PackedRow &pr = h->h_out[i];
-        s->kept = pr.kept;
-        if (pr.used) s->rng = h->batch_probe[i];
-        tokens[i] = pr.token;
-        s->remember(pr.token);
+        s->kept = h->res_kept()[i];
+        if (h->res_used()[i]) s->rng = h->batch_probe[i];
+        tokens[i] = h->res_token()[i];
+        s->remember(tokens[i]);
     }
     return RL_OK;
 }

@@ -1,25 +1,37 @@
-// Library-private: the host mirror's per-call result block. After a sampling
-// call, one small kernel writes every row's token, kept count, used flag and
-// first PACK_CANDS candidates into host memory the device can write
-// (coherent pinned memory), so the host reads a call's results after one
-// stream synchronisation, with no copy per array and none per row; only a row
-// that keeps more candidates needs a copy of the rest.
+// Library-private: the host mirror's per-call result block and the plan
+// query it needs. A call's results land in coherent pinned host memory, in
+// one layout whatever the call's rows: every row's token, kept count and used
+// flag, and its first PACK_CANDS candidates. A call whose rows all take the
+// stream path (at most 64 candidates a row, outputs written once at the end)
+// has its kernel write there directly; any other call writes to device
+// memory and one small kernel packs the results there. The host reads them
+// after one stream synchronisation; only a row that keeps more than
+// PACK_CANDS candidates needs a copy of the rest.
 #pragma once
 #include <stdint.h>
+
+#include "rl_sampler.h"
 
 namespace rl {
 
 constexpr uint32_t PACK_CANDS = 64;
 
-struct PackedRow {
-    uint32_t token, kept, used, pad;
+struct PackedCands {
     uint32_t ids[PACK_CANDS];
     float probs[PACK_CANDS];
 };
+// Candidate stride of the block, in 32-bit words: ids and probs of row r are
+// at cands[r].ids / cands[r].probs, i.e. r * PACK_STRIDE words past row 0's.
+constexpr uint64_t PACK_STRIDE = sizeof(PackedCands) / 4;
 
-// out: the device's address of rows PackedRow entries in coherent pinned host
-// memory. Candidates are read from ids/probs rows of cand_stride entries.
+// Packs rows 0..rows-1 of device outputs into the block's arrays (device
+// addresses of coherent pinned host memory): out_token/out_kept/out_used
+// [rows], out_cands[rows].
 int launch_pack_rows(const uint32_t *token, const uint32_t *kept, const uint8_t *used, const uint32_t *ids,
-                     const float *probs, uint64_t cand_stride, uint32_t rows, PackedRow *out, void *stream);
+                     const float *probs, uint64_t cand_stride, uint32_t rows, uint32_t *out_token,
+                     uint32_t *out_kept, uint8_t *out_used, PackedCands *out_cands, void *stream);
+
+// Whether rows 0..rows-1 of the configured context all take the stream path.
+bool rows_all_stream(const rl_sampler_ctx *ctx, uint32_t rows);
 
 }  // namespace rl

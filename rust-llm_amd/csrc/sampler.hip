@@ -115,23 +115,28 @@ int noalloc_scratch(int device, uint64_t **out) {
 }
 
 // One wave per row: the row's token, kept count and used flag, and its first
-// PACK_CANDS candidates, into the host's result block.
+// PACK_CANDS candidates, into the host's result block (the kept count last).
 __global__ __launch_bounds__(WAVE) void k_pack_rows(const uint32_t *token, const uint32_t *kept, const uint8_t *used,
                                                     const uint32_t *ids, const float *probs, uint64_t cand_stride,
-                                                    PackedRow *out) {
+                                                    uint32_t *out_token, uint32_t *out_kept, uint8_t *out_used,
+                                                    PackedCands *out_cands) {
     const uint32_t row = blockIdx.x, lane = threadIdx.x;
     const uint32_t k = kept[row];
     const uint32_t n = k < PACK_CANDS ? k : PACK_CANDS;
-    PackedRow *o = out + row;
     if (lane < n) {
-        o->ids[lane] = ids[(uint64_t)row * cand_stride + lane];
-        o->probs[lane] = probs[(uint64_t)row * cand_stride + lane];
+        out_cands[row].ids[lane] = ids[(uint64_t)row * cand_stride + lane];
+        out_cands[row].probs[lane] = probs[(uint64_t)row * cand_stride + lane];
     }
     if (lane == 0) {
-        o->token = token[row];
-        o->kept = k;
-        o->used = used[row];
+        out_token[row] = token[row];
+        out_used[row] = used[row];
     }
+    // The kept count last, once the row's other stores have completed: the
+    // host polls it.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (lane == 0) out_kept[row] = k;
 }
 
 }  // namespace
@@ -139,11 +144,12 @@ __global__ __launch_bounds__(WAVE) void k_pack_rows(const uint32_t *token, const
 void rl::set_last_error(const std::string &msg) { g_last_error = msg; }
 
 int rl::launch_pack_rows(const uint32_t *token, const uint32_t *kept, const uint8_t *used, const uint32_t *ids,
-                         const float *probs, uint64_t cand_stride, uint32_t rows, PackedRow *out, void *stream) {
+                         const float *probs, uint64_t cand_stride, uint32_t rows, uint32_t *out_token,
+                         uint32_t *out_kept, uint8_t *out_used, PackedCands *out_cands, void *stream) {
     if (rows == 0) return RL_OK;
     static_assert(PACK_CANDS <= WAVE, "one lane per packed candidate");
     hipLaunchKernelGGL(k_pack_rows, dim3(rows), dim3(WAVE), 0, static_cast<hipStream_t>(stream), token, kept, used,
-                       ids, probs, cand_stride, out);
+                       ids, probs, cand_stride, out_token, out_kept, out_used, out_cands);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "pack kernel");
     return RL_OK;
@@ -173,6 +179,7 @@ struct rl_sampler_ctx {
     // Host copy of the plan made by configure.
     uint32_t configured = 0;
     std::vector<uint32_t> stream_rows, full_rows;  // ascending; capacity max_rows
+    std::vector<uint64_t> need_upto;               // [r]: candidates rows 0..r can keep; capacity max_rows
     uint64_t cand_need = 0;
     bool any_drawing = false;
 
@@ -190,6 +197,10 @@ struct rl_sampler_ctx {
         for (void *p : owned) (void)hipFree(p);
     }
 };
+
+bool rl::rows_all_stream(const rl_sampler_ctx *ctx, uint32_t rows) {
+    return ctx->full_rows.empty() || ctx->full_rows.front() >= rows;  // ascending
+}
 
 extern "C" {
 
@@ -215,6 +226,7 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     try {  // configure fills these in place
         c->stream_rows.reserve(max_rows);
         c->full_rows.reserve(max_rows);
+        c->need_upto.reserve(max_rows);
     } catch (const std::bad_alloc &) {
         delete c;
         return fail(RL_ERR_CAPACITY, "out of host memory");
@@ -273,12 +285,14 @@ int rl_sampler_configure(rl_sampler_ctx *ctx, const rl_sampling *settings, uint3
     ctx->configured = 0;
     ctx->stream_rows.clear();
     ctx->full_rows.clear();
+    ctx->need_upto.clear();
     uint64_t need = 0;
     bool drawing = false;
     for (uint32_t r = 0; r < rows; ++r) {
         const Path p = plan_row(settings[r], ctx->vocab);
         (p == Path::Stream ? ctx->stream_rows : ctx->full_rows).push_back(r);
         need = std::max(need, row_cand_need(settings[r], ctx->vocab));
+        ctx->need_upto.push_back(need);
         drawing = drawing || !(settings[r].temperature <= 0.0f);
     }
     const auto &sr = ctx->stream_rows;
@@ -319,8 +333,11 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
     if (rows > 1 && row_stride < vocab) return fail(RL_ERR_ARGUMENT, "row_stride below vocab");
     if ((out_cand_ids == nullptr) != (out_cand_probs == nullptr))
         return fail(RL_ERR_ARGUMENT, "candidate ids and probs must both be given or both be null");
-    if (out_cand_ids && cand_stride < ctx->cand_need)
-        return fail(RL_ERR_CAPACITY, "cand_stride below rl_sampler_required_cand_stride");
+    // The call's own rows decide the stride it needs (a prefix of the
+    // configured rows may keep fewer candidates than all of them).
+    if (out_cand_ids && cand_stride < ctx->need_upto[rows - 1])
+        return fail(RL_ERR_CAPACITY, "cand_stride below what the call's rows can keep "
+                                     "(rl_sampler_required_cand_stride for all configured rows)");
     if (window_len && windows && window_stride > ctx->max_window)
         return fail(RL_ERR_CAPACITY, "window_stride above max_window");
     if (ctx->any_drawing && !uniforms) return fail(RL_ERR_ARGUMENT, "uniforms are null");

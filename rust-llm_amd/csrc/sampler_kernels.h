@@ -61,14 +61,25 @@ __device__ __forceinline__ uint32_t window_len(const RowIO &a, uint32_t row) {
     return l < a.wstride ? l : a.wstride;
 }
 
+// A row's kept count is the last of its outputs to be written, after the
+// wave's other stores have completed, so that a host polling the kept count
+// of results in host memory sees the row's other outputs once it changes.
+__device__ __forceinline__ void store_kept_last(const RowIO &a, uint32_t row, uint32_t kept, bool writer) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);  // this wave's stores have completed
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (writer) a.out_kept[row] = kept;
+}
+
+// A row with one candidate; called by one lane.
 __device__ __forceinline__ void write_single(const RowIO &a, uint32_t row, uint32_t tok) {
     a.out_token[row] = tok;
-    a.out_kept[row] = 1;
     a.out_used[row] = 0;
     if (a.out_ids) {
         a.out_ids[(uint64_t)row * a.cand_stride] = tok;
         a.out_probs[(uint64_t)row * a.cand_stride] = 1.0f;
     }
+    store_kept_last(a, row, 1, true);
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -406,9 +417,9 @@ __device__ __forceinline__ void finalize_row(const RowIO &a, uint32_t row, const
     }
     if (lane == 0) {
         a.out_token[row] = tok;
-        a.out_kept[row] = m;
         a.out_used[row] = 1;
     }
+    store_kept_last(a, row, m, lane == 0);
 }
 
 // Merges the window's distinct ids, with their penalised values
