@@ -684,7 +684,9 @@ def main():
         rate, n, el = cpu_baseline(wl, logits, windows, wlen, uniforms, settings, args.cpu_seconds)
         cpu = {"value": round(rate, 2), "unit": "rows/s", "cores": 1, "kind": "port",
                "sample": "%d rows of the same workload (%s) through the oracle (the C restatement of the "
-                         "reference sampler) on one host core in %.1f s" % (n, name, el),
+                         "reference sampler) on one host core in %.1f s; the reference's own Rust sampler is "
+                         "published at 0.62-0.65 ms a row (1 540-1 610 rows/s, one thread) for these settings "
+                         "at V = 248 320 (docs/decisions.md:969-970), on another host" % (n, name, el),
                "host": info}
         print("[bench] cpu baseline %.1f rows/s over %d rows" % (rate, n), file=sys.stderr, flush=True)
         nt = host_threads(info)

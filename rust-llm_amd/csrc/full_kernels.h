@@ -59,15 +59,11 @@ __device__ __forceinline__ bool identity_order(const rl_sampling &s, uint32_t V)
 }
 
 // Chunk c of n items split into `chunks`: [chunk_lo(c), chunk_lo(c + 1)).
+// Callers split a row's float4 (n <= 2^19, the vocabulary being at most 2^21)
+// into at most MAX_CHUNKS, so n * c fits 32 bits.
+static_assert((uint64_t)MAX_CHUNKS * (1u << 19) < (1ull << 32), "chunk bounds in 32 bits");
 __device__ __forceinline__ uint32_t chunk_lo(uint32_t n, uint32_t c, uint32_t chunks) {
-    return (uint32_t)((uint64_t)n * c / chunks);
-}
-
-// Binary exponent of a finite nonzero f32 (subnormals count as -126): every
-// such value is a multiple of 2^(exponent - 23).
-__device__ __forceinline__ int f32_exponent(float p) {
-    const int e = (int)((__float_as_uint(p) >> 23) & 0xFFu);
-    return e == 0 ? -126 : e - 127;
+    return n * c / chunks;
 }
 
 // The argument (l - max) / t of the reference's p = exp((l - max) / t)
@@ -417,12 +413,9 @@ __global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScra
     __shared__ uint32_t red_cnt[MAX_CHUNKS];   // the finisher: each chunk's listed candidates
     const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
     const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / WAVE;
-    const uint32_t row = a.rows[slot];
-    const rl_sampling s = a.settings[row];
+    const uint32_t row = a.rows ? a.rows[slot] : a.row0 + slot;
     const uint32_t V = a.vocab;
     const uint32_t C = a.chunks;
-    const uint32_t wl = window_len(a, row);
-    const bool pen = penalises(s) && wl > 0;
     const float *rowp = a.logits + (uint64_t)row * a.stride;
     const uint32_t n4 = V / 4;
     const uint32_t q0 = chunk_lo(n4, chunk, C), q1 = chunk_lo(n4, chunk + 1, C);
@@ -431,18 +424,25 @@ __global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScra
     // The window's ids and the exp table load first; then the first step's
     // loads (clamped: no branch around them). Vector loads complete in order,
     // so anything loaded after the step would wait for all of it. The window
-    // bitmap and the tables are built while the step is in flight.
+    // bitmap and the tables are built while the step is in flight. The id
+    // loads are clamped to the call's window stride, so they wait for neither
+    // the row's settings nor its window length (which ids count is decided
+    // when the bitmap is built).
     constexpr uint32_t WIN_PER = 8;  // window ids per thread (max_window <= 2048)
     static_assert(WIN_PER * FULL_THREADS >= 2048, "a window's ids fit the threads");
     // Unconditional (clamped) loads: a load under a divergent branch makes
     // the compiler wait for every load in flight, the step's included.
     uint32_t wid[WIN_PER];
-    const uint32_t *win = a.windows + (uint64_t)row * a.wstride;
-    if (pen) {
+    {
+        const bool have_win = a.windows && a.wlen && a.wstride > 0;  // kernel arguments only
+        // With no windows the loads read the row's settings (never used).
+        const uint32_t *win = have_win ? a.windows + (uint64_t)row * a.wstride
+                                       : reinterpret_cast<const uint32_t *>(a.settings + row);
+        const uint32_t wn = !have_win ? 1u : a.wstride < WIN_PER * FULL_THREADS ? a.wstride : WIN_PER * FULL_THREADS;
 #pragma unroll
         for (uint32_t k = 0; k < WIN_PER; ++k) {
             const uint32_t i = k * FULL_THREADS + tid;
-            wid[k] = win[i < wl ? i : wl - 1];
+            wid[k] = ((const RL_GLB uint32_t *)win)[i < wn ? i : wn - 1];
         }
     }
     const uint64_t tab = EXP2_32_TAB[tid & 31u];
@@ -454,14 +454,23 @@ __global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScra
 #pragma unroll
         for (uint32_t u = 0; u < PASS_U; ++u) A[u] = pass_load<VEC>(rs, rowp, q0 + u * FULL_THREADS + tid, q0, q1);
     }
+    // The row's settings and window length, needed from here on.
+    const rl_sampling s = a.settings[row];
+    const uint32_t wl = window_len(a, row);
+    const bool pen = penalises(s) && wl > 0;
+    // Which of this thread's ids fall in the chunk, worked out outside the
+    // branch below so that the compiler keeps their loads ahead of the step's.
+    uint32_t in_chunk = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < WIN_PER; ++k)
+        if (k * FULL_THREADS + tid < wl && wid[k] >= e0 && wid[k] < e1) in_chunk |= 1u << k;
     if (pen) {
         for (uint32_t i = tid; i < nwords; i += FULL_THREADS) bm[i] = 0;
         __syncthreads();
 #pragma unroll
         for (uint32_t k = 0; k < WIN_PER; ++k) {
             const uint32_t id = wid[k];
-            if (k * FULL_THREADS + tid < wl && id >= e0 && id < e1)
-                atomicOr((uint32_t *)&bm[(id - e0) >> 5], 1u << ((id - e0) & 31));
+            if ((in_chunk >> k) & 1u) atomicOr((uint32_t *)&bm[(id - e0) >> 5], 1u << ((id - e0) & 31));
         }
     }
     if (tid == 0) {

@@ -717,7 +717,7 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
     const FullRow st = f.row[slot];
     if (st.done) return;
     const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / WAVE;
-    const uint32_t row = a.rows[slot];
+    const uint32_t row = a.rows ? a.rows[slot] : a.row0 + slot;
     const rl_sampling s = a.settings[row];
     const uint32_t V = a.vocab;
     const uint32_t k = full_k(s, V);

@@ -231,7 +231,11 @@ struct rl_host_sampler {
             if (e != hipSuccess) return herr(RL_ERR_DEVICE, hipGetErrorString(e));
             in = d_in;
         }
-        const uint32_t *win = in + 2 * (size_t)max_rows, *wlen = in + max_rows;
+        // No window arrays when no row has a window: the kernels then read none.
+        bool any_win = false;
+        for (uint32_t r = 0; r < rows; ++r) any_win = any_win || h_wlen()[r] > 0;
+        const uint32_t *win = any_win ? in + 2 * (size_t)max_rows : nullptr;
+        const uint32_t *wlen = any_win ? in + max_rows : nullptr;
         const float *uni = reinterpret_cast<const float *>(in);
         int rc;
         if (direct) {

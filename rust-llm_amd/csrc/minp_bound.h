@@ -41,10 +41,12 @@
 #pragma once
 #include <stdint.h>
 
+#ifndef RL_HD
 #ifdef __HIPCC__
 #define RL_HD __host__ __device__
 #else
 #define RL_HD
+#endif
 #endif
 
 namespace rl {

@@ -373,29 +373,34 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
         // The stream rows are ascending and distinct: they are 0 .. ns-1
         // exactly when the last is ns - 1, and the kernel then needs no list.
         s.rows = ctx->stream_rows[ns - 1] == ns - 1 ? nullptr : ctx->d_stream_rows;
+        s.row0 = 0;
         const uint32_t n4 = vocab / 4;
-        // Few rows are split into chunks; as many as fill the GPU, but no more
-        // than it takes for every chunk to fit in one tile (a chunk a little
+        // Rows are split into chunks while there are fewer workgroups than
+        // fill the GPU, but no further than one tile a chunk (a chunk a little
         // over one tile pays a second round trip to memory for its rest).
         constexpr uint32_t STEP4 = FAST_THREADS * UNROLL;
         uint32_t chunks = (TARGET_WGS + ns - 1) / ns;
         chunks = std::min(chunks, MAX_CHUNKS);
         chunks = std::min(chunks, std::max(1u, (n4 + STEP4 - 1) / STEP4));
         s.chunks = std::max(chunks, 1u);
+        const size_t wlds = window_lds_bytes(io.hash_bits);
         FastScratch sc{ctx->d_chunk_cands, ctx->d_chunk_counts, ctx->d_arrive};
-        const size_t lds = window_lds_bytes(io.hash_bits);
         dim3 grid(s.chunks, ns);
         if (vec)
-            hipLaunchKernelGGL(k_stream<true>, grid, dim3(FAST_THREADS), lds, st, s, sc);
+            hipLaunchKernelGGL((k_stream<true, UNROLL, FAST_THREADS>), grid, dim3(FAST_THREADS), wlds, st, s, sc);
         else
-            hipLaunchKernelGGL(k_stream<false>, grid, dim3(FAST_THREADS), lds, st, s, sc);
+            hipLaunchKernelGGL((k_stream<false, UNROLL, FAST_THREADS>), grid, dim3(FAST_THREADS), wlds, st, s, sc);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return hip_fail(e, "stream kernels");
     }
     for (uint32_t g0 = 0; g0 < nf; g0 += ctx->full_group) {
         const uint32_t ng = std::min(ctx->full_group, nf - g0);
         RowIO f = io;
-        f.rows = ctx->d_full_rows + g0;
+        // A group whose rows are consecutive needs no list: the kernels index
+        // row0 + slot directly (no dependent load before the row's address).
+        const bool consecutive = ctx->full_rows[g0 + ng - 1] - ctx->full_rows[g0] == ng - 1;
+        f.rows = consecutive ? nullptr : ctx->d_full_rows + g0;
+        f.row0 = ctx->full_rows[g0];
         f.chunks = std::max(1u, std::min(MAX_CHUNKS, (TARGET_WGS + ng - 1) / ng));
         f.chunks = std::min(f.chunks, std::max(1u, vocab / 4096));
         FullScratch fs{ctx->d_keyA,    ctx->d_idA,     ctx->d_keyB, ctx->d_idB,     ctx->d_probs, ctx->d_part_max,

@@ -34,7 +34,8 @@ struct RowIO {
     uint64_t stride;
     uint32_t vocab;
     const rl_sampling *settings;  // indexed by row
-    const uint32_t *rows;         // this path's rows: rows[slot] = row index (k_stream: null = slot)
+    const uint32_t *rows;         // this path's rows: rows[slot] = row index; null: row0 + slot
+    uint32_t row0;                // the first row when rows is null
     const uint32_t *windows;
     uint32_t wstride;
     const uint32_t *wlen;
@@ -55,10 +56,13 @@ struct FastScratch {
     uint32_t *arrive;        // [slot]: chunks of the row done; zero between calls
 };
 
+// The row's window length, at most the call's stride. The load is
+// unconditional (from the row's settings when the call has no windows), so
+// no branch around it holds up the loads issued after it.
 __device__ __forceinline__ uint32_t window_len(const RowIO &a, uint32_t row) {
-    if (!a.wlen || !a.windows) return 0;
-    const uint32_t l = a.wlen[row];
-    return l < a.wstride ? l : a.wstride;
+    const bool have = a.wlen && a.windows;
+    const uint32_t l = *(const RL_GLB uint32_t *)(have ? a.wlen + row : (const uint32_t *)(a.settings + row));
+    return have ? (l < a.wstride ? l : a.wstride) : 0u;
 }
 
 // A row's kept count is the last of its outputs to be written, after the
@@ -98,16 +102,16 @@ __device__ __forceinline__ f32x4 load4(const float *row, uint32_t f) {
     }
 }
 
-// One tile is UNROLL float4 per thread, starting at float4 index `base`.
+// One tile is U float4 per thread, starting at float4 index `base`.
 // The same tile with indices at or past `end` clamped to end - 1 (end >= 1):
 // every lane loads, so no branch surrounds the loads. A branch around a load
 // keeps the compiler from counting the loads in flight, and it then waits for
 // all of them, the next tile's included, before the current tile is filtered.
-template <bool VEC>
+template <bool VEC, uint32_t U = UNROLL, uint32_t NT = FAST_THREADS>
 __device__ __forceinline__ void load_tile_clamped(f32x4 *dst, const float *row, uint32_t base, uint32_t end) {
 #pragma unroll
-    for (uint32_t u = 0; u < UNROLL; ++u) {
-        const uint32_t f = base + u * FAST_THREADS + threadIdx.x;
+    for (uint32_t u = 0; u < U; ++u) {
+        const uint32_t f = base + u * NT + threadIdx.x;
         dst[u] = load4<VEC>(row, f < end ? f : end - 1);
     }
 }
@@ -126,10 +130,16 @@ __device__ __forceinline__ uint64_t read_lane_u64(uint64_t v, uint32_t lane) {
 // runs before every half-tile whose passers might not fit. The kernel makes
 // no function calls: a call would give every wave a scratch frame, and with
 // it a slower launch and spills around the call sites.
-constexpr uint32_t HALF = UNROLL / 2;                  // float4 per thread per half-tile
-constexpr uint32_t HALF_ELEMS = HALF * 4 * WAVE;        // elements a wave filters per half-tile
-constexpr uint32_t SLACK = 48;                          // new candidates between compactions
-constexpr uint32_t CBUF = KMAX + SLACK + HALF_ELEMS;    // per-wave candidate buffer
+constexpr uint32_t SLACK = 48;  // new candidates between compactions
+// A tile of U float4 per thread is filtered in two halves (the first the
+// larger when U is odd); a wave's buffer holds KMAX candidates, SLACK more,
+// and one half-tile's worth.
+template <uint32_t U>
+struct TileShape {
+    static constexpr uint32_t HALF = (U + 1) / 2;                // float4 per thread in the first half
+    static constexpr uint32_t HALF_ELEMS = HALF * 4 * WAVE;      // most elements a wave filters per half
+    static constexpr uint32_t CBUF = KMAX + SLACK + HALF_ELEMS;  // per-wave candidate buffer
+};
 
 struct Stream {
     RL_LDS uint64_t *buf;
@@ -232,16 +242,17 @@ __device__ __forceinline__ void offer_group(Stream &w, f32x4 v, uint32_t id0, ui
     }
 }
 
-// Filters one tile (UNROLL float4 per thread) in two halves, compacting
+// Filters one tile (U float4 per thread) in two halves, compacting
 // before a half whose passers might not fit.
-template <bool GUARD>
+template <bool GUARD, uint32_t U, uint32_t NT>
 __device__ __forceinline__ void process_tile(Stream &w, const f32x4 *T, uint32_t base, uint32_t end) {
+    constexpr uint32_t HALF = TileShape<U>::HALF;
 #pragma unroll
     for (uint32_t h = 0; h < 2; ++h) {
         if (w.cnt >= w.k + SLACK) compact(w);  // then cnt <= k, and k + SLACK + HALF_ELEMS <= CBUF
 #pragma unroll
-        for (uint32_t u = h * HALF; u < (h + 1) * HALF; ++u) {
-            const uint32_t f = base + u * FAST_THREADS + threadIdx.x;
+        for (uint32_t u = h * HALF; u < ((h + 1) * HALF < U ? (h + 1) * HALF : U); ++u) {
+            const uint32_t f = base + u * NT + threadIdx.x;
             offer_group<GUARD>(w, T[u], 4 * f, (!GUARD || f < end) ? 4u : 0u);
         }
     }
@@ -255,15 +266,16 @@ __device__ __forceinline__ void process_tile(Stream &w, const f32x4 *T, uint32_t
 // past `end` were clamped (duplicates of the chunk's last element under other
 // ids) and are left out; a lane with none contributes nothing, and with fewer
 // than k contributing lanes t is 0 (no threshold).
+template <uint32_t U, uint32_t NT>
 __device__ __forceinline__ void bootstrap(Stream &w, const f32x4 *A, uint32_t base, uint32_t end) {
     const uint32_t tid = threadIdx.x;
     uint64_t bound = ~0ull, best = 0;
     for (uint32_t attempt = 0; attempt < 4; ++attempt) {
         best = 0;
 #pragma unroll
-        for (uint32_t u = 0; u < UNROLL; ++u) {
+        for (uint32_t u = 0; u < U; ++u) {
             const float x[4] = {A[u].x, A[u].y, A[u].z, A[u].w};
-            const uint32_t f = base + u * FAST_THREADS + tid;
+            const uint32_t f = base + u * NT + tid;
             const uint32_t id0 = 4 * f;
 #pragma unroll
             for (uint32_t c = 0; c < 4; ++c) {
@@ -318,6 +330,13 @@ __device__ __forceinline__ void rescan_row(const float *rowp, uint32_t vocab, co
     *out_tok = comp_key(am) == 0 ? 0u : comp_id(am);
 }
 
+// Binary exponent of a finite nonzero f32 (subnormals count as -126): every
+// such value is a multiple of 2^(exponent - 23).
+__device__ __forceinline__ int f32_exponent(float p) {
+    const int e = (int)((__float_as_uint(p) >> 23) & 0xFFu);
+    return e == 0 ? -126 : e - 127;
+}
+
 // The reference's tail (sample.rs:259-358) over the row's best nL candidates,
 // by one wave: lane j holds candidate j (composite c, 0 past nL), in
 // descending order. The sequential f64 and f32 sums are replayed in candidate
@@ -365,17 +384,31 @@ __device__ __forceinline__ void finalize_row(const RowIO &a, uint32_t row, const
 
     // exp and the f64 mass (sample.rs:307-311).
     const float p = in ? expf_libm((v - M) / s.temperature) : 0.0f;
+    // Every nonzero p is a multiple of 2^(e - 23) for its exponent e, and
+    // there are at most 64 terms of at most 1, so every partial sum is below
+    // 2^7: when the smallest exponent is -23 or more, every f64 partial sum
+    // needs at most 53 bits and is exact, and a wave scan (or total) gives the
+    // reference's sequential sums bit for bit.
+    const int pe = (in && p != 0.0f) ? f32_exponent(p) : (1 << 20);
+    const bool exact = wave_min_i32(pe) >= -23;
     uint32_t m = nL;
     if (s.top_p < 1.0f) {  // sample.rs:313-324
-        double sum = 0.0;
-        for (uint32_t j = 0; j < nL; ++j) sum += (double)read_lane_f32(p, j);
-        const double target = (double)s.top_p * sum;
-        double cum = 0.0;
-        for (uint32_t j = 0; j < nL; ++j) {
-            cum += (double)read_lane_f32(p, j);
-            if (cum >= target) {
-                m = j + 1;
-                break;
+        if (exact) {
+            const double cum = wave_incl_f64(in ? (double)p : 0.0);
+            const double target = (double)s.top_p * uniform_f64(f64_from_bits(read_lane_u64(f64_bits(cum), nL - 1)));
+            const uint64_t hit = ballot(in && cum >= target);
+            if (hit != 0) m = (uint32_t)__ffsll((unsigned long long)hit);
+        } else {
+            double sum = 0.0;
+            for (uint32_t j = 0; j < nL; ++j) sum += (double)read_lane_f32(p, j);
+            const double target = (double)s.top_p * sum;
+            double cum = 0.0;
+            for (uint32_t j = 0; j < nL; ++j) {
+                cum += (double)read_lane_f32(p, j);
+                if (cum >= target) {
+                    m = j + 1;
+                    break;
+                }
             }
         }
     }
@@ -397,7 +430,10 @@ __device__ __forceinline__ void finalize_row(const RowIO &a, uint32_t row, const
     }
     const uint64_t km = ballot(keep);
     double total = 0.0;  // sample.rs:342
-    for (uint64_t mm = km; mm; mm &= mm - 1) total += (double)read_lane_f32(p, (uint32_t)__ffsll((long long)mm) - 1);
+    if (exact)
+        total = uniform_f64(wave_total_f64(keep ? (double)p : 0.0));
+    else
+        for (uint64_t mm = km; mm; mm &= mm - 1) total += (double)read_lane_f32(p, (uint32_t)__ffsll((long long)mm) - 1);
     const float inv = (float)(1.0 / total);  // sample.rs:343
     const float q = p * inv;
     const float u = a.uniforms[row];
@@ -457,25 +493,23 @@ __device__ __forceinline__ uint64_t ascending_from(const uint64_t *list, uint32_
     return j < n ? list[j] : 0ull;
 }
 
-// grid (chunks, rows on this path), FAST_THREADS threads. Dynamic LDS: the
-// window set. A row split into chunks is finished by whichever of its chunks
+// grid (chunks, rows on this path), NT threads (NT / 64 waves, each with its
+// own candidate buffer), U float4 a thread per tile. Dynamic LDS: the window
+// set. A row split into chunks is finished by whichever of its chunks
 // publishes its list last (a per-row arrival counter), so no second launch.
-template <bool VEC>
-__global__ __launch_bounds__(FAST_THREADS) __attribute__((amdgpu_waves_per_eu(4))) void k_stream(RowIO a, FastScratch sc) {
-    __shared__ uint64_t s_buf[FAST_WAVES * CBUF];
+template <bool VEC, uint32_t U, uint32_t NT>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_stream(RowIO a, FastScratch sc) {
+    constexpr uint32_t NW = NT / WAVE;
+    constexpr uint32_t CBUF = TileShape<U>::CBUF;
+    __shared__ uint64_t s_buf[NW * CBUF];
     __shared__ uint64_t s_T;
-    __shared__ uint32_t s_cnt[FAST_WAVES];
+    __shared__ uint32_t s_cnt[NW];
     extern __shared__ __align__(16) uint8_t smem[];
     const WindowSet ws = window_set(smem, a.hash_bits);
     const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
     // The common case, every row on this path, needs no lookup before the
     // row's address is known.
-    const uint32_t row = a.rows ? a.rows[slot] : slot;
-    const rl_sampling s = a.settings[row];
-    const bool greedy = s.temperature <= 0.0f;
-    const uint32_t k = uniform_u32(greedy ? 1u : (uint32_t)s.top_k);
-    const uint32_t wl = window_len(a, row);
-    const bool pen = penalises(s) && wl > 0;
+    const uint32_t row = a.rows ? a.rows[slot] : a.row0 + slot;
     const float *rowp = a.logits + (uint64_t)row * a.stride;
     const uint32_t V = a.vocab;
     const uint32_t tid = threadIdx.x;
@@ -483,35 +517,50 @@ __global__ __launch_bounds__(FAST_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     const uint32_t lane = lane_id();
 
     // Loop bounds are wave-uniform; readfirstlane keeps them in SGPRs so the
-    // loop control is scalar (the 64-bit division would leave them in VGPRs).
+    // loop control is scalar. chunk * n4 < MAX_CHUNKS * 2^19 fits 32 bits.
+    static_assert((uint64_t)MAX_CHUNKS * (1u << 19) < (1ull << 32), "chunk bounds in 32 bits");
     const uint32_t n4 = V / 4;
-    const uint32_t q0 = uniform_u32((uint32_t)((uint64_t)chunk * n4 / a.chunks));
-    const uint32_t q1 = uniform_u32((uint32_t)((uint64_t)(chunk + 1) * n4 / a.chunks));
-    constexpr uint32_t STEP = FAST_THREADS * UNROLL;
+    const uint32_t q0 = uniform_u32(chunk * n4 / a.chunks);
+    const uint32_t q1 = uniform_u32((chunk + 1) * n4 / a.chunks);
+    constexpr uint32_t STEP = NT * U;
     const uint32_t nfull = (q1 - q0) / STEP;                    // whole tiles
     const uint32_t ntiles = nfull + ((q1 - q0) % STEP ? 1 : 0);  // plus a partial one
 
     // Set-up, ordered so that no wait for one load also waits for a tile:
     // the window ids are loaded first, then the first tile; the ids go into
     // the set, and each id's raw logit is loaded and stored only after the
-    // bootstrap has consumed the tile. A window longer than the workgroup
-    // (rare) is built in full before any tile load.
+    // bootstrap has consumed the tile. Neither load waits for the row's
+    // settings or window length (both are addressed from kernel arguments
+    // alone: the id load is clamped to the call's window stride, and which
+    // ids count is decided once the settings and length have arrived). A
+    // window longer than the workgroup (rare) is built in full after the tile
+    // loads, its own loads waiting behind the tile.
     const uint32_t *wrow = a.windows + (uint64_t)row * a.wstride;
-    const bool small_win = pen && wl <= FAST_THREADS;
-    if (pen && !small_win) window_build(ws, wrow, wl, V, rowp, true);
-    const uint32_t *idp = small_win ? wrow + (tid < wl ? tid : wl - 1) : reinterpret_cast<const uint32_t *>(a.settings + row);
+    const uint32_t *idp = (a.windows && a.wlen && a.wstride > 0)
+                              ? wrow + (tid < a.wstride ? tid : a.wstride - 1)
+                              : reinterpret_cast<const uint32_t *>(a.settings + row);
     const uint32_t id_loaded = *(const RL_GLB uint32_t *)idp;  // unconditional, see load_tile_clamped
     // The first tile. A row of fewer than 4 logits has no tile; it loads 16
     // bytes of its own settings instead, so that this load needs no branch
     // either.
-    f32x4 A[UNROLL], B[UNROLL];
+    f32x4 A[U], B[U];
     {
         const bool any = ntiles > 0;
-        load_tile_clamped<VEC>(A, any ? rowp : (const float *)(a.settings + row), any ? q0 : 0u, any ? q1 : 1u);
+        load_tile_clamped<VEC, U, NT>(A, any ? rowp : (const float *)(a.settings + row), any ? q0 : 0u, any ? q1 : 1u);
     }
+    // The row's settings and window length, needed from here on.
+    const rl_sampling s = a.settings[row];
+    const bool greedy = s.temperature <= 0.0f;
+    const uint32_t k = uniform_u32(greedy ? 1u : (uint32_t)s.top_k);
+    const uint32_t wl = window_len(a, row);
+    const bool pen = penalises(s) && wl > 0;
     RL_LDS uint64_t *lT = (RL_LDS uint64_t *)&s_T;
     if (tid == 0) *lT = 0;
-    if (!pen || small_win) window_clear(ws);
+    const bool small_win = pen && wl <= NT;
+    if (pen && !small_win)
+        window_build(ws, wrow, wl, V, rowp, true);  // ends with a barrier
+    else
+        window_clear(ws);
     __syncthreads();
     const uint32_t my_id = (small_win && tid < wl) ? id_loaded : EMPTY_ID;
     const uint32_t my_slot = my_id < V ? window_insert(ws, my_id) : EMPTY_ID;
@@ -532,7 +581,7 @@ __global__ __launch_bounds__(FAST_THREADS) __attribute__((amdgpu_waves_per_eu(4)
 
     // Wave priority falls as the row progresses (see set_progress_priority).
     __builtin_amdgcn_s_setprio(3);
-    if (ntiles > 0) bootstrap(w, A, q0, q1);
+    if (ntiles > 0) bootstrap<U, NT>(w, A, q0, q1);
     if (ntiles <= 1) {
         // One tile or none (a chunk of a split row): nothing more to load.
         // The window's raw logits were loaded behind the tile, so they are
@@ -540,9 +589,9 @@ __global__ __launch_bounds__(FAST_THREADS) __attribute__((amdgpu_waves_per_eu(4)
         // checks every candidate against the window set); merge_window reads
         // them at the end.
         if (nfull == 1)
-            process_tile<false>(w, A, q0, q1);
+            process_tile<false, U, NT>(w, A, q0, q1);
         else if (ntiles == 1)
-            process_tile<true>(w, A, q0, q1);
+            process_tile<true, U, NT>(w, A, q0, q1);
         if (my_slot != EMPTY_ID) window_store(ws, my_slot, my_id, my_raw);
         __syncthreads();
         w.wtop = window_top(ws);
@@ -555,16 +604,16 @@ __global__ __launch_bounds__(FAST_THREADS) __attribute__((amdgpu_waves_per_eu(4)
         // wave), so the last, partial tile runs through the same loop.
         for (uint32_t t = 0; t < ntiles; t += 2) {
             const uint32_t b0 = q0 + t * STEP, b1 = b0 + STEP;
-            load_tile_clamped<VEC>(B, rowp, b1, q1);
+            load_tile_clamped<VEC, U, NT>(B, rowp, b1, q1);
             if (t < nfull)
-                process_tile<false>(w, A, b0, q1);
+                process_tile<false, U, NT>(w, A, b0, q1);
             else
-                process_tile<true>(w, A, b0, q1);
-            load_tile_clamped<VEC>(A, rowp, b1 + STEP, q1);
+                process_tile<true, U, NT>(w, A, b0, q1);
+            load_tile_clamped<VEC, U, NT>(A, rowp, b1 + STEP, q1);
             if (t + 1 < nfull)
-                process_tile<false>(w, B, b1, q1);
+                process_tile<false, U, NT>(w, B, b1, q1);
             else if (t + 1 < ntiles)
-                process_tile<true>(w, B, b1, q1);
+                process_tile<true, U, NT>(w, B, b1, q1);
             raise_threshold(w, load_shared_T(lT));
             set_progress_priority(t + 2, ntiles);
         }
@@ -588,7 +637,7 @@ __global__ __launch_bounds__(FAST_THREADS) __attribute__((amdgpu_waves_per_eu(4)
         uint64_t top = lane < s_cnt[0] ? lb[lane] : 0ull;
         uint32_t total = s_cnt[0];
 #pragma unroll
-        for (uint32_t j = 1; j < FAST_WAVES; ++j) {
+        for (uint32_t j = 1; j < NW; ++j) {
             top = wave_merge64(top, ascending_from(lb + j * CBUF, s_cnt[j]));
             total += s_cnt[j];
         }
@@ -622,18 +671,19 @@ __global__ __launch_bounds__(FAST_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     __syncthreads();
     if (!s_last) return;
     // The last chunk of the row: every chunk's list is published. Each wave
-    // merges the lists j = wave (mod FAST_WAVES), all loaded at once, then wave
+    // merges the lists j = wave (mod NW), all loaded at once, then wave
     // 0 merges the four results and runs the tail. The lists are read with
     // device-scope loads, which bypass this XCD's L2, issued after the
     // arrival that saw every other chunk's.
     const uint64_t *lists = sc.chunk_cands + (uint64_t)slot * a.chunks * KMAX;
     const uint32_t *counts = sc.chunk_counts + slot * a.chunks;
-    constexpr uint32_t PER = MAX_CHUNKS / FAST_WAVES;
+    // A many-row call (U == UNROLL) splits a row into at most MAX_CHUNKS.
+    constexpr uint32_t PER = (MAX_CHUNKS + NW - 1) / NW;
     uint64_t v[PER];
     uint32_t n[PER];
 #pragma unroll
     for (uint32_t i = 0; i < PER; ++i) {
-        const uint32_t j = wave + FAST_WAVES * i;
+        const uint32_t j = wave + NW * i;
         const bool ok = j < a.chunks;
         n[i] = ok ? __hip_atomic_load(counts + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
         v[i] = ok ? __hip_atomic_load(lists + (uint64_t)j * KMAX + (WAVE - 1 - lane), __ATOMIC_RELAXED,
@@ -644,7 +694,7 @@ __global__ __launch_bounds__(FAST_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     uint32_t total = 0;
 #pragma unroll
     for (uint32_t i = 0; i < PER; ++i) {
-        if (wave + FAST_WAVES * i >= a.chunks) break;
+        if (wave + NW * i >= a.chunks) break;
         top = wave_merge64(top, WAVE - 1 - lane < n[i] ? v[i] : 0ull);  // lane i: list[63 - i], ascending
         total += n[i];
     }
@@ -656,7 +706,7 @@ __global__ __launch_bounds__(FAST_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     if (wave != 0) return;
     total = s_cnt[0];
 #pragma unroll
-    for (uint32_t j = 1; j < FAST_WAVES; ++j) {
+    for (uint32_t j = 1; j < NW; ++j) {
         top = wave_merge64(top, part[j * WAVE + (WAVE - 1 - lane)]);
         total += s_cnt[j];
     }
