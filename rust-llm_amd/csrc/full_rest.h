@@ -47,8 +47,8 @@ struct RestLds {
     } u;
     uint32_t hist[4][256];           // the row's digit histograms (digits flipped: 255 - d)
     uint32_t offs[256];              // a pass's next output position per digit
-    uint32_t cnt[REST_WAVES][256];   // per wave: the tile's count per digit
-    uint32_t pos[REST_WAVES][256];   // per wave: its start within the digit's run of the tile
+    uint32_t cnt[REST_WAVES][256];   // per wave: the tile's count per digit, then its start within the digit's run
+    uint64_t peer[REST_WAVES][256];  // per wave: the lanes of one item with each digit (zero between items)
     uint32_t tcount[256], tstart[256];
     uint32_t bm[HIST_STEP / 32];     // window ids in the current step, one bit per element
     uint32_t cls[4];                 // OR and AND of the keys with the top bit clear, then set
@@ -519,8 +519,18 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
         if constexpr (PACKED && !FROM_LOGITS) {
             // Each element's digit 2 from the run it sits in: the waves
             // write the tile's map run by run, then read it by position.
-            for (uint32_t f = wave; f < 256; f += REST_WAVES) {
-                const uint32_t lo = max(L->run0[f], tb), hi = min(L->run0[f + 1], tb + tn);
+            // Wave w takes the runs w, w + REST_WAVES, ...; lane q reads the
+            // bounds of its q-th run, so all are read at once.
+            constexpr uint32_t FR = 256 / REST_WAVES;
+            uint32_t rb = 0, re = 0;
+            if (lane < FR) {
+                rb = L->run0[wave + REST_WAVES * lane];
+                re = L->run0[wave + REST_WAVES * lane + 1];
+            }
+#pragma unroll
+            for (uint32_t q = 0; q < FR; ++q) {
+                const uint32_t f = wave + REST_WAVES * q;
+                const uint32_t lo = max(read_lane_u32(rb, q), tb), hi = min(read_lane_u32(re, q), tb + tn);
                 for (uint32_t j = lo + lane; j < hi; j += WAVE) L->dmap[j - tb] = (uint8_t)(255u - f);
             }
             __syncthreads();
@@ -583,20 +593,27 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
         auto ranked = [&](uint32_t i) { return hot_out ? i * WAVE + lane < packed : e0 + i * WAVE < n; };
         for (uint32_t d = lane; d < 256; d += WAVE) L->cnt[wave][d] = 0;
         // Rank: item i's lanes with digit d follow the wave's earlier items'.
+        // The lanes with digit d are found by each setting its bit in the
+        // wave's word for d and reading the word back; the wave's LDS
+        // accesses run in order, so every lane reads the word after all the
+        // item's bits are in and before it is cleared, and every peer reads
+        // the wave's count before this item and writes the same count after.
         uint32_t rk[REST_ITEMS];
+        const uint64_t my_bit = 1ull << lane;
 #pragma unroll
         for (uint32_t i = 0; i < REST_ITEMS; ++i) {
             rk[i] = 0;
             if (hot_out && i * WAVE >= packed) continue;  // wave-uniform
-            const bool valid = ranked(i);
-            const uint32_t d = 255u - ((kk[i] >> shift) & 255u);
-            const uint64_t peers = match_digit(d, valid);
-            // The wave's own counter: its LDS accesses run in order, so every
-            // peer reads the count before this item and writes the same count
-            // after it.
-            const uint32_t base = L->cnt[wave][d];
-            rk[i] = base + lanes_below(peers);
-            if (valid) L->cnt[wave][d] = base + (uint32_t)__popcll(peers);
+            if (ranked(i)) {
+                const uint32_t d = 255u - ((kk[i] >> shift) & 255u);
+                RL_LDS uint64_t *w = &L->peer[wave][d];
+                __hip_atomic_fetch_or(w, my_bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+                const uint64_t peers = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+                const uint32_t base = L->cnt[wave][d];
+                rk[i] = base + lanes_below(peers);
+                __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+                L->cnt[wave][d] = base + (uint32_t)__popcll(peers);
+            }
         }
         if (hot_out && lane == 0) L->hcnt[wave] = wave_hot;
         __syncthreads();
@@ -617,10 +634,14 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
         // Per digit: each wave's start within the digit's run of the tile, and
         // the run's length; then the runs' starts.
         if (tid < 256) {
+            uint32_t c[REST_WAVES];
+#pragma unroll
+            for (uint32_t w = 0; w < REST_WAVES; ++w) c[w] = L->cnt[w][tid];
             uint32_t run = 0;
+#pragma unroll
             for (uint32_t w = 0; w < REST_WAVES; ++w) {
-                L->pos[w][tid] = run;
-                run += L->cnt[w][tid];
+                L->cnt[w][tid] = run;
+                run += c[w];
             }
             L->tcount[tid] = run;
         }
@@ -631,7 +652,7 @@ __device__ __forceinline__ void rest_pass(RL_LDS RestLds *L, const RestRow &r, c
         for (uint32_t i = 0; i < REST_ITEMS; ++i) {
             if (ranked(i)) {
                 const uint32_t d = 255u - ((kk[i] >> shift) & 255u);
-                const uint32_t at = L->tstart[d] + L->pos[wave][d] + rk[i];
+                const uint32_t at = L->tstart[d] + L->cnt[wave][d] + rk[i];
                 L->u.tile.k[at] = kk[i];
                 L->u.tile.i[at] = ii[i];
             }
@@ -741,6 +762,7 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
 
     // ---- the candidates in order: fid[0..V), fp[0..k) ----
     if (tid == 0) stats_reset(L);
+    for (uint32_t i = tid; i < REST_WAVES * 256; i += REST_THREADS) (&L->peer[0][0])[i] = 0;
     PStats ps;                 // this thread's share of the list's statistics
     bool sorted = false;       // the last sort pass gathered the statistics
     RestHot hot{false, 0u, 0u, 0u, 0.0f};
