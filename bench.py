@@ -733,6 +733,10 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
+            # The same bytes over the wall-clock time per step, and over the
+            # median time of a call launched on its own.
+            "frac_ms_per_step": round(alg_bytes / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "frac_alone": round(alg_bytes / (median_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
             "traffic": traffic_bytes(name) if args.op == "sample" else None,
             "traffic_source": traffic_source(name) if args.op == "sample" else None,
             "algorithmic_bytes_per_call": alg_bytes,
