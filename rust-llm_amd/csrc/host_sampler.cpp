@@ -373,6 +373,7 @@ int rl_host_sampler_new(int device, size_t vocab, const rl_sampling *set, uint32
         delete s;
         return rc;
     }
+    rl::set_results_polled(s->ctx, true);  // wait_results polls the kept counts
     int prev = 0;
     (void)hipGetDevice(&prev);
     (void)hipSetDevice(device);

@@ -4,9 +4,10 @@
 // flag, and its first PACK_CANDS candidates. A call whose rows all take the
 // stream path (at most 64 candidates a row, outputs written once at the end)
 // has its kernel write there directly; any other call writes to device
-// memory and one small kernel packs the results there. The host reads them
-// after one stream synchronisation; only a row that keeps more than
-// PACK_CANDS candidates needs a copy of the rest.
+// memory and one small kernel packs the results there. Either kernel writes
+// a row's results with system-scope stores and its kept count last, and the
+// host polls the kept counts; only a row that keeps more than PACK_CANDS
+// candidates needs a copy of the rest.
 #pragma once
 #include <stdint.h>
 
@@ -33,5 +34,10 @@ int launch_pack_rows(const uint32_t *token, const uint32_t *kept, const uint8_t 
 
 // Whether rows 0..rows-1 of the configured context all take the stream path.
 bool rows_all_stream(const rl_sampler_ctx *ctx, uint32_t rows);
+
+// Marks the context's calls as writing results that a host polls in host
+// memory: the stream kernel then stores each row's results with system-scope
+// stores, its kept count last (other callers wait on the stream instead).
+void set_results_polled(rl_sampler_ctx *ctx, bool polled);
 
 }  // namespace rl

@@ -123,20 +123,20 @@ __global__ __launch_bounds__(WAVE) void k_pack_rows(const uint32_t *token, const
     const uint32_t row = blockIdx.x, lane = threadIdx.x;
     const uint32_t k = kept[row];
     const uint32_t n = k < PACK_CANDS ? k : PACK_CANDS;
+    // System-scope stores into host memory, the kept count last once the
+    // row's other stores have completed: the host polls it (store_sys).
     if (lane < n) {
-        out_cands[row].ids[lane] = ids[(uint64_t)row * cand_stride + lane];
-        out_cands[row].probs[lane] = probs[(uint64_t)row * cand_stride + lane];
+        store_sys(out_cands[row].ids + lane, ids[(uint64_t)row * cand_stride + lane]);
+        store_sys(out_cands[row].probs + lane, probs[(uint64_t)row * cand_stride + lane]);
     }
     if (lane == 0) {
-        out_token[row] = token[row];
-        out_used[row] = used[row];
+        store_sys(out_token + row, token[row]);
+        store_sys(out_used + row, used[row]);
     }
-    // The kept count last, once the row's other stores have completed: the
-    // host polls it.
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (lane == 0) out_kept[row] = k;
+    if (lane == 0) store_sys(out_kept + row, k);
 }
 
 }  // namespace
@@ -182,6 +182,7 @@ struct rl_sampler_ctx {
     std::vector<uint64_t> need_upto;               // [r]: candidates rows 0..r can keep; capacity max_rows
     uint64_t cand_need = 0;
     bool any_drawing = false;
+    bool polled = false;  // set_results_polled
 
     template <class T>
     hipError_t alloc(T **p, size_t count) {
@@ -197,6 +198,8 @@ struct rl_sampler_ctx {
         for (void *p : owned) (void)hipFree(p);
     }
 };
+
+void rl::set_results_polled(rl_sampler_ctx *ctx, bool polled) { ctx->polled = polled; }
 
 bool rl::rows_all_stream(const rl_sampler_ctx *ctx, uint32_t rows) {
     return ctx->full_rows.empty() || ctx->full_rows.front() >= rows;  // ascending
@@ -361,6 +364,7 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
     io.out_probs = out_cand_probs;
     io.cand_stride = cand_stride;
     io.hash_bits = window_hash_bits(io.wstride);
+    io.polled = ctx->polled ? 1u : 0u;
     const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (io.stride % 4 == 0);
 
     // Rows below `rows` on each path (the lists are ascending).

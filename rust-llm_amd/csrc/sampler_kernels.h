@@ -48,6 +48,7 @@ struct RowIO {
     uint64_t cand_stride;
     uint32_t hash_bits;
     uint32_t chunks;
+    uint32_t polled;  // a host polls the kept counts of results in host memory
 };
 
 struct FastScratch {
@@ -65,23 +66,45 @@ __device__ __forceinline__ uint32_t window_len(const RowIO &a, uint32_t row) {
     return have ? (l < a.wstride ? l : a.wstride) : 0u;
 }
 
-// A row's kept count is the last of its outputs to be written, after the
-// wave's other stores have completed, so that a host polling the kept count
-// of results in host memory sees the row's other outputs once it changes.
+// A system-scope store: written through to memory (sc0 sc1). A plain store
+// to host memory can stay in this XCD's L2 and reach the host after a later
+// one.
+template <class T>
+__device__ __forceinline__ void store_sys(T *p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// A row's results. When a host polls the kept counts of results in host
+// memory (a.polled: the host Sampler's calls), each is a system-scope store
+// and the kept count is stored last, once the wave's other stores have
+// completed, so that the host sees the row's other outputs when it sees the
+// kept count change; other callers wait on the stream and get plain stores.
+template <class T>
+__device__ __forceinline__ void store_out(const RowIO &a, T *p, T v) {
+    if (a.polled)
+        store_sys(p, v);
+    else
+        *p = v;
+}
+
 __device__ __forceinline__ void store_kept_last(const RowIO &a, uint32_t row, uint32_t kept, bool writer) {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);  // this wave's stores have completed
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (writer) a.out_kept[row] = kept;
+    if (a.polled) {
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);  // this wave's stores have completed
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (writer) store_sys(a.out_kept + row, kept);
+    } else if (writer) {
+        a.out_kept[row] = kept;
+    }
 }
 
 // A row with one candidate; called by one lane.
 __device__ __forceinline__ void write_single(const RowIO &a, uint32_t row, uint32_t tok) {
-    a.out_token[row] = tok;
-    a.out_used[row] = 0;
+    store_out(a, a.out_token + row, tok);
+    store_out(a, a.out_used + row, (uint8_t)0);
     if (a.out_ids) {
-        a.out_ids[(uint64_t)row * a.cand_stride] = tok;
-        a.out_probs[(uint64_t)row * a.cand_stride] = 1.0f;
+        store_out(a, a.out_ids + (uint64_t)row * a.cand_stride, tok);
+        store_out(a, a.out_probs + (uint64_t)row * a.cand_stride, 1.0f);
     }
     store_kept_last(a, row, 1, true);
 }
@@ -448,12 +471,12 @@ __device__ __forceinline__ void finalize_row(const RowIO &a, uint32_t row, const
         }
     }
     if (keep && a.out_ids) {
-        a.out_ids[(uint64_t)row * a.cand_stride + pos] = id;
-        a.out_probs[(uint64_t)row * a.cand_stride + pos] = q;
+        store_out(a, a.out_ids + (uint64_t)row * a.cand_stride + pos, id);
+        store_out(a, a.out_probs + (uint64_t)row * a.cand_stride + pos, q);
     }
     if (lane == 0) {
-        a.out_token[row] = tok;
-        a.out_used[row] = 1;
+        store_out(a, a.out_token + row, tok);
+        store_out(a, a.out_used + row, (uint8_t)1);
     }
     store_kept_last(a, row, m, lane == 0);
 }
