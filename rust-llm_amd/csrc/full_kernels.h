@@ -421,13 +421,15 @@ __global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScra
     const uint32_t q0 = chunk_lo(n4, chunk, C), q1 = chunk_lo(n4, chunk + 1, C);
     const uint32_t e0 = 4 * q0, e1 = chunk == C - 1 ? V : 4 * q1;
     const uint32_t nwords = (e1 - e0 + 31) / 32;
-    // The window's ids and the exp table load first; then the first step's
-    // loads (clamped: no branch around them). Vector loads complete in order,
-    // so anything loaded after the step would wait for all of it. The window
+    // The row's settings and window length (one vector load, row_words), the
+    // window's ids and the exp table load first; then the first step's loads
+    // (clamped: no branch around them). Vector loads complete in order, so
+    // anything loaded after the step would wait for all of it. The window
     // bitmap and the tables are built while the step is in flight. The id
     // loads are clamped to the call's window stride, so they wait for neither
     // the row's settings nor its window length (which ids count is decided
     // when the bitmap is built).
+    const uint32_t head_w = row_words(a, row);
     constexpr uint32_t WIN_PER = 8;  // window ids per thread (max_window <= 2048)
     static_assert(WIN_PER * FULL_THREADS >= 2048, "a window's ids fit the threads");
     // Unconditional (clamped) loads: a load under a divergent branch makes
@@ -454,9 +456,12 @@ __global__ __launch_bounds__(FULL_THREADS, 4) void k_full_pass(RowIO a, FullScra
 #pragma unroll
         for (uint32_t u = 0; u < PASS_U; ++u) A[u] = pass_load<VEC>(rs, rowp, q0 + u * FULL_THREADS + tid, q0, q1);
     }
-    // The row's settings and window length, needed from here on.
-    const rl_sampling s = a.settings[row];
-    const uint32_t wl = window_len(a, row);
+    // The row's settings and window length, needed from here on (the
+    // barrier keeps the wait for them below the step's loads).
+    __builtin_amdgcn_sched_barrier(0);
+    rl_sampling s;
+    uint32_t wl;
+    row_head(a, head_w, s, wl);
     const bool pen = penalises(s) && wl > 0;
     // Which of this thread's ids fall in the chunk, worked out outside the
     // branch below so that the compiler keeps their loads ahead of the step's.

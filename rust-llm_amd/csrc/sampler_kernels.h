@@ -66,6 +66,37 @@ __device__ __forceinline__ uint32_t window_len(const RowIO &a, uint32_t row) {
     return have ? (l < a.wstride ? l : a.wstride) : 0u;
 }
 
+// A row's settings and window length by one vector load: lane i < 10 reads
+// dword i of the row's settings, lane 10 its window length (or a settings
+// dword when the call has no windows). The values reach every lane through
+// readlane (row_head). Scalar loads of the same words are the slow way in at
+// kernel start: they miss in the scalar cache, which several CUs share and
+// which then serves its misses nearly one at a time; with 1024 workgroups
+// starting together they took until about 13 us for most of them, where
+// vector loads take one round trip.
+static_assert(sizeof(rl_sampling) == 40, "ten dwords of settings");
+__device__ __forceinline__ uint32_t row_words(const RowIO &a, uint32_t row) {
+    const uint32_t lane = lane_id();
+    const bool have = a.wlen && a.windows;
+    const uint32_t *set = reinterpret_cast<const uint32_t *>(a.settings + row);
+    const uint32_t *p = lane < 10 ? set + lane : have && lane == 10 ? a.wlen + row : set;
+    return *(const RL_GLB uint32_t *)p;
+}
+
+// The settings and the window length (at most the call's stride) from
+// row_words' result.
+__device__ __forceinline__ void row_head(const RowIO &a, uint32_t w, rl_sampling &s, uint32_t &wl) {
+    s.temperature = __uint_as_float(read_lane_u32(w, 0));
+    s.top_p = __uint_as_float(read_lane_u32(w, 1));
+    s.min_p = __uint_as_float(read_lane_u32(w, 2));
+    s.repeat_penalty = __uint_as_float(read_lane_u32(w, 3));
+    s.top_k = (uint64_t)read_lane_u32(w, 4) | ((uint64_t)read_lane_u32(w, 5) << 32);
+    s.repeat_last_n = (uint64_t)read_lane_u32(w, 6) | ((uint64_t)read_lane_u32(w, 7) << 32);
+    s.seed = (uint64_t)read_lane_u32(w, 8) | ((uint64_t)read_lane_u32(w, 9) << 32);
+    const uint32_t l = read_lane_u32(w, 10);
+    wl = (a.wlen && a.windows) ? (l < a.wstride ? l : a.wstride) : 0u;
+}
+
 // A system-scope store: written through to memory (sc0 sc1). A plain store
 // to host memory can stay in this XCD's L2 and reach the host after a later
 // one.
@@ -550,14 +581,16 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     const uint32_t ntiles = nfull + ((q1 - q0) % STEP ? 1 : 0);  // plus a partial one
 
     // Set-up, ordered so that no wait for one load also waits for a tile:
+    // the row's settings and window length (one vector load, row_words) and
     // the window ids are loaded first, then the first tile; the ids go into
     // the set, and each id's raw logit is loaded and stored only after the
-    // bootstrap has consumed the tile. Neither load waits for the row's
-    // settings or window length (both are addressed from kernel arguments
-    // alone: the id load is clamped to the call's window stride, and which
-    // ids count is decided once the settings and length have arrived). A
-    // window longer than the workgroup (rare) is built in full after the tile
-    // loads, its own loads waiting behind the tile.
+    // bootstrap has consumed the tile. The id and tile loads are addressed
+    // from kernel arguments alone (the id load is clamped to the call's
+    // window stride, and which ids count is decided once the settings and
+    // length have arrived). A window longer than the workgroup (rare) is
+    // built in full after the tile loads, its own loads waiting behind the
+    // tile.
+    const uint32_t head_w = row_words(a, row);
     const uint32_t *wrow = a.windows + (uint64_t)row * a.wstride;
     const uint32_t *idp = (a.windows && a.wlen && a.wstride > 0)
                               ? wrow + (tid < a.wstride ? tid : a.wstride - 1)
@@ -571,11 +604,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         const bool any = ntiles > 0;
         load_tile_clamped<VEC, U, NT>(A, any ? rowp : (const float *)(a.settings + row), any ? q0 : 0u, any ? q1 : 1u);
     }
-    // The row's settings and window length, needed from here on.
-    const rl_sampling s = a.settings[row];
+    // The settings and window length are needed from here on (the barrier
+    // keeps the wait for them below the tile's loads).
+    __builtin_amdgcn_sched_barrier(0);
+    rl_sampling s;
+    uint32_t wl;
+    row_head(a, head_w, s, wl);
     const bool greedy = s.temperature <= 0.0f;
     const uint32_t k = uniform_u32(greedy ? 1u : (uint32_t)s.top_k);
-    const uint32_t wl = window_len(a, row);
     const bool pen = penalises(s) && wl > 0;
     RL_LDS uint64_t *lT = (RL_LDS uint64_t *)&s_T;
     if (tid == 0) *lT = 0;
