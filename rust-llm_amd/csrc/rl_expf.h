@@ -114,4 +114,24 @@ struct LdsExpTable {
     __device__ uint64_t operator()(uint32_t i) const { return t[i]; }
 };
 
+// This lane's entry of the table spread over a wave: entry i sits in lanes i
+// and 32 + i.
+__device__ __forceinline__ uint64_t lane_exp_entry() { return EXP2_32_TAB[__lane_id() & 31u]; }
+
+// The table spread over a wave (v = lane_exp_entry(), loaded ahead of need),
+// read by index through the wave's lane permute: a tail evaluating a few exps
+// waits for no memory round trip. Every lane of the wave must be active
+// where it is called (a permute reads nothing from an inactive lane), so use
+// it only with the branch-free expf_libm_nonpos_t, outside any divergent
+// branch.
+struct LaneExpTable {
+    uint64_t v;
+    __device__ uint64_t operator()(uint32_t i) const {
+        const int at = (int)(i << 2);
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(at, (int)(uint32_t)v);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(at, (int)(uint32_t)(v >> 32));
+        return ((uint64_t)hi << 32) | lo;
+    }
+};
+
 }  // namespace rl

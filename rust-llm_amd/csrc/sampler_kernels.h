@@ -391,13 +391,20 @@ __device__ __forceinline__ int f32_exponent(float p) {
     return e == 0 ? -126 : e - 127;
 }
 
+// The row's uniform (0 when the call has none: then no row draws).
+__device__ __forceinline__ float row_uniform(const RowIO &a, uint32_t row) {
+    return a.uniforms ? a.uniforms[row] : 0.0f;
+}
+
 // The reference's tail (sample.rs:259-358) over the row's best nL candidates,
 // by one wave: lane j holds candidate j (composite c, 0 past nL), in
 // descending order. The sequential f64 and f32 sums are replayed in candidate
 // order with readlane, so every lane computes the bits the reference does.
+// tab_v (lane_exp_entry) and u (row_uniform) are loaded by the caller ahead
+// of the tail, so that it waits for no memory round trip.
 __device__ __forceinline__ void finalize_row(const RowIO &a, uint32_t row, const rl_sampling &s, uint32_t k,
                                              uint64_t c, uint32_t nL, const WindowSet &ws, bool pen,
-                                             const float *rowp) {
+                                             const float *rowp, uint64_t tab_v, float u) {
     const uint32_t lane = lane_id();
     if (s.temperature <= 0.0f) {  // greedy: argmax (sample.rs:259-265)
         const uint64_t c0 = read_lane_u64(c, 0);
@@ -436,8 +443,13 @@ __device__ __forceinline__ void finalize_row(const RowIO &a, uint32_t row, const
         return;
     }
 
-    // exp and the f64 mass (sample.rs:307-311).
-    const float p = in ? expf_libm((v - M) / s.temperature) : 0.0f;
+    // exp and the f64 mass (sample.rs:307-311). The argument is never
+    // positive (v <= M, T > 0) unless it is NaN (a NaN candidate, or an
+    // infinite T): the branch-free non-positive exp runs on every lane (its
+    // table is read across lanes), and a NaN gives NaN, as libm's does.
+    const float xe = (v - M) / s.temperature;
+    const float ee = expf_libm_nonpos_t(xe, LaneExpTable{tab_v});
+    const float p = in ? (xe != xe ? xe + xe : ee) : 0.0f;
     // Every nonzero p is a multiple of 2^(e - 23) for its exponent e, and
     // there are at most 64 terms of at most 1, so every partial sum is below
     // 2^7: when the smallest exponent is -23 or more, every f64 partial sum
@@ -490,7 +502,6 @@ __device__ __forceinline__ void finalize_row(const RowIO &a, uint32_t row, const
         for (uint64_t mm = km; mm; mm &= mm - 1) total += (double)read_lane_f32(p, (uint32_t)__ffsll((long long)mm) - 1);
     const float inv = (float)(1.0 / total);  // sample.rs:343
     const float q = p * inv;
-    const float u = a.uniforms[row];
     float cum = 0.0f;  // the draw, sample.rs:349-358
     uint32_t tok = read_lane_u32(id, 63u - (uint32_t)__clzll((long long)km));
     for (uint64_t mm = km; mm; mm &= mm - 1) {
@@ -678,6 +689,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         }
     }
     __builtin_amdgcn_s_setprio(0);
+    // The tail's table entry and uniform, in flight through the row's end.
+    const uint64_t tab_v = lane_exp_entry();
+    const float u_row = row_uniform(a, row);
     // The row's last vocab % 4 elements.
     if (chunk == a.chunks - 1) {
         if (w.cnt >= w.k + SLACK) compact(w);
@@ -706,7 +720,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         const uint32_t nL = total < k ? total : k;
         if (lane >= nL) top = 0;
         if (a.chunks == 1) {
-            finalize_row(a, row, s, k, top, nL, ws, pen, rowp);
+            finalize_row(a, row, s, k, top, nL, ws, pen, rowp, tab_v, u_row);
         } else {
             // Publish this chunk's list; the row's last chunk to arrive finishes
             // it. The list is written with device-scope stores, which write
@@ -772,7 +786,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     if (lane == 0) sc.arrive[slot] = 0;  // ready for the next call
     const uint32_t nL = total < k ? total : k;
     if (lane >= nL) top = 0;
-    finalize_row(a, row, s, k, top, nL, ws, pen, rowp);
+    finalize_row(a, row, s, k, top, nL, ws, pen, rowp, tab_v, u_row);
 }
 
 // ------------------------------------------------------------ argmax ---
