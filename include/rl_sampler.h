@@ -77,13 +77,20 @@ typedef struct rl_sampler_ctx rl_sampler_ctx;
  * entries and windows of up to `max_window` token ids. Replaces the allocation
  * half of Sampler::new (sample.rs:156-172). `device` is a HIP device index.
  *
- * Two limits the reference does not have (RL_ERR_CAPACITY above them):
- *   max_window <= 2048. The reference sizes its ring from any repeat_last_n
- *     (sample.rs:166; the CLI parses it as any usize, main.rs:604, :641-644).
- *     Here a row's distinct window ids live in on-chip memory while its logits
- *     stream past: an open-addressed set of twice the call's window stride in
- *     LDS (up to 32 KiB) on the stream path, eight ids a thread on the full
- *     path's pass. Windows of 65..2048 ids are tested against the oracle.
+ * Windows of any length, as the reference sizes its ring from any
+ * repeat_last_n (sample.rs:166; the CLI parses it as any usize, main.rs:604,
+ * :641-644). A call whose window_stride is at most 2048 keeps each row's
+ * distinct window ids on chip while its logits stream past (an open-addressed
+ * set of twice the stride in LDS on the stream path, eight ids a thread on the
+ * full path's pass). A longer stride takes the reference's own route
+ * (sample.rs:242-257): the call's rows are copied into the context, each
+ * window id is penalised in the copy, and the copy is sampled with no window:
+ * two more launches and three times the logits' HBM traffic. A context with
+ * max_window above 2048 holds that copy, max_rows * vocab floats (rounded up
+ * to a multiple of 4 per row). Windows of 65..2048 ids and of 2049 ids up to
+ * longer than the vocabulary are tested against the oracle.
+ *
+ * One limit the reference does not have (RL_ERR_CAPACITY above it):
  *   vocab <= 2^21 (2 097 152). The reference takes any vocabulary
  *     (sample.rs:156-172). Every index and count on the device paths is 32-bit
  *     with this much room; Qwen's 248 320 is far below it.

@@ -348,7 +348,7 @@ int rl_host_sampler_new(int device, size_t vocab, const rl_sampling *set, uint32
     if (!out || !set || vocab == 0 || vocab > 0xFFFFFFF0u || max_rows == 0)
         return herr(RL_ERR_ARGUMENT, "bad argument");
     *out = nullptr;
-    if (set->repeat_last_n > 2048) return herr(RL_ERR_CAPACITY, "repeat_last_n above 2048");
+    if (set->repeat_last_n > 0xFFFFFFFFull) return herr(RL_ERR_CAPACITY, "repeat_last_n above 2^32 - 1");
     auto *s = new (std::nothrow) rl_host_sampler();
     if (!s) return herr(RL_ERR_CAPACITY, "out of host memory");
     s->device = device;

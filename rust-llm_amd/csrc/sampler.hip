@@ -23,7 +23,10 @@ namespace {
 
 thread_local std::string g_last_error;
 
-constexpr uint32_t MAX_WINDOW = 2048;
+// The longest window the kernels hold on chip (the stream path's LDS set, the
+// full path's ids per thread). A call with a longer window stride runs on a
+// penalised copy of its rows (k_pen_copy, k_pen_window) with no window.
+constexpr uint32_t SET_WINDOW_MAX = 2048;
 // Vocabularies up to 2^21 ids (every index and count on the device paths
 // fits 32 bits with room to spare).
 constexpr uint32_t MAX_VOCAB = 1u << 21;
@@ -139,6 +142,56 @@ __global__ __launch_bounds__(WAVE) void k_pack_rows(const uint32_t *token, const
     if (lane == 0) store_sys(out_kept + row, k);
 }
 
+// Windows longer than SET_WINDOW_MAX ids take the reference's own route
+// (sample.rs:239-257): the row is copied (:242), then each window id below the
+// vocabulary is penalised in the copy (:248-255), and the call samples the copy
+// with no window. Every occurrence of an id writes the same value,
+// penalize(raw[t]), so writing it once per occurrence leaves what the
+// reference's once-per-distinct-id loop leaves, and repeats need no
+// deduplication. The copy's rows are `pen_stride` floats (a multiple of 4), 16-byte
+// aligned.
+constexpr uint32_t PEN_THREADS = 256;
+constexpr uint32_t PEN_TARGET_WGS = 2048;
+
+// grid (x, min(rows, 65535)), PEN_THREADS: rows 0..rows-1 of src into dst.
+template <bool VEC>
+__global__ __launch_bounds__(PEN_THREADS) void k_pen_copy(const float *src, uint64_t stride, uint32_t vocab,
+                                                          uint32_t rows, float *dst, uint64_t dstride) {
+    const uint32_t t0 = blockIdx.x * PEN_THREADS + threadIdx.x, step = gridDim.x * PEN_THREADS;
+    for (uint32_t row = blockIdx.y; row < rows; row += gridDim.y) {
+        const float *s = src + (uint64_t)row * stride;
+        float *d = dst + (uint64_t)row * dstride;
+        uint32_t from = 0;
+        if constexpr (VEC) {
+            const uint32_t n4 = vocab / 4;
+            for (uint32_t q = t0; q < n4; q += step)
+                __builtin_nontemporal_store(__builtin_nontemporal_load((const f32x4 *)s + q), (f32x4 *)d + q);
+            from = 4 * n4;
+        }
+        for (uint32_t i = from + t0; i < vocab; i += step) d[i] = s[i];
+    }
+}
+
+// grid (x, min(rows, 65535)), PEN_THREADS: for each penalising row, every id t
+// < vocab of recent[..filled] gets penalize(src[t]) in dst (after k_pen_copy).
+__global__ __launch_bounds__(PEN_THREADS) void k_pen_window(const float *src, uint64_t stride, uint32_t vocab,
+                                                            uint32_t rows, const rl_sampling *settings,
+                                                            const uint32_t *windows, uint32_t wstride,
+                                                            const uint32_t *wlen, float *dst, uint64_t dstride) {
+    const uint32_t t0 = blockIdx.x * PEN_THREADS + threadIdx.x, step = gridDim.x * PEN_THREADS;
+    for (uint32_t row = blockIdx.y; row < rows; row += gridDim.y) {
+        const rl_sampling s = settings[row];
+        if (!penalises(s)) continue;
+        const uint32_t l = wlen[row];
+        const uint32_t wl = l < wstride ? l : wstride;
+        const uint32_t *w = windows + (uint64_t)row * wstride;
+        for (uint32_t i = t0; i < wl; i += step) {
+            const uint32_t t = w[i];
+            if (t < vocab) dst[(uint64_t)row * dstride + t] = penalize(src[(uint64_t)row * stride + t], s.repeat_penalty);
+        }
+    }
+}
+
 }  // namespace
 
 void rl::set_last_error(const std::string &msg) { g_last_error = msg; }
@@ -175,6 +228,8 @@ struct rl_sampler_ctx {
     uint32_t *d_tp_nan = nullptr;
     double *d_tp_sum = nullptr;
     uint32_t *d_tp_small = nullptr;  // per chunk: nonzero terms below 2^-26
+    float *d_pen = nullptr;          // max_window > SET_WINDOW_MAX: the penalised rows
+    uint64_t pen_stride = 0;         // floats per row of d_pen
     std::vector<void *> owned;
     // Host copy of the plan made by configure.
     uint32_t configured = 0;
@@ -214,8 +269,6 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     if (!out) return fail(RL_ERR_ARGUMENT, "out is null");
     *out = nullptr;
     if (max_rows == 0 || vocab == 0) return fail(RL_ERR_ARGUMENT, "max_rows and vocab must be positive");
-    if (max_window > MAX_WINDOW)
-        return fail(RL_ERR_CAPACITY, "max_window above " + std::to_string(MAX_WINDOW));
     if (vocab > MAX_VOCAB) return fail(RL_ERR_CAPACITY, "vocab above " + std::to_string(MAX_VOCAB));
     DeviceGuard g(device);
     if (!g.ok) return fail(RL_ERR_DEVICE, "cannot select device " + std::to_string(device));
@@ -262,6 +315,10 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     if (e == hipSuccess) e = c->alloc(&c->d_tp_nan, std::max<size_t>(CHUNK_SLOTS, max_rows));
     if (e == hipSuccess) e = c->alloc(&c->d_tp_sum, std::max<size_t>(CHUNK_SLOTS, max_rows));
     if (e == hipSuccess) e = c->alloc(&c->d_tp_small, std::max<size_t>(CHUNK_SLOTS, max_rows));
+    if (max_window > SET_WINDOW_MAX) {
+        c->pen_stride = (V + 3) & ~(size_t)3;
+        if (e == hipSuccess) e = c->alloc(&c->d_pen, (size_t)max_rows * c->pen_stride);
+    }
     if (e != hipSuccess) {
         delete c;
         return hip_fail(e, "hipMalloc");
@@ -363,9 +420,33 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
     io.out_ids = out_cand_ids;
     io.out_probs = out_cand_probs;
     io.cand_stride = cand_stride;
-    io.hash_bits = window_hash_bits(io.wstride);
     io.polled = ctx->polled ? 1u : 0u;
-    const bool vec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (io.stride % 4 == 0);
+    if (io.windows && io.wstride > SET_WINDOW_MAX) {
+        // A window longer than the kernels hold on chip: sample a penalised
+        // copy of the rows, with no window (k_pen_copy).
+        const bool svec = (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (io.stride % 4 == 0);
+        const uint32_t gy = std::min(rows, 65535u);
+        const uint32_t per_row = std::max(1u, (PEN_TARGET_WGS + rows - 1) / rows);
+        const uint32_t cx = std::max(1u, std::min(per_row, (vocab / 4 + PEN_THREADS - 1) / PEN_THREADS));
+        const uint32_t wx = std::max(1u, std::min(per_row, (io.wstride + PEN_THREADS - 1) / PEN_THREADS));
+        if (svec)
+            hipLaunchKernelGGL(k_pen_copy<true>, dim3(cx, gy), dim3(PEN_THREADS), 0, st, logits, io.stride, vocab, rows,
+                               ctx->d_pen, ctx->pen_stride);
+        else
+            hipLaunchKernelGGL(k_pen_copy<false>, dim3(cx, gy), dim3(PEN_THREADS), 0, st, logits, io.stride, vocab,
+                               rows, ctx->d_pen, ctx->pen_stride);
+        hipLaunchKernelGGL(k_pen_window, dim3(wx, gy), dim3(PEN_THREADS), 0, st, logits, io.stride, vocab, rows,
+                           ctx->d_settings, io.windows, io.wstride, io.wlen, ctx->d_pen, ctx->pen_stride);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return hip_fail(e, "penalty copy kernels");
+        io.logits = ctx->d_pen;
+        io.stride = ctx->pen_stride;
+        io.windows = nullptr;
+        io.wstride = 0;
+        io.wlen = nullptr;
+    }
+    io.hash_bits = window_hash_bits(io.wstride);
+    const bool vec = (reinterpret_cast<uintptr_t>(io.logits) % 16 == 0) && (io.stride % 4 == 0);
 
     // Rows below `rows` on each path (the lists are ascending).
     const uint32_t ns = (uint32_t)(std::lower_bound(ctx->stream_rows.begin(), ctx->stream_rows.end(), rows) -

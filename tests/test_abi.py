@@ -34,8 +34,9 @@ def test_status_codes_without_a_device():
     lib = R.lib()
     h = ctypes.c_void_p()
     assert lib.rl_sampler_create(0, 0, 100, 64, ctypes.byref(h)) == R.RL_ERR_ARGUMENT
-    assert lib.rl_sampler_create(0, 4, 100, 5000, ctypes.byref(h)) == R.RL_ERR_CAPACITY
-    assert b"max_window" in lib.rl_sampler_last_error()
+    # Windows of any length are accepted (sample.rs:166): with no GPU here the
+    # call gets as far as selecting the device.
+    assert lib.rl_sampler_create(0, 4, 100, 5000, ctypes.byref(h)) == R.RL_ERR_DEVICE
     assert lib.rl_sampler_create(0, 4, (1 << 21) + 1, 64, ctypes.byref(h)) == R.RL_ERR_CAPACITY
     assert b"vocab" in lib.rl_sampler_last_error()
     assert lib.rl_sampler_create(0, 4, 100, 64, None) == R.RL_ERR_ARGUMENT

@@ -1,4 +1,5 @@
-"""Repetition-penalty windows of 65 to 2048 ids on the GPU, against the oracle.
+"""Repetition-penalty windows of 65 ids up to longer than the vocabulary on the
+GPU, against the oracle.
 
 The reference penalises each distinct id of recent[..filled] once
 (sample.rs:239-257), whatever the window's length. These tests run windows
@@ -13,7 +14,10 @@ wave, and at the context's largest (2048), on every device path:
 Rows carry spikes on window ids (so the penalty decides the kept set), ids
 past the vocabulary, repeats, and ids in the row's last vocab % 4 elements.
 Windows are given with the context's stride (2048) and with a stride equal to
-the window (the stream kernel sizes its set from the call's stride).
+the window (the stream kernel sizes its set from the call's stride). Windows
+past 2048 ids (2049, 3000, 4096, 6000, and 12 000 over a vocabulary of 5003)
+run on a penalised copy of the rows, on both paths and through the host's
+verify walk.
 Results must match bit for bit."""
 import numpy as np
 import pytest
@@ -58,14 +62,14 @@ def window_rows(rng, rows, V, wl):
     return logits, win
 
 
-def run_case(device, logits, settings, windows, wlen, uniforms, stride_mode):
+def run_case(device, logits, settings, windows, wlen, uniforms, stride_mode, max_window=MAX_WINDOW):
     import torch
     rows, V = logits.shape
     wl = windows.shape[1]
-    wstride = MAX_WINDOW if stride_mode == "max" else wl
+    wstride = max_window if stride_mode == "max" else wl
     wbuf = np.zeros((rows, wstride), np.uint32)
     wbuf[:, :wl] = windows
-    ctx = R.DeviceSampler(rows, V, max_window=MAX_WINDOW)
+    ctx = R.DeviceSampler(rows, V, max_window=max_window)
     ctx.configure(settings)
     cs = ctx.required_cand_stride()
     tok = torch.empty(rows, dtype=torch.int32, device=device)
@@ -134,6 +138,61 @@ def test_a_long_window_on_one_row_and_on_many(device):
         assert_rows_match("%d rows" % rows, got, want, settings)
 
 
+@pytest.mark.parametrize("V", [151936, 100003])
+@pytest.mark.parametrize("wl", [2049, 6000])
+def test_windows_longer_than_the_on_chip_set(device, V, wl):
+    """Windows past 2048 ids run on a penalised copy of the rows (the copy
+    takes float4 loads for V = 151936 and single floats for the odd 100003),
+    with the window's stride equal to it and inside a context made for 8192."""
+    rng = np.random.default_rng(V + 11 * wl)
+    settings = long_window_settings(wl)
+    rows = len(settings)
+    logits, windows = window_rows(rng, rows, V, wl)
+    wlen = np.full(rows, wl, np.uint32)
+    wlen[6] = wl // 2
+    wlen[1] = 0  # a penalising row with an empty window: no penalty
+    uniforms = rng.random(rows).astype(np.float32)
+    plain = O.pick_rows(logits, [as_oracle_settings(s) for s in settings], windows, np.zeros(rows, np.uint32),
+                        uniforms, cand_cap=V)
+    for stride_mode, mw in (("exact", wl), ("max", 8192)):
+        print("windows past the set: V=%d wl=%d stride=%s max_window=%d" % (V, wl, stride_mode, mw), flush=True)
+        got, want = run_case(device, logits, settings, windows, wlen, uniforms, stride_mode, max_window=mw)
+        assert_rows_match("V=%d wl=%d stride=%s" % (V, wl, stride_mode), got, want, settings)
+    assert any(plain["token"][r] != want["token"][r] or plain["kept"][r] != want["kept"][r] for r in range(rows))
+
+
+def test_a_window_longer_than_the_vocabulary(device):
+    """A ring longer than the vocabulary (sample.rs:166 takes any length):
+    12 000 ids over V = 5003, so every id repeats and most of the vocabulary
+    is penalised, ids past V among them."""
+    V, wl = 5003, 12000
+    rng = np.random.default_rng(12000)
+    settings = long_window_settings(wl)
+    rows = len(settings)
+    logits, windows = window_rows(rng, rows, V, wl)
+    wlen = np.full(rows, wl, np.uint32)
+    wlen[3] = 4000
+    uniforms = rng.random(rows).astype(np.float32)
+    got, want = run_case(device, logits, settings, windows, wlen, uniforms, "exact", max_window=wl)
+    assert_rows_match("V=%d wl=%d" % (V, wl), got, want, settings)
+
+
+def test_a_window_past_the_set_on_many_rows(device):
+    """160 rows with 3000-id windows: the copy kernels' grid walks the rows."""
+    V = 151936
+    rows = 160
+    rng = np.random.default_rng(300)
+    base = long_window_settings(3000)
+    settings = [base[r % len(base)] for r in range(rows)]
+    logits, windows = window_rows(rng, rows, V, 3000)
+    wlen = np.full(rows, 3000, np.uint32)
+    wlen[::5] = rng.integers(0, 3001, wlen[::5].size)
+    uniforms = rng.random(rows).astype(np.float32)
+    print("windows past the set: %d rows" % rows, flush=True)
+    got, want = run_case(device, logits, settings, windows, wlen, uniforms, "max", max_window=4096)
+    assert_rows_match("%d rows" % rows, got, want, settings)
+
+
 def oracle_walk(o, rows, drafts):
     picks = []
     for i in range(rows.shape[0]):
@@ -144,7 +203,7 @@ def oracle_walk(o, rows, drafts):
     return picks
 
 
-@pytest.mark.parametrize("last_n", [300, 2048])
+@pytest.mark.parametrize("last_n", [300, 2048, 4096])
 @pytest.mark.parametrize("kind", ["top_k", "min_p", "greedy"])
 def test_the_verify_walk_with_a_long_window(device, kind, last_n):
     """generate.rs:389-451 with a ring of 300 or 2048 ids, wrapped by a long
