@@ -1123,10 +1123,35 @@ __global__ __launch_bounds__(REST_THREADS) void k_full_rest(RowIO a, FullScratch
         // The draw stores q over p for the rounds it stages (when the caller
         // wants the candidates), so the normalisation below reads only the rest.
         double unused;
-        const uint32_t j = chunk_replay<24, REST_THREADS>(
-            fpw, [inv](uint32_t bits) { return __uint_as_float(bits) * inv; }, m,
-            [u](double c) { return c > (double)u; }, cr, &unused, out ? (uint32_t *)fp : nullptr, &qdone, hr);
-        pick = j < m ? j : m - 1;
+        const auto qterm = [inv](uint32_t bits) { return __uint_as_float(bits) * inv; };
+        const auto over_u = [u](double c) { return c > (double)u; };
+        const uint32_t hlo = min(hr.lo, m), hhi = min(hr.hi, m);
+        if (hhi > hlo) {
+            // The hot key's block of equal terms is crossed in closed form, a
+            // step per binade of the sum (equal_run_walk): the replay runs up
+            // to the block, and from its end with the sum there. Only the
+            // first replay stores q; the normalisation below writes the rest.
+            double sb;
+            const uint32_t j0 =
+                chunk_replay<24, REST_THREADS>(fpw, qterm, hlo, over_u, cr, &sb, out ? (uint32_t *)fp : nullptr, &qdone);
+            if (j0 < hlo) {
+                pick = j0;
+            } else {
+                const uint32_t jh = equal_run_walk<24>(sb, __float_as_uint(qterm(hr.word)), hhi - hlo, over_u);
+                if (jh < hhi - hlo) {
+                    pick = hlo + jh;
+                } else {
+                    __syncthreads();  // every thread has read the first replay's sum
+                    const uint32_t j1 = chunk_replay<24, REST_THREADS>(fpw + hhi, qterm, m - hhi, over_u, cr, &unused,
+                                                                       nullptr, nullptr, HotRange(), sb);
+                    pick = j1 < m - hhi ? hhi + j1 : m - 1;
+                }
+            }
+        } else {
+            const uint32_t j = chunk_replay<24, REST_THREADS>(fpw, qterm, m, over_u, cr, &unused,
+                                                              out ? (uint32_t *)fp : nullptr, &qdone, hr);
+            pick = j < m ? j : m - 1;
+        }
     } else {
         if (tid == 0) L->sh_tok = m - 1;
         __syncthreads();

@@ -310,6 +310,70 @@ RL_HD inline bool seg_multiple(const SumSeg &g, int gx) {
     return g.uexp >= gx || (int)__builtin_ctzll(g.n) >= gx - g.uexp;
 }
 
+// Adds `count` equal terms x (bits xb: finite, >= 0) in order to the running
+// sum s (a P-bit value >= 0, pred(s) false), one segment of the sum at a time.
+// On the grid of s's segment the first term adds map_inc(t, parity) steps and
+// every later one t.i0: a term that is not an exact tie adds the same steps
+// from either parity, and a tie leaves the significand even. So the partial
+// sums inside the segment are n + first + (j - 1) * rest for the j-th term, up
+// to the term whose sum would reach the segment's end, which is added with the
+// IEEE addition and starts the next segment. pred must be monotone in the
+// partial sum. Returns the index of the first term whose partial sum meets
+// pred, with that sum in s, or count, with the sum of all of them in s. The
+// cost is a step per segment the sum crosses (and a bisection where pred is
+// met), whatever count is.
+template <int P, class Pred>
+RL_HD inline uint32_t equal_run_walk(double &s, uint32_t xb, uint32_t count, Pred pred) {
+    if (xb == 0u) return count;  // +0 adds nothing
+    const float x = f32_from_bits(xb);
+    uint32_t done = 0;
+    while (done < count) {
+        if (!(s > 0.0)) {  // from +0 the first term is the sum
+            s = add_p<P>(s, x);
+            if (pred(s)) return done;
+            ++done;
+            continue;
+        }
+        const SumSeg g = seg_of<P>(s);
+        const TermMap t = map_of(xb, g.uexp);
+        const uint64_t first = map_inc(t, (uint32_t)(g.n & 1u)), rest = t.i0;
+        const uint64_t left = count - done;
+        // K: the terms whose sums stay below the segment's end (at most left).
+        uint64_t K;
+        if (g.n + first >= g.lim) {
+            K = 0;
+        } else if (rest == 0) {
+            K = left;
+        } else {
+            const uint64_t a = g.lim - g.n - first;  // the first j with sum >= lim is 1 + ceil(a / rest)
+            const uint64_t jl = 1 + (a + rest - 1) / rest;
+            K = jl - 1 < left ? jl - 1 : left;
+        }
+        if (K > 0) {
+            auto sum_at = [&](uint64_t j) { return scaled(g.n + first + (j - 1) * rest, g.uexp); };
+            if (pred(sum_at(K))) {
+                uint64_t lo = 1, hi = K;  // the first j in [1, K] meeting pred
+                while (lo < hi) {
+                    const uint64_t mid = lo + (hi - lo) / 2;
+                    if (pred(sum_at(mid)))
+                        hi = mid;
+                    else
+                        lo = mid + 1;
+                }
+                s = sum_at(lo);
+                return done + (uint32_t)(lo - 1);
+            }
+            s = sum_at(K);
+            done += (uint32_t)K;
+            if (done == count) return count;
+        }
+        s = add_p<P>(s, x);  // this term's sum leaves the segment
+        if (pred(s)) return done;
+        ++done;
+    }
+    return count;
+}
+
 #if defined(__HIPCC__)
 // ------------------------------------------------------------- device ---
 // LDS a workgroup of NT threads needs for seq_replay. The per-wave records
@@ -905,15 +969,17 @@ struct HotRange {
 };
 
 // Returns as seq_replay does, for the terms x_j = term(src[j]) (raw 32-bit
-// words; src[j] read as hr.word for j in hr), j < n; every thread of the
-// workgroup (1024) calls it. With wb, the
+// words; src[j] read as hr.word for j in hr), j < n, added to the running sum
+// s0 (a P-bit value >= 0; +0 by default); every thread of the workgroup
+// (1024) calls it. With wb, the
 // terms of every round it stages are also stored to wb[j] (wb may be src: a
 // round's words are read two rounds before they are written), and *staged
 // gets how many: a prefix of [0, n).
 template <int P, uint32_t NT, class Term, class Pred>
 __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term, uint32_t n, Pred pred,
                                                  RL_LDS ChunkLds *L, double *sum, uint32_t *wb = nullptr,
-                                                 uint32_t *staged = nullptr, const HotRange &hr_in = HotRange()) {
+                                                 uint32_t *staged = nullptr, const HotRange &hr_in = HotRange(),
+                                                 double s0 = 0.0) {
     static_assert(NT / 64 - 1 == CR_WORKERS, "wave 0 chains, the other waves stage two chunks each");
     // The range cut at n: the words past n are zeros.
     HotRange hr = hr_in;
@@ -946,13 +1012,13 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
     const __amdgpu_buffer_rsrc_t rw =
         __builtin_amdgcn_make_buffer_rsrc((void *)wb, (short)0, wb ? (int)(n * 4u) : 0, 0x00020000);
     if (staged) *staged = 0;
-    if (n > 0 && pred(0.0)) {
-        // A predicate that +0 already meets is met by the first term's sum.
-        *sum = add_p<P>(0.0, term(hr.fix(0, __builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 0))));
+    if (n > 0 && pred(s0)) {
+        // A predicate that s0 already meets is met by the first term's sum.
+        *sum = add_p<P>(s0, term(hr.fix(0, __builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 0))));
         return 0;
     }
     if (rounds == 0) {
-        *sum = 0.0;
+        *sum = s0;
         return n;
     }
     // A worker's terms of the round it stages, and their f64 chunk sum.
@@ -1026,12 +1092,12 @@ __device__ __forceinline__ uint32_t chunk_replay(const uint32_t *src, Term term,
         if (rounds > 1) fetch_round(1);
     }
     if (tid == 0) {
-        L->s[0] = 0.0;
+        L->s[0] = s0;
         L->hit[0] = n;
     }
     __syncthreads();
     if (worker) {
-        prepare(0, 0.0);
+        prepare(0, s0);
         if (rounds > 1) {
             stage(1);
             if (rounds > 2) fetch_round(2);

@@ -359,6 +359,83 @@ static void check_runs() {
     }
 }
 
+// equal_run_walk (a run of equal terms crossed a segment at a time) against
+// the plain loop from the same start: the sum after the run, and the first
+// index meeting `partial > thr` and `partial >= thr` for thresholds at, just
+// below and just above partial sums, 0 and past the end. Terms are drawn as
+// exact ties on the start's grid, multiples of it, zeros, subnormals, terms
+// far below half a step, and terms larger than the start.
+template <int P>
+static void check_equal_runs(int &cases) {
+    for (int rep = 0; rep < 3000; ++rep) {
+        double s0 = 0.0;
+        const int sk = (int)(rnd() % 6);
+        if (sk == 1) s0 = (double)from_bits(1u + (uint32_t)(rnd() % 0x7FFFFFu));      // subnormal f32
+        if (sk >= 2) s0 = (double)(float)ldexp(unit() + 0.5, -(int)(rnd() % 40));
+        if (P == 53 && sk == 5) s0 = ldexp(1.0 + unit(), -(int)(rnd() % 40));        // a full f64
+        float x;
+        const int xk = (int)(rnd() % 8);
+        const int gx = s0 > 0.0 ? seg_of<P>(s0).uexp : -149;
+        switch (xk) {
+        case 0: x = (float)ldexp((double)(2 * (rnd() % 64) + 1), gx - 1); break;     // an exact tie
+        case 1: x = (float)ldexp((double)(rnd() % 4096), gx); break;                 // a multiple of the step
+        case 2: x = 0.0f; break;
+        case 3: x = from_bits(1u + (uint32_t)(rnd() % 0x7FFFFFu)); break;            // subnormal
+        case 4: x = (float)ldexp(unit(), gx - 3); break;                             // below half a step
+        case 5: x = (float)(s0 * (1.0 + 4.0 * unit()) + 1e-30); break;               // larger than the start
+        default: x = (float)ldexp(unit() + 0.5, -(int)(rnd() % 30) - 4); break;
+        }
+        if (!(x >= 0.0f) || !std::isfinite(x)) x = 0.0f;
+        if (P == 24) s0 = (double)(float)s0;
+        const uint32_t n = 1 + (uint32_t)(rnd() % (rep % 10 == 0 ? 300000 : 3000));
+        std::vector<double> partial(n);
+        if (P == 24) {
+            float a = (float)s0;
+            for (uint32_t i = 0; i < n; ++i) partial[i] = a = a + x;
+        } else {
+            double a = s0;
+            for (uint32_t i = 0; i < n; ++i) partial[i] = a = a + (double)x;
+        }
+        double sum = s0;
+        const uint32_t all = equal_run_walk<P>(sum, fbits(x), n, [](double) { return false; });
+        if (all != n || memcmp(&sum, &partial[n - 1], 8) != 0) {
+            if (failures++ < 5)
+                printf("FAIL equal run P=%d s0=%.17g x=%a n=%u: sum %.17g want %.17g\n", P, s0, (double)x, n, sum,
+                       partial[n - 1]);
+            return;
+        }
+        for (int t = 0; t < 12; ++t) {
+            const uint32_t j = (uint32_t)(rnd() % n);
+            double thr = partial[j];
+            const int wiggle = (int)(rnd() % 3) - 1;
+            if (wiggle) thr = std::nextafter(thr, wiggle > 0 ? INFINITY : -INFINITY);
+            if (t == 10) thr = partial[n - 1] * 2.0 + 1.0;  // never met
+            if (t == 11) thr = s0;                           // met by the first term that moves the sum
+            if (thr < s0 || (thr == s0 && false)) continue;
+            for (int strict = 0; strict < 2; ++strict) {
+                if (!strict && !(s0 < thr)) continue;  // pred must be false at the start
+                uint32_t w = n;
+                for (uint32_t i = 0; i < n; ++i)
+                    if (strict ? partial[i] > thr : partial[i] >= thr) {
+                        w = i;
+                        break;
+                    }
+                double at = s0;
+                const uint32_t got = equal_run_walk<P>(
+                    at, fbits(x), n, [thr, strict](double c) { return strict ? c > thr : c >= thr; });
+                const double want_at = w < n ? partial[w] : partial[n - 1];
+                if (got != w || memcmp(&at, &want_at, 8) != 0) {
+                    if (failures++ < 5)
+                        printf("FAIL equal run P=%d s0=%.17g x=%a n=%u thr=%.17g strict=%d: index %u want %u\n", P,
+                               s0, (double)x, n, thr, strict, got, w);
+                    return;
+                }
+            }
+        }
+        ++cases;
+    }
+}
+
 template <int P>
 static void run_all(int &cases) {
     const uint32_t tiles[] = {1, 7, 64, 2048};
@@ -405,6 +482,8 @@ int main() {
     check_runs();
     run_all<24>(cases);
     run_all<53>(cases);
+    check_equal_runs<24>(cases);
+    check_equal_runs<53>(cases);
     if (failures) {
         printf("%d failures\n", failures);
         return 1;
