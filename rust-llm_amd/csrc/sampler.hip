@@ -559,15 +559,15 @@ int rl_top_probability_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t r
         hipLaunchKernelGGL(k_tp_max<true>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
                            ctx->d_argmax_part, ctx->d_tp_nan);
         hipLaunchKernelGGL(k_tp_sum<true>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
-                           ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum, ctx->d_tp_small);
+                           ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum, ctx->d_tp_small, ctx->d_arrive,
+                           out_token, out_prob);
     } else {
         hipLaunchKernelGGL(k_tp_max<false>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
                            ctx->d_argmax_part, ctx->d_tp_nan);
         hipLaunchKernelGGL(k_tp_sum<false>, grid, dim3(FAST_THREADS), 0, st, logits, stride, vocab, chunks,
-                           ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum, ctx->d_tp_small);
+                           ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum, ctx->d_tp_small, ctx->d_arrive,
+                           out_token, out_prob);
     }
-    hipLaunchKernelGGL(k_tp_final, dim3(rows), dim3(TP_FINAL_THREADS), 0, st, logits, stride, vocab, chunks,
-                       ctx->d_argmax_part, ctx->d_tp_nan, ctx->d_tp_sum, ctx->d_tp_small, out_token, out_prob);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "top_probability kernels");
     return RL_OK;

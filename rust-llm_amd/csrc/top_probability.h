@@ -3,12 +3,13 @@
 // order, of exp(l_i - l_best). The MTP draft loop compares it with MTP_P_MIN
 // (forward.rs:341, :1014-1015), so the bits matter.
 //
-// Three launches: the argmax per chunk (and whether a NaN occurs), the f64
-// sum of the terms per chunk in any order, then per row a certificate: an
-// interval that holds both the chunked sum's exact value and the reference's
-// sequential sum; (float)(1.0 / s) is monotone in s, so when both ends of the
-// interval give the same f32 that is the answer. Otherwise the row's
-// sequential sum is replayed exactly (rl_seqsum.h).
+// Two launches: the argmax per chunk (and whether a NaN occurs), then the f64
+// sum of the terms per chunk in any order, whose last chunk of a row to finish
+// computes a certificate: an interval that holds both the chunked sum's exact
+// value and the reference's sequential sum; (float)(1.0 / s) is monotone in s,
+// so when both ends of the interval give the same f32 that is the answer.
+// Otherwise that workgroup replays the row's sequential sum exactly
+// (rl_seqsum.h).
 //
 // The interval. Every term is at most 1 (exp of a value <= 0) and the best
 // one is exactly 1, so the sum S is at least 1; let E >= 0 be its binade and
@@ -165,8 +166,8 @@ constexpr uint32_t TP_SMALL = 0x32800000u;
 
 // The depth of k_tp_sum's summation (the additions any term's value passes
 // through): 32 within a tile, one per tile of the thread, the tail element,
-// six across the wave and three across its waves, then the chunks in
-// k_tp_final.
+// six across the wave and three across its waves, then the chunks in the
+// row's finishing workgroup.
 __host__ __device__ inline uint32_t tp_sum_depth(uint32_t vocab, uint32_t chunks) {
     const uint32_t n4 = vocab / 4;
     const uint32_t per = (n4 + chunks - 1) / chunks;
@@ -204,21 +205,71 @@ __device__ __forceinline__ void load_sum_tile(f32x4 *dst, const float *row, uint
     }
 }
 
+// The row's result from its chunk sums S and small-term counts (the
+// interval of the file's header), or, when the interval does not decide the
+// f32 of 1 / s, from the row's sequential sum replayed exactly by the
+// workgroup. Every thread of the workgroup calls it; thread 0 writes.
+__device__ __forceinline__ void tp_finish(const float *rowp, uint32_t vocab, uint32_t chunks, uint32_t tok,
+                                          double S, uint32_t small, const LdsExpTable &etab,
+                                          SeqLds<FAST_THREADS> *seq, uint32_t *out_token, float *out_prob) {
+    // S is within dS of the exact sum, the sequential sum within dq of it.
+    const double dS = 2.0 * (double)tp_sum_depth(vocab, chunks) * 0x1p-53 * S;
+    const double S_up = S * (1.0 + 4.0 * ((double)vocab + 64.0) * 0x1p-53);  // above both sums
+    const int E = (int)((f64_bits(S_up) >> 52) & 0x7FF) - 1023;
+    double dq;
+    if (E <= 3) {
+        dq = ((double)small + 200.0) * mul_pow2(1.0, E - 53);
+    } else {
+        dq = 2.0 * ((double)vocab + 64.0) * 0x1p-53 * S_up;  // gamma_(V-1) * S, with margin
+    }
+    const double D = dS + dq;
+    const double s_lo = (S - D) * (1.0 - 0x1p-50), s_hi = (S + D) * (1.0 + 0x1p-50);
+    const float lo = (float)(1.0 / s_hi), hi = (float)(1.0 / s_lo);
+    float prob = lo;
+    if (lo != hi) {
+        const float best = ((const RL_GLB float *)rowp)[tok];
+        double sum;
+        seq_replay<53, FAST_THREADS, SEQ_ITEMS>(
+            [rowp](uint32_t j) { return ((const RL_GLB uint32_t *)rowp)[j]; },
+            [best, etab](uint32_t bits) { return expf_libm_nonpos_t(__uint_as_float(bits) - best, etab); }, vocab,
+            NeverStop{}, seq, &sum);
+        prob = (float)(1.0 / sum);
+    }
+    if (threadIdx.x == 0) {
+        *out_token = tok;
+        *out_prob = prob;
+    }
+}
+
 // grid (chunks, rows), FAST_THREADS: per chunk the f64 sum of exp(l_i - best)
-// (forward.rs:1678), in any order, and how many terms are small (above).
+// (forward.rs:1678), in any order, and how many terms are small (above). The
+// row's last chunk to publish its sum (a per-row arrival counter, zero
+// between calls) finishes the row (tp_finish); a row whose sum is NaN is
+// written by its chunk 0 (every chunk reaches the same verdict).
 template <bool VEC>
 __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, uint64_t stride, uint32_t vocab,
                                                          uint32_t chunks, const uint64_t *part_am,
                                                          const uint32_t *part_nan, double *part_sum,
-                                                         uint32_t *part_small) {
+                                                         uint32_t *part_small, uint32_t *arrive,
+                                                         uint32_t *out_token, float *out_prob) {
     __shared__ uint64_t exp_tab[32];
     __shared__ double red[FAST_WAVES];
     __shared__ uint32_t red_c[FAST_WAVES];
+    __shared__ SeqLds<FAST_THREADS> seq;
+    __shared__ uint32_t s_last;
     const uint32_t row = blockIdx.y, chunk = blockIdx.x;
     uint64_t am;
-    if (tp_row(part_am, part_nan, row, chunks, &am)) return;
+    if (tp_row(part_am, part_nan, row, chunks, &am)) {
+        // The reference's sum is NaN (tp_row).
+        if (chunk == 0 && threadIdx.x == 0) {
+            out_token[row] = comp_key(am) == 0 ? 0u : comp_id(am);
+            out_prob[row] = __builtin_nanf("");
+        }
+        return;
+    }
     const float *rowp = logits + (uint64_t)row * stride;
-    const float best = ((const RL_GLB float *)rowp)[comp_id(am)];
+    const uint32_t tok = comp_id(am);
+    const float best = ((const RL_GLB float *)rowp)[tok];
     copy_exp_table((RL_LDS uint64_t *)exp_tab);
     const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab};
     const uint32_t n4 = vocab / 4;
@@ -290,77 +341,40 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
         red_c[wave] = small;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (uint32_t w = 1; w < FAST_WAVES; ++w) {
-            sum += red[w];
-            small += red_c[w];
-        }
-        const uint64_t at = (uint64_t)row * chunks + chunk;
-        part_sum[at] = sum;
-        part_small[at] = small;
+    // The chunk's sum, waves in order (the same in every thread).
+    sum = red[0];
+    small = red_c[0];
+    for (uint32_t w = 1; w < FAST_WAVES; ++w) {
+        sum += red[w];
+        small += red_c[w];
     }
-}
-
-constexpr uint32_t TP_FINAL_THREADS = 512;  // 8 waves a row for the exact sum replay
-
-// grid (rows), TP_FINAL_THREADS: the token, and 1 / sum certified from the
-// chunk sums or from the replayed sequential sum.
-__global__ __launch_bounds__(TP_FINAL_THREADS) void k_tp_final(const float *logits, uint64_t stride, uint32_t vocab,
-                                                             uint32_t chunks, const uint64_t *part_am,
-                                                             const uint32_t *part_nan, const double *part_sum,
-                                                             const uint32_t *part_small, uint32_t *out_token,
-                                                             float *out_prob) {
-    __shared__ SeqLds<TP_FINAL_THREADS> seq;
-    __shared__ uint64_t exp_tab[32];
-    const uint32_t row = blockIdx.x;
-    uint64_t am;
-    const bool nan = tp_row(part_am, part_nan, row, chunks, &am);
-    const uint32_t tok = comp_key(am) == 0 ? 0u : comp_id(am);
-    if (nan) {
-        if (threadIdx.x == 0) {
-            out_token[row] = tok;
-            out_prob[row] = __builtin_nanf("");
-        }
+    if (chunks == 1) {  // the row's only chunk: its sum is the row's
+        tp_finish(rowp, vocab, 1, tok, sum, small, etab, &seq, out_token + row, out_prob + row);
         return;
     }
+    if (threadIdx.x == 0) {
+        // Publish: device-scope stores, which write through this XCD's L2,
+        // completed before the arrival; the last chunk reads them with
+        // device-scope loads issued after its arrival saw every other one.
+        const uint64_t at = (uint64_t)row * chunks + chunk;
+        __hip_atomic_store(part_sum + at, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(part_small + at, small, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);  // the stores have completed
+        s_last = atomicAdd(arrive + row, 1u) == chunks - 1 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    // The row's last chunk: every chunk's sum is published. Chunk order, as
+    // the certificate's depth (tp_sum_depth) counts it.
     double S = 0.0;
-    uint32_t small = 0;
+    uint32_t nsmall = 0;
     for (uint32_t c = 0; c < chunks; ++c) {
         const uint64_t at = (uint64_t)row * chunks + c;
-        S += part_sum[at];
-        small += part_small[at];
+        S += __hip_atomic_load(part_sum + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        nsmall += __hip_atomic_load(part_small + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // The interval (the file's header): S is within dS of the exact sum, the
-    // sequential sum within dq of it.
-    const double dS = 2.0 * (double)tp_sum_depth(vocab, chunks) * 0x1p-53 * S;
-    const double S_up = S * (1.0 + 4.0 * ((double)vocab + 64.0) * 0x1p-53);  // above both sums
-    const int E = (int)((f64_bits(S_up) >> 52) & 0x7FF) - 1023;
-    double dq;
-    if (E <= 3) {
-        dq = ((double)small + 200.0) * mul_pow2(1.0, E - 53);
-    } else {
-        dq = 2.0 * ((double)vocab + 64.0) * 0x1p-53 * S_up;  // gamma_(V-1) * S, with margin
-    }
-    const double D = dS + dq;
-    const double s_lo = (S - D) * (1.0 - 0x1p-50), s_hi = (S + D) * (1.0 + 0x1p-50);
-    const float lo = (float)(1.0 / s_hi), hi = (float)(1.0 / s_lo);
-    float prob = lo;
-    if (lo != hi) {
-        const float *rowp = logits + (uint64_t)row * stride;
-        const float best = ((const RL_GLB float *)rowp)[tok];
-        copy_exp_table((RL_LDS uint64_t *)exp_tab);
-        const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab};
-        double sum;
-        seq_replay<53, TP_FINAL_THREADS, SEQ_ITEMS>(
-            [rowp](uint32_t j) { return ((const RL_GLB uint32_t *)rowp)[j]; },
-            [best, etab](uint32_t bits) { return expf_libm_nonpos_t(__uint_as_float(bits) - best, etab); }, vocab,
-            NeverStop{}, &seq, &sum);
-        prob = (float)(1.0 / sum);
-    }
-    if (threadIdx.x == 0) {
-        out_token[row] = tok;
-        out_prob[row] = prob;
-    }
+    if (threadIdx.x == 0) arrive[row] = 0;  // ready for the next call
+    tp_finish(rowp, vocab, chunks, tok, S, nsmall, etab, &seq, out_token + row, out_prob + row);
 }
 
 }  // namespace rl

@@ -97,7 +97,7 @@ int launch(const float *terms, const uint64_t *off, const uint32_t *n, const dou
 }  // namespace
 
 // shape 0: REST_THREADS threads, SEQ_ITEMS terms each; shape 1: 128
-// threads, 3 terms each; shape 2: top_probability's (TP_FINAL_THREADS
+// threads, 3 terms each; shape 2: top_probability's (FAST_THREADS
 // threads, SEQ_ITEMS terms each); shape 3: the chunked replay the sampler
 // uses (REST_THREADS threads). Every pointer is device memory; a
 // case's terms are terms[off[c] .. off[c] + n[c]).
@@ -127,9 +127,9 @@ extern "C" int seqsum_gpu_run(int precision, int shape, const float *terms, cons
         }
     } else if (shape == 2) {
         if (precision == 24)
-            return launch<24, rl::TP_FINAL_THREADS, rl::SEQ_ITEMS>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
+            return launch<24, rl::FAST_THREADS, rl::SEQ_ITEMS>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
         if (precision == 53)
-            return launch<53, rl::TP_FINAL_THREADS, rl::SEQ_ITEMS>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
+            return launch<53, rl::FAST_THREADS, rl::SEQ_ITEMS>(terms, off, n, thr, mode, cases, out_idx, out_sum, st);
     }
     return -1;
 }

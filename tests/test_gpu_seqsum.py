@@ -6,7 +6,7 @@ cumulative sum and the normalising total (sample.rs:307-324, :342) and for
 top_probability (forward.rs:1678), f32 for the draw (sample.rs:349-356). The
 harness tests/native/seqsum_gpu.hip runs the device replay on arbitrary term
 arrays, one workgroup per case, with 1024 threads, top_probability's shape
-(512), a third one (128 threads of 3 terms), and the chunked replay the
+(256), a third one (128 threads of 3 terms), and the chunked replay the
 sampler uses (chunk summaries chained by one wave, which replays the chunks
 holding a binade crossing or the event term by term). Each case asks for the whole sum or for
 the first partial sum >= or > a threshold (every partial sum, its neighbours,

@@ -182,8 +182,10 @@ def test_rows_match_the_oracle(device, rows, V, scale):
 
 
 @pytest.mark.gpu
-def test_special_rows(device):
-    V = 5000
+@pytest.mark.parametrize("V", [5000, 151936])
+def test_special_rows(device, V):
+    # At 5000 a row is one chunk; at 151936 it is split, and a NaN row is
+    # written by its first chunk while the others finish through the last.
     rng = np.random.default_rng(3)
     x = rng.normal(0, 1, (10, V)).astype(np.float32)
     x[0, :] = -np.inf
