@@ -210,7 +210,7 @@ __device__ __forceinline__ void load_sum_tile(f32x4 *dst, const float *row, uint
 // f32 of 1 / s, from the row's sequential sum replayed exactly by the
 // workgroup. Every thread of the workgroup calls it; thread 0 writes.
 __device__ __forceinline__ void tp_finish(const float *rowp, uint32_t vocab, uint32_t chunks, uint32_t tok,
-                                          double S, uint32_t small, const LdsExpTable &etab,
+                                          float best, double S, uint32_t small, const LdsExpTable &etab,
                                           SeqLds<FAST_THREADS> *seq, uint32_t *out_token, float *out_prob) {
     // S is within dS of the exact sum, the sequential sum within dq of it.
     const double dS = 2.0 * (double)tp_sum_depth(vocab, chunks) * 0x1p-53 * S;
@@ -227,7 +227,6 @@ __device__ __forceinline__ void tp_finish(const float *rowp, uint32_t vocab, uin
     const float lo = (float)(1.0 / s_hi), hi = (float)(1.0 / s_lo);
     float prob = lo;
     if (lo != hi) {
-        const float best = ((const RL_GLB float *)rowp)[tok];
         double sum;
         seq_replay<53, FAST_THREADS, SEQ_ITEMS>(
             [rowp](uint32_t j) { return ((const RL_GLB uint32_t *)rowp)[j]; },
@@ -258,6 +257,19 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
     __shared__ SeqLds<FAST_THREADS> seq;
     __shared__ uint32_t s_last;
     const uint32_t row = blockIdx.y, chunk = blockIdx.x;
+    const float *rowp = logits + (uint64_t)row * stride;
+    const uint32_t n4 = vocab / 4;
+    const uint32_t q0 = chunk_lo(n4, chunk, chunks), q1 = chunk_lo(n4, chunk + 1, chunks);
+    // The first tile is loaded before the row's argmax partials, so the two
+    // round trips overlap (vector loads complete in order: waiting for the
+    // partials waits for the tile too). A chunk with no float4 (a row of
+    // fewer than 4 logits) loads 16 bytes of the partials instead, with no
+    // branch around the loads.
+    f32x4 A[UNROLL], B[UNROLL];
+    {
+        const bool any = q1 > q0;
+        load_sum_tile<VEC>(A, any ? rowp : (const float *)part_am, any ? n4 : 1u, any ? q0 : 0u, any ? q1 : 1u);
+    }
     uint64_t am;
     if (tp_row(part_am, part_nan, row, chunks, &am)) {
         // The reference's sum is NaN (tp_row).
@@ -267,13 +279,13 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
         }
         return;
     }
-    const float *rowp = logits + (uint64_t)row * stride;
     const uint32_t tok = comp_id(am);
-    const float best = ((const RL_GLB float *)rowp)[tok];
+    // The best value from its composite: argmax_key(v) = total_key(v + 0), so
+    // this is the logit itself, or +0 where it is -0; x - best then differs
+    // only in the sign of a zero result (x = -0), whose exp is 1 either way.
+    const float best = key_value(comp_key(am));
     copy_exp_table((RL_LDS uint64_t *)exp_tab);
     const LdsExpTable etab{(RL_LDS uint64_t *)exp_tab};
-    const uint32_t n4 = vocab / 4;
-    const uint32_t q0 = chunk_lo(n4, chunk, chunks), q1 = chunk_lo(n4, chunk + 1, chunks);
     double sum = 0.0;
     uint32_t small = 0;   // this lane's count: the last, partial tile and the tail element
     uint32_t wsmall = 0;  // the wave's count over the full tiles (the same in every lane)
@@ -293,8 +305,6 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
     // sum, which bounds the depth of the summation (tp_sum_depth).
     constexpr uint32_t STEP = FAST_THREADS * UNROLL;
     if (q1 > q0) {
-        f32x4 A[UNROLL], B[UNROLL];
-        load_sum_tile<VEC>(A, rowp, n4, q0, q1);
         for (uint32_t b = q0; b < q1; b += STEP) {
             load_sum_tile<VEC>(B, rowp, n4, b + STEP, q1);
             double ts = 0.0;
@@ -349,7 +359,7 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
         small += red_c[w];
     }
     if (chunks == 1) {  // the row's only chunk: its sum is the row's
-        tp_finish(rowp, vocab, 1, tok, sum, small, etab, &seq, out_token + row, out_prob + row);
+        tp_finish(rowp, vocab, 1, tok, best, sum, small, etab, &seq, out_token + row, out_prob + row);
         return;
     }
     if (threadIdx.x == 0) {
@@ -374,7 +384,7 @@ __global__ __launch_bounds__(FAST_THREADS) void k_tp_sum(const float *logits, ui
         nsmall += __hip_atomic_load(part_small + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (threadIdx.x == 0) arrive[row] = 0;  // ready for the next call
-    tp_finish(rowp, vocab, chunks, tok, S, nsmall, etab, &seq, out_token + row, out_prob + row);
+    tp_finish(rowp, vocab, chunks, tok, best, S, nsmall, etab, &seq, out_token + row, out_prob + row);
 }
 
 }  // namespace rl
