@@ -15,6 +15,7 @@
 #include "rl_runtime.h"
 #include "rl_sampler.h"
 #include "full_rest.h"
+#include "greedy.h"
 #include "top_probability.h"
 
 using namespace rl;
@@ -34,7 +35,7 @@ constexpr uint32_t TARGET_WGS = 1024;  // enough workgroups to cover 256 CUs fou
 constexpr uint32_t FULL_GROUP_MAX = 256;
 constexpr uint32_t CHUNK_SLOTS = 2 * TARGET_WGS;
 
-enum class Path : uint8_t { Stream, Full };
+enum class Path : uint8_t { Greedy, Stream, Full };
 
 // log2 of the stream kernel's window-set slots for windows of up to n ids: at
 // least twice n (a half-full open-addressed set), at least 64. The set is
@@ -49,7 +50,7 @@ uint32_t window_hash_bits(uint32_t n) {
 
 // Which device path a row's settings take (see sampler_kernels.h).
 Path plan_row(const rl_sampling &s, uint32_t vocab) {
-    if (s.temperature <= 0.0f) return Path::Stream;
+    if (s.temperature <= 0.0f) return Path::Greedy;
     if (s.top_k >= 1 && s.top_k <= KMAX && s.top_k < vocab) return Path::Stream;
     return Path::Full;
 }
@@ -212,7 +213,9 @@ struct rl_sampler_ctx {
     int device = 0;
     uint32_t max_rows = 0, vocab = 0, max_window = 0, full_group = 0;
     rl_sampling *d_settings = nullptr;
-    uint32_t *d_stream_rows = nullptr, *d_full_rows = nullptr;
+    uint32_t *d_stream_rows = nullptr, *d_full_rows = nullptr, *d_greedy_rows = nullptr;
+    uint64_t *d_greedy_best = nullptr;   // the greedy path's row slots, zero between calls
+    uint32_t *d_greedy_arrive = nullptr; // and arrival counters
     uint64_t *d_chunk_cands = nullptr;
     uint32_t *d_chunk_counts = nullptr;
     uint32_t *d_arrive = nullptr;
@@ -233,7 +236,7 @@ struct rl_sampler_ctx {
     std::vector<void *> owned;
     // Host copy of the plan made by configure.
     uint32_t configured = 0;
-    std::vector<uint32_t> stream_rows, full_rows;  // ascending; capacity max_rows
+    std::vector<uint32_t> stream_rows, full_rows, greedy_rows;  // ascending; capacity max_rows
     std::vector<uint64_t> need_upto;               // [r]: candidates rows 0..r can keep; capacity max_rows
     uint64_t cand_need = 0;
     bool any_drawing = false;
@@ -282,6 +285,7 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     try {  // configure fills these in place
         c->stream_rows.reserve(max_rows);
         c->full_rows.reserve(max_rows);
+        c->greedy_rows.reserve(max_rows);
         c->need_upto.reserve(max_rows);
     } catch (const std::bad_alloc &) {
         delete c;
@@ -292,6 +296,11 @@ int rl_sampler_create(int device, uint32_t max_rows, uint32_t vocab, uint32_t ma
     if (e == hipSuccess) e = c->alloc(&c->d_settings, max_rows);
     if (e == hipSuccess) e = c->alloc(&c->d_stream_rows, max_rows);
     if (e == hipSuccess) e = c->alloc(&c->d_full_rows, max_rows);
+    if (e == hipSuccess) e = c->alloc(&c->d_greedy_rows, max_rows);
+    if (e == hipSuccess) e = c->alloc(&c->d_greedy_best, max_rows);
+    if (e == hipSuccess) e = c->alloc(&c->d_greedy_arrive, max_rows);
+    if (e == hipSuccess) e = hipMemset(c->d_greedy_best, 0, (size_t)max_rows * sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMemset(c->d_greedy_arrive, 0, (size_t)max_rows * sizeof(uint32_t));
     // Rows are split into chunks only while rows < TARGET_WGS, with
     // chunks <= ceil(TARGET_WGS / rows), so rows * chunks < 2 * TARGET_WGS.
     if (e == hipSuccess) e = c->alloc(&c->d_chunk_cands, (size_t)CHUNK_SLOTS * KMAX);
@@ -345,23 +354,27 @@ int rl_sampler_configure(rl_sampler_ctx *ctx, const rl_sampling *settings, uint3
     ctx->configured = 0;
     ctx->stream_rows.clear();
     ctx->full_rows.clear();
+    ctx->greedy_rows.clear();
     ctx->need_upto.clear();
     uint64_t need = 0;
     bool drawing = false;
     for (uint32_t r = 0; r < rows; ++r) {
         const Path p = plan_row(settings[r], ctx->vocab);
-        (p == Path::Stream ? ctx->stream_rows : ctx->full_rows).push_back(r);
+        (p == Path::Greedy ? ctx->greedy_rows : p == Path::Stream ? ctx->stream_rows : ctx->full_rows).push_back(r);
         need = std::max(need, row_cand_need(settings[r], ctx->vocab));
         ctx->need_upto.push_back(need);
         drawing = drawing || !(settings[r].temperature <= 0.0f);
     }
     const auto &sr = ctx->stream_rows;
     const auto &fr = ctx->full_rows;
+    const auto &gr = ctx->greedy_rows;
     hipError_t e = hipMemcpy(ctx->d_settings, settings, rows * sizeof(rl_sampling), hipMemcpyHostToDevice);
     if (e == hipSuccess && !sr.empty())
         e = hipMemcpy(ctx->d_stream_rows, sr.data(), sr.size() * sizeof(uint32_t), hipMemcpyHostToDevice);
     if (e == hipSuccess && !fr.empty())
         e = hipMemcpy(ctx->d_full_rows, fr.data(), fr.size() * sizeof(uint32_t), hipMemcpyHostToDevice);
+    if (e == hipSuccess && !gr.empty())
+        e = hipMemcpy(ctx->d_greedy_rows, gr.data(), gr.size() * sizeof(uint32_t), hipMemcpyHostToDevice);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpy (configure)");
     ctx->configured = rows;
     ctx->cand_need = need;
@@ -453,6 +466,31 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
                                    ctx->stream_rows.begin());
     const uint32_t nf = (uint32_t)(std::lower_bound(ctx->full_rows.begin(), ctx->full_rows.end(), rows) -
                                    ctx->full_rows.begin());
+    const uint32_t ngr = (uint32_t)(std::lower_bound(ctx->greedy_rows.begin(), ctx->greedy_rows.end(), rows) -
+                                   ctx->greedy_rows.begin());
+    if (ngr > 0) {
+        RowIO gio = io;
+        gio.rows = ctx->greedy_rows[ngr - 1] == ngr - 1 ? nullptr : ctx->d_greedy_rows;
+        gio.row0 = 0;
+        // Chunks as the stream path's: while rows are few, at most one tile a chunk.
+        const uint32_t n4 = vocab / 4;
+        constexpr uint32_t STEP4 = FAST_THREADS * UNROLL;
+        uint32_t chunks = (TARGET_WGS + ngr - 1) / ngr;
+        chunks = std::min(chunks, MAX_CHUNKS);
+        chunks = std::min(chunks, std::max(1u, (n4 + STEP4 - 1) / STEP4));
+        gio.chunks = std::max(chunks, 1u);
+        // The window bitmap: the largest chunk's elements (the last one also
+        // takes the row's vocab % 4).
+        const size_t glds = gio.windows ? greedy_bitmap_words(4 * ((n4 + gio.chunks - 1) / gio.chunks) + 3) * 4 : 0;
+        GreedyScratch gs{ctx->d_greedy_best, ctx->d_greedy_arrive};
+        const dim3 grid(gio.chunks, ngr);
+        if (vec)
+            hipLaunchKernelGGL(k_greedy<true>, grid, dim3(FAST_THREADS), glds, st, gio, gs);
+        else
+            hipLaunchKernelGGL(k_greedy<false>, grid, dim3(FAST_THREADS), glds, st, gio, gs);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return hip_fail(e, "greedy kernel");
+    }
     if (ns > 0) {
         RowIO s = io;
         // The stream rows are ascending and distinct: they are 0 .. ns-1

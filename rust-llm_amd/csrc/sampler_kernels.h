@@ -1,6 +1,13 @@
 // The sampler's kernels. Two device paths, chosen per row from its settings:
 //
-//  STREAM (greedy rows, and 1 <= top_k <= 64 with top_k < vocab): one pass
+//  GREEDY (temperature <= 0): argmax of the penalised row, k_greedy in
+//  greedy.h. The stream kernel below still takes such a row as top-k 1 with
+//  argmax's keys (w.greedy), which sample_rows no longer sends it: taking
+//  that handling out changes the register allocation of the kernel, which
+//  then spills (28 bytes a lane of scratch) and runs the 1024-row batch 11 %
+//  slower (measured).
+//
+//  STREAM (1 <= top_k <= 64 with top_k < vocab): one pass
 //  over the row in HBM. Each wave keeps the row's best candidates seen so far
 //  in LDS under a rising threshold (a workgroup-wide one, shared through an
 //  LDS atomic max), so almost every element costs one compare. Penalised
