@@ -26,11 +26,8 @@ struct GreedyScratch {
 constexpr uint32_t GREEDY_WIN_PER = 8;  // window ids per thread: windows of up to 2048 ids
 static_assert(GREEDY_WIN_PER * FAST_THREADS >= 2048, "a window's ids fit the threads");
 
-// LDS words of the window bitmap for chunks of at most `elems` elements.
-__host__ __device__ constexpr uint32_t greedy_bitmap_words(uint32_t elems) { return (elems + 31) / 32 + 1; }
-
 // grid (chunks, rows on this path), FAST_THREADS; dynamic LDS: the window
-// bitmap (greedy_bitmap_words of the largest chunk, when the call has
+// bitmap (chunk_bitmap_words of the largest chunk, when the call has
 // windows).
 template <bool VEC>
 __global__ __launch_bounds__(FAST_THREADS) void k_greedy(RowIO a, GreedyScratch g) {

@@ -481,7 +481,7 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
         gio.chunks = std::max(chunks, 1u);
         // The window bitmap: the largest chunk's elements (the last one also
         // takes the row's vocab % 4).
-        const size_t glds = gio.windows ? greedy_bitmap_words(4 * ((n4 + gio.chunks - 1) / gio.chunks) + 3) * 4 : 0;
+        const size_t glds = gio.windows ? chunk_bitmap_words(4 * ((n4 + gio.chunks - 1) / gio.chunks) + 3) * 4 : 0;
         GreedyScratch gs{ctx->d_greedy_best, ctx->d_greedy_arrive};
         const dim3 grid(gio.chunks, ngr);
         if (vec)
@@ -506,13 +506,26 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
         chunks = std::min(chunks, MAX_CHUNKS);
         chunks = std::min(chunks, std::max(1u, (n4 + STEP4 - 1) / STEP4));
         s.chunks = std::max(chunks, 1u);
-        const size_t wlds = window_lds_bytes(io.hash_bits);
         FastScratch sc{ctx->d_chunk_cands, ctx->d_chunk_counts, ctx->d_arrive};
         dim3 grid(s.chunks, ns);
-        if (vec)
+        // Chunks of at most one tile each take the one-tile kernel, whose
+        // window is a bitmap over the chunk's elements (the last chunk's
+        // take the row's vocab % 4 more).
+        const uint32_t per = (n4 + s.chunks - 1) / s.chunks;
+        size_t wlds = window_lds_bytes(io.hash_bits);
+        if (per <= STEP4) {
+            wlds = std::max(wlds, (size_t)chunk_bitmap_words(4 * per + 3) * sizeof(uint32_t));
+            if (vec)
+                hipLaunchKernelGGL((k_stream<true, UNROLL, FAST_THREADS, true>), grid, dim3(FAST_THREADS), wlds, st, s,
+                                   sc);
+            else
+                hipLaunchKernelGGL((k_stream<false, UNROLL, FAST_THREADS, true>), grid, dim3(FAST_THREADS), wlds, st, s,
+                                   sc);
+        } else if (vec) {
             hipLaunchKernelGGL((k_stream<true, UNROLL, FAST_THREADS>), grid, dim3(FAST_THREADS), wlds, st, s, sc);
-        else
+        } else {
             hipLaunchKernelGGL((k_stream<false, UNROLL, FAST_THREADS>), grid, dim3(FAST_THREADS), wlds, st, s, sc);
+        }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return hip_fail(e, "stream kernels");
     }

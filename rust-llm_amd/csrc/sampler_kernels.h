@@ -391,6 +391,19 @@ __device__ __forceinline__ void rescan_row(const float *rowp, uint32_t vocab, co
     *out_tok = comp_key(am) == 0 ? 0u : comp_id(am);
 }
 
+// By one wave: the row's window ids (window[0..len), those below vocab) into
+// an empty set, for rescan_row where the workgroup kept no set of its own.
+__device__ __forceinline__ void window_build_wave(const WindowSet &w, const uint32_t *window, uint32_t len,
+                                                  uint32_t vocab) {
+    for (uint32_t i = lane_id(); i < w.slots; i += WAVE) w.ids[i] = EMPTY_ID;
+    wave_lds_sync();
+    for (uint32_t i = lane_id(); i < len; i += WAVE) {
+        const uint32_t id = window[i];
+        if (id < vocab) (void)window_insert(w, id);
+    }
+    wave_lds_sync();
+}
+
 // Binary exponent of a finite nonzero f32 (subnormals count as -126): every
 // such value is a multiple of 2^(exponent - 23).
 __device__ __forceinline__ int f32_exponent(float p) {
@@ -409,9 +422,13 @@ __device__ __forceinline__ float row_uniform(const RowIO &a, uint32_t row) {
 // order with readlane, so every lane computes the bits the reference does.
 // tab_v (lane_exp_entry) and u (row_uniform) are loaded by the caller ahead
 // of the tail, so that it waits for no memory round trip.
+// With BUILD_SET, `ws` holds no ids yet: the rare rescan first builds it
+// from the row's window (wrow, wl).
+template <bool BUILD_SET = false>
 __device__ __forceinline__ void finalize_row(const RowIO &a, uint32_t row, const rl_sampling &s, uint32_t k,
                                              uint64_t c, uint32_t nL, const WindowSet &ws, bool pen,
-                                             const float *rowp, uint64_t tab_v, float u) {
+                                             const float *rowp, uint64_t tab_v, float u,
+                                             const uint32_t *wrow = nullptr, uint32_t wl = 0) {
     const uint32_t lane = lane_id();
     if (s.temperature <= 0.0f) {  // greedy: argmax (sample.rs:259-265)
         const uint64_t c0 = read_lane_u64(c, 0);
@@ -436,6 +453,9 @@ __device__ __forceinline__ void finalize_row(const RowIO &a, uint32_t row, const
         if (negnan != 0 || nL < k) {
             M = -__builtin_inff();
         } else {
+            if constexpr (BUILD_SET) {
+                if (pen) window_build_wave(ws, wrow, wl, a.vocab);
+            }
             rescan_row(rowp, a.vocab, ws, pen, s.repeat_penalty, &M, &tok_nf);
         }
     } else {
@@ -565,11 +585,25 @@ __device__ __forceinline__ uint64_t ascending_from(const uint64_t *list, uint32_
     return j < n ? list[j] : 0ull;
 }
 
+// LDS words of a bitmap over a chunk of at most `elems` elements (one word
+// more: a chunk that starts mid-word never reads past it).
+__host__ __device__ constexpr uint32_t chunk_bitmap_words(uint32_t elems) { return (elems + 31) / 32 + 1; }
+
 // grid (chunks, rows on this path), NT threads (NT / 64 waves, each with its
 // own candidate buffer), U float4 a thread per tile. Dynamic LDS: the window
 // set. A row split into chunks is finished by whichever of its chunks
 // publishes its list last (a per-row arrival counter), so no second launch.
-template <bool VEC, uint32_t U, uint32_t NT>
+//
+// ONE_TILE: every chunk of the launch holds at most one tile (q1 - q0 <=
+// NT * U; the rows of a small call, split over many workgroups). The window
+// is then applied where the reference applies it: the chunk marks the window
+// ids that fall in it in an LDS bitmap over its elements and penalises those
+// logits in its tile's registers before filtering, so its candidates carry
+// the penalised values (each id once, however often the window repeats it),
+// with no set of the whole window, no gather of window logits and no
+// separate merge. Dynamic LDS: that bitmap, then, for the rare rescan of a
+// row whose best are all NaN, a set of the window built by one wave.
+template <bool VEC, uint32_t U, uint32_t NT, bool ONE_TILE = false>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_stream(RowIO a, FastScratch sc) {
     constexpr uint32_t NW = NT / WAVE;
     constexpr uint32_t CBUF = TileShape<U>::CBUF;
@@ -610,10 +644,25 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     // tile.
     const uint32_t head_w = row_words(a, row);
     const uint32_t *wrow = a.windows + (uint64_t)row * a.wstride;
-    const uint32_t *idp = (a.windows && a.wlen && a.wstride > 0)
-                              ? wrow + (tid < a.wstride ? tid : a.wstride - 1)
-                              : reinterpret_cast<const uint32_t *>(a.settings + row);
-    const uint32_t id_loaded = *(const RL_GLB uint32_t *)idp;  // unconditional, see load_tile_clamped
+    const bool have_win = a.windows && a.wlen && a.wstride > 0;
+    const uint32_t *idp = have_win ? wrow + (tid < a.wstride ? tid : a.wstride - 1)
+                                   : reinterpret_cast<const uint32_t *>(a.settings + row);
+    // ONE_TILE loads the window's ids WIN_PER a thread (windows of up to
+    // WIN_PER * NT ids; longer ones never reach this kernel), clamped to the
+    // call's stride.
+    constexpr uint32_t WIN_PER = ONE_TILE ? 8 : 1;
+    uint32_t wid[WIN_PER];
+    if constexpr (ONE_TILE) {
+        const uint32_t *wsrc = have_win ? wrow : reinterpret_cast<const uint32_t *>(a.settings + row);
+        const uint32_t wn = have_win ? (a.wstride < WIN_PER * NT ? a.wstride : WIN_PER * NT) : 1u;
+#pragma unroll
+        for (uint32_t j = 0; j < WIN_PER; ++j) {
+            const uint32_t i = j * NT + tid;
+            wid[j] = ((const RL_GLB uint32_t *)wsrc)[i < wn ? i : wn - 1];
+        }
+    } else {
+        wid[0] = *(const RL_GLB uint32_t *)idp;  // unconditional, see load_tile_clamped
+    }
     // The first tile. A row of fewer than 4 logits has no tile; it loads 16
     // bytes of its own settings instead, so that this load needs no branch
     // either.
@@ -633,16 +682,52 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     const bool pen = penalises(s) && wl > 0;
     RL_LDS uint64_t *lT = (RL_LDS uint64_t *)&s_T;
     if (tid == 0) *lT = 0;
-    const bool small_win = pen && wl <= NT;
-    if (pen && !small_win)
-        window_build(ws, wrow, wl, V, rowp, true);  // ends with a barrier
-    else
-        window_clear(ws);
-    __syncthreads();
-    const uint32_t my_id = (small_win && tid < wl) ? id_loaded : EMPTY_ID;
-    const uint32_t my_slot = my_id < V ? window_insert(ws, my_id) : EMPTY_ID;
-    const float my_raw = ((const RL_GLB float *)rowp)[my_slot != EMPTY_ID ? my_id : 0u];
-    __syncthreads();
+    // The chunk's elements [e0, e1): the last chunk also holds the row's
+    // last vocab % 4 elements.
+    const uint32_t e0 = 4 * q0, e1 = chunk == a.chunks - 1 ? V : 4 * q1;
+    RL_LDS uint32_t *bm = (RL_LDS uint32_t *)smem;
+    uint32_t my_slot = EMPTY_ID, my_id = EMPTY_ID;
+    float my_raw = 0.0f;
+    if constexpr (ONE_TILE) {
+        if (pen) {
+            const uint32_t nwords = (e1 - e0 + 31) / 32;
+            for (uint32_t i = tid; i < nwords; i += NT) bm[i] = 0;
+            __syncthreads();
+#pragma unroll
+            for (uint32_t j = 0; j < WIN_PER; ++j) {
+                const uint32_t id = wid[j];
+                if (j * NT + tid < wl && id >= e0 && id < e1)
+                    (void)__hip_atomic_fetch_or(&bm[(id - e0) >> 5], 1u << ((id - e0) & 31), __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+            __syncthreads();
+            // The tile's window elements take their penalised values: the
+            // four bits of float4 f sit in one word (e0 is a multiple of 4).
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                const uint32_t f = q0 + u * NT + tid;
+                const uint32_t r = f < q1 ? f - q0 : 0u;
+                const uint32_t bits = f < q1 ? (bm[r >> 3] >> ((r & 7) * 4)) & 0xFu : 0u;
+                if (bits) {
+                    if (bits & 1u) A[u].x = penalize(A[u].x, s.repeat_penalty);
+                    if (bits & 2u) A[u].y = penalize(A[u].y, s.repeat_penalty);
+                    if (bits & 4u) A[u].z = penalize(A[u].z, s.repeat_penalty);
+                    if (bits & 8u) A[u].w = penalize(A[u].w, s.repeat_penalty);
+                }
+            }
+        }
+    } else {
+        const bool small_win = pen && wl <= NT;
+        if (pen && !small_win)
+            window_build(ws, wrow, wl, V, rowp, true);  // ends with a barrier
+        else
+            window_clear(ws);
+        __syncthreads();
+        my_id = (small_win && tid < wl) ? wid[0] : EMPTY_ID;
+        my_slot = my_id < V ? window_insert(ws, my_id) : EMPTY_ID;
+        my_raw = ((const RL_GLB float *)rowp)[my_slot != EMPTY_ID ? my_id : 0u];
+        __syncthreads();
+    }
 
     Stream w;
     w.buf = (RL_LDS uint64_t *)s_buf + wave * CBUF;
@@ -654,7 +739,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     w.cnt = 0;
     w.k = k;
     w.greedy = greedy;
-    w.pen = pen;
+    w.pen = ONE_TILE ? false : pen;  // ONE_TILE: the tile is penalised already
 
     // Wave priority falls as the row progresses (see set_progress_priority).
     __builtin_amdgcn_s_setprio(3);
@@ -669,10 +754,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
             process_tile<false, U, NT>(w, A, q0, q1);
         else if (ntiles == 1)
             process_tile<true, U, NT>(w, A, q0, q1);
-        if (my_slot != EMPTY_ID) window_store(ws, my_slot, my_id, my_raw);
-        __syncthreads();
-        w.wtop = window_top(ws);
-    } else {
+        if constexpr (!ONE_TILE) {
+            if (my_slot != EMPTY_ID) window_store(ws, my_slot, my_id, my_raw);
+            __syncthreads();
+            w.wtop = window_top(ws);
+        }
+    } else if constexpr (!ONE_TILE) {
         if (my_slot != EMPTY_ID) window_store(ws, my_slot, my_id, my_raw);
         __syncthreads();
         w.wtop = window_top(ws);
@@ -704,7 +791,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         if (w.cnt >= w.k + SLACK) compact(w);
         const uint32_t e = 4 * n4 + tid;
         const bool ok = e < V;
-        const float x = ok ? ((const RL_GLB float *)rowp)[e] : 0.0f;
+        float x = ok ? ((const RL_GLB float *)rowp)[e] : 0.0f;
+        if constexpr (ONE_TILE) {
+            if (pen && ok && ((bm[(e - e0) >> 5] >> ((e - e0) & 31)) & 1u)) x = penalize(x, s.repeat_penalty);
+        }
         offer_group<true>(w, f32x4{x, 0.f, 0.f, 0.f}, e, ok ? 1u : 0u);
     }
     compact(w);
@@ -722,12 +812,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
             total += s_cnt[j];
         }
         // The window's ids with their penalised values, once per row.
-        if (pen && chunk == 0)
+        if (!ONE_TILE && pen && chunk == 0)
             total += merge_window(top, ws, s.repeat_penalty, greedy, total >= k ? read_lane_u64(top, k - 1) : 0ull);
         const uint32_t nL = total < k ? total : k;
         if (lane >= nL) top = 0;
         if (a.chunks == 1) {
-            finalize_row(a, row, s, k, top, nL, ws, pen, rowp, tab_v, u_row);
+            finalize_row<ONE_TILE>(a, row, s, k, top, nL, ws, pen, rowp, tab_v, u_row, wrow, wl);
         } else {
             // Publish this chunk's list; the row's last chunk to arrive finishes
             // it. The list is written with device-scope stores, which write
@@ -793,7 +883,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     if (lane == 0) sc.arrive[slot] = 0;  // ready for the next call
     const uint32_t nL = total < k ? total : k;
     if (lane >= nL) top = 0;
-    finalize_row(a, row, s, k, top, nL, ws, pen, rowp, tab_v, u_row);
+    finalize_row<ONE_TILE>(a, row, s, k, top, nL, ws, pen, rowp, tab_v, u_row, wrow, wl);
 }
 
 // ------------------------------------------------------------ argmax ---

@@ -326,3 +326,55 @@ def test_full_path_rows_with_a_dominant_key(device, candidates):
     t, k = tok.cpu().numpy().view(np.uint32), kept.cpu().numpy().view(np.uint32)
     for r in range(rows):
         assert (t[r], k[r]) == (want["token"][r], want["kept"][r]), "%s %r" % (names[r], settings[r])
+
+
+@pytest.mark.parametrize("V", [151936, 100003])
+def test_split_rows_with_windows(device, V):
+    """Rows split into one-tile chunks, where each chunk penalises the window
+    ids that fall in it: window ids on chunk edges and on the row's last
+    vocab % 4 elements, penalties above and below 1 on positive and negative
+    logits, repeats and ids past the vocabulary, and rows whose k best are
+    all NaN (the rescan, which needs the whole window)."""
+    rng = np.random.default_rng(V + 5)
+    rows, W = 6, 48
+    n4 = V // 4
+    chunks = min(1024 // rows, 32, -(-n4 // 2048))
+    edges = [4 * (c * n4 // chunks) for c in range(1, chunks)]
+    x = rng.normal(0.0, 1.0, (rows, V)).astype(np.float32)
+    windows = np.full((rows, W), V + 2, np.uint32)
+    settings = []
+    spread = rng.choice(V, 40, replace=False)
+    # 0, 1: the 40 NaNs beat every value (k = 20): the rescan decides, with
+    # the largest value on a window id that the penalty lowers or lifts.
+    x[0, spread] = np.nan
+    x[0, 777] = 10.0; x[0, V - 5] = 7.0
+    windows[0, :3] = [777, 777, 12]
+    settings.append(R.sampling(0.7, 20, 0.9, 0.0, 2.0, W, 1))
+    x[1, spread] = np.nan
+    x[1, 777] = 10.0; x[1, edges[0]] = 6.0
+    windows[1, :2] = [edges[0], V + 9]
+    settings.append(R.sampling(0.7, 20, 0.9, 0.0, 0.5, W, 2))
+    # 2: the row's best values sit on window ids at the chunk edges.
+    ids = sorted({e + d for e in edges for d in (-1, 0, 1)})[:W]
+    x[2, ids] = rng.uniform(5.0, 9.0, len(ids))
+    windows[2, :len(ids)] = ids
+    settings.append(R.sampling(1.0, 40, 0.95, 0.0, 1.5, W, 3))
+    # 3: the last elements of the row (vocab % 4 of them when V is not a
+    # multiple of 4) and repeats.
+    x[3, V - 3:] = [8.0, 9.0, 10.0]
+    windows[3, :6] = [V - 1, V - 2, V - 1, V - 3, V, V + 1]
+    settings.append(R.sampling(0.8, 5, 1.0, 0.0, 3.0, W, 4))
+    # 4: a penalty below 1 lifts a negative window logit toward 0, above the rest.
+    x[4] = -np.abs(x[4]) - 1.0
+    x[4, 5000] = -1.2; x[4, 9000] = -1.1
+    windows[4, :2] = [5000, 5000]
+    settings.append(R.sampling(0.5, 10, 0.9, 0.05, 0.25, W, 5))
+    # 5: a full window of random ids with min-p.
+    windows[5] = rng.integers(0, V, W)
+    x[5, windows[5]] += 4.0
+    settings.append(R.sampling(0.6, 64, 0.99, 0.02, 1.3, W, 6))
+    wlen = np.full(rows, W, np.uint32)
+    uniforms = rng.random(rows).astype(np.float32)
+    print("split rows with windows: V=%d chunks=%d" % (V, chunks), flush=True)
+    got, want = run_both(device, x, settings, windows, wlen, uniforms)
+    assert_match("split V=%d" % V, got, want, settings)
