@@ -327,8 +327,9 @@ __device__ __forceinline__ void process_tile(Stream &w, const f32x4 *T, uint32_t
 // past `end` were clamped (duplicates of the chunk's last element under other
 // ids) and are left out; a lane with none contributes nothing, and with fewer
 // than k contributing lanes t is 0 (no threshold).
+// Returns the sorted lane maxima (lane i: the i-th best).
 template <uint32_t U, uint32_t NT>
-__device__ __forceinline__ void bootstrap(Stream &w, const f32x4 *A, uint32_t base, uint32_t end) {
+__device__ __forceinline__ uint64_t bootstrap(Stream &w, const f32x4 *A, uint32_t base, uint32_t end) {
     const uint32_t tid = threadIdx.x;
     uint64_t bound = ~0ull, best = 0;
     for (uint32_t attempt = 0; attempt < 4; ++attempt) {
@@ -353,6 +354,7 @@ __device__ __forceinline__ void bootstrap(Stream &w, const f32x4 *A, uint32_t ba
     const uint64_t t = read_lane_u64(sorted, w.k - 1);
     raise_threshold(w, t ? t - 1 : 0ull);
     publish_threshold(w.shared_T, w.T);
+    return sorted;
 }
 
 // The workgroups sharing a CU are otherwise served oldest first: the first
@@ -610,6 +612,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     __shared__ uint64_t s_buf[NW * CBUF];
     __shared__ uint64_t s_T;
     __shared__ uint32_t s_cnt[NW];
+    __shared__ uint64_t s_lo;  // ONE_TILE: the chunk's bound from the bootstrap
     extern __shared__ __align__(16) uint8_t smem[];
     const WindowSet ws = window_set(smem, a.hash_bits);
     const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
@@ -682,6 +685,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     const bool pen = penalises(s) && wl > 0;
     RL_LDS uint64_t *lT = (RL_LDS uint64_t *)&s_T;
     if (tid == 0) *lT = 0;
+    if constexpr (ONE_TILE) {
+        if (tid == 0) s_lo = ~0ull;
+    }
     // The chunk's elements [e0, e1): the last chunk also holds the row's
     // last vocab % 4 elements.
     const uint32_t e0 = 4 * q0, e1 = chunk == a.chunks - 1 ? V : 4 * q1;
@@ -692,7 +698,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         if (pen) {
             const uint32_t nwords = (e1 - e0 + 31) / 32;
             for (uint32_t i = tid; i < nwords; i += NT) bm[i] = 0;
-            __syncthreads();
+        }
+        __syncthreads();  // the slots above are set, the bitmap is clear
+        if (pen) {
 #pragma unroll
             for (uint32_t j = 0; j < WIN_PER; ++j) {
                 const uint32_t id = wid[j];
@@ -743,7 +751,21 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
 
     // Wave priority falls as the row progresses (see set_progress_priority).
     __builtin_amdgcn_s_setprio(3);
-    if (ntiles > 0) bootstrap<U, NT>(w, A, q0, q1);
+    if (ntiles > 0) {
+        const uint64_t sorted = bootstrap<U, NT>(w, A, q0, q1);
+        if constexpr (ONE_TILE) {
+            // A bound for the whole chunk: every wave has at least
+            // ceil(k / NW) lane maxima (distinct elements) at or above its
+            // tq, so at least k elements of the chunk are at or above the
+            // least tq of the NW waves, and nothing below it is among the
+            // chunk's k best. Much tighter than one wave's k-th lane maximum.
+            const uint64_t tq = read_lane_u64(sorted, (k + NW - 1) / NW - 1);
+            if (lane == 0) (void)__hip_atomic_fetch_min(&s_lo, tq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __syncthreads();
+            const uint64_t tc = uniform_u64(__hip_atomic_load(&s_lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+            raise_threshold(w, tc ? tc - 1 : 0ull);
+        }
+    }
     if (ntiles <= 1) {
         // One tile or none (a chunk of a split row): nothing more to load.
         // The window's raw logits were loaded behind the tile, so they are
