@@ -819,19 +819,53 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         }
         offer_group<true>(w, f32x4{x, 0.f, 0.f, 0.f}, e, ok ? 1u : 0u);
     }
-    compact(w);
-    if (lane == 0) s_cnt[wave] = w.cnt;
-    __syncthreads();
+    // ONE_TILE: when the waves' buffers hold at most 64 candidates in all
+    // (the usual case under the chunk's bound), wave 0 sorts them together
+    // once, in place of a sort per wave and a merge per list.
+    bool gathered = false;
+    if constexpr (ONE_TILE) {
+        if (lane == 0) s_cnt[wave] = w.cnt;
+        __syncthreads();
+        uint32_t all = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < NW; ++j) all += s_cnt[j];
+        gathered = all <= WAVE;
+        if (!gathered) {
+            compact(w);
+            __syncthreads();  // every wave has read the counts
+            if (lane == 0) s_cnt[wave] = w.cnt;
+            __syncthreads();
+        }
+    } else {
+        compact(w);
+        if (lane == 0) s_cnt[wave] = w.cnt;
+        __syncthreads();
+    }
     __shared__ uint32_t s_last;
     if (wave == 0) {
-        // Merge the four sorted lists: lane i of list j is candidate i of wave j.
         const uint64_t *lb = (const uint64_t *)s_buf;
-        uint64_t top = lane < s_cnt[0] ? lb[lane] : 0ull;
-        uint32_t total = s_cnt[0];
+        uint64_t top;
+        uint32_t total;
+        if (ONE_TILE && gathered) {
+            // Lane i takes candidate i: wave j's follow wave j - 1's.
+            uint32_t at = 0, base = 0;
 #pragma unroll
-        for (uint32_t j = 1; j < NW; ++j) {
-            top = wave_merge64(top, ascending_from(lb + j * CBUF, s_cnt[j]));
-            total += s_cnt[j];
+            for (uint32_t j = 0; j < NW; ++j) {
+                const uint32_t c = s_cnt[j];
+                if (lane >= base && lane < base + c) at = j * CBUF + (lane - base);
+                base += c;
+            }
+            total = base;
+            top = wave_sort64<true>(lane < total ? lb[at] : 0ull);
+        } else {
+            // Merge the four sorted lists: lane i of list j is candidate i of wave j.
+            top = lane < s_cnt[0] ? lb[lane] : 0ull;
+            total = s_cnt[0];
+#pragma unroll
+            for (uint32_t j = 1; j < NW; ++j) {
+                top = wave_merge64(top, ascending_from(lb + j * CBUF, s_cnt[j]));
+                total += s_cnt[j];
+            }
         }
         // The window's ids with their penalised values, once per row.
         if (!ONE_TILE && pen && chunk == 0)
