@@ -28,6 +28,8 @@ thread_local std::string g_last_error;
 // full path's ids per thread). A call with a longer window stride runs on a
 // penalised copy of its rows (k_pen_copy, k_pen_window) with no window.
 constexpr uint32_t SET_WINDOW_MAX = 2048;
+static_assert(SET_WINDOW_MAX <= ONE_TILE_WIN_MAX, "the one-tile kernel marks every window the stream path takes");
+static_assert(ONE_TILE_U * ONE_TILE_THREADS == UNROLL * FAST_THREADS, "both stream instantiations have one tile size");
 // Vocabularies up to 2^21 ids (every index and count on the device paths
 // fits 32 bits with room to spare).
 constexpr uint32_t MAX_VOCAB = 1u << 21;
@@ -516,11 +518,11 @@ int rl_sampler_sample_rows(rl_sampler_ctx *ctx, const float *logits, uint64_t ro
         if (per <= STEP4) {
             wlds = std::max(wlds, (size_t)chunk_bitmap_words(4 * per + 3) * sizeof(uint32_t));
             if (vec)
-                hipLaunchKernelGGL((k_stream<true, UNROLL, FAST_THREADS, true>), grid, dim3(FAST_THREADS), wlds, st, s,
-                                   sc);
+                hipLaunchKernelGGL((k_stream<true, ONE_TILE_U, ONE_TILE_THREADS, true>), grid, dim3(ONE_TILE_THREADS),
+                                   wlds, st, s, sc);
             else
-                hipLaunchKernelGGL((k_stream<false, UNROLL, FAST_THREADS, true>), grid, dim3(FAST_THREADS), wlds, st, s,
-                                   sc);
+                hipLaunchKernelGGL((k_stream<false, ONE_TILE_U, ONE_TILE_THREADS, true>), grid, dim3(ONE_TILE_THREADS),
+                                   wlds, st, s, sc);
         } else if (vec) {
             hipLaunchKernelGGL((k_stream<true, UNROLL, FAST_THREADS>), grid, dim3(FAST_THREADS), wlds, st, s, sc);
         } else {

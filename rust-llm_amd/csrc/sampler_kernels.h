@@ -32,6 +32,13 @@ constexpr uint32_t FAST_THREADS = 256;
 constexpr uint32_t FAST_WAVES = FAST_THREADS / WAVE;
 constexpr uint32_t KMAX = 64;     // largest top_k the stream path takes (one per lane)
 constexpr uint32_t UNROLL = 8;    // float4 loads per thread per tile
+// The one-tile instantiation of the stream kernel: the same tile (NT * U
+// float4) over twice the waves, two a SIMD, so that each wave's filter,
+// bootstrap and sort have half the elements and a second wave to hide their
+// latency; and the longest window it marks in its bitmap.
+constexpr uint32_t ONE_TILE_THREADS = 512;
+constexpr uint32_t ONE_TILE_U = UNROLL * FAST_THREADS / ONE_TILE_THREADS;
+constexpr uint32_t ONE_TILE_WIN_MAX = 2048;
 constexpr uint32_t MAX_CHUNKS = 32;
 constexpr uint32_t FULL_THREADS = 256;
 constexpr uint32_t STAGE = 4096;  // elements staged in LDS per sequential block
@@ -612,7 +619,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     __shared__ uint64_t s_buf[NW * CBUF];
     __shared__ uint64_t s_T;
     __shared__ uint32_t s_cnt[NW];
-    __shared__ uint64_t s_lo;  // ONE_TILE: the chunk's bound from the bootstrap
+    __shared__ uint64_t s_tq[NW];  // ONE_TILE: each wave's candidate bound from the bootstrap
+    __shared__ uint32_t s_tn[NW];  // ONE_TILE: lane maxima of the chunk at or above s_tq[j]
     extern __shared__ __align__(16) uint8_t smem[];
     const WindowSet ws = window_set(smem, a.hash_bits);
     const uint32_t slot = blockIdx.y, chunk = blockIdx.x;
@@ -651,9 +659,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     const uint32_t *idp = have_win ? wrow + (tid < a.wstride ? tid : a.wstride - 1)
                                    : reinterpret_cast<const uint32_t *>(a.settings + row);
     // ONE_TILE loads the window's ids WIN_PER a thread (windows of up to
-    // WIN_PER * NT ids; longer ones never reach this kernel), clamped to the
-    // call's stride.
-    constexpr uint32_t WIN_PER = ONE_TILE ? 8 : 1;
+    // ONE_TILE_WIN_MAX ids; longer ones never reach this kernel), clamped to
+    // the call's stride.
+    constexpr uint32_t WIN_PER = ONE_TILE ? (ONE_TILE_WIN_MAX + NT - 1) / NT : 1;
     uint32_t wid[WIN_PER];
     if constexpr (ONE_TILE) {
         const uint32_t *wsrc = have_win ? wrow : reinterpret_cast<const uint32_t *>(a.settings + row);
@@ -686,7 +694,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     RL_LDS uint64_t *lT = (RL_LDS uint64_t *)&s_T;
     if (tid == 0) *lT = 0;
     if constexpr (ONE_TILE) {
-        if (tid == 0) s_lo = ~0ull;
+        if (tid < NW) s_tn[tid] = 0;
     }
     // The chunk's elements [e0, e1): the last chunk also holds the row's
     // last vocab % 4 elements.
@@ -754,15 +762,33 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     if (ntiles > 0) {
         const uint64_t sorted = bootstrap<U, NT>(w, A, q0, q1);
         if constexpr (ONE_TILE) {
-            // A bound for the whole chunk: every wave has at least
-            // ceil(k / NW) lane maxima (distinct elements) at or above its
-            // tq, so at least k elements of the chunk are at or above the
-            // least tq of the NW waves, and nothing below it is among the
-            // chunk's k best. Much tighter than one wave's k-th lane maximum.
+            // A bound for the whole chunk: any t with at least k of the
+            // chunk's lane maxima (distinct elements) at or above it is at
+            // most the chunk's k-th best, so nothing below it is among the
+            // chunk's k best. The candidates are each wave's ceil(k / NW)-th
+            // lane maximum tq (the least of them always qualifies: every
+            // wave has ceil(k / NW) lane maxima at or above it); each wave
+            // counts its lane maxima at or above every candidate, and the
+            // largest candidate with k in all is the bound. Much tighter
+            // than one wave's k-th lane maximum.
+            // Lane j < NW handles candidate j: one LDS read of the
+            // candidates, one atomic add of this wave's counts, one read of
+            // the totals.
             const uint64_t tq = read_lane_u64(sorted, (k + NW - 1) / NW - 1);
-            if (lane == 0) (void)__hip_atomic_fetch_min(&s_lo, tq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (lane == 0) s_tq[wave] = tq;
             __syncthreads();
-            const uint64_t tc = uniform_u64(__hip_atomic_load(&s_lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+            const uint64_t cand = lane < NW ? s_tq[lane] : 0ull;
+            uint32_t cnt = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < NW; ++j) {
+                const uint64_t t = read_lane_u64(cand, j);
+                const uint32_t c = (uint32_t)__popcll(ballot(sorted != 0 && sorted >= t));
+                cnt = lane == j ? c : cnt;
+            }
+            if (lane < NW && cnt) (void)__hip_atomic_fetch_add(&s_tn[lane], cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __syncthreads();
+            const bool qualifies = lane < NW && s_tn[lane] >= k;
+            const uint64_t tc = wave_max_u64(qualifies ? cand : 0ull);
             raise_threshold(w, tc ? tc - 1 : 0ull);
         }
     }
@@ -858,7 +884,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
             total = base;
             top = wave_sort64<true>(lane < total ? lb[at] : 0ull);
         } else {
-            // Merge the four sorted lists: lane i of list j is candidate i of wave j.
+            // Merge the NW sorted lists: lane i of list j is candidate i of wave j.
             top = lane < s_cnt[0] ? lb[lane] : 0ull;
             total = s_cnt[0];
 #pragma unroll
@@ -896,21 +922,24 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     if (a.chunks == 1) return;
     __syncthreads();
     if (!s_last) return;
-    // The last chunk of the row: every chunk's list is published. Each wave
-    // merges the lists j = wave (mod NW), all loaded at once, then wave
-    // 0 merges the four results and runs the tail. The lists are read with
-    // device-scope loads, which bypass this XCD's L2, issued after the
-    // arrival that saw every other chunk's.
+    // The last chunk of the row: every chunk's list is published. Each of
+    // the first FW waves merges the lists j = wave (mod FW), all loaded at
+    // once, then wave 0 merges their results and runs the tail (more waves
+    // would add more to wave 0's merges than they take off theirs). The
+    // lists are read with device-scope loads, which bypass this XCD's L2,
+    // issued after the arrival that saw every other chunk's.
     const uint64_t *lists = sc.chunk_cands + (uint64_t)slot * a.chunks * KMAX;
     const uint32_t *counts = sc.chunk_counts + slot * a.chunks;
-    // A many-row call (U == UNROLL) splits a row into at most MAX_CHUNKS.
-    constexpr uint32_t PER = (MAX_CHUNKS + NW - 1) / NW;
+    constexpr uint32_t FW = NW < 4 ? NW : 4;
+    const bool merging = FW == NW || wave < FW;
+    // A row is split into at most MAX_CHUNKS.
+    constexpr uint32_t PER = (MAX_CHUNKS + FW - 1) / FW;
     uint64_t v[PER];
     uint32_t n[PER];
 #pragma unroll
     for (uint32_t i = 0; i < PER; ++i) {
-        const uint32_t j = wave + NW * i;
-        const bool ok = j < a.chunks;
+        const uint32_t j = wave + FW * i;
+        const bool ok = merging && j < a.chunks;
         n[i] = ok ? __hip_atomic_load(counts + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
         v[i] = ok ? __hip_atomic_load(lists + (uint64_t)j * KMAX + (WAVE - 1 - lane), __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT)
@@ -920,7 +949,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     uint32_t total = 0;
 #pragma unroll
     for (uint32_t i = 0; i < PER; ++i) {
-        if (wave + NW * i >= a.chunks) break;
+        if (!merging || wave + FW * i >= a.chunks) break;
         top = wave_merge64(top, WAVE - 1 - lane < n[i] ? v[i] : 0ull);  // lane i: list[63 - i], ascending
         total += n[i];
     }
@@ -932,7 +961,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     if (wave != 0) return;
     total = s_cnt[0];
 #pragma unroll
-    for (uint32_t j = 1; j < NW; ++j) {
+    for (uint32_t j = 1; j < FW; ++j) {
         top = wave_merge64(top, part[j * WAVE + (WAVE - 1 - lane)]);
         total += s_cnt[j];
     }
