@@ -594,6 +594,100 @@ __device__ __forceinline__ uint64_t ascending_from(const uint64_t *list, uint32_
     return j < n ? list[j] : 0ull;
 }
 
+// Merges for lists of at most 32 entries (top-k <= 32), two to a wave: a
+// vector whose lanes 0-31 and 32-63 hold two independent sequences. half_merge
+// takes x with lists A (lanes 0-31) and C (32-63) descending and y with B and
+// D ascending, and returns the 32 best of A and B descending in lanes 0-31 and
+// of C and D ascending in lanes 32-63 (max(desc, asc) is bitonic and holds
+// the 32 best; one 32-lane merge network sorts both halves, five stages
+// against the six of a 64-lane merge, for two pairs at once). fold_halves
+// then merges the two halves: lanes 0-31 get the 32 best of both, in the
+// order DESC (lanes 32-63: the same set in the other order).
+__device__ __forceinline__ uint64_t half_merge(uint64_t x, uint64_t y) {
+    return bitonic_merge<32, 16, true>(x > y ? x : y);
+}
+template <bool DESC>
+__device__ __forceinline__ uint64_t fold_halves(uint64_t v) {
+    const uint64_t o = lane_xor64<32>(v);
+    return bitonic_merge<32, 16, DESC>(o > v ? o : v);
+}
+
+// The one-tile kernel's finishing chunk when every list holds at most 32
+// entries (k <= 32): the row's k best of the chunks' lists by half_merge and
+// fold_halves. Each of the first four waves takes the lists j = wave (mod 4)
+// in groups of four: a group is two loads a lane (lists 0 and 2 of the group
+// descending in x, 1 and 3 ascending in y), one half_merge and one fold;
+// the second group's result, folded ascending, merges into the first's.
+// Wave 0 then merges the four waves' results the same way. Ends with wave
+// 0's finalize_row; the other waves return.
+template <uint32_t NW>
+__device__ __forceinline__ void finish_top32(const RowIO &a, const FastScratch &sc, uint32_t slot, uint32_t row,
+                                             uint32_t k, uint32_t lane, uint32_t wave, uint64_t *part,
+                                             uint32_t *s_cnt, const rl_sampling &s, const WindowSet &ws, bool pen,
+                                             const float *rowp, uint64_t tab_v, float u_row, const uint32_t *wrow,
+                                             uint32_t wl) {
+    constexpr uint32_t FW = NW < 4 ? NW : 4;
+    constexpr uint32_t GROUPS = (MAX_CHUNKS + 4 * FW - 1) / (4 * FW);
+    const uint32_t C = a.chunks;
+    const uint64_t *lists = sc.chunk_cands + (uint64_t)slot * C * KMAX;
+    const uint32_t *counts = sc.chunk_counts + slot * C;
+    const bool merging = wave < FW;
+    const uint32_t h = lane >> 5, e = lane & 31u;
+    // List i of this wave (i = 4g + pos) is chunk wave + FW * i; lane l loads
+    // entry e (x, descending) or 31 - e (y, ascending) of list pos = 2h (x)
+    // or 2h + 1 (y).
+    uint64_t x[GROUPS], y[GROUPS];
+    uint32_t nx[GROUPS], ny[GROUPS];
+#pragma unroll
+    for (uint32_t g = 0; g < GROUPS; ++g) {
+        const uint32_t jx = wave + FW * (4 * g + 2 * h), jy = jx + FW;
+        const bool okx = merging && jx < C, oky = merging && jy < C;
+        nx[g] = okx ? __hip_atomic_load(counts + jx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+        ny[g] = oky ? __hip_atomic_load(counts + jy, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+        x[g] = okx ? __hip_atomic_load(lists + (uint64_t)jx * KMAX + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+        y[g] = oky ? __hip_atomic_load(lists + (uint64_t)jy * KMAX + (31u - e), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT)
+                   : 0ull;
+    }
+    uint32_t total = 0;
+    uint64_t top = 0;
+#pragma unroll
+    for (uint32_t g = 0; g < GROUPS; ++g) {
+        // Each list's count once: lane 0 holds lists 0 and 1 of the group, lane 32 lists 2 and 3.
+        total += read_lane_u32(nx[g] + ny[g], 0) + read_lane_u32(nx[g] + ny[g], 32);
+        const uint64_t xv = e < nx[g] ? x[g] : 0ull, yv = 31u - e < ny[g] ? y[g] : 0ull;
+        if (g == 0) {
+            top = fold_halves<true>(half_merge(xv, yv));
+        } else if (merging && wave + FW * 4 * g < C) {
+            const uint64_t r = fold_halves<false>(half_merge(xv, yv));
+            top = bitonic_merge<32, 16, true>(top > r ? top : r);
+        }
+    }
+    // The waves' results (lanes 0-31, descending) through LDS; wave 0 merges
+    // them as one group: results 0 and 2 descending, 1 and 3 ascending.
+    __syncthreads();  // the candidate buffers are free
+    if (lane < 32) part[wave * 32 + lane] = top;
+    if (lane == 0) s_cnt[wave] = total;
+    __syncthreads();
+    if (wave != 0) return;
+    uint32_t all = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < FW; ++j) all += s_cnt[j];
+    if constexpr (FW == 4) {
+        top = fold_halves<true>(half_merge(part[(2 * h) * 32 + e], part[(2 * h + 1) * 32 + (31u - e)]));
+    } else {
+#pragma unroll
+        for (uint32_t j = 1; j < FW; ++j) {
+            const uint64_t r = lane < 32 ? part[j * 32 + (31u - lane)] : 0ull;
+            top = bitonic_merge<32, 16, true>(top > r ? top : r);
+        }
+    }
+    if (lane == 0) sc.arrive[slot] = 0;  // ready for the next call
+    const uint32_t nL = all < k ? all : k;
+    if (lane >= nL) top = 0;
+    finalize_row<true>(a, row, s, k, top, nL, ws, pen, rowp, tab_v, u_row, wrow, wl);
+}
+
 // LDS words of a bitmap over a chunk of at most `elems` elements (one word
 // more: a chunk that starts mid-word never reads past it).
 __host__ __device__ constexpr uint32_t chunk_bitmap_words(uint32_t elems) { return (elems + 31) / 32 + 1; }
@@ -882,7 +976,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
                 base += c;
             }
             total = base;
-            top = wave_sort64<true>(lane < total ? lb[at] : 0ull);
+            const uint64_t c = lane < total ? lb[at] : 0ull;
+            // Up to 32: a 32-lane network (lanes 32-63 hold zeros).
+            top = total <= 32 ? bitonic_sort<32, true>(c) : wave_sort64<true>(c);
         } else {
             // Merge the NW sorted lists: lane i of list j is candidate i of wave j.
             top = lane < s_cnt[0] ? lb[lane] : 0ull;
@@ -922,6 +1018,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     if (a.chunks == 1) return;
     __syncthreads();
     if (!s_last) return;
+    if constexpr (ONE_TILE) {
+        if (k <= 32) {
+            finish_top32<NW>(a, sc, slot, row, k, lane, wave, (uint64_t *)s_buf, s_cnt, s, ws, pen, rowp, tab_v, u_row,
+                             wrow, wl);
+            return;
+        }
+    }
     // The last chunk of the row: every chunk's list is published. Each of
     // the first FW waves merges the lists j = wave (mod FW), all loaded at
     // once, then wave 0 merges their results and runs the tail (more waves

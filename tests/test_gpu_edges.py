@@ -378,3 +378,23 @@ def test_split_rows_with_windows(device, V):
     print("split rows with windows: V=%d chunks=%d" % (V, chunks), flush=True)
     got, want = run_both(device, x, settings, windows, wlen, uniforms)
     assert_match("split V=%d" % V, got, want, settings)
+
+
+@pytest.mark.parametrize("V", [9000, 16400, 40000, 100003, 248320])
+def test_split_rows_across_chunk_counts(device, V):
+    """Rows split into 2 to 31 one-tile chunks, with top-k on both sides of
+    32 (lists of at most 32 entries are merged two to a wave), a penalty
+    window and ties at the top."""
+    rng = np.random.default_rng(V)
+    ks = [1, 5, 20, 32, 33, 64]
+    rows, W = len(ks), 16
+    x = rng.normal(0.0, 2.0, (rows, V)).astype(np.float32)
+    x[:, rng.choice(V, 48, replace=False)] = 9.0  # ties among the best
+    windows = rng.integers(0, V, (rows, W)).astype(np.uint32)
+    settings = [R.sampling(0.8, k, 0.97, 0.0, 1.4 if k % 2 else 1.0, W, 10 + k) for k in ks]
+    wlen = np.full(rows, W, np.uint32)
+    uniforms = rng.random(rows).astype(np.float32)
+    chunks = min(1024 // rows, 32, -(-(V // 4) // 2048))
+    print("split rows: V=%d chunks=%d" % (V, chunks), flush=True)
+    got, want = run_both(device, x, settings, windows, wlen, uniforms)
+    assert_match("chunks V=%d" % V, got, want, settings)
