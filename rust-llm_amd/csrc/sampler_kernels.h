@@ -635,16 +635,21 @@ __device__ __forceinline__ void finish_top32(const RowIO &a, const FastScratch &
     const uint32_t h = lane >> 5, e = lane & 31u;
     // List i of this wave (i = 4g + pos) is chunk wave + FW * i; lane l loads
     // entry e (x, descending) or 31 - e (y, ascending) of list pos = 2h (x)
-    // or 2h + 1 (y).
+    // or 2h + 1 (y). A later group holding one list only (`single`) is
+    // loaded ascending into lanes 0-31 instead and merged into the first
+    // group's result directly.
     uint64_t x[GROUPS], y[GROUPS];
     uint32_t nx[GROUPS], ny[GROUPS];
+    bool single[GROUPS];
 #pragma unroll
     for (uint32_t g = 0; g < GROUPS; ++g) {
         const uint32_t jx = wave + FW * (4 * g + 2 * h), jy = jx + FW;
+        single[g] = g > 0 && wave + FW * (4 * g + 1) >= C;
         const bool okx = merging && jx < C, oky = merging && jy < C;
+        const uint32_t ex = single[g] ? 31u - e : e;
         nx[g] = okx ? __hip_atomic_load(counts + jx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
         ny[g] = oky ? __hip_atomic_load(counts + jy, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
-        x[g] = okx ? __hip_atomic_load(lists + (uint64_t)jx * KMAX + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+        x[g] = okx ? __hip_atomic_load(lists + (uint64_t)jx * KMAX + ex, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
         y[g] = oky ? __hip_atomic_load(lists + (uint64_t)jy * KMAX + (31u - e), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT)
                    : 0ull;
@@ -655,9 +660,14 @@ __device__ __forceinline__ void finish_top32(const RowIO &a, const FastScratch &
     for (uint32_t g = 0; g < GROUPS; ++g) {
         // Each list's count once: lane 0 holds lists 0 and 1 of the group, lane 32 lists 2 and 3.
         total += read_lane_u32(nx[g] + ny[g], 0) + read_lane_u32(nx[g] + ny[g], 32);
-        const uint64_t xv = e < nx[g] ? x[g] : 0ull, yv = 31u - e < ny[g] ? y[g] : 0ull;
+        const uint64_t xv = (single[g] ? 31u - e : e) < nx[g] ? x[g] : 0ull, yv = 31u - e < ny[g] ? y[g] : 0ull;
         if (g == 0) {
             top = fold_halves<true>(half_merge(xv, yv));
+        } else if (single[g]) {
+            if (merging && wave + FW * 4 * g < C) {
+                const uint64_t r = lane < 32 ? xv : 0ull;
+                top = bitonic_merge<32, 16, true>(top > r ? top : r);
+            }
         } else if (merging && wave + FW * 4 * g < C) {
             const uint64_t r = fold_halves<false>(half_merge(xv, yv));
             top = bitonic_merge<32, 16, true>(top > r ? top : r);
