@@ -207,6 +207,26 @@ __device__ __forceinline__ uint64_t bitonic_stage(uint64_t v) {
     return (keep_max == o_big) ? o : v;
 }
 
+// The same network on 32-bit values, whose compare-exchange is one max and
+// one min: sorts one u32 per lane descending across the wave.
+template <uint32_t SIZE, uint32_t STRIDE>
+__device__ __forceinline__ uint32_t bitonic_merge_u32(uint32_t v) {
+    const uint32_t lane = lane_id();
+    const uint32_t o = lane_xor<STRIDE>(v);
+    const bool lower = (lane & STRIDE) == 0;
+    const bool block_desc = (lane & SIZE) == 0 || SIZE == WAVE;
+    const uint32_t hi = v > o ? v : o, lo = v > o ? o : v;
+    v = lower == block_desc ? hi : lo;
+    if constexpr (STRIDE > 1) v = bitonic_merge_u32<SIZE, STRIDE / 2>(v);
+    return v;
+}
+template <uint32_t SIZE>
+__device__ __forceinline__ uint32_t bitonic_sort_u32(uint32_t v) {
+    if constexpr (SIZE > 2) v = bitonic_sort_u32<SIZE / 2>(v);
+    return bitonic_merge_u32<SIZE, SIZE / 2>(v);
+}
+__device__ __forceinline__ uint32_t wave_sort_u32_desc(uint32_t v) { return bitonic_sort_u32<WAVE>(v); }
+
 template <uint32_t SIZE, uint32_t STRIDE, bool DESC>
 __device__ __forceinline__ uint64_t bitonic_merge(uint64_t v) {
     v = bitonic_stage<SIZE, STRIDE, DESC>(v);

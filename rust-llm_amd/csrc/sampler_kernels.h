@@ -364,6 +364,35 @@ __device__ __forceinline__ uint64_t bootstrap(Stream &w, const f32x4 *A, uint32_
     return sorted;
 }
 
+// The one-tile kernel's bootstrap, on 32-bit keys: each lane's largest key
+// over its elements of the tile (the filter's order refines keys by id, so
+// every element with a key at or above key t has a composite at or above
+// t << 32), and the 64 lane maxima sorted descending across the wave by a
+// bitonic network of max and min, half the instructions of one on 64-bit
+// composites. Loads at or past `end` (clamped) and, in greedy mode, -inf and
+// NaN are left out; a lane with nothing keeps key 0, which no element's
+// composite bound uses. Raises the wave's threshold to the k-th lane maximum's
+// key (at least k elements are at or above it) and returns the sorted keys.
+template <uint32_t U, uint32_t NT>
+__device__ __forceinline__ uint32_t bootstrap_keys(Stream &w, const f32x4 *A, uint32_t base, uint32_t end) {
+    uint32_t best = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+        const float x[4] = {A[u].x, A[u].y, A[u].z, A[u].w};
+        const bool in = base + u * NT + threadIdx.x < end;
+#pragma unroll
+        for (uint32_t c = 0; c < 4; ++c) {
+            const bool ok = in && (!w.greedy || x[c] >= -3.40282347e38f);
+            const uint32_t key = stream_key(w, x[c]);
+            best = ok && key > best ? key : best;
+        }
+    }
+    const uint32_t sorted = wave_sort_u32_desc(best);
+    const uint32_t t = read_lane_u32(sorted, w.k - 1);
+    raise_threshold(w, t ? ((uint64_t)t << 32) - 1 : 0ull);
+    return sorted;
+}
+
 // The workgroups sharing a CU are otherwise served oldest first: the first
 // one dispatched finishes its row long before the last, and the CU then
 // streams with fewer and fewer waves. Lowering a wave's priority as its row
@@ -723,7 +752,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     __shared__ uint64_t s_buf[NW * CBUF];
     __shared__ uint64_t s_T;
     __shared__ uint32_t s_cnt[NW];
-    __shared__ uint64_t s_tq[NW];  // ONE_TILE: each wave's candidate bound from the bootstrap
+    __shared__ uint32_t s_tq[NW];  // ONE_TILE: each wave's candidate bound (a key) from the bootstrap
     __shared__ uint32_t s_tn[NW];  // ONE_TILE: lane maxima of the chunk at or above s_tq[j]
     extern __shared__ __align__(16) uint8_t smem[];
     const WindowSet ws = window_set(smem, a.hash_bits);
@@ -864,7 +893,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     // Wave priority falls as the row progresses (see set_progress_priority).
     __builtin_amdgcn_s_setprio(3);
     if (ntiles > 0) {
-        const uint64_t sorted = bootstrap<U, NT>(w, A, q0, q1);
         if constexpr (ONE_TILE) {
             // A bound for the whole chunk: any t with at least k of the
             // chunk's lane maxima (distinct elements) at or above it is at
@@ -877,23 +905,26 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
             // than one wave's k-th lane maximum.
             // Lane j < NW handles candidate j: one LDS read of the
             // candidates, one atomic add of this wave's counts, one read of
-            // the totals.
-            const uint64_t tq = read_lane_u64(sorted, (k + NW - 1) / NW - 1);
+            // the totals. Keys, as in bootstrap_keys.
+            const uint32_t sorted = bootstrap_keys<U, NT>(w, A, q0, q1);
+            const uint32_t tq = read_lane_u32(sorted, (k + NW - 1) / NW - 1);
             if (lane == 0) s_tq[wave] = tq;
             __syncthreads();
-            const uint64_t cand = lane < NW ? s_tq[lane] : 0ull;
+            const uint32_t cand = lane < NW ? s_tq[lane] : 0u;
             uint32_t cnt = 0;
 #pragma unroll
             for (uint32_t j = 0; j < NW; ++j) {
-                const uint64_t t = read_lane_u64(cand, j);
+                const uint32_t t = read_lane_u32(cand, j);
                 const uint32_t c = (uint32_t)__popcll(ballot(sorted != 0 && sorted >= t));
                 cnt = lane == j ? c : cnt;
             }
             if (lane < NW && cnt) (void)__hip_atomic_fetch_add(&s_tn[lane], cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             __syncthreads();
             const bool qualifies = lane < NW && s_tn[lane] >= k;
-            const uint64_t tc = wave_max_u64(qualifies ? cand : 0ull);
-            raise_threshold(w, tc ? tc - 1 : 0ull);
+            const uint32_t tc = wave_fold_u32(qualifies ? cand : 0u, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
+            raise_threshold(w, tc ? ((uint64_t)tc << 32) - 1 : 0ull);
+        } else {
+            (void)bootstrap<U, NT>(w, A, q0, q1);
         }
     }
     if (ntiles <= 1) {
