@@ -211,7 +211,8 @@ __device__ __forceinline__ bool finish_wave(const RowIO &a, uint32_t row, const 
     const uint32_t lane = lane_id();
     const bool in = lane < c;
     const float u = a.uniforms[row];
-    x = wave_sort64<true>(in ? x : 0ull);
+    // Up to 32 survivors: a 32-lane network (lanes 32-63 hold zeros).
+    x = c <= 32 ? bitonic_sort<32, true>(in ? x : 0ull) : wave_sort64<true>(in ? x : 0ull);
     const uint32_t key = keep_key(x, by_id);
     const uint32_t id = keep_id(x, by_id);
     const float p = in ? expf_libm_t((key_value(key) - M) / s.temperature, etab) : 0.0f;
