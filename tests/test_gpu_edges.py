@@ -398,3 +398,21 @@ def test_split_rows_across_chunk_counts(device, V):
     print("split rows: V=%d chunks=%d" % (V, chunks), flush=True)
     got, want = run_both(device, x, settings, windows, wlen, uniforms)
     assert_match("chunks V=%d" % V, got, want, settings)
+
+
+@pytest.mark.parametrize("k", [1, 20, 32, 64])
+def test_split_rows_of_ties(device, k):
+    """Rows split into 19 one-tile chunks where a third of every chunk ties
+    at the top value: the chunk's bound admits every tied element, each
+    wave's buffer overflows and compacts, the candidates exceed one wave's
+    sort, and the lists' order among equal keys is by id."""
+    rng = np.random.default_rng(k)
+    V, rows, W = 151936, 3, 8
+    x = random_rows(rng, rows, V, "ties")
+    windows = rng.integers(0, V, (rows, W)).astype(np.uint32)
+    settings = [R.sampling(1.0, k, 0.9, 0.0, pen, W, 100 + k) for pen in (1.0, 1.3, 0.7)]
+    wlen = np.full(rows, W, np.uint32)
+    uniforms = rng.random(rows).astype(np.float32)
+    print("split ties: k=%d" % k, flush=True)
+    got, want = run_both(device, x, settings, windows, wlen, uniforms)
+    assert_match("ties k=%d" % k, got, want, settings)
