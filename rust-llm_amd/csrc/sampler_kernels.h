@@ -943,6 +943,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
             w.wtop = window_top(ws);
         }
     } else if constexpr (!ONE_TILE) {
+        // Tile 1 goes out before the window's raw logits are stored, so the
+        // store's wait covers the gather alone and the memory pipe stays full.
+        load_tile_clamped<VEC, U, NT>(B, rowp, q0 + STEP, q1);
         if (my_slot != EMPTY_ID) window_store(ws, my_slot, my_id, my_raw);
         __syncthreads();
         w.wtop = window_top(ws);
@@ -951,7 +954,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         // wave), so the last, partial tile runs through the same loop.
         for (uint32_t t = 0; t < ntiles; t += 2) {
             const uint32_t b0 = q0 + t * STEP, b1 = b0 + STEP;
-            load_tile_clamped<VEC, U, NT>(B, rowp, b1, q1);
             if (t < nfull)
                 process_tile<false, U, NT>(w, A, b0, q1);
             else
@@ -961,6 +963,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
                 process_tile<false, U, NT>(w, B, b1, q1);
             else if (t + 1 < ntiles)
                 process_tile<true, U, NT>(w, B, b1, q1);
+            load_tile_clamped<VEC, U, NT>(B, rowp, b1 + 2 * STEP, q1);
             raise_threshold(w, load_shared_T(lT));
             set_progress_priority(t + 2, ntiles);
         }
