@@ -2,17 +2,15 @@
 // argmax (sample.rs:118-128) of the penalised row (:239-257) and draw nothing.
 //
 // One launch. Each chunk of a row scans its logits for the largest argmax
-// composite (argmax_key, then the lowest id), leaving out the row's window
-// ids; chunk 0 adds the window ids' penalised values. A window id's raw
-// logit is replaced by its penalised one in the reference's vector, so the
-// row's argmax is the larger of the two maxima. A chunk's best goes to the
-// row's slot by a 64-bit atomic max, and the row's last chunk to arrive (a
-// per-row counter) writes the token: kept 1, candidate (token, 1.0), no
-// uniform used. Slot and counter are zero between calls.
-//
-// The exclusion costs a look-up only when an element beats its lane's best
-// so far (a few times per lane): window ids in the chunk are bits of an LDS
-// bitmap over the chunk's elements.
+// composite (argmax_key, then the lowest id) of the penalised row: the window
+// ids that fall in the chunk are bits of an LDS bitmap over its elements, and
+// their logits are penalised in registers as they are scanned (the four bits
+// of a float4 sit in one word: one LDS read a float4), as the reference
+// replaces them in its vector, each id once however often the window repeats
+// it. A chunk's best goes to the row's slot by a 64-bit atomic max, and the
+// row's last chunk to arrive (a per-row counter) writes the token: kept 1,
+// candidate (token, 1.0), no uniform used. Slot and counter are zero between
+// calls.
 #pragma once
 #include "sampler_kernels.h"
 
@@ -47,7 +45,8 @@ __global__ __launch_bounds__(FAST_THREADS) void k_greedy(RowIO a, GreedyScratch 
     // length (one vector load), the window's ids (clamped to the call's
     // stride; which of them count is decided once the length is in), then
     // the first tile. A chunk with no float4 loads 16 bytes of its row's
-    // settings instead, with no branch around the loads.
+    // settings instead, with no branch around the loads. No window logit is
+    // gathered: the penalty is applied to the tile's own registers.
     const uint32_t head_w = row_words(a, row);
     const bool have_win = a.windows && a.wlen && a.wstride > 0;
     const uint32_t *wrow = have_win ? a.windows + (uint64_t)row * a.wstride
@@ -65,15 +64,6 @@ __global__ __launch_bounds__(FAST_THREADS) void k_greedy(RowIO a, GreedyScratch 
     {
         const bool any = q1 > q0;
         load_tile_clamped<VEC>(A, any ? rowp : (const float *)(a.settings + row), any ? q0 : 0u, any ? q1 : 1u);
-    }
-    // Chunk 0 gathers the window ids' raw logits now (clamped ids: no branch
-    // on the row's settings), behind the tile, for the penalised values it
-    // adds after its scan.
-    float wraw[GREEDY_WIN_PER];
-    if (chunk == 0 && have_win) {
-#pragma unroll
-        for (uint32_t k = 0; k < GREEDY_WIN_PER; ++k)
-            wraw[k] = ((const RL_GLB float *)rowp)[wid[k] < V ? wid[k] : V - 1];
     }
     __builtin_amdgcn_sched_barrier(0);
     rl_sampling s;
@@ -98,14 +88,23 @@ __global__ __launch_bounds__(FAST_THREADS) void k_greedy(RowIO a, GreedyScratch 
 
     // The scan: a lane's elements in ascending id order, so a strictly larger
     // composite is the only update (ties keep the lower id by the composite
-    // itself); a window id is looked up only when it would be an update.
+    // itself); window ids take their penalised values first.
     uint64_t best = 0;
     auto take = [&](const f32x4 &v, uint32_t f, bool ok) {
-        const float x[4] = {v.x, v.y, v.z, v.w};
+        float x[4] = {v.x, v.y, v.z, v.w};
+        if (pen && ok) {
+            const uint32_t r = 4 * f - e0;
+            const uint32_t bits = (bm[r >> 5] >> (r & 31)) & 0xFu;
+            if (bits) {
+#pragma unroll
+                for (uint32_t c = 0; c < 4; ++c)
+                    if ((bits >> c) & 1u) x[c] = penalize(x[c], s.repeat_penalty);
+            }
+        }
 #pragma unroll
         for (uint32_t c = 0; c < 4; ++c) {
             const uint64_t cc = ok ? composite(argmax_key(x[c]), 4 * f + c) : 0ull;
-            if (cc > best && !(pen && windowed(4 * f + c))) best = cc;
+            if (cc > best) best = cc;
         }
     };
     if (q1 > q0) {
@@ -123,21 +122,10 @@ __global__ __launch_bounds__(FAST_THREADS) void k_greedy(RowIO a, GreedyScratch 
     if (chunk == a.chunks - 1) {  // the row's last vocab % 4 elements
         const uint32_t e = 4 * n4 + tid;
         if (e < V) {
-            const uint64_t cc = composite(argmax_key(((const RL_GLB float *)rowp)[e]), e);
-            if (cc > best && !(pen && windowed(e))) best = cc;
-        }
-    }
-    if (pen && chunk == 0) {
-        // The window ids' penalised logits (each id once or more: the
-        // maximum does not care).
-#pragma unroll
-        for (uint32_t k = 0; k < GREEDY_WIN_PER; ++k) {
-            const uint32_t id = wid[k];
-            if (k * FAST_THREADS + tid < wl && id < V) {
-                const float v = penalize(wraw[k], s.repeat_penalty);
-                const uint64_t cc = composite(argmax_key(v), id);
-                best = cc > best ? cc : best;
-            }
+            float x = ((const RL_GLB float *)rowp)[e];
+            if (pen && windowed(e)) x = penalize(x, s.repeat_penalty);
+            const uint64_t cc = composite(argmax_key(x), e);
+            if (cc > best) best = cc;
         }
     }
     best = wave_max_u64(best);
